@@ -1,0 +1,473 @@
+/* e2_oracle.c — CPU restatement of the reference's int8 kernels (test infrastructure only).
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load this library. It is the
+ * checker the HIP kernels are compared with; it is never part of the product path.
+ *
+ * Built WITHOUT -ffast-math and with -ffp-contract=off (see oracle/Makefile) so every rounding step
+ * below is the one written. Where the reference was built with -ffast-math, the step restated is the
+ * one GCC emitted for it (inspected in the x86 assembly of oracle/_ref, built here from source).
+ *
+ * Parity status (how each function is pinned; the tests named are under tests/):
+ *   or_q8w_from_f32/pack/unpack  — bit-exact vs oracle/_ref e2_q8w_from_f32 + layout closed form
+ *                                   (test_oracle_ref.py), golden vectors (test_oracle_golden.py)
+ *   or_quantize                  — bit-exact vs _ref e2_quantize_blocks_avx512 and _scalar on random,
+ *                                   outlier, zero and tie-breaking rows; golden vectors
+ *   or_i8_gemm / _acc / _mt      — int32: brute-force integer dot (order independent); f32: bit-exact
+ *                                   vs _ref e2_i8_gemm_avx512; golden vectors
+ *   or_i8_gemm_scalar            — within 1e-5 of _ref e2_i8_gemm_scalar (its fold is mul+add)
+ *   or_gelu_tanh / mul_quant     — GELU within 3e-6 of a double-precision GELU (test_softmax.c:52
+ *                                   bar); quant bytes exact given the f32 values (closed form)
+ *   or_rmsnorm / split / add     — within 1e-6 rel of _ref's AVX-512 vtable (it uses rsqrtss+NR)
+ *   or_rope_*                    — closed form vs a double-precision rotation; _ref has no exported
+ *                                   table builder (text.c rope_init is static): table pinned by
+ *                                   the formula test
+ *   or_softmax / or_attention    — softmax within 3e-7 of double (test_softmax.c:33); attention vs
+ *                                   a float64 brute force (test_oracle_attention.py)
+ *   or_meanpool / or_l2norm      — within 1e-6 of _ref e2_meanpool_f32 / e2_l2norm_f32
+ *   or_embed                     — closed form
+ *   text recipe (e2_oracle_model.c) — composed of the above; layer order restated from text.c:939-984
+ */
+#define _GNU_SOURCE
+#include "e2_oracle.h"
+
+#include <immintrin.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* RN(1/127) = 0x3c010204: the constant GCC folds amax/127.0f into under -freciprocal-math. */
+static float inv127(void) {
+    union { uint32_t u; float f; } c = { 0x3c010204u };
+    return c.f;
+}
+
+/* ------------------------------------------------------------------ weights (int8.c:19-66) */
+int or_q8w_from_f32(const float *w, int N, int K, int8_t *wq, float *scale, int32_t *bsq) {
+    const int nb = (K + 127) / 128, kq = (K + 3) / 4, Npad = (N + 7) & ~7;
+    memset(wq, 0, (size_t)(Npad / 8) * kq * 32);
+    memset(scale, 0, sizeof(float) * (size_t)Npad);
+    memset(bsq, 0, sizeof(int32_t) * (size_t)nb * Npad);
+    for (int n = 0; n < N; n++) {
+        const float *row = w + (size_t)n * K;
+        float amax = 0.f;
+        for (int k = 0; k < K; k++) {
+            const float a = fabsf(row[k]);
+            if (a > amax) amax = a;
+        }
+        /* int8.c:41-42 as compiled: amax*RN(1/127) and 127/amax */
+        const float sc = amax > 0.f ? amax * inv127() : 1.0f;
+        const float inv = amax > 0.f ? 127.0f / amax : 1.0f;
+        for (int b = 0; b < nb; b++) {
+            int32_t sum = 0;
+            const int k1 = (b + 1) * 128 < K ? (b + 1) * 128 : K;
+            for (int k = b * 128; k < k1; k++) {
+                long r = lrintf(row[k] * inv);
+                if (r > 127) r = 127;
+                if (r < -127) r = -127;
+                wq[(size_t)(n >> 3) * kq * 32 + (size_t)(k >> 2) * 32 + (n & 7) * 4 + (k & 3)] =
+                    (int8_t)r;
+                sum += (int32_t)r;
+            }
+            bsq[(size_t)b * Npad + n] = sum;
+        }
+        scale[n] = sc;
+    }
+    return 0;
+}
+
+/* [N/8][K/4][8][4] -> [N][K] (the layout formula of int8.h:17) */
+void or_q8w_unpack(const int8_t *wq, int N, int K, int8_t *rm) {
+    const int kq = (K + 3) / 4;
+    for (int n = 0; n < N; n++)
+        for (int k = 0; k < K; k++)
+            rm[(size_t)n * K + k] =
+                wq[(size_t)(n >> 3) * kq * 32 + (size_t)(k >> 2) * 32 + (n & 7) * 4 + (k & 3)];
+}
+
+void or_q8w_pack(const int8_t *rm, int N, int K, int8_t *wq, int32_t *bsq) {
+    const int nb = (K + 127) / 128, kq = (K + 3) / 4, Npad = (N + 7) & ~7;
+    memset(wq, 0, (size_t)(Npad / 8) * kq * 32);
+    memset(bsq, 0, sizeof(int32_t) * (size_t)nb * Npad);
+    for (int n = 0; n < N; n++)
+        for (int k = 0; k < K; k++) {
+            const int8_t v = rm[(size_t)n * K + k];
+            wq[(size_t)(n >> 3) * kq * 32 + (size_t)(k >> 2) * 32 + (n & 7) * 4 + (k & 3)] = v;
+            bsq[(size_t)(k / 128) * Npad + n] += v;
+        }
+}
+
+/* ------------------------------------------------------------------ quantizer */
+/* One (row, block): the arithmetic of kernels_i8_avx512_vnni.c:321-363 as compiled. Saturation is
+ * the packs instruction's [-128,127]; |x*inv| <= 127 * (1 + 2^-23) so it never triggers. */
+static void quant_block(const float *x, int n, int8_t *q, float *sc_out) {
+    float amax = 0.f;
+    for (int k = 0; k < n; k++) {
+        const float a = fabsf(x[k]);
+        if (a > amax) amax = a;
+    }
+    const float sc = amax > 0.f ? amax * inv127() : 1.0f;
+    const float inv = amax > 0.f ? 127.0f / amax : 1.0f;
+    for (int k = 0; k < n; k++) {
+        float r = rintf(x[k] * inv);
+        if (r > 127.f) r = 127.f;
+        if (r < -128.f) r = -128.f;
+        q[k] = (int8_t)r;
+    }
+    *sc_out = sc;
+}
+
+void or_quantize(const float *x, int M, int K, int ldx, int block, int8_t *q, float *scales) {
+    const int nb = (K + block - 1) / block;
+    for (int m = 0; m < M; m++)
+        for (int b = 0; b < nb; b++) {
+            const int k0 = b * block, n = (k0 + block < K ? k0 + block : K) - k0;
+            quant_block(x + (size_t)m * ldx + k0, n, q + (size_t)m * K + k0,
+                        scales + (size_t)m * nb + b);
+        }
+}
+
+/* ------------------------------------------------------------------ int8 GEMM */
+void or_i8_gemm_acc(const int8_t *qa, const int8_t *w, int M, int N, int K, int block,
+                    int32_t *acc) {
+    const int nb = (K + block - 1) / block;
+    for (int b = 0; b < nb; b++) {
+        const int k0 = b * block, k1 = k0 + block < K ? k0 + block : K;
+        for (int m = 0; m < M; m++)
+            for (int n = 0; n < N; n++) {
+                int32_t s = 0;
+                const int8_t *a = qa + (size_t)m * K, *wr = w + (size_t)n * K;
+                for (int k = k0; k < k1; k++) s += (int32_t)a[k] * (int32_t)wr[k];
+                acc[((size_t)b * M + m) * N + n] = s;
+            }
+    }
+}
+
+void or_i8_gemm(const int8_t *qa, const float *as, const int8_t *w, const float *ws,
+                const float *bias, int M, int N, int K, int block, float lo, float hi, float *y) {
+    const int nb = (K + block - 1) / block;
+    for (int m = 0; m < M; m++) {
+        const int8_t *a = qa + (size_t)m * K;
+        for (int n = 0; n < N; n++) {
+            const int8_t *wr = w + (size_t)n * K;
+            float f = 0.f;
+            for (int b = 0; b < nb; b++) {
+                const int k0 = b * block, k1 = k0 + block < K ? k0 + block : K;
+                int32_t s = 0;
+                for (int k = k0; k < k1; k++) s += (int32_t)a[k] * (int32_t)wr[k];
+                const float sc = as[(size_t)m * nb + b] * ws[n];
+                f = fmaf((float)s, sc, f);
+            }
+            if (bias) f = f + bias[n];
+            f = f < lo ? lo : (f > hi ? hi : f);
+            y[(size_t)m * N + n] = f;
+        }
+    }
+}
+
+void or_i8_gemm_scalar(const int8_t *qa, const float *as, const int8_t *w, const float *ws, int M,
+                       int N, int K, float *y) {
+    const int nb = (K + 127) / 128;
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            float f = 0.f;
+            for (int b = 0; b < nb; b++) {
+                const int k1 = (b + 1) * 128 < K ? (b + 1) * 128 : K;
+                int32_t s = 0;
+                for (int k = b * 128; k < k1; k++)
+                    s += (int32_t)qa[(size_t)m * K + k] * (int32_t)w[(size_t)n * K + k];
+                f += (float)s * (as[(size_t)m * nb + b] * ws[n]);
+            }
+            y[(size_t)m * N + n] = f;
+        }
+}
+
+/* ------------------------------------------------------------------ fork-join pool (threads.c)
+ * A claim counter shared by short-lived workers: the same work-claiming model as the reference's
+ * persistent pool (threads.c:143-160), without its persistence, which the oracle does not need. */
+typedef void (*or_task_fn)(void *arg, int item);
+typedef struct {
+    or_task_fn fn;
+    void *arg;
+    int n;
+    _Atomic int next;
+} or_job;
+
+static void *or_worker(void *p) {
+    or_job *j = p;
+    for (;;) {
+        const int i = atomic_fetch_add_explicit(&j->next, 1, memory_order_relaxed);
+        if (i >= j->n) break;
+        j->fn(j->arg, i);
+    }
+    return NULL;
+}
+
+static void or_parallel(or_task_fn fn, void *arg, int n, int nthreads) {
+    or_job j = { fn, arg, n, 0 };
+    if (nthreads <= 1 || n <= 1) {
+        or_worker(&j);
+        return;
+    }
+    if (nthreads > 64) nthreads = 64;
+    pthread_t th[64];
+    int started = 0;
+    for (int t = 1; t < nthreads; t++)
+        if (pthread_create(&th[started], NULL, or_worker, &j) == 0) started++;
+    or_worker(&j);
+    for (int t = 0; t < started; t++) pthread_join(th[t], NULL);
+}
+
+/* ---- threaded VNNI GEMM. Same fold as or_i8_gemm, computed with vpdpbusd on biased activations
+ * (u8 = q + 128) and the 128 * sum(w) correction, 16 output columns x 8 tokens per register tile. */
+typedef struct {
+    const uint8_t *ab;   /* biased activations [M][K] */
+    const float *as;
+    const int8_t *wp;    /* [K/4][Np][4] */
+    const int32_t *bz;   /* [nb][Np] */
+    const float *ws, *bias;
+    float *y;
+    int M, N, K, Np, nb;
+} vnni_task;
+
+static void vnni_cols16(void *arg, int item) {
+    const vnni_task *t = arg;
+    const int n0 = item * 16, nn = t->N - n0 < 16 ? t->N - n0 : 16;
+    const __mmask16 nm = (__mmask16)(nn == 16 ? 0xffffu : ((1u << nn) - 1u));
+    const __m512 wsv = _mm512_maskz_loadu_ps(nm, t->ws + n0);
+    const __m512 bv = t->bias ? _mm512_maskz_loadu_ps(nm, t->bias + n0) : _mm512_setzero_ps();
+    for (int m0 = 0; m0 < t->M; m0 += 8) {
+        const int mm = t->M - m0 < 8 ? t->M - m0 : 8;
+        __m512 f[8];
+        for (int i = 0; i < 8; i++) f[i] = _mm512_setzero_ps();
+        for (int b = 0; b < t->nb; b++) {
+            __m512i acc[8];
+            for (int i = 0; i < 8; i++) acc[i] = _mm512_setzero_si512();
+            for (int k4 = b * 32; k4 < b * 32 + 32; k4++) {
+                const __m512i wv = _mm512_loadu_si512(t->wp + ((size_t)k4 * t->Np + n0) * 4);
+                for (int i = 0; i < mm; i++) {
+                    int32_t a4;
+                    memcpy(&a4, t->ab + (size_t)(m0 + i) * t->K + k4 * 4, 4);
+                    acc[i] = _mm512_dpbusd_epi32(acc[i], _mm512_set1_epi32(a4), wv);
+                }
+            }
+            const __m512i zp = _mm512_slli_epi32(_mm512_loadu_si512(t->bz + (size_t)b * t->Np + n0), 7);
+            for (int i = 0; i < mm; i++) {
+                const __m512 sc = _mm512_mul_ps(_mm512_set1_ps(t->as[(size_t)(m0 + i) * t->nb + b]), wsv);
+                f[i] = _mm512_fmadd_ps(_mm512_cvtepi32_ps(_mm512_sub_epi32(acc[i], zp)), sc, f[i]);
+            }
+        }
+        for (int i = 0; i < mm; i++) {
+            const __m512 r = t->bias ? _mm512_add_ps(f[i], bv) : f[i];
+            _mm512_mask_storeu_ps(t->y + (size_t)(m0 + i) * t->N + n0, nm, r);
+        }
+    }
+}
+
+void or_i8_gemm_mt(const int8_t *qa, const float *as, const int8_t *w, const float *ws,
+                   const float *bias, int M, int N, int K, float *y, int nthreads) {
+    const int Np = (N + 15) & ~15, nb = K / 128;
+    uint8_t *ab = malloc((size_t)M * K);
+    int8_t *wp = calloc((size_t)K * Np, 1);
+    int32_t *bz = calloc((size_t)nb * Np, sizeof(int32_t));
+    if (!ab || !wp || !bz) { free(ab); free(wp); free(bz); return; }
+    for (size_t i = 0; i < (size_t)M * K; i++) ab[i] = (uint8_t)qa[i] ^ 0x80u;
+    for (int n = 0; n < N; n++)
+        for (int k = 0; k < K; k++) {
+            const int8_t v = w[(size_t)n * K + k];
+            wp[((size_t)(k >> 2) * Np + n) * 4 + (k & 3)] = v;
+            bz[(size_t)(k >> 7) * Np + n] += v;
+        }
+    vnni_task t = { ab, as, wp, bz, ws, bias, y, M, N, K, Np, nb };
+    or_parallel(vnni_cols16, &t, Np / 16, nthreads);
+    free(ab);
+    free(wp);
+    free(bz);
+}
+
+typedef struct {
+    const float *x;
+    int8_t *q;
+    float *s;
+    int M, K;
+} quant_task;
+
+static void quant_rows16(void *arg, int item) {
+    const quant_task *t = arg;
+    const int m0 = item * 16, mm = t->M - m0 < 16 ? t->M - m0 : 16;
+    const int nb = t->K / 128;
+    or_quantize(t->x + (size_t)m0 * t->K, mm, t->K, t->K, 128, t->q + (size_t)m0 * t->K,
+                t->s + (size_t)m0 * nb);
+}
+
+void or_quantize_mt(const float *x, int M, int K, int8_t *q, float *scales, int nthreads) {
+    quant_task t = { x, q, scales, M, K };
+    or_parallel(quant_rows16, &t, (M + 15) / 16, nthreads);
+}
+
+/* ------------------------------------------------------------------ GELU / norms / RoPE */
+float or_gelu_tanh(float v) {
+    const float c = 0.7978845608028654f;
+    return 0.5f * v * (1.f + tanhf(c * (v + 0.044715f * v * v * v)));
+}
+
+void or_gelu_mul_quant(float *gate, int ldg, const float *up, int ldu, int rows, int D, int block,
+                       int8_t *q, float *scales) {
+    for (int r = 0; r < rows; r++) {
+        float *g = gate + (size_t)r * ldg;
+        const float *u = up + (size_t)r * ldu;
+        for (int d = 0; d < D; d++) g[d] = or_gelu_tanh(g[d]) * u[d];
+    }
+    or_quantize(gate, rows, D, ldg, block, q, scales);
+}
+
+static float row_inv(const float *x, int D, float eps) {
+    float ss = 0.f;
+    for (int d = 0; d < D; d++) ss += x[d] * x[d];
+    return 1.0f / sqrtf(ss / (float)D + eps);
+}
+
+void or_rmsnorm(float *x, int rows, int D, const float *gamma, float eps) {
+    for (int r = 0; r < rows; r++) {
+        float *row = x + (size_t)r * D;
+        const float inv = row_inv(row, D, eps);
+        for (int d = 0; d < D; d++) row[d] = gamma ? row[d] * inv * gamma[d] : row[d] * inv;
+    }
+}
+
+void or_norm_split(float *x, float *res, int rows, int D, const float *gamma, float eps) {
+    for (int r = 0; r < rows; r++) {
+        float *xr = x + (size_t)r * D, *rr = res + (size_t)r * D;
+        const float inv = row_inv(xr, D, eps);
+        for (int d = 0; d < D; d++) {
+            const float v = xr[d];
+            rr[d] = v;
+            xr[d] = v * inv * (gamma ? gamma[d] : 1.0f);
+        }
+    }
+}
+
+void or_norm_add(float *out, const float *src, const float *res, int rows, int D,
+                 const float *gamma, float eps) {
+    for (int r = 0; r < rows; r++) {
+        const float *sr = src + (size_t)r * D, *rr = res + (size_t)r * D;
+        float *o = out + (size_t)r * D;
+        const float inv = row_inv(sr, D, eps);
+        for (int d = 0; d < D; d++) o[d] = sr[d] * inv * (gamma ? gamma[d] : 1.0f) + rr[d];
+    }
+}
+
+void or_rope_table(int max_pos, int head_dim, float theta, float *cs, float *sn) {
+    for (int p = 0; p < max_pos; p++) {
+        float *c = cs + (size_t)p * head_dim, *s = sn + (size_t)p * head_dim;
+        for (int i = 0; i < head_dim / 2; i++) {
+            const float inv = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+            const float f = (float)p * inv;
+            c[i] = c[i + head_dim / 2] = cosf(f);
+            s[i] = s[i + head_dim / 2] = sinf(f);
+        }
+    }
+}
+
+void or_rope_rows(float *x, int rows, int ngroups, int head_dim, const float *cs, const float *sn) {
+    const int half = head_dim / 2;
+    for (int r = 0; r < rows; r++) {
+        float *v = x + (size_t)r * head_dim;
+        const float *c = cs + (size_t)(r / ngroups) * head_dim;
+        const float *s = sn + (size_t)(r / ngroups) * head_dim;
+        for (int i = 0; i < half; i++) {
+            const float a = v[i], y = v[half + i];
+            v[i] = a * c[i] - y * s[i];
+            v[half + i] = y * c[i] + a * s[i];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ softmax / attention */
+void or_softmax(float *x, int n) {
+    float m = x[0];
+    for (int i = 1; i < n; i++)
+        if (x[i] > m) m = x[i];
+    float sum = 0.f;
+    for (int i = 0; i < n; i++) {
+        x[i] = expf(x[i] - m);
+        sum += x[i];
+    }
+    const float inv = 1.f / sum;
+    for (int i = 0; i < n; i++) x[i] *= inv;
+}
+
+typedef struct {
+    const float *q, *k, *v;
+    int ldq, ldk, ldv, ldc;
+    const uint8_t *valid;
+    int S, H, KV, D;
+    float scale;
+    float *ctx;
+} attn_task;
+
+/* One (head, query row): text.c:534-572. Keys outside `valid` are skipped, an invalid query row
+ * gets a zero context, the logits are scaled by `scale` (1.0 in the reference, text.c:8-9). */
+static void attn_item(void *arg, int item) {
+    const attn_task *t = arg;
+    const int h = item / t->S, i = item % t->S;
+    float *o = t->ctx + (size_t)i * t->ldc + (size_t)h * t->D;
+    memset(o, 0, sizeof(float) * (size_t)t->D);
+    if (!t->valid[i]) return;
+    const int kvh = h / (t->H / t->KV);
+    const float *qh = t->q + (size_t)i * t->ldq + (size_t)h * t->D;
+    float *sc = malloc(sizeof(float) * (size_t)t->S);
+    if (!sc) return;
+    int n = 0;
+    for (int j = 0; j < t->S; j++) {
+        if (!t->valid[j]) continue;
+        const float *kj = t->k + (size_t)j * t->ldk + (size_t)kvh * t->D;
+        float s = 0.f;
+        for (int d = 0; d < t->D; d++) s += qh[d] * kj[d];
+        sc[n++] = s * t->scale;
+    }
+    if (n) {
+        or_softmax(sc, n);
+        n = 0;
+        for (int j = 0; j < t->S; j++) {
+            if (!t->valid[j]) continue;
+            const float *vj = t->v + (size_t)j * t->ldv + (size_t)kvh * t->D;
+            const float p = sc[n++];
+            for (int d = 0; d < t->D; d++) o[d] += p * vj[d];
+        }
+    }
+    free(sc);
+}
+
+void or_attention(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                  const uint8_t *valid, int S, int H, int KV, int D, float scale, float *ctx,
+                  int ldc, int nthreads) {
+    attn_task t = { q, k, v, ldq, ldk, ldv, ldc, valid, S, H, KV, D, scale, ctx };
+    or_parallel(attn_item, &t, H * S, nthreads);
+}
+
+/* ------------------------------------------------------------------ pooling / embedding */
+void or_meanpool(const float *x, int M, int D, const uint8_t *valid, float *out) {
+    memset(out, 0, sizeof(float) * (size_t)D);
+    int cnt = 0;
+    for (int m = 0; m < M; m++) {
+        if (valid && !valid[m]) continue;
+        for (int d = 0; d < D; d++) out[d] += x[(size_t)m * D + d];
+        cnt++;
+    }
+    if (cnt > 0)
+        for (int d = 0; d < D; d++) out[d] /= (float)cnt;
+}
+
+void or_l2norm(float *x, int n) {
+    float s = 0.f;
+    for (int i = 0; i < n; i++) s += x[i] * x[i];
+    const float inv = 1.f / sqrtf(s);
+    for (int i = 0; i < n; i++) x[i] *= inv;
+}
+
+void or_embed(const float *table, const int32_t *ids, int n, int D, float scale, float *x) {
+    for (int i = 0; i < n; i++)
+        for (int d = 0; d < D; d++) x[(size_t)i * D + d] = table[(size_t)ids[i] * D + d] * scale;
+}

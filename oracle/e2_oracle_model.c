@@ -1,0 +1,150 @@
+/* e2_oracle_model.c — the text tower's layer recipe at the BASELINE geometry (test infrastructure).
+ *
+ * Restates text.c:924-984 (text_forward), text.c:817-891 (attention) and text.c:893-903 (mlp) with
+ * the pieces the tier drops removed: no PLE block, no layer_scalar, no embed_proj, no sliding
+ * window (every key of a 512-token sequence is inside the reference's +-512 window). Per layer:
+ *
+ *   res = x; x = rms(x)*input_ln                       norm_split   text.c:942
+ *   q|k|v = int8 GEMM(quant(x))                        gemm_segs    text.c:826-833
+ *   q,k rms*gamma, v rms (no gamma)                    map_norm     text.c:836-838
+ *   per sequence: trim trailing pad, RoPE, attention   text.c:840-887
+ *   tmp = int8 GEMM(quant(ctx), O)                     text.c:890
+ *   x = rms(tmp)*post_attn_ln + res                    norm_add     text.c:946
+ *   res = x; x = rms(x)*pre_ffn_ln                     norm_split   text.c:949
+ *   g|u = int8 GEMM(quant(x)); quant(gelu(g)*u); down  mlp          text.c:893-903
+ *   x = rms(tmp)*post_ffn_ln + res                     norm_add     text.c:953
+ *
+ * then rms(x)*final_norm, masked mean pool, L2 (text.c:963-981). Every GEMM runs on the threaded
+ * VNNI kernel, which tests/test_oracle_ref.py pins bit-exact to the single-threaded restatement.
+ */
+#include "e2_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define OR_CHECK(p) do { if (!(p)) goto fail; } while (0)
+
+int or_attention_sublayer(const or_model *m, int l, const float *x, int B, int S,
+                          const uint8_t *valid, float *out, int nthreads) {
+    const or_layer *L = &m->layers[l];
+    const int M = B * S, Dm = m->hidden, H = m->n_heads, KV = m->n_kv, D = m->head_dim;
+    const int GD = H * D, NQKV = (H + 2 * KV) * D, nb = Dm / 128, nbg = GD / 128;
+    int rc = -1;
+    int8_t *qa = malloc((size_t)M * (Dm > GD ? Dm : GD));
+    float *as = malloc(sizeof(float) * (size_t)M * (nb > nbg ? nb : nbg));
+    float *qkv = malloc(sizeof(float) * (size_t)M * NQKV);
+    float *q = malloc(sizeof(float) * (size_t)M * GD);
+    float *k = malloc(sizeof(float) * (size_t)M * KV * D);
+    float *v = malloc(sizeof(float) * (size_t)M * KV * D);
+    float *ctx = calloc((size_t)M * GD, sizeof(float));
+    float *cs = malloc(sizeof(float) * (size_t)S * D), *sn = malloc(sizeof(float) * (size_t)S * D);
+    OR_CHECK(qa && as && qkv && q && k && v && ctx && cs && sn);
+
+    or_quantize_mt(x, M, Dm, qa, as, nthreads);
+    or_i8_gemm_mt(qa, as, L->wqkv, L->sqkv, NULL, M, NQKV, Dm, qkv, nthreads);
+    for (int r = 0; r < M; r++) {
+        memcpy(q + (size_t)r * GD, qkv + (size_t)r * NQKV, sizeof(float) * GD);
+        memcpy(k + (size_t)r * KV * D, qkv + (size_t)r * NQKV + GD, sizeof(float) * KV * D);
+        memcpy(v + (size_t)r * KV * D, qkv + (size_t)r * NQKV + GD + KV * D, sizeof(float) * KV * D);
+    }
+    or_rmsnorm(q, M * H, D, L->q_norm, m->eps);
+    or_rmsnorm(k, M * KV, D, L->k_norm, m->eps);
+    or_rmsnorm(v, M * KV, D, NULL, m->eps);
+    or_rope_table(S, D, m->rope_theta, cs, sn);
+    for (int b = 0; b < B; b++) {
+        const uint8_t *vb = valid + (size_t)b * S;
+        int Sb = S;
+        while (Sb && !vb[Sb - 1]) Sb--; /* trailing padding is trimmed: text.c:849-852 */
+        if (!Sb) continue;
+        or_rope_rows(q + (size_t)b * S * GD, Sb * H, H, D, cs, sn);
+        or_rope_rows(k + (size_t)b * S * KV * D, Sb * KV, KV, D, cs, sn);
+        or_attention(q + (size_t)b * S * GD, GD, k + (size_t)b * S * KV * D, KV * D,
+                     v + (size_t)b * S * KV * D, KV * D, vb, Sb, H, KV, D, m->attn_scale,
+                     ctx + (size_t)b * S * GD, GD, nthreads);
+    }
+    or_quantize_mt(ctx, M, GD, qa, as, nthreads);
+    or_i8_gemm_mt(qa, as, L->wo, L->so, NULL, M, Dm, GD, out, nthreads);
+    rc = 0;
+fail:
+    free(qa); free(as); free(qkv); free(q); free(k); free(v); free(ctx); free(cs); free(sn);
+    return rc;
+}
+
+static int ffn_core(const or_model *m, const or_layer *L, const float *xin, int rows, float *tmp,
+                    int nthreads) {
+    const int Dm = m->hidden, F = m->ffn;
+    int rc = -1;
+    int8_t *qa = malloc((size_t)rows * (F > Dm ? F : Dm));
+    float *as = malloc(sizeof(float) * (size_t)rows * ((F > Dm ? F : Dm) / 128));
+    float *g = malloc(sizeof(float) * (size_t)rows * F), *u = malloc(sizeof(float) * (size_t)rows * F);
+    OR_CHECK(qa && as && g && u);
+    or_quantize_mt(xin, rows, Dm, qa, as, nthreads);
+    or_i8_gemm_mt(qa, as, L->wgate, L->sgate, NULL, rows, F, Dm, g, nthreads);
+    or_i8_gemm_mt(qa, as, L->wup, L->sup, NULL, rows, F, Dm, u, nthreads);
+    or_gelu_mul_quant(g, F, u, F, rows, F, 128, qa, as);
+    or_i8_gemm_mt(qa, as, L->wdown, L->sdown, NULL, rows, Dm, F, tmp, nthreads);
+    rc = 0;
+fail:
+    free(qa); free(as); free(g); free(u);
+    return rc;
+}
+
+int or_ffn_sublayer(const or_model *m, int l, float *x, int rows, int nthreads) {
+    const or_layer *L = &m->layers[l];
+    const int Dm = m->hidden;
+    float *res = malloc(sizeof(float) * (size_t)rows * Dm);
+    float *tmp = malloc(sizeof(float) * (size_t)rows * Dm);
+    int rc = -1;
+    OR_CHECK(res && tmp);
+    or_norm_split(x, res, rows, Dm, L->pre_ffn_ln, m->eps);
+    OR_CHECK(ffn_core(m, L, x, rows, tmp, nthreads) == 0);
+    or_norm_add(x, tmp, res, rows, Dm, L->post_ffn_ln, m->eps);
+    rc = 0;
+fail:
+    free(res); free(tmp);
+    return rc;
+}
+
+int or_layer_forward(const or_model *m, int l, float *x, int B, int S, const uint8_t *valid,
+                     int nthreads) {
+    const or_layer *L = &m->layers[l];
+    const int M = B * S, Dm = m->hidden;
+    float *res = malloc(sizeof(float) * (size_t)M * Dm);
+    float *tmp = malloc(sizeof(float) * (size_t)M * Dm);
+    int rc = -1;
+    OR_CHECK(res && tmp);
+    or_norm_split(x, res, M, Dm, L->input_ln, m->eps);
+    OR_CHECK(or_attention_sublayer(m, l, x, B, S, valid, tmp, nthreads) == 0);
+    or_norm_add(x, tmp, res, M, Dm, L->post_attn_ln, m->eps);
+    or_norm_split(x, res, M, Dm, L->pre_ffn_ln, m->eps);
+    OR_CHECK(ffn_core(m, L, x, M, tmp, nthreads) == 0);
+    or_norm_add(x, tmp, res, M, Dm, L->post_ffn_ln, m->eps);
+    rc = 0;
+fail:
+    free(res); free(tmp);
+    return rc;
+}
+
+int or_encode(const or_model *m, const int32_t *ids, const uint8_t *valid, int B, int S,
+              float *out, int nthreads) {
+    const int M = B * S, Dm = m->hidden;
+    for (int i = 0; i < M; i++)
+        if (ids[i] < 0 || ids[i] >= m->vocab) return -1;
+    float *x = malloc(sizeof(float) * (size_t)M * Dm);
+    if (!x) return -1;
+    or_embed(m->embed, ids, M, Dm, m->embed_scale, x);
+    for (int l = 0; l < m->n_layers; l++)
+        if (or_layer_forward(m, l, x, B, S, valid, nthreads)) { free(x); return -1; }
+    or_rmsnorm(x, M, Dm, m->final_norm, m->eps);
+    for (int b = 0; b < B; b++) {
+        float *o = out + (size_t)b * Dm;
+        const uint8_t *vb = valid + (size_t)b * S;
+        or_meanpool(x + (size_t)b * S * Dm, S, Dm, vb, o);
+        int any = 0;
+        for (int i = 0; i < S; i++) any |= vb[i];
+        if (any) or_l2norm(o, Dm); /* all-invalid stays an exact zero vector: text.c:968-980 */
+    }
+    free(x);
+    return 0;
+}
