@@ -1,0 +1,366 @@
+#!/usr/bin/env python3
+"""Benchmark of the int8 encoder hot path on one MI355X (BASELINE.json metric).
+
+Step (the timed unit): the BASELINE config-5 sweep — four int8 GEMMs at M = 65536 tokens,
+(K, N) in {(768,1152), (1152,768), (768,1280), (768,768)}, each consuming int8 activations +
+per-128 scales already resident in HBM and producing the next GEMM's int8 activations + scales
+(the requantizing epilogue the encoder feeds forward). `value` is the aggregate int8 TOPS over the
+step. Reported beside it on the same line: the same sweep with the reference's f32-output
+contract, the activation quantizer's HBM rate, the `roofline` object for the dominant kernel, and
+the CPU baseline (the reference's own AVX512-VNNI kernel built from its sources, on the host).
+
+Inputs are synthetic, as BASELINE config 5 specifies: Student-t(nu=3) activations with 0.1 % of
+the channels scaled x50, quantized per (token, 128 block); int8 weights uniform in [-127,127] with
+per-row scales U(0.001, 0.02), handed over as the reference's packed (E8CQ-style) blobs and
+re-laid out on the device at load.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import threading
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "e2.c_amd"))
+
+SHAPES = [(768, 1152), (1152, 768), (768, 1280), (768, 768)]
+M = 65536
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, TOPS
+PEAK_HBM_GBS = 8000.0
+METRIC = "int8 GEMM TOPS (% of int8 MFMA peak); encoder embeddings/sec @ seq 512"
+
+
+def student_t_acts(torch, K, gen, dev):
+    z = torch.randn((M, K), generator=gen, device=dev)
+    chi = torch.randn((3, M, K), generator=gen, device=dev).pow_(2).sum(0)
+    x = z / torch.sqrt(chi / 3.0)
+    n_out = max(1, int(np.ceil(0.001 * K)))
+    cols = torch.randperm(K, generator=gen, device=dev)[:n_out]
+    x[:, cols] *= 50.0
+    return x.contiguous()
+
+
+def packed_weight(rng, N, K):
+    """int8 W uniform [-127,127] + scales in the reference's quad-interleaved layout."""
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    Npad = (N + 7) & ~7
+    wp = np.zeros((Npad, K), np.int8)
+    wp[:N] = w
+    # [Npad/8][K/4][8][4]: (n>>3, k>>2, n&7, k&3)
+    wq = wp.reshape(Npad // 8, 8, K // 4, 4).transpose(0, 2, 1, 3).copy().reshape(-1)
+    return w, ws, wq
+
+
+def time_calls(torch, fn, iters):
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters * 1e-3
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_flags():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("flags"):
+                return set(line.split(":")[1].split())
+    except OSError:
+        pass
+    return set()
+
+
+def physical_cores():
+    """One thread per physical core (the reference's default pool policy, threads.c:177-215),
+    capped by the affinity mask and by this box's share (16 per GPU)."""
+    try:
+        allowed = os.sched_getaffinity(0)
+    except AttributeError:
+        allowed = set(range(os.cpu_count() or 1))
+    seen, cores = set(), []
+    for c in sorted(allowed):
+        try:
+            sib = open(f"/sys/devices/system/cpu/cpu{c}/topology/thread_siblings_list").read().strip()
+        except OSError:
+            sib = str(c)
+        if sib not in seen:
+            seen.add(sib)
+            cores.append(c)
+    return max(1, min(len(cores), 16))
+
+
+def cpu_baseline(budget_s=12.0):
+    """The reference's e2_i8_gemm_avx512 (oracle/_ref, built from its sources) on the host cores,
+    N-split across threads like text.c's gemm_segs, over a bounded sample of the same sweep:
+    M_s = 2048 rows of each shape."""
+    sys.path.insert(0, ROOT)
+    from oracle.binding import Oracle, Ref, Q8W
+    flags = cpu_flags()
+    threads = physical_cores()
+    Ms = 2048
+    rng = np.random.default_rng(7)
+    use_ref = Ref.available() and {"avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512_vnni"} <= flags
+    kind, which = ("reference", "avx512") if use_ref else ("port", None)
+    if not use_ref and Ref.available() and "avx_vnni" in flags:
+        kind, which = "reference", "vnni_range"
+    ref = Ref() if kind == "reference" else None
+    orc = Oracle() if ref is None else None
+    work = []
+    for K, N in SHAPES:
+        qa = rng.integers(-127, 128, (Ms, K), dtype=np.int8)
+        qb = (qa.view(np.uint8) ^ 0x80).view(np.int8).copy()
+        as_ = rng.uniform(0.001, 0.05, (Ms, K // 128)).astype(np.float32)
+        w, ws, wq = packed_weight(rng, N, K)
+        bsq = np.zeros((K // 128 * N + 32,), np.int32)
+        bsq[: K // 128 * N] = w.reshape(N, K // 128, 128).sum(-1).T.astype(np.int32).reshape(-1)
+        wsp = np.zeros(N + 32, np.float32)
+        wsp[:N] = ws
+        wqp = np.concatenate([wq, np.zeros(4 * K * 8, np.int8)])
+        y = np.zeros((Ms, N), np.float32)
+        work.append((K, N, qa, qb, as_, w, ws, wqp, wsp, bsq, y))
+
+    def run_shape(item):
+        K, N, qa, qb, as_, w, ws, wqp, wsp, bsq, y = item
+        if ref is None:
+            orc.i8_gemm_mt(qa, as_, w, ws, nthreads=threads)
+            return
+        q = Q8W(wqp.ctypes.data, bsq.ctypes.data, wsp.ctypes.data, N, K, K // 128, N, -1e31, 1e31, 1)
+        fn = getattr(ref.lib, f"e2_i8_gemm_{which}")
+        tile = max(16, (N // (threads * 2)) // 16 * 16)
+        ranges = [(a, min(N, a + tile)) for a in range(0, N, tile)]
+        nxt = [0]
+        lock = threading.Lock()
+
+        def worker():
+            while True:
+                with lock:
+                    i = nxt[0]
+                    nxt[0] += 1
+                if i >= len(ranges):
+                    return
+                fn(y.ctypes.data_as(C.c_void_p), qb.ctypes.data_as(C.c_void_p),
+                   as_.ctypes.data_as(C.c_void_p), C.byref(q), Ms, N, ranges[i][0], ranges[i][1])
+
+        ts = [threading.Thread(target=worker) for _ in range(threads)]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join()
+
+    for item in work:  # warm-up (3 runs, text_bench.c:52-80)
+        run_shape(item)
+    ops_per_pass = sum(2.0 * Ms * N * K for K, N, *_ in work)
+    times = []
+    t_start = time.time()
+    while len(times) < 5 or (time.time() - t_start < budget_s and len(times) < 200):
+        t0 = time.perf_counter()
+        for item in work:
+            run_shape(item)
+        times.append(time.perf_counter() - t0)
+    best = min(times)
+    return {
+        "value": round(ops_per_pass / best / 1e12, 4),
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"the config-5 sweep on M={Ms} rows per shape (of 65536), f32 output "
+                   f"(e2_i8_gemm_{which or 'port'} N-split over {threads} threads); best of "
+                   f"{len(times)} passes; median {ops_per_pass / float(np.median(times)) / 1e12:.4f} TOPS"),
+        "kernel": f"e2_i8_gemm_{which}" if which else "or_i8_gemm_mt",
+        "cpu_avx512_vnni": "avx512_vnni" in flags,
+    }
+
+
+# ------------------------------------------------------------------ HBM traffic from PMC runs
+COPY_BYTES = 256 << 20
+
+
+def summarize_pmc(fetch_csv, write_csv):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the --probe run, each scaled by what the same
+    counter reads for the calibration copy of COPY_BYTES, into HBM bytes per GEMM launch."""
+    import csv
+
+    def read(path, counter):
+        rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        return [(r["Kernel_Name"], float(r["Counter_Value"]) * 1024) for r in rows]
+
+    out = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = read(path, counter)
+        copy = [v for k, v in rows if "copy" in k.lower() or "elementwise" in k.lower()]
+        gemms = [v for k, v in rows if "k_gemm" in k]
+        if not copy or len(gemms) < len(SHAPES):
+            raise SystemExit(f"{path}: expected a copy kernel and {len(SHAPES)} GEMM dispatches")
+        scale = COPY_BYTES / copy[-1]
+        for (K, N), v in zip(SHAPES, gemms[-len(SHAPES):]):
+            d = out.setdefault(f"{K}x{N}", {})
+            d[counter] = v
+            d[counter + "_scale"] = scale
+            d["fetch_bytes" if counter == "FETCH_SIZE" else "write_bytes"] = v * scale
+    for d in out.values():
+        d["hbm_bytes"] = d.get("fetch_bytes", 0) + d.get("write_bytes", 0)
+    res = {k: round(v["hbm_bytes"]) for k, v in out.items()}
+    res["detail"] = out
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    with open(os.path.join(ROOT, "profiles", "gemm_q_traffic.json"), "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps(res, indent=1))
+
+
+# ------------------------------------------------------------------ main
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--probe", action="store_true",
+                    help="one calibration copy + one launch per GEMM (for rocprofv3 --pmc runs)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="turn FETCH_SIZE / WRITE_SIZE counter CSVs of a --probe run into "
+                         "profiles/gemm_q_traffic.json")
+    args = ap.parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the "
+              "path shards by token rows with replicated weights and needs no collective, see "
+              "DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import e2mi
+    e2mi.load()
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1005)
+    rng = np.random.default_rng(1005)
+
+    cases = []
+    for K, N in SHAPES:
+        x = student_t_acts(torch, K, gen, dev)
+        qa, as_ = e2mi.quantize(x)
+        w, ws, wq = packed_weight(rng, N, K)
+        W = e2mi.DeviceWeight.from_packed(wq, ws, N, K)
+        yq = torch.empty((M, N), dtype=torch.int8, device=dev)
+        ys = torch.empty((M, N // 128), dtype=torch.float32, device=dev)
+        yf = torch.empty((M, N), dtype=torch.float32, device=dev)
+        cases.append(dict(K=K, N=N, x=x, qa=qa, as_=as_, W=W, yq=yq, ys=ys, yf=yf))
+    torch.cuda.synchronize()
+
+    lib = e2mi.load()
+    stream = torch.cuda.current_stream()
+    sp = e2mi.stream_ptr(stream)
+
+    def gemm_q(c):
+        e2mi.check(lib.e2mi_i8_gemm_q(sp, e2mi.ptr(c["yq"]), e2mi.ptr(c["ys"]), e2mi.ptr(c["qa"]),
+                                      e2mi.ptr(c["as_"]), c["W"].ref, M), "i8_gemm_q")
+
+    def gemm_f32(c):
+        e2mi.check(lib.e2mi_i8_gemm(sp, e2mi.ptr(c["yf"]), c["N"], e2mi.ptr(c["qa"]),
+                                    e2mi.ptr(c["as_"]), c["W"].ref, M, 0, c["N"]), "i8_gemm")
+
+    def step():
+        for c in cases:
+            gemm_q(c)
+
+    if args.probe:
+        # calibration: a plain copy of COPY_BYTES (read COPY_BYTES, write COPY_BYTES), then one
+        # launch of each GEMM of the step, in SHAPES order
+        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).uniform_()
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        step()
+        torch.cuda.synchronize()
+        print("probe done")
+        return
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # timed region: exactly K steps, synchronised on both sides; per-launch HIP events on the
+    # launching stream give each kernel's average duration for the roofline
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in cases] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        for i, c in enumerate(cases):
+            ev[s][i][0].record(stream)
+            gemm_q(c)
+            ev[s][i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_launch = [np.mean([ev[s][i][0].elapsed_time(ev[s][i][1]) * 1e-3 for s in range(args.steps)])
+                  for i in range(len(cases))]
+    ops = [2.0 * M * c["N"] * c["K"] for c in cases]
+    ms_per_step = wall / args.steps * 1e3
+    value = sum(ops) / (wall / args.steps) / 1e12
+
+    # the reference contract (f32 output) on the same inputs, and the quantizer
+    f32_t = [time_calls(torch, lambda c=c: gemm_f32(c), max(3, args.steps // 2)) for c in cases]
+    q_t = time_calls(torch, lambda: e2mi.quantize(cases[0]["x"], q=cases[0]["qa"],
+                                                  scales=cases[0]["as_"]), 10)
+    q_bytes = M * 768 * (4 + 1) + M * 6 * 4
+
+    # roofline: the dominant launch of the step (longest average duration)
+    dom = int(np.argmax(per_launch))
+    c = cases[dom]
+    algo_bytes = M * c["K"] + 4 * M * c["K"] // 128 + c["N"] * c["K"] + 4 * c["N"] + M * c["N"] + 4 * M * c["N"] // 128
+    ach = ops[dom] / per_launch[dom] / 1e12
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemm_q_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            tj = json.load(open(tpath))
+            traffic = tj.get(f"{c['K']}x{c['N']}")
+            traffic = None if traffic is None else int(traffic)
+        except (OSError, ValueError):
+            traffic = None
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (BASELINE config 5: Student-t nu=3 activations, 0.1% outlier channels x50; uniform int8 weights from packed blobs)",
+        "config": {"workload": "config-5 int8 GEMM sweep, M=65536, (K,N) in " + str(SHAPES)
+                   + ", int8-requant epilogue", "global_batch": M, "seq_len": 512,
+                   "parallelism": "none (1 GPU)"},
+        "pct_of_int8_mfma_peak": round(100 * value / PEAK_INT8_TOPS, 2),
+        "per_shape_us": {f"{c['K']}x{c['N']}": round(t * 1e6, 2) for c, t in zip(cases, per_launch)},
+        "f32_out": {"tops": round(sum(ops) / sum(f32_t) / 1e12, 2),
+                    "per_shape_us": {f"{c['K']}x{c['N']}": round(t * 1e6, 2) for c, t in zip(cases, f32_t)}},
+        "quantize_65536x768": {"us": round(q_t * 1e6, 2), "GB/s": round(q_bytes / q_t / 1e9, 1)},
+        "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS,
+                     "unit": "TFLOP/s", "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic,
+                     "kernel": f"k_gemm requant epilogue {c['K']}x{c['N']}",
+                     "algorithmic_bytes": algo_bytes, "ops": ops[dom],
+                     "note": "int8 ops counted as TFLOP/s; bound by the algorithmic roofline max(t_mfma, t_hbm)"},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

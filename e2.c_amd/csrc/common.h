@@ -1,0 +1,86 @@
+// common.h — shared definitions of the gfx950 int8 encoder backend (device and host side).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/e2mi.h"
+
+namespace e2mi {
+
+// One activation/weight quantization block (reference src/int8.h:61-70, E2_I8_BLOCK).
+constexpr int kQBlock = 128;
+
+// RN(1/127): the constant the reference's amax/127.0f folds into under -freciprocal-math
+// (kernels_i8_avx512_vnni.c:341 as compiled with CMakeLists.txt:110).
+__host__ __device__ inline float inv127() { return __builtin_bit_cast(float, 0x3c010204u); }
+
+// ---- error reporting (the e2_hip_last_error convention, reference src/gpu/hip/hip.c:27-49)
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+int check_hip(hipError_t e, const char *what);
+#define E2MI_HIP(call)                                                                     \
+    do {                                                                                   \
+        if (::e2mi::check_hip((call), #call)) return -1;                                   \
+    } while (0)
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace e2mi
+
+// ---- device helpers
+#if defined(__HIPCC__)
+namespace e2mi {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// The quantizer's per-block arithmetic: scale = amax * RN(1/127), inv = 127 / amax (correctly
+// rounded division), q = rne(x * inv) saturated to [-128,127] like the SIMD pack.
+struct QScale {
+    float sc, inv;
+};
+__device__ inline QScale qscale(float amax) {
+    QScale r;
+    if (amax > 0.f) {
+        r.sc = __fmul_rn(amax, inv127());
+        r.inv = __fdiv_rn(127.0f, amax);
+    } else {
+        r.sc = 1.0f;
+        r.inv = 1.0f;
+    }
+    return r;
+}
+__device__ inline int qbyte(float x, float inv) {
+    float r = __builtin_rintf(__fmul_rn(x, inv));
+    r = fminf(fmaxf(r, -128.f), 127.f);
+    return (int)r;
+}
+__device__ inline uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+// max over the 2^k lanes of a lane group (width <= 64), every lane gets the result
+template <int W>
+__device__ inline float group_max(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, W));
+    return v;
+}
+template <int W>
+__device__ inline float group_sum(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, W);
+    return v;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs; remap so each XCD walks a contiguous
+// range of logical tiles (consecutive N tiles of one M block share that XCD's L2).
+__device__ inline int xcd_swizzle(int pid, int total) {
+    constexpr int kXcd = 8;
+    if (total % kXcd) return pid;
+    return (pid % kXcd) * (total / kXcd) + pid / kXcd;
+}
+
+}  // namespace e2mi
+#endif

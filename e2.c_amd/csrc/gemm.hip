@@ -1,0 +1,431 @@
+// gemm.hip — W8A8 GEMM on gfx950 int8 MFMA (v_mfma_i32_32x32x32_i8) with the fused per-block
+// dequantization of the reference's e2_i8_gemm (src/int8.h:94-97; fold order of
+// src/kernels_i8_avx512_vnni.c:100-122):
+//
+//   y[m,n] = sum_b fma((float)acc_b[m,n], RN(as[m,b] * ws[n]), .)      acc_b exact int32
+//
+// then one of the fused epilogues:
+//   EPI_F32   y (+bias), clamped to [lo,hi], stored f32 (the reference contract)
+//   EPI_I8Q   y (+bias) requantized per (row, 128 output columns) for the next GEMM: int8 + scale
+//   EPI_GEGLU W rows interleaved per 256 as [128 gate | 128 up]; g = gelu_tanh(gate) * up is
+//             quantized per 128 (text.c:424-468 fused into the producing GEMM), g optionally kept
+//
+// Tiling: BM x BN workgroup tile, K walked in 128-deep steps (one quantization block per step, so
+// the int32 accumulators are folded into f32 once per step). A and W tiles are staged through LDS
+// with a 144-byte row pitch (16 B of padding: the ds_read_b128 fragment loads of 16 consecutive
+// lanes then hit 16 distinct 4-bank groups), double-buffered so the next step's global loads are in
+// flight while the MFMAs run. Each wave owns a WM x WN sub-tile of 32x32 MFMA tiles.
+#include "common.h"
+
+namespace e2mi {
+
+enum { EPI_F32 = 0, EPI_I8Q = 1, EPI_GEGLU = 2 };
+
+struct GemmArgs {
+    const int8_t *A;
+    const float *as;
+    const int8_t *W;
+    const float *ws;
+    const float *bias;
+    float *Y;        // EPI_F32 output, EPI_GEGLU optional f32 g
+    int8_t *Yq;      // EPI_I8Q / EPI_GEGLU quantized output
+    float *ys;       // ... and its per-128 scales [M][ldys]
+    int32_t *accd;   // optional int32 accumulator dump [nb][M][N] (parity tests)
+    int lda, ldw, ldy, ldyq, ldys;
+    int M, N, K;
+    float lo, hi;
+};
+
+
+__device__ inline float gelu_tanh(float v) {
+    const float c = 0.7978845608028654f;
+    return 0.5f * v * (1.f + tanhf(c * (v + 0.044715f * v * v * v)));
+}
+
+// LDS tiles hold 128-byte K slices of consecutive rows with no padding; the 16-byte chunk c of row
+// r sits at slot c ^ (r & 7), so the fragment reads of eight consecutive rows (one LDS pass) hit
+// eight different bank groups. Each global_load_lds_dwordx4 fills 1 KB = 8 rows of a tile: lane l
+// writes slot l of that kilobyte, so it loads row l/8's chunk (l%8) ^ (row & 7).
+__device__ inline int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 128 * 128) ? 1 : 2) void k_gemm(GemmArgs p) {
+    constexpr int NWN = BN / WN, NWAVE = (BM / WM) * NWN, NT = NWAVE * 64;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int AI = BM / 8 / NWAVE, BI = BN / 8 / NWAVE;  // 1-KB loads per wave per step
+    static_assert(AI * NWAVE * 8 == BM && BI * NWAVE * 8 == BN, "tile/threads mismatch");
+    static_assert(BM <= 64 * NWAVE, "one scale per lane");
+    constexpr int STAGE = (BM + BN) * 128 + 64 * NWAVE * 4;  // A | W | scales (one per lane)
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int tiles_n = (p.N + BN - 1) / BN;
+    const int pid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int m0 = (pid / tiles_n) * BM, n0 = (pid % tiles_n) * BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / NWN, wn = wave % NWN;
+    const int nb = p.K / kQBlock;
+
+    // per-lane global byte offsets (32-bit: the host checks both operands span < 4 GiB); rows past
+    // M/N are clamped, their outputs are never stored
+    uint32_t oa[AI], ob[BI];
+#pragma unroll
+    for (int i = 0; i < AI; i++) {
+        const int r = (i * NWAVE + wave) * 8 + (lane >> 3);
+        oa[i] = (uint32_t)min(m0 + r, p.M - 1) * (uint32_t)p.lda + (((lane & 7) ^ (r & 7)) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < BI; i++) {
+        const int r = (i * NWAVE + wave) * 8 + (lane >> 3);
+        ob[i] = (uint32_t)min(n0 + r, p.N - 1) * (uint32_t)p.ldw + (((lane & 7) ^ (r & 7)) << 4);
+    }
+    // scales: lane (wave, lane) fetches row wave*64+lane (waves past BM/64 fetch a clamped copy
+    // into their own slot, so every wave issues the same number of loads per step)
+    const float *gas = p.as + (size_t)min(m0 + wave * 64 + lane, p.M - 1) * nb;
+
+    auto issue = [&](int kb, int st) {
+        unsigned char *s = smem + st * STAGE;
+        const int ko = kb * kQBlock;
+#pragma unroll
+        for (int i = 0; i < AI; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(p.A + oa[i] + ko),
+                                             (lds_void *)(s + (i * NWAVE + wave) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < BI; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(p.W + ob[i] + ko),
+                                             (lds_void *)(s + BM * 128 + (i * NWAVE + wave) * 1024),
+                                             16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void *)(gas + kb),
+                                         (lds_void *)(s + (BM + BN) * 128 + wave * 256), 4, 0, 0);
+    };
+
+    float wsr[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++)
+        wsr[tn] = p.ws[min(n0 + wn * WN + tn * 32 + (lane & 31), p.N - 1)];
+
+    v16i acc[TM][TN];
+    float f[TM][TN][16];
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) f[tm][tn][r] = 0.f;
+
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++)
+        if (st < nb) issue(st, st);
+    const v16i zero = {};
+    constexpr int L = AI + BI + 1;  // loads per wave per step
+    for (int kb = 0; kb < nb; kb++) {
+        // wait for this step's tiles (later steps may stay in flight), then the barrier both
+        // publishes them and retires every wave's reads of the buffer refilled next
+        const int rem = min(nb - 1 - kb, NS - 2);
+        if (rem <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else if (rem == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
+        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * L) : "memory");
+        __syncthreads();
+        if (kb + NS - 1 < nb) issue(kb + NS - 1, (kb + NS - 1) % NS);
+        const int cur = kb % NS;
+        const unsigned char *sb0 = smem + cur * STAGE;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const int cc = kk * 2 + (lane >> 5);
+            v4i af[TM], bf[TN];
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
+                af[tm] = *(const v4i *)(sb0 + swz(wm * WM + tm * 32 + (lane & 31), cc));
+#pragma unroll
+            for (int tn = 0; tn < TN; tn++)
+                bf[tn] = *(const v4i *)(sb0 + BM * 128 + swz(wn * WN + tn * 32 + (lane & 31), cc));
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+                for (int tn = 0; tn < TN; tn++)
+                    acc[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                        af[tm], bf[tn], kk == 0 ? zero : acc[tm][tn], 0, 0, 0);
+        }
+        // fold this block: f = fma((float)acc, RN(as*ws), f), the reference's order
+        const float *asb = (const float *)(sb0 + (BM + BN) * 128) + wm * WM + (lane >> 5) * 4;
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 a4 = *(const float4 *)(asb + tm * 32 + g * 8);
+                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+                for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int r = g * 4 + j;
+                        f[tm][tn][r] = __builtin_fmaf((float)acc[tm][tn][r], __fmul_rn(av[j], wsr[tn]),
+                                                      f[tm][tn][r]);
+                    }
+            }
+        if constexpr (DUMP) {
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+                for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int m = m0 + wm * WM + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                        const int n = n0 + wn * WN + tn * 32 + (lane & 31);
+                        if (m < p.M && n < p.N)
+                            p.accd[((size_t)kb * p.M + m) * p.N + n] = acc[tm][tn][r];
+                    }
+        }
+    }
+    __syncthreads();  // the epilogue may reuse the staging buffers
+
+    if constexpr (EPI == EPI_F32) {
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++) {
+            const int n = n0 + wn * WN + tn * 32 + (lane & 31);
+            if (n >= p.N) continue;
+            const float b = p.bias ? p.bias[n] : 0.f;
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int m = m0 + wm * WM + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                    if (m < p.M) {
+                        float v = f[tm][tn][r];
+                        if (p.bias) v = v + b;
+                        v = fminf(fmaxf(v, p.lo), p.hi);
+                        p.Y[(size_t)m * p.ldy + n] = v;
+                    }
+                }
+        }
+    } else {
+        // Stage the f32 tile through LDS (the A/W staging buffers are free now), then each group of
+        // threads owns whole 128-column quantization blocks of a row.
+        constexpr int FP = BN + 4;  // f32 row pitch
+        static_assert(BM * FP * 4 <= NS * STAGE, "epilogue tile does not fit");
+        float *sf = (float *)smem;
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++) {
+            const int nl = wn * WN + tn * 32 + (lane & 31);
+            const float b = p.bias ? p.bias[min(n0 + nl, p.N - 1)] : 0.f;
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int ml = wm * WM + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                    float v = f[tm][tn][r];
+                    if (p.bias) v = v + b;
+                    sf[ml * FP + nl] = fminf(fmaxf(v, p.lo), p.hi);
+                }
+        }
+        __syncthreads();
+        // output columns per tile and per thread: I8Q keeps BN columns, GEGLU halves them
+        constexpr int OUTC = (EPI == EPI_GEGLU) ? BN / 2 : BN;
+        constexpr int TPR = OUTC / 16;  // threads per row, 16 columns each
+        constexpr int RPP = NT / TPR;   // rows per pass
+        static_assert(OUTC % 128 == 0 && TPR <= 64, "quantization block must be tile-local");
+        const int oc0 = (EPI == EPI_GEGLU) ? n0 / 2 : n0;  // first output column of this tile
+        const int ldo = (EPI == EPI_GEGLU) ? p.N / 2 : p.N;
+        const int t_r = tid / TPR, t_c = tid % TPR;
+        for (int rr = 0; rr < BM; rr += RPP) {
+            const int ml = rr + t_r, m = m0 + ml;
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int oc = t_c * 16 + i;  // output column within the tile
+                if constexpr (EPI == EPI_GEGLU) {
+                    // W rows are interleaved per 256: [128 gate | 128 up] for output block oc/128
+                    const int blk = oc >> 7, w = oc & 127;
+                    const float g = sf[ml * FP + blk * 256 + w], u = sf[ml * FP + blk * 256 + 128 + w];
+                    v[i] = gelu_tanh(g) * u;
+                } else {
+                    v[i] = sf[ml * FP + oc];
+                }
+            }
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) a = fmaxf(a, fabsf(v[i]));
+            a = group_max<8>(a);  // 8 threads x 16 columns = one 128-column block
+            const QScale s = qscale(a);
+            const int oc = oc0 + t_c * 16;
+            if (m < p.M && oc < ldo) {
+                uint32_t w4[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    w4[i] = pack4(qbyte(v[4 * i], s.inv), qbyte(v[4 * i + 1], s.inv),
+                                  qbyte(v[4 * i + 2], s.inv), qbyte(v[4 * i + 3], s.inv));
+                *(uint4 *)(p.Yq + (size_t)m * p.ldyq + oc) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                if ((t_c & 7) == 0) p.ys[(size_t)m * p.ldys + (oc >> 7)] = s.sc;
+                if (EPI == EPI_GEGLU && p.Y) {
+#pragma unroll
+                    for (int i = 0; i < 16; i += 4)
+                        *(float4 *)(p.Y + (size_t)m * p.ldy + oc + i) =
+                            make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP>
+static int launch_tile(hipStream_t s, const GemmArgs &p) {
+    constexpr int NT = (BM / WM) * (BN / WN) * 64;
+    constexpr int NWAVE = (BM / WM) * (BN / WN);
+    constexpr size_t lds = NS * ((size_t)(BM + BN) * 128 + 64 * NWAVE * 4);
+    static_assert(NS >= 2 && NS <= 4 && lds <= 160 * 1024, "LDS budget");
+    auto kern = k_gemm<BM, BN, WM, WN, NS, EPI, DUMP>;
+    static bool attr = false;
+    if (!attr) {
+        if (check_hip(hipFuncSetAttribute((const void *)kern,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                      "gemm lds attribute"))
+            return -1;
+        attr = true;
+    }
+    const long tiles = (long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NT), lds, s, p);
+    return check_hip(hipGetLastError(), "gemm launch");
+}
+
+static int check_args(const GemmArgs &p, const char *who) {
+    if (p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % kQBlock) {
+        set_error("%s: bad geometry M=%d N=%d K=%d (K must be a positive multiple of 128)", who, p.M,
+                  p.N, p.K);
+        return -1;
+    }
+    if (!p.A || !p.as || !p.W || !p.ws || !aligned16(p.A) || !aligned16(p.W) || p.lda % 16 ||
+        p.ldw % 16 || p.lda < p.K || p.ldw < p.K) {
+        set_error("%s: operands must be non-null, 16-byte aligned, with 16-byte row pitches >= K", who);
+        return -1;
+    }
+    if ((long)p.M * (long)p.N > (1L << 31) || (long)p.M * p.lda >= (1L << 32) ||
+        (long)p.N * p.ldw >= (1L << 32)) {
+        set_error("%s: problem too large", who);
+        return -1;
+    }
+    return 0;
+}
+
+int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump) {
+    if (check_args(p, "i8_gemm")) return -1;
+    if (!p.Y || p.ldy < p.N) {
+        set_error("i8_gemm: null output or ldy < N");
+        return -1;
+    }
+    if (dump) {
+        if (!p.accd) {
+            set_error("i8_gemm: null accumulator dump");
+            return -1;
+        }
+        return launch_tile<128, 128, 64, 64, 2, EPI_F32, true>(s, p);
+    }
+    return launch_tile<128, 128, 64, 64, 2, EPI_F32, false>(s, p);
+}
+
+int launch_gemm_i8q(hipStream_t s, GemmArgs p) {
+    if (check_args(p, "i8_gemm_q")) return -1;
+    if (p.N % 128 || !p.Yq || !p.ys || p.ldyq < p.N || p.ldyq % 16 || !aligned16(p.Yq) ||
+        p.ldys < p.N / 128) {
+        set_error("i8_gemm_q: N must be a multiple of 128 with a 16-byte aligned int8 output");
+        return -1;
+    }
+    return launch_tile<128, 128, 64, 64, 2, EPI_I8Q, false>(s, p);
+}
+
+int launch_gemm_geglu(hipStream_t s, GemmArgs p) {
+    if (check_args(p, "i8_gemm_geglu")) return -1;
+    if (p.N % 256 || !p.Yq || !p.ys || p.ldyq < p.N / 2 || p.ldyq % 16 || !aligned16(p.Yq) ||
+        p.ldys < p.N / 256 || (p.Y && (p.ldy < p.N / 2 || p.ldy % 4 || !aligned16(p.Y)))) {
+        set_error("i8_gemm_geglu: N (gate|up interleaved) must be a multiple of 256, outputs aligned");
+        return -1;
+    }
+    return launch_tile<64, 256, 32, 128, 2, EPI_GEGLU, false>(s, p);
+}
+
+}  // namespace e2mi
+
+// ------------------------------------------------------------------ C ABI
+using namespace e2mi;
+
+static int weight_ok(const e2mi_q8w *w, const char *who) {
+    if (!w || !w->w || !w->scale || w->N <= 0 || w->K <= 0 || w->K % 128 || w->ld < w->K ||
+        w->ld % 16) {
+        set_error("%s: invalid weight handle", who);
+        return 0;
+    }
+    return 1;
+}
+
+static GemmArgs make_args(const int8_t *qa, const float *as, const e2mi_q8w *w, int M, int n0,
+                          int n1) {
+    GemmArgs p = {};
+    p.A = qa;
+    p.as = as;
+    p.W = w->w + (size_t)n0 * w->ld;
+    p.ws = w->scale + n0;
+    p.bias = w->bias ? w->bias + n0 : nullptr;
+    p.lda = w->K;
+    p.ldw = w->ld;
+    p.M = M;
+    p.N = n1 - n0;
+    p.K = w->K;
+    p.lo = w->out_min;
+    p.hi = w->out_max;
+    return p;
+}
+
+extern "C" int e2mi_i8_gemm(e2mi_stream stream, float *y, int ldy, const int8_t *qa,
+                            const float *a_scales, const e2mi_q8w *w, int M, int n0, int n1) {
+    if (!weight_ok(w, "i8_gemm")) return -1;
+    if (n0 < 0 || n1 > w->N || n0 >= n1 || !y) {
+        set_error("i8_gemm: bad column range [%d,%d) for N=%d", n0, n1, w ? w->N : 0);
+        return -1;
+    }
+    GemmArgs p = make_args(qa, a_scales, w, M, n0, n1);
+    p.Y = y + n0;
+    p.ldy = ldy;
+    return launch_gemm_f32((hipStream_t)stream, p, false);
+}
+
+extern "C" int e2mi_i8_gemm_acc(e2mi_stream stream, float *y, int ldy, int32_t *acc,
+                                const int8_t *qa, const float *a_scales, const e2mi_q8w *w, int M,
+                                int n0, int n1) {
+    if (!weight_ok(w, "i8_gemm_acc")) return -1;
+    if (n0 < 0 || n1 > w->N || n0 >= n1 || !y || !acc) {
+        set_error("i8_gemm_acc: bad column range [%d,%d) or null output", n0, n1);
+        return -1;
+    }
+    GemmArgs p = make_args(qa, a_scales, w, M, n0, n1);
+    p.Y = y + n0;
+    p.ldy = ldy;
+    p.accd = acc;
+    return launch_gemm_f32((hipStream_t)stream, p, true);
+}
+
+extern "C" int e2mi_i8_gemm_q(e2mi_stream stream, int8_t *yq, float *ys, const int8_t *qa,
+                              const float *a_scales, const e2mi_q8w *w, int M) {
+    if (!weight_ok(w, "i8_gemm_q")) return -1;
+    GemmArgs p = make_args(qa, a_scales, w, M, 0, w->N);
+    p.Yq = yq;
+    p.ldyq = w->N;
+    p.ys = ys;
+    p.ldys = w->N / 128;
+    return launch_gemm_i8q((hipStream_t)stream, p);
+}
+
+extern "C" int e2mi_i8_gemm_geglu(e2mi_stream stream, int8_t *q, float *qs, float *g,
+                                  const int8_t *qa, const float *a_scales,
+                                  const e2mi_q8w *w_gate_up, int M) {
+    if (!weight_ok(w_gate_up, "i8_gemm_geglu")) return -1;
+    GemmArgs p = make_args(qa, a_scales, w_gate_up, M, 0, w_gate_up->N);
+    const int F = w_gate_up->N / 2;
+    p.Yq = q;
+    p.ldyq = F;
+    p.ys = qs;
+    p.ldys = F / 128;
+    p.Y = g;
+    p.ldy = F;
+    return launch_gemm_geglu((hipStream_t)stream, p);
+}

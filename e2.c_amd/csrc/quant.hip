@@ -1,0 +1,76 @@
+// quant.hip — per-(row, 128-block) symmetric int8 activation quantizer for gfx950.
+//
+// Same contract as the reference's e2_i8_quantize (src/kernels.h:70-72; arithmetic of
+// src/kernels_i8_avx512_vnni.c:312-366 as compiled): per block amax, scale = amax*RN(1/127),
+// inv = 127/amax, q = rne(x*inv). Bytes are stored signed (include/e2hip.h:19-21), scales in the
+// reference's [M][nb] layout. HBM-bound: each 128-element block is one half-wave's float4 loads,
+// a 5-step xor-shuffle max, and one 4-byte store per lane.
+#include "common.h"
+
+namespace e2mi {
+
+// block == 128: a half-wave per (row, block); 8 blocks per 256-thread workgroup.
+__global__ __launch_bounds__(256) void k_quant128(int8_t *__restrict__ q, float *__restrict__ sc,
+                                                  const float *__restrict__ x, int M, int K,
+                                                  int ldx, int ldq) {
+    const int nb = K / kQBlock;
+    const long item = (long)blockIdx.x * 8 + (threadIdx.x >> 5);
+    if (item >= (long)M * nb) return;
+    const int m = (int)(item / nb), b = (int)(item % nb), l = threadIdx.x & 31;
+    const float4 v = *(const float4 *)(x + (size_t)m * ldx + b * kQBlock + l * 4);
+    float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    a = group_max<32>(a);
+    const QScale s = qscale(a);
+    *(uint32_t *)(q + (size_t)m * ldq + b * kQBlock + l * 4) =
+        pack4(qbyte(v.x, s.inv), qbyte(v.y, s.inv), qbyte(v.z, s.inv), qbyte(v.w, s.inv));
+    if (l == 0) sc[(size_t)m * nb + b] = s.sc;
+}
+
+// block == K (the per-token variant, the reference rebuilt with -DE2_I8_BLOCK=K): one wave per row.
+__global__ __launch_bounds__(256) void k_quant_row(int8_t *__restrict__ q, float *__restrict__ sc,
+                                                   const float *__restrict__ x, int M, int K,
+                                                   int ldx, int ldq) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (m >= M) return;
+    const float *xr = x + (size_t)m * ldx;
+    float a = 0.f;
+    for (int k = l * 4; k < K; k += 256) {
+        const float4 v = *(const float4 *)(xr + k);
+        a = fmaxf(a, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    a = group_max<64>(a);
+    const QScale s = qscale(a);
+    for (int k = l * 4; k < K; k += 256) {
+        const float4 v = *(const float4 *)(xr + k);
+        *(uint32_t *)(q + (size_t)m * ldq + k) =
+            pack4(qbyte(v.x, s.inv), qbyte(v.y, s.inv), qbyte(v.z, s.inv), qbyte(v.w, s.inv));
+    }
+    if (l == 0) sc[m] = s.sc;
+}
+
+int launch_quantize(hipStream_t s, int8_t *q, int ldq, float *scales, const float *x, int M,
+                    int K, int ldx, int block) {
+    if (M <= 0 || K <= 0 || K % 128 || ldx < K || ldq < K || ldx % 4 || ldq % 4) {
+        set_error("quantize: bad geometry M=%d K=%d ldx=%d ldq=%d (K %% 128 == 0, ld >= K, ld %% 4 == 0)",
+                  M, K, ldx, ldq);
+        return -1;
+    }
+    if (!q || !scales || !x || !aligned16(x) || ((uintptr_t)q & 3)) {
+        set_error("quantize: null or misaligned pointer (x 16-B, q 4-B aligned)");
+        return -1;
+    }
+    if (block == kQBlock) {
+        const long items = (long)M * (K / kQBlock);
+        hipLaunchKernelGGL(k_quant128, dim3((unsigned)((items + 7) / 8)), dim3(256), 0, s, q,
+                           scales, x, M, K, ldx, ldq);
+    } else if (block == K) {
+        hipLaunchKernelGGL(k_quant_row, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, s, q, scales,
+                           x, M, K, ldx, ldq);
+    } else {
+        set_error("quantize: block must be 128 or K (got %d, K=%d)", block, K);
+        return -1;
+    }
+    return check_hip(hipGetLastError(), "quantize launch");
+}
+
+}  // namespace e2mi

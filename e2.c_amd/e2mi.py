@@ -1,0 +1,190 @@
+"""Python mirror of include/e2mi.h over ctypes.
+
+The product is the C-ABI library lib/libe2mi.so (hand-written HIP for gfx950). This module only
+binds it for tests and bench.py: device buffers are torch tensors (plumbing for HBM allocation and
+streams), passed to the library as raw pointers. There is no fallback: if the library is missing,
+`load()` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libe2mi.so")
+
+_P, _I, _F = C.c_void_p, C.c_int, C.c_float
+
+
+class Q8W(C.Structure):
+    """e2mi_q8w (include/e2mi.h)."""
+    _fields_ = [("w", _P), ("scale", _P), ("bias", _P), ("N", _I), ("K", _I), ("ld", _I),
+                ("out_min", _F), ("out_max", _F)]
+
+
+# name -> (restype, argtypes); every symbol include/*.h declares appears here
+SIGNATURES = {
+    "e2mi_last_error": (C.c_char_p, []),
+    "e2mi_device_info": (_I, [_I, C.c_char_p, _I, C.POINTER(_I), C.POINTER(_I)]),
+    "e2mi_q8w_upload_packed": (_I, [C.POINTER(Q8W), _P, _P, _P, _I, _I, _P]),
+    "e2mi_q8w_upload_rowmajor": (_I, [C.POINTER(Q8W), _P, _P, _P, _I, _I, _P]),
+    "e2mi_q8w_free": (None, [C.POINTER(Q8W)]),
+    "e2mi_quantize": (_I, [_P, _P, _P, _P, _I, _I, _I, _I]),
+    "e2mi_i8_gemm": (_I, [_P, _P, _I, _P, _P, C.POINTER(Q8W), _I, _I, _I]),
+    "e2mi_i8_gemm_acc": (_I, [_P, _P, _I, _P, _P, _P, C.POINTER(Q8W), _I, _I, _I]),
+    "e2mi_i8_gemm_q": (_I, [_P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
+    "e2mi_i8_gemm_geglu": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
+    "e2mi_interleave_gate_up": (_I, [_P, _P, _P, _P, _P, _P, _I, _I]),
+}
+
+_lib = None
+
+
+class E2MIError(RuntimeError):
+    pass
+
+
+def load(path: str = LIB_PATH):
+    """Load lib/libe2mi.so and declare every entry point. Raises if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise E2MIError(f"{path} is missing: the HIP backend was not built (run __graft_entry__.build())")
+    lib = C.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().e2mi_last_error().decode(errors="replace")
+
+
+def check(rc: int, what: str = "e2mi"):
+    if rc != 0:
+        raise E2MIError(f"{what}: {last_error()}")
+
+
+def ptr(t):
+    """Raw device (or host numpy) pointer of a tensor/array, None for None."""
+    if t is None:
+        return None
+    if hasattr(t, "data_ptr"):
+        return C.c_void_p(t.data_ptr())
+    return t.ctypes.data_as(C.c_void_p)
+
+
+def stream_ptr(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+class DeviceWeight:
+    """An uploaded e2mi_q8w; freed with the object."""
+
+    def __init__(self, q8w: Q8W):
+        self.q = q8w
+
+    @classmethod
+    def from_rowmajor(cls, w, scale, bias=None, stream=None):
+        import numpy as np
+        w = np.ascontiguousarray(w, np.int8)
+        scale = np.ascontiguousarray(scale, np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        q = Q8W()
+        check(load().e2mi_q8w_upload_rowmajor(C.byref(q), ptr(w), ptr(scale), ptr(b), w.shape[0],
+                                              w.shape[1], stream_ptr(stream)), "q8w_upload_rowmajor")
+        return cls(q)
+
+    @classmethod
+    def from_packed(cls, wq, scale, N, K, bias=None, stream=None):
+        import numpy as np
+        wq = np.ascontiguousarray(wq, np.int8)
+        scale = np.ascontiguousarray(scale, np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        q = Q8W()
+        check(load().e2mi_q8w_upload_packed(C.byref(q), ptr(wq), ptr(scale), ptr(b), N, K,
+                                            stream_ptr(stream)), "q8w_upload_packed")
+        return cls(q)
+
+    def set_clamp(self, lo, hi):
+        self.q.out_min, self.q.out_max = lo, hi
+
+    def __del__(self):
+        if _lib is not None and self.q.w:
+            _lib.e2mi_q8w_free(C.byref(self.q))
+
+    @property
+    def ref(self):
+        return C.byref(self.q)
+
+
+def interleave_gate_up(gate, sgate, up, sup):
+    import numpy as np
+    F, K = gate.shape
+    w = np.empty((2 * F, K), np.int8)
+    s = np.empty(2 * F, np.float32)
+    args = [np.ascontiguousarray(a) for a in (gate, sgate, up, sup)]
+    check(load().e2mi_interleave_gate_up(ptr(w), ptr(s), ptr(args[0]), ptr(args[1]), ptr(args[2]),
+                                         ptr(args[3]), F, K), "interleave_gate_up")
+    return w, s
+
+
+# ---- kernel wrappers over torch device tensors
+def quantize(x, block=128, q=None, scales=None, stream=None):
+    import torch
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device) if q is None else q
+    nb = K // block
+    scales = torch.empty((M, nb), dtype=torch.float32, device=x.device) if scales is None else scales
+    check(load().e2mi_quantize(stream_ptr(stream), ptr(q), ptr(scales), ptr(x), M, K, x.stride(0),
+                               block), "quantize")
+    return q, scales
+
+
+def i8_gemm(qa, as_, w: DeviceWeight, n0=0, n1=None, y=None, stream=None):
+    import torch
+    M = qa.shape[0]
+    n1 = w.q.N if n1 is None else n1
+    y = torch.zeros((M, w.q.N), dtype=torch.float32, device=qa.device) if y is None else y
+    check(load().e2mi_i8_gemm(stream_ptr(stream), ptr(y), y.stride(0), ptr(qa), ptr(as_), w.ref, M,
+                              n0, n1), "i8_gemm")
+    return y
+
+
+def i8_gemm_acc(qa, as_, w: DeviceWeight, n0=0, n1=None, stream=None):
+    import torch
+    M = qa.shape[0]
+    n1 = w.q.N if n1 is None else n1
+    y = torch.zeros((M, w.q.N), dtype=torch.float32, device=qa.device)
+    acc = torch.zeros((w.q.K // 128, M, n1 - n0), dtype=torch.int32, device=qa.device)
+    check(load().e2mi_i8_gemm_acc(stream_ptr(stream), ptr(y), y.stride(0), ptr(acc), ptr(qa),
+                                  ptr(as_), w.ref, M, n0, n1), "i8_gemm_acc")
+    return y, acc
+
+
+def i8_gemm_q(qa, as_, w: DeviceWeight, stream=None):
+    import torch
+    M = qa.shape[0]
+    yq = torch.empty((M, w.q.N), dtype=torch.int8, device=qa.device)
+    ys = torch.empty((M, w.q.N // 128), dtype=torch.float32, device=qa.device)
+    check(load().e2mi_i8_gemm_q(stream_ptr(stream), ptr(yq), ptr(ys), ptr(qa), ptr(as_), w.ref, M),
+          "i8_gemm_q")
+    return yq, ys
+
+
+def i8_gemm_geglu(qa, as_, w: DeviceWeight, want_g=True, stream=None):
+    import torch
+    M = qa.shape[0]
+    F = w.q.N // 2
+    q = torch.empty((M, F), dtype=torch.int8, device=qa.device)
+    qs = torch.empty((M, F // 128), dtype=torch.float32, device=qa.device)
+    g = torch.empty((M, F), dtype=torch.float32, device=qa.device) if want_g else None
+    check(load().e2mi_i8_gemm_geglu(stream_ptr(stream), ptr(q), ptr(qs), ptr(g), ptr(qa), ptr(as_),
+                                    w.ref, M), "i8_gemm_geglu")
+    return q, qs, g

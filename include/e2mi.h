@@ -1,0 +1,98 @@
+/* e2mi.h — the gfx950 (MI355X) int8 encoder backend: a C ABI over hand-written HIP kernels.
+ *
+ * The device sibling of the reference's include/e2hip.h (Damix48/e2.c): the same int8 recipe
+ * (per-output-row int8 weights with f32 scales, per-(token, 128-element block) dynamic activation
+ * scales, exact int32 accumulation, per-block f32 fold), rebuilt for CDNA4 int8 MFMA. Paths in the
+ * citations below are relative to the reference's root.
+ *
+ * Conventions (all entry points):
+ *   - return 0 on success, -1 on error with a message in e2mi_last_error() (hip.c:27-49);
+ *   - arguments are validated before anything is launched or written (hip.c:287-342);
+ *   - kernel-level entry points take DEVICE pointers and enqueue on `stream` (a hipStream_t, NULL
+ *     for the default stream); they do not synchronise;
+ *   - int8 activations are SIGNED (e2hip.h:19-21): the CPU reference's biased byte is
+ *     (uint8_t)(q ^ 0x80);
+ *   - activation scales use the reference's [M][K/128] layout (int8.h:94-97, a_scales[m*nb + b]).
+ */
+#ifndef E2MI_H
+#define E2MI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *e2mi_stream; /* hipStream_t */
+
+/* Device-resident int8 weight: the reference's e2_q8w (int8.h:79-92) re-laid out for MFMA.
+ * w is row-major [N][ld] (K contiguous, ld % 16 == 0), scale is [N], bias [N] or NULL.
+ * out_min/out_max: optional output saturation (int8.h:85-88); +-1e31 means none. */
+typedef struct {
+    int8_t *w;
+    float *scale;
+    float *bias;
+    int N, K, ld;
+    float out_min, out_max;
+} e2mi_q8w;
+
+/* Last error of this process (e2hip.h:64 e2_hip_last_error). Never NULL. */
+const char *e2mi_last_error(void);
+
+/* Name, compute-unit count and peak clock of device `dev` (e2hip.h:39 e2_hip_device). */
+int e2mi_device_info(int dev, char *name, int cap, int *cus, int *clock_khz);
+
+/* ---- weights: the reference's load-time path (e2.c:393-414, q8cache.c:357-385) */
+
+/* Upload a reference-packed weight (quad-interleaved [Npad/8][K/4][8][4] int8 plus per-row scales,
+ * int8.h:14-22) and re-lay it out on the device. bias may be NULL. The bsq block sums of the CPU
+ * format are not needed: the device path multiplies signed bytes directly. */
+int e2mi_q8w_upload_packed(e2mi_q8w *out, const int8_t *wq, const float *scale, const float *bias,
+                           int N, int K, e2mi_stream stream);
+/* Upload a row-major [N][K] int8 weight. */
+int e2mi_q8w_upload_rowmajor(e2mi_q8w *out, const int8_t *w, const float *scale, const float *bias,
+                             int N, int K, e2mi_stream stream);
+void e2mi_q8w_free(e2mi_q8w *w);
+
+/* ---- kernels (device pointers) */
+
+/* Per-(row, block) activation quantizer: replaces e2_i8_quantize (kernels.h:70-72;
+ * kernels_i8_avx512_vnni.c:312-366). block = 128 (the reference default) or K (per-token).
+ * x [M][ldx] f32 -> q [M][K] int8 (row pitch K), scales [M][K/block]. K % 128 == 0. */
+int e2mi_quantize(e2mi_stream stream, int8_t *q, float *scales, const float *x, int M, int K,
+                  int ldx, int block);
+
+/* W8A8 GEMM with fused dequant: replaces e2_i8_gemm (int8.h:94-97, kernels.h:69):
+ * y[m][n] for n in [n0, n1) = sum_b fma(acc_b, as[m,b]*ws[n], .) (+bias[n]), clamped to the
+ * weight's [out_min, out_max]; y row pitch ldy (columns are absolute, as in the reference). */
+int e2mi_i8_gemm(e2mi_stream stream, float *y, int ldy, const int8_t *qa, const float *a_scales,
+                 const e2mi_q8w *w, int M, int n0, int n1);
+
+/* Same GEMM, also writing every block's exact int32 accumulator to acc [K/128][M][n1-n0]
+ * (the parity hook for "bit-exact int32 accumulators"). */
+int e2mi_i8_gemm_acc(e2mi_stream stream, float *y, int ldy, int32_t *acc, const int8_t *qa,
+                     const float *a_scales, const e2mi_q8w *w, int M, int n0, int n1);
+
+/* GEMM whose epilogue requantizes the output per (row, 128 columns) for the next GEMM instead of
+ * writing f32: the quantization the reference runs on y (text.c:321-339), fused. N % 128 == 0.
+ * yq [M][N] int8, ys [M][N/128]. */
+int e2mi_i8_gemm_q(e2mi_stream stream, int8_t *yq, float *ys, const int8_t *qa,
+                   const float *a_scales, const e2mi_q8w *w, int M);
+
+/* gate|up GEMM with the GeGLU product and its quantization fused in the epilogue (text.c:424-468
+ * gate_quant, fused into the producing GEMM). w holds 2*F rows interleaved per 256 as
+ * [128 gate rows | 128 up rows] (see e2mi_interleave_gate_up). Writes q [M][F] int8, qs [M][F/128]
+ * and, when g != NULL, the f32 product g [M][F] (the reference writes it back into gate). */
+int e2mi_i8_gemm_geglu(e2mi_stream stream, int8_t *q, float *qs, float *g, const int8_t *qa,
+                       const float *a_scales, const e2mi_q8w *w_gate_up, int M);
+
+/* Host helper: interleave row-major gate [F][K] and up [F][K] int8 (and their scales) into the
+ * [F/128][gate 128 | up 128] row order e2mi_i8_gemm_geglu consumes. F % 128 == 0. */
+int e2mi_interleave_gate_up(int8_t *w_out, float *s_out, const int8_t *gate, const float *sgate,
+                            const int8_t *up, const float *sup, int F, int K);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* E2MI_H */
