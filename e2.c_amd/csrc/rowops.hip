@@ -1,0 +1,400 @@
+// rowops.hip — the memory-bound row kernels of the encoder layer (gfx950, wave64).
+//
+// Reference semantics (paths relative to the reference root):
+//   RMSNorm        x * (1/sqrt(sum(x^2)/D + eps)) * gamma         kernels.c:76-87
+//   norm_split     res := x, x := rmsnorm(x) * gamma              kernels.c:149-160, text.c:236-248
+//   norm_add       out := rmsnorm(src) * gamma + res              kernels.c:161-171, text.c:250-264
+//   embed          x := table[id] * embed_scale                   text.c:917-921
+//   q/k/v norm     q,k rmsnorm*gamma, v rmsnorm without gamma     text.c:836-838
+//   RoPE           rotate-half, pair (i, i+D/2), positions restart per sequence  kernels.c:112-126
+//   GeGLU quant    g := gelu_tanh(gate) * up, quantized per 128   text.c:424-468
+//   pooling        masked mean over valid rows, then L2           kernels.c:22-39, text.c:963-981
+//
+// Each row is held by one wave (D/256 float4 per lane): the sum of squares is a wave reduction,
+// and a 128-element quantization block is exactly one half-wave's float4 slice, so the per-block
+// amax is a 32-lane reduction. The fused variants read each row once and write the next GEMM's int8
+// operand directly, instead of the reference's separate norm, copy and quantize passes.
+#include "common.h"
+
+namespace e2mi {
+
+enum { ROW_PLAIN = 0, ROW_EMBED = 1, ROW_ADDNORM = 2 };
+
+struct RowArgs {
+    const float *src;      // PLAIN/ADDNORM input rows [M][D] (ld = D)
+    const float *res;      // ADDNORM residual [M][D]
+    const float *table;    // EMBED table [vocab][D]
+    const int32_t *ids;    // EMBED token ids [M]
+    float embed_scale;
+    const float *gamma_a;  // ADDNORM: gamma of the norm applied to src
+    const float *gamma_n;  // gamma of the norm producing the quantized operand (NULL: no norm)
+    float eps;
+    float *x_out;          // new residual stream x (may alias res), or NULL
+    float *xn_out;         // normed rows (f32), or NULL
+    int8_t *q;             // quantized normed rows [M][D], or NULL
+    float *qs;             // their per-128 scales [M][D/128]
+    int M, D;
+};
+
+__device__ inline float4 ld4(const float *p) { return *(const float4 *)p; }
+__device__ inline void st4(float *p, float4 v) { *(float4 *)p = v; }
+__device__ inline float sumsq4(float4 v) { return v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w; }
+__device__ inline float amax4(float4 v) {
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+__device__ inline float rms_inv(float ss, int D, float eps) {
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)D) + eps));
+}
+__device__ inline float4 scale4(float4 v, float inv, float4 g) {
+    return make_float4(__fmul_rn(__fmul_rn(v.x, inv), g.x), __fmul_rn(__fmul_rn(v.y, inv), g.y),
+                       __fmul_rn(__fmul_rn(v.z, inv), g.z), __fmul_rn(__fmul_rn(v.w, inv), g.w));
+}
+
+// NC = float4 chunks per lane = D / 256 (rounded up); chunk i of lane l covers elements
+// 4*(l + 64 i) .. +3, so quantization block (4*(l+64i))/128 = 2i + l/32.
+template <int MODE, int NC>
+__global__ __launch_bounds__(256) void k_rows(RowArgs a) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (m >= a.M) return;
+    const int D = a.D, nch = D / 4;
+    float4 v[NC];
+    const float *row;
+    float escale = 1.f;
+    if (MODE == ROW_EMBED) {
+        row = a.table + (size_t)a.ids[m] * D;
+        escale = a.embed_scale;
+    } else {
+        row = a.src + (size_t)m * D;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        const int c = l + 64 * i;
+        v[i] = c < nch ? ld4(row + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (MODE == ROW_EMBED)
+            v[i] = make_float4(__fmul_rn(v[i].x, escale), __fmul_rn(v[i].y, escale),
+                               __fmul_rn(v[i].z, escale), __fmul_rn(v[i].w, escale));
+        ss += sumsq4(v[i]);
+    }
+    if (MODE == ROW_ADDNORM) {
+        // x = rmsnorm(src) * gamma_a + res
+        const float inv = rms_inv(group_sum<64>(ss), D, a.eps);
+        ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NC; i++) {
+            const int c = l + 64 * i;
+            if (c < nch) {
+                const float4 g = ld4(a.gamma_a + 4 * c), r = ld4(a.res + (size_t)m * D + 4 * c);
+                const float4 t = scale4(v[i], inv, g);
+                v[i] = make_float4(t.x + r.x, t.y + r.y, t.z + r.z, t.w + r.w);
+            }
+            ss += sumsq4(v[i]);
+        }
+    }
+    if (a.x_out) {
+#pragma unroll
+        for (int i = 0; i < NC; i++)
+            if (l + 64 * i < nch) st4(a.x_out + (size_t)m * D + 4 * (l + 64 * i), v[i]);
+    }
+    if (!a.gamma_n) return;
+    const float inv = rms_inv(group_sum<64>(ss), D, a.eps);
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        const int c = l + 64 * i;
+        if (c < nch) v[i] = scale4(v[i], inv, ld4(a.gamma_n + 4 * c));
+        if (a.xn_out && c < nch) st4(a.xn_out + (size_t)m * D + 4 * c, v[i]);
+    }
+    if (!a.q) return;
+    const int nb = D / kQBlock;
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        const int c = l + 64 * i;
+        // both half-waves of chunk i are either fully inside D or fully outside (D % 128 == 0)
+        if (64 * i >= nch) break;
+        const float am = group_max<32>(c < nch ? amax4(v[i]) : 0.f);
+        if (c < nch) {
+            const QScale s = qscale(am);
+            *(uint32_t *)(a.q + (size_t)m * D + 4 * c) =
+                pack4(qbyte(v[i].x, s.inv), qbyte(v[i].y, s.inv), qbyte(v[i].z, s.inv),
+                      qbyte(v[i].w, s.inv));
+            if ((l & 31) == 0) a.qs[(size_t)m * nb + (4 * c) / kQBlock] = s.sc;
+        }
+    }
+}
+
+// ---- q/k/v RMSNorm + RoPE: one wave per (row, head) of 256 dims, outputs f16 for the attention.
+struct QkvArgs {
+    const float *qkv;          // [M][(H + 2 KV) * D]: q heads, k heads, v heads
+    const float *q_gamma, *k_gamma;
+    const float *cs, *sn;      // [S][D] RoPE tables (cos(f_i) at i and i + D/2)
+    float eps;
+    uint16_t *q16;             // [M][H*D] f16
+    uint16_t *k16;             // [M][KV*D] f16
+    uint16_t *vt16;            // [B][KV][D][S] f16 (V transposed per sequence)
+    float *q32, *k32, *v32;    // optional f32 copies (parity tests), same layouts as q16/k16/[M][KV*D]
+    int M, S, H, KV;
+};
+
+__device__ inline uint16_t f2h(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+
+__global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a) {
+    constexpr int D = 256;
+    const int heads = a.H + 2 * a.KV;
+    const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= (long)a.M * heads) return;
+    const int m = (int)(item / heads), h = (int)(item % heads), l = threadIdx.x & 63;
+    const int kind = h < a.H ? 0 : (h < a.H + a.KV ? 1 : 2);  // q, k, v
+    float4 v = ld4(a.qkv + (size_t)m * heads * D + h * D + 4 * l);
+    const float inv = rms_inv(group_sum<64>(sumsq4(v)), D, a.eps);
+    if (kind == 2) {
+        v = make_float4(__fmul_rn(v.x, inv), __fmul_rn(v.y, inv), __fmul_rn(v.z, inv),
+                        __fmul_rn(v.w, inv));
+    } else {
+        v = scale4(v, inv, ld4((kind == 0 ? a.q_gamma : a.k_gamma) + 4 * l));
+        // rotate-half: lane l < 32 holds a = x[i], lane l + 32 holds y = x[i + 128]
+        const int pos = m % a.S;
+        const float4 c = ld4(a.cs + (size_t)pos * D + 4 * l), s = ld4(a.sn + (size_t)pos * D + 4 * l);
+        const float4 o = make_float4(__shfl_xor(v.x, 32), __shfl_xor(v.y, 32), __shfl_xor(v.z, 32),
+                                     __shfl_xor(v.w, 32));
+        if (l < 32) {  // a' = a c - y s
+            v = make_float4(__fmul_rn(v.x, c.x) - __fmul_rn(o.x, s.x), __fmul_rn(v.y, c.y) - __fmul_rn(o.y, s.y),
+                            __fmul_rn(v.z, c.z) - __fmul_rn(o.z, s.z), __fmul_rn(v.w, c.w) - __fmul_rn(o.w, s.w));
+        } else {       // y' = y c + a s
+            v = make_float4(__fmul_rn(v.x, c.x) + __fmul_rn(o.x, s.x), __fmul_rn(v.y, c.y) + __fmul_rn(o.y, s.y),
+                            __fmul_rn(v.z, c.z) + __fmul_rn(o.z, s.z), __fmul_rn(v.w, c.w) + __fmul_rn(o.w, s.w));
+        }
+    }
+    const uint32_t lo = (uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16);
+    const uint32_t hi = (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16);
+    if (kind == 0) {
+        *(uint2 *)(a.q16 + (size_t)m * a.H * D + h * D + 4 * l) = make_uint2(lo, hi);
+        if (a.q32) st4(a.q32 + (size_t)m * a.H * D + h * D + 4 * l, v);
+    } else if (kind == 1) {
+        const int kh = h - a.H;
+        *(uint2 *)(a.k16 + (size_t)m * a.KV * D + kh * D + 4 * l) = make_uint2(lo, hi);
+        if (a.k32) st4(a.k32 + (size_t)m * a.KV * D + kh * D + 4 * l, v);
+    } else {
+        const int vh = h - a.H - a.KV, b = m / a.S, p = m % a.S;
+        uint16_t *dst = a.vt16 + ((size_t)(b * a.KV + vh) * D + 4 * l) * a.S + p;
+        dst[0] = (uint16_t)lo;
+        dst[a.S] = (uint16_t)(lo >> 16);
+        dst[2 * a.S] = (uint16_t)hi;
+        dst[3 * a.S] = (uint16_t)(hi >> 16);
+        if (a.v32) st4(a.v32 + (size_t)m * a.KV * D + vh * D + 4 * l, v);
+    }
+}
+
+// ---- standalone GeGLU * up + quantize (the unfused gate_quant of text.c:424-468)
+__device__ inline float gelu_tanh_f(float v) {
+    const float c = 0.7978845608028654f;
+    return 0.5f * v * (1.f + tanhf(c * (v + 0.044715f * v * v * v)));
+}
+
+__global__ __launch_bounds__(256) void k_gelu_mul_quant(float *__restrict__ gate, int ldg,
+                                                        const float *__restrict__ up, int ldu,
+                                                        int M, int D, int8_t *__restrict__ q,
+                                                        float *__restrict__ qs, int write_back) {
+    const int nb = D / kQBlock;
+    const long item = (long)blockIdx.x * 8 + (threadIdx.x >> 5);
+    if (item >= (long)M * nb) return;
+    const int m = (int)(item / nb), b = (int)(item % nb), l = threadIdx.x & 31;
+    float4 g = ld4(gate + (size_t)m * ldg + b * kQBlock + 4 * l);
+    const float4 u = ld4(up + (size_t)m * ldu + b * kQBlock + 4 * l);
+    g = make_float4(gelu_tanh_f(g.x) * u.x, gelu_tanh_f(g.y) * u.y, gelu_tanh_f(g.z) * u.z,
+                    gelu_tanh_f(g.w) * u.w);
+    if (write_back) st4(gate + (size_t)m * ldg + b * kQBlock + 4 * l, g);
+    const QScale s = qscale(group_max<32>(amax4(g)));
+    *(uint32_t *)(q + (size_t)m * D + b * kQBlock + 4 * l) =
+        pack4(qbyte(g.x, s.inv), qbyte(g.y, s.inv), qbyte(g.z, s.inv), qbyte(g.w, s.inv));
+    if (l == 0) qs[(size_t)m * nb + b] = s.sc;
+}
+
+// ---- masked mean pool + L2: partial sums per (sequence, 64-row chunk), then a finishing pass
+__global__ __launch_bounds__(256) void k_pool_partial(const float *__restrict__ x,
+                                                      const uint8_t *__restrict__ valid, int S,
+                                                      int D, int chunks, float *__restrict__ part,
+                                                      int *__restrict__ cnt) {
+    const int b = blockIdx.x / chunks, ch = blockIdx.x % chunks;
+    const int r0 = ch * 64, r1 = min(S, r0 + 64);
+    int n = 0;
+    for (int c = threadIdx.x; c < D / 4; c += blockDim.x) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        n = 0;
+        for (int r = r0; r < r1; r++) {
+            if (!valid[(size_t)b * S + r]) continue;
+            const float4 v = ld4(x + ((size_t)b * S + r) * D + 4 * c);
+            acc = make_float4(acc.x + v.x, acc.y + v.y, acc.z + v.z, acc.w + v.w);
+            n++;
+        }
+        st4(part + ((size_t)b * chunks + ch) * D + 4 * c, acc);
+    }
+    if (threadIdx.x == 0) {
+        n = 0;
+        for (int r = r0; r < r1; r++) n += valid[(size_t)b * S + r] != 0;
+        cnt[b * chunks + ch] = n;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_pool_finish(const float *__restrict__ part,
+                                                     const int *__restrict__ cnt, int chunks,
+                                                     int D, float *__restrict__ out) {
+    const int b = blockIdx.x;
+    __shared__ float red[256 / 64];
+    int n = 0;
+    for (int ch = 0; ch < chunks; ch++) n += cnt[b * chunks + ch];
+    float ss = 0.f;
+    float vals[4];
+    int k = 0;
+    for (int d = threadIdx.x; d < D; d += blockDim.x, k++) {
+        float s = 0.f;
+        for (int ch = 0; ch < chunks; ch++) s += part[((size_t)b * chunks + ch) * D + d];
+        const float mean = n > 0 ? __fdiv_rn(s, (float)n) : 0.f;
+        if (k < 4) vals[k] = mean;
+        ss += mean * mean;
+    }
+    ss = group_sum<64>(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int w = 0; w < (int)blockDim.x / 64; w++) tot += red[w];
+    // all-invalid sequences stay an exact zero vector (text.c:968-980)
+    const float inv = n > 0 ? __fdiv_rn(1.0f, __fsqrt_rn(tot)) : 1.0f;
+    k = 0;
+    for (int d = threadIdx.x; d < D && k < 4; d += blockDim.x, k++)
+        out[(size_t)b * D + d] = n > 0 ? __fmul_rn(vals[k], inv) : 0.f;
+}
+
+// ------------------------------------------------------------------ launchers
+static int row_launch(hipStream_t s, int mode, const RowArgs &a) {
+    if (a.M <= 0 || a.D <= 0 || a.D % 128 || a.D > 1280) {
+        set_error("row kernel: D must be a multiple of 128 up to 1280 (D=%d, M=%d)", a.D, a.M);
+        return -1;
+    }
+    const int nc = (a.D / 4 + 63) / 64;
+    dim3 grid((a.M + 3) / 4), block(256);
+#define ROWK(MODE)                                                                          \
+    switch (nc) {                                                                           \
+    case 1: hipLaunchKernelGGL((k_rows<MODE, 1>), grid, block, 0, s, a); break;             \
+    case 2: hipLaunchKernelGGL((k_rows<MODE, 2>), grid, block, 0, s, a); break;             \
+    case 3: hipLaunchKernelGGL((k_rows<MODE, 3>), grid, block, 0, s, a); break;             \
+    case 4: hipLaunchKernelGGL((k_rows<MODE, 4>), grid, block, 0, s, a); break;             \
+    default: hipLaunchKernelGGL((k_rows<MODE, 5>), grid, block, 0, s, a); break;            \
+    }
+    if (mode == ROW_EMBED) { ROWK(ROW_EMBED) }
+    else if (mode == ROW_ADDNORM) { ROWK(ROW_ADDNORM) }
+    else { ROWK(ROW_PLAIN) }
+#undef ROWK
+    return check_hip(hipGetLastError(), "row kernel launch");
+}
+
+int launch_rows(hipStream_t s, int mode, const RowArgs &a) { return row_launch(s, mode, a); }
+
+int launch_qkv_norm_rope(hipStream_t s, const QkvArgs &a) {
+    const long items = (long)a.M * (a.H + 2 * a.KV);
+    hipLaunchKernelGGL(k_qkv_norm_rope, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
+    return check_hip(hipGetLastError(), "qkv_norm_rope launch");
+}
+
+int launch_pool(hipStream_t s, const float *x, const uint8_t *valid, int B, int S, int D,
+                float *part, int *cnt, float *out) {
+    const int chunks = (S + 63) / 64;
+    hipLaunchKernelGGL(k_pool_partial, dim3(B * chunks), dim3(256), 0, s, x, valid, S, D, chunks,
+                       part, cnt);
+    hipLaunchKernelGGL(k_pool_finish, dim3(B), dim3(256), 0, s, part, cnt, chunks, D, out);
+    return check_hip(hipGetLastError(), "pool launch");
+}
+
+}  // namespace e2mi
+
+// ------------------------------------------------------------------ C ABI
+using namespace e2mi;
+
+static bool al16(const void *p) { return !p || aligned16(p); }
+
+extern "C" int e2mi_norm_quant(e2mi_stream stream, const float *x, const float *gamma, float eps,
+                               int M, int D, float *xn_out, int8_t *q, float *qs) {
+    if (!x || !gamma || !al16(x) || !al16(xn_out) || !al16(gamma) || (!q) != (!qs)) {
+        set_error("norm_quant: null/misaligned pointer");
+        return -1;
+    }
+    RowArgs a = {};
+    a.src = x; a.gamma_n = gamma; a.eps = eps; a.xn_out = xn_out; a.q = q; a.qs = qs; a.M = M; a.D = D;
+    return launch_rows((hipStream_t)stream, ROW_PLAIN, a);
+}
+
+extern "C" int e2mi_add_norm_quant(e2mi_stream stream, const float *src, const float *res,
+                                   const float *gamma_add, const float *gamma_next, float eps,
+                                   int M, int D, float *x_out, float *xn_out, int8_t *q, float *qs) {
+    if (!src || !res || !gamma_add || !al16(src) || !al16(res) || !al16(x_out) || !al16(xn_out) ||
+        (q && !gamma_next) || (!q) != (!qs)) {
+        set_error("add_norm_quant: null/misaligned pointer, or quantized output without gamma_next");
+        return -1;
+    }
+    RowArgs a = {};
+    a.src = src; a.res = res; a.gamma_a = gamma_add; a.gamma_n = gamma_next; a.eps = eps;
+    a.x_out = x_out; a.xn_out = xn_out; a.q = q; a.qs = qs; a.M = M; a.D = D;
+    return launch_rows((hipStream_t)stream, ROW_ADDNORM, a);
+}
+
+extern "C" int e2mi_embed_norm_quant(e2mi_stream stream, const float *table, const int32_t *ids,
+                                     float embed_scale, const float *gamma, float eps, int M, int D,
+                                     float *x_out, int8_t *q, float *qs) {
+    if (!table || !ids || !gamma || !x_out || !al16(table) || !al16(x_out) || (!q) != (!qs)) {
+        set_error("embed_norm_quant: null/misaligned pointer");
+        return -1;
+    }
+    RowArgs a = {};
+    a.table = table; a.ids = ids; a.embed_scale = embed_scale; a.gamma_n = gamma; a.eps = eps;
+    a.x_out = x_out; a.q = q; a.qs = qs; a.M = M; a.D = D;
+    return launch_rows((hipStream_t)stream, ROW_EMBED, a);
+}
+
+extern "C" int e2mi_qkv_norm_rope(e2mi_stream stream, const float *qkv, int M, int S, int H, int KV,
+                                  int D, const float *q_gamma, const float *k_gamma, float eps,
+                                  const float *cos_tab, const float *sin_tab, uint16_t *q16,
+                                  uint16_t *k16, uint16_t *vt16, float *q32, float *k32, float *v32) {
+    if (D != 256 || H <= 0 || KV <= 0 || H % KV || M <= 0 || S <= 0 || M % S) {
+        set_error("qkv_norm_rope: needs head_dim 256, H %% KV == 0 and M a multiple of S (M=%d S=%d H=%d KV=%d D=%d)",
+                  M, S, H, KV, D);
+        return -1;
+    }
+    if (!qkv || !q_gamma || !k_gamma || !cos_tab || !sin_tab || !q16 || !k16 || !vt16 ||
+        !aligned16(qkv) || !al16(q32) || !al16(k32) || !al16(v32) || ((uintptr_t)q16 & 7) ||
+        ((uintptr_t)k16 & 7)) {
+        set_error("qkv_norm_rope: null/misaligned pointer");
+        return -1;
+    }
+    QkvArgs a = {qkv, q_gamma, k_gamma, cos_tab, sin_tab, eps, q16, k16, vt16, q32, k32, v32, M, S, H, KV};
+    return launch_qkv_norm_rope((hipStream_t)stream, a);
+}
+
+extern "C" int e2mi_gelu_mul_quant(e2mi_stream stream, float *gate, int ldg, const float *up,
+                                   int ldu, int M, int D, int8_t *q, float *qs, int write_back) {
+    if (!gate || !up || !q || !qs || M <= 0 || D <= 0 || D % 128 || ldg < D || ldu < D ||
+        ldg % 4 || ldu % 4 || !aligned16(gate) || !aligned16(up)) {
+        set_error("gelu_mul_quant: bad geometry or pointers (D %% 128 == 0)");
+        return -1;
+    }
+    const long items = (long)M * (D / 128);
+    hipLaunchKernelGGL(k_gelu_mul_quant, dim3((unsigned)((items + 7) / 8)), dim3(256), 0,
+                       (hipStream_t)stream, gate, ldg, up, ldu, M, D, q, qs, write_back);
+    return check_hip(hipGetLastError(), "gelu_mul_quant launch");
+}
+
+extern "C" int e2mi_pool_l2(e2mi_stream stream, const float *x, const uint8_t *valid, int B, int S,
+                            int D, float *workspace, float *out) {
+    if (!x || !valid || !workspace || !out || B <= 0 || S <= 0 || D <= 0 || D % 4 || D > 1024 ||
+        !aligned16(x) || !aligned16(workspace)) {
+        set_error("pool_l2: bad geometry or pointers");
+        return -1;
+    }
+    const int chunks = (S + 63) / 64;
+    float *part = workspace;
+    int *cnt = (int *)(workspace + (size_t)B * chunks * D);
+    return launch_pool((hipStream_t)stream, x, valid, B, S, D, part, cnt, out);
+}
+
+extern "C" size_t e2mi_pool_workspace_bytes(int B, int S, int D) {
+    const size_t chunks = (size_t)(S + 63) / 64;
+    return (size_t)B * chunks * (D + 1) * sizeof(float);
+}

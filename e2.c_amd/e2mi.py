@@ -35,6 +35,14 @@ SIGNATURES = {
     "e2mi_i8_gemm_q": (_I, [_P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
     "e2mi_i8_gemm_geglu": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
     "e2mi_interleave_gate_up": (_I, [_P, _P, _P, _P, _P, _P, _I, _I]),
+    "e2mi_norm_quant": (_I, [_P, _P, _P, _F, _I, _I, _P, _P, _P]),
+    "e2mi_add_norm_quant": (_I, [_P, _P, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P]),
+    "e2mi_embed_norm_quant": (_I, [_P, _P, _P, _F, _P, _F, _I, _I, _P, _P, _P]),
+    "e2mi_qkv_norm_rope": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "e2mi_gelu_mul_quant": (_I, [_P, _P, _I, _P, _I, _I, _I, _P, _P, _I]),
+    "e2mi_pool_l2": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
+    "e2mi_pool_workspace_bytes": (C.c_size_t, [_I, _I, _I]),
+    "e2mi_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
 }
 
 _lib = None
@@ -188,3 +196,98 @@ def i8_gemm_geglu(qa, as_, w: DeviceWeight, want_g=True, stream=None):
     check(load().e2mi_i8_gemm_geglu(stream_ptr(stream), ptr(q), ptr(qs), ptr(g), ptr(qa), ptr(as_),
                                     w.ref, M), "i8_gemm_geglu")
     return q, qs, g
+
+
+# ---- row kernels
+def norm_quant(x, gamma, eps=1e-6, want_xn=True, quant=True, stream=None):
+    import torch
+    M, D = x.shape
+    xn = torch.empty_like(x) if want_xn else None
+    q = torch.empty((M, D), dtype=torch.int8, device=x.device) if quant else None
+    qs = torch.empty((M, D // 128), dtype=torch.float32, device=x.device) if quant else None
+    check(load().e2mi_norm_quant(stream_ptr(stream), ptr(x), ptr(gamma), eps, M, D, ptr(xn), ptr(q),
+                                 ptr(qs)), "norm_quant")
+    return xn, q, qs
+
+
+def add_norm_quant(src, res, gamma_add, gamma_next=None, eps=1e-6, x_out=None, want_xn=True,
+                   quant=True, stream=None):
+    import torch
+    M, D = src.shape
+    x_out = torch.empty_like(src) if x_out is None else x_out
+    has_next = gamma_next is not None
+    xn = torch.empty_like(src) if (want_xn and has_next) else None
+    q = torch.empty((M, D), dtype=torch.int8, device=src.device) if (quant and has_next) else None
+    qs = torch.empty((M, D // 128), dtype=torch.float32, device=src.device) if q is not None else None
+    check(load().e2mi_add_norm_quant(stream_ptr(stream), ptr(src), ptr(res), ptr(gamma_add),
+                                     ptr(gamma_next), eps, M, D, ptr(x_out), ptr(xn), ptr(q),
+                                     ptr(qs)), "add_norm_quant")
+    return x_out, xn, q, qs
+
+
+def embed_norm_quant(table, ids, embed_scale, gamma, eps=1e-6, stream=None):
+    import torch
+    M = ids.shape[0]
+    D = table.shape[1]
+    x = torch.empty((M, D), dtype=torch.float32, device=table.device)
+    q = torch.empty((M, D), dtype=torch.int8, device=table.device)
+    qs = torch.empty((M, D // 128), dtype=torch.float32, device=table.device)
+    check(load().e2mi_embed_norm_quant(stream_ptr(stream), ptr(table), ptr(ids), embed_scale,
+                                       ptr(gamma), eps, M, D, ptr(x), ptr(q), ptr(qs)),
+          "embed_norm_quant")
+    return x, q, qs
+
+
+def qkv_norm_rope(qkv, S, H, KV, q_gamma, k_gamma, cos_tab, sin_tab, eps=1e-6, want_f32=True,
+                  stream=None):
+    import torch
+    M = qkv.shape[0]
+    D = 256
+    B = M // S
+    dev = qkv.device
+    q16 = torch.empty((M, H * D), dtype=torch.float16, device=dev)
+    k16 = torch.empty((M, KV * D), dtype=torch.float16, device=dev)
+    vt16 = torch.empty((B, KV, D, S), dtype=torch.float16, device=dev)
+    f = (lambda *s: torch.empty(s, dtype=torch.float32, device=dev)) if want_f32 else (lambda *s: None)
+    q32, k32, v32 = f(M, H * D), f(M, KV * D), f(M, KV * D)
+    check(load().e2mi_qkv_norm_rope(stream_ptr(stream), ptr(qkv), M, S, H, KV, D, ptr(q_gamma),
+                                    ptr(k_gamma), eps, ptr(cos_tab), ptr(sin_tab), ptr(q16),
+                                    ptr(k16), ptr(vt16), ptr(q32), ptr(k32), ptr(v32)),
+          "qkv_norm_rope")
+    return q16, k16, vt16, q32, k32, v32
+
+
+def gelu_mul_quant(gate, up, write_back=True, stream=None):
+    import torch
+    M, D = gate.shape
+    q = torch.empty((M, D), dtype=torch.int8, device=gate.device)
+    qs = torch.empty((M, D // 128), dtype=torch.float32, device=gate.device)
+    check(load().e2mi_gelu_mul_quant(stream_ptr(stream), ptr(gate), gate.stride(0), ptr(up),
+                                     up.stride(0), M, D, ptr(q), ptr(qs), int(write_back)),
+          "gelu_mul_quant")
+    return q, qs
+
+
+def pool_l2(x, valid, B, S, stream=None):
+    import torch
+    D = x.shape[1]
+    lib = load()
+    ws = torch.empty(lib.e2mi_pool_workspace_bytes(B, S, D) // 4 + 64, dtype=torch.float32,
+                     device=x.device)
+    out = torch.empty((B, D), dtype=torch.float32, device=x.device)
+    check(lib.e2mi_pool_l2(stream_ptr(stream), ptr(x), ptr(valid), B, S, D, ptr(ws), ptr(out)),
+          "pool_l2")
+    return out
+
+
+def attention(q16, k16, vt16, valid, B, S, H, KV, scale=1.0, want_f32=True, stream=None):
+    import torch
+    M = B * S
+    D = 256
+    dev = q16.device
+    cq = torch.empty((M, H * D), dtype=torch.int8, device=dev)
+    cs = torch.empty((M, H * D // 128), dtype=torch.float32, device=dev)
+    c32 = torch.empty((M, H * D), dtype=torch.float32, device=dev) if want_f32 else None
+    check(load().e2mi_attention(stream_ptr(stream), ptr(q16), ptr(k16), ptr(vt16), ptr(valid), B, S,
+                                H, KV, D, scale, ptr(cq), ptr(cs), ptr(c32)), "attention")
+    return cq, cs, c32

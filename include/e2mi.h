@@ -92,6 +92,61 @@ int e2mi_i8_gemm_geglu(e2mi_stream stream, int8_t *q, float *qs, float *g, const
 int e2mi_interleave_gate_up(int8_t *w_out, float *s_out, const int8_t *gate, const float *sgate,
                             const int8_t *up, const float *sup, int F, int K);
 
+/* ---- memory-bound row kernels (D % 128 == 0, D <= 1280; rows are contiguous, ld = D) */
+
+/* RMSNorm (kernels.c:76-87) then quantize: xn = x * (1/sqrt(mean(x^2) + eps)) * gamma, written to
+ * xn_out (optional) and, when q != NULL, quantized per 128 into q [M][D] / qs [M][D/128]. */
+int e2mi_norm_quant(e2mi_stream stream, const float *x, const float *gamma, float eps, int M, int D,
+                    float *xn_out, int8_t *q, float *qs);
+
+/* norm_add then norm_split then quantize, one pass per row (kernels.c:149-171, text.c:946-949):
+ * x = rmsnorm(src)*gamma_add + res -> x_out (the new residual; may alias res); then, when
+ * gamma_next != NULL, xn = rmsnorm(x)*gamma_next -> xn_out (optional) and q/qs (optional). */
+int e2mi_add_norm_quant(e2mi_stream stream, const float *src, const float *res,
+                        const float *gamma_add, const float *gamma_next, float eps, int M, int D,
+                        float *x_out, float *xn_out, int8_t *q, float *qs);
+
+/* Embedding gather (text.c:917-921) fused with the first layer's norm_split + quantize:
+ * x = table[ids[m]] * embed_scale -> x_out; rmsnorm(x)*gamma quantized into q/qs. */
+int e2mi_embed_norm_quant(e2mi_stream stream, const float *table, const int32_t *ids,
+                          float embed_scale, const float *gamma, float eps, int M, int D,
+                          float *x_out, int8_t *q, float *qs);
+
+/* q/k/v RMSNorm + rotate-half RoPE (text.c:836-838,853-854; kernels.c:112-126) on the QKV GEMM
+ * output qkv [M][(H+2KV)*D] (q heads, k heads, v heads), M = B*S with positions m % S.
+ * q, k get rmsnorm*gamma then RoPE from cos/sin tables [S][D]; v gets rmsnorm without gamma.
+ * Writes f16: q16 [M][H*D], k16 [M][KV*D], vt16 [B][KV][D][S] (V transposed per sequence), and
+ * optional f32 copies q32/k32 (same layouts) and v32 [M][KV*D]. head_dim D must be 256. */
+int e2mi_qkv_norm_rope(e2mi_stream stream, const float *qkv, int M, int S, int H, int KV, int D,
+                       const float *q_gamma, const float *k_gamma, float eps, const float *cos_tab,
+                       const float *sin_tab, uint16_t *q16, uint16_t *k16, uint16_t *vt16,
+                       float *q32, float *k32, float *v32);
+
+/* Standalone GeGLU product + quantize (text.c:424-468 gate_quant): g = gelu_tanh(gate)*up per
+ * element, quantized per 128 into q [M][D] / qs [M][D/128]; g written back into gate when
+ * write_back != 0 (the reference overwrites gate). */
+int e2mi_gelu_mul_quant(e2mi_stream stream, float *gate, int ldg, const float *up, int ldu, int M,
+                        int D, int8_t *q, float *qs, int write_back);
+
+/* Masked mean pool over each sequence's valid rows, then L2 normalisation (kernels.c:22-39,
+ * text.c:963-981): x [B*S][D] -> out [B][D]; an all-invalid sequence gives an exact zero vector.
+ * workspace: e2mi_pool_workspace_bytes(B, S, D) bytes of device memory. */
+int e2mi_pool_l2(e2mi_stream stream, const float *x, const uint8_t *valid, int B, int S, int D,
+                 float *workspace, float *out);
+size_t e2mi_pool_workspace_bytes(int B, int S, int D);
+
+/* ---- attention */
+
+/* Fused bidirectional GQA attention (text.c:534-572,817-891): per sequence b, head h (kv head
+ * h/(H/KV)), query i with valid[b*S+i]: ctx = softmax(scale * q.k_j over valid keys j) . v; an
+ * invalid query row, or one with no valid key, gets ctx = 0. f16 inputs from e2mi_qkv_norm_rope,
+ * f32 softmax and accumulation. The context is quantized per 128 dims into ctx_q [B*S][H*D] /
+ * ctx_s [B*S][H*D/128] (the O-projection's operand); ctx32 (optional) receives it in f32.
+ * head_dim D must be 256. */
+int e2mi_attention(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
+                   const uint16_t *vt16, const uint8_t *valid, int B, int S, int H, int KV, int D,
+                   float scale, int8_t *ctx_q, float *ctx_s, float *ctx32);
+
 #ifdef __cplusplus
 }
 #endif
