@@ -1,0 +1,449 @@
+// forward.cpp — the encoder on the device: weight upload, workspace, the per-layer kernel sequence,
+// hipGraph capture per (batch, seq_len) shape, and the e2hip-style entry points.
+//
+// Layer recipe (text.c:939-961 without PLE / layer_scalar), as fused launches:
+//   [embed | add_norm] + norm + quant -> int8 x     (e2mi_embed_norm_quant / e2mi_add_norm_quant)
+//   q|k|v int8 GEMM -> f32                          (one GEMM over the concatenated N = (H+2KV)*D)
+//   q/k/v RMSNorm + RoPE -> f16 q, k, V^T           (e2mi_qkv_norm_rope)
+//   attention -> int8 context + scales              (e2mi_attention)
+//   O int8 GEMM -> f32
+//   norm_add(post_attn) + norm_split(pre_ffn) + quant
+//   gate|up int8 GEMM + GeGLU + quant -> int8       (e2mi_i8_gemm_geglu)
+//   down int8 GEMM -> f32
+// and after the last layer norm_add(post_ffn) + final RMSNorm, masked mean pool, L2
+// (text.c:963-981). The recorded graph is replayed for every later call of the same shape, like
+// the reference's HIP backend (forward.c:553-579).
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#include <map>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/e2.h"
+#include "../../include/e2_dispatch.h"
+#include "common.h"
+#include "model_internal.h"
+
+namespace e2mi {
+
+struct LayerDev {
+    e2mi_q8w qkv{}, o{}, gu{}, down{};
+    float *ln_in = nullptr, *ln_attn = nullptr, *ln_pre = nullptr, *ln_ffn = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr;
+};
+
+static double now_ms() {
+    timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return t.tv_sec * 1e3 + t.tv_nsec * 1e-6;
+}
+
+}  // namespace e2mi
+
+using namespace e2mi;
+
+struct e2mi_engine {
+    e2_config cfg{};
+    int dev = 0;
+    hipStream_t stream = nullptr;
+    char devname[256] = "";
+    std::vector<LayerDev> layers;
+    float *embed = nullptr, *final_norm = nullptr, *cos_tab = nullptr, *sin_tab = nullptr;
+    int R = 0;  // workspace capacity in rows (tokens)
+    // activations
+    float *x = nullptr, *tmp = nullptr, *qkv = nullptr, *xn = nullptr, *pool_ws = nullptr;
+    int8_t *qa = nullptr, *qg = nullptr, *cq = nullptr;
+    float *as = nullptr, *gs = nullptr, *cs = nullptr;
+    uint16_t *q16 = nullptr, *k16 = nullptr, *vt16 = nullptr;
+    int32_t *ids = nullptr;
+    uint8_t *valid = nullptr;
+    float *out = nullptr;
+    int bmax = 0;  // sequences per chunk (pinned output staging)
+    int32_t *h_ids = nullptr;
+    uint8_t *h_valid = nullptr;
+    float *h_out = nullptr;
+    std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+    bool use_graph = true;
+    int layer_limit = 0;
+    long calls = 0, kernels_last = 0;
+    double last_ms = 0.0;
+    std::vector<void *> allocs;
+};
+
+namespace e2mi {
+
+template <class T>
+static int dalloc(e2mi_engine *g, T **p, size_t count) {
+    *p = nullptr;
+    void *v = nullptr;
+    if (check_hip(hipMalloc(&v, count * sizeof(T) + 256), "hipMalloc workspace")) return -1;
+    g->allocs.push_back(v);
+    *p = (T *)v;
+    return 0;
+}
+
+static int upload_f32(e2mi_engine *g, float **dst, const float *src, size_t n) {
+    if (!src) {
+        set_error("create: missing f32 tensor");
+        return -1;
+    }
+    if (dalloc(g, dst, n)) return -1;
+    return check_hip(hipMemcpyAsync(*dst, src, n * 4, hipMemcpyHostToDevice, g->stream), "upload f32");
+}
+
+// concatenate / interleave the reference's separate weights into the fused device operands
+static int upload_layer(e2mi_engine *g, const e2_model *m, int l, LayerDev &L) {
+    const e2_config &c = g->cfg;
+    const HostQ8W *w[7];
+    for (int s = 0; s < 7; s++) {
+        w[s] = model_q8(m, layer_name(l, q8_suffix(s)));
+        if (!w[s]) {
+            set_error("create: layer %d: %s missing", l, q8_suffix(s));
+            return -1;
+        }
+    }
+    const int K = c.hidden, qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    auto make = [&](e2mi_q8w &d, int N, int Kd) {
+        memset(&d, 0, sizeof d);
+        d.N = N;
+        d.K = Kd;
+        d.ld = (Kd + 15) & ~15;
+        d.out_min = -1e31f;
+        d.out_max = 1e31f;
+        if (dalloc(g, &d.w, (size_t)N * d.ld) || dalloc(g, &d.scale, (size_t)N)) return -1;
+        return 0;
+    };
+    // q|k|v rows
+    if (make(L.qkv, qd + 2 * kvd, K)) return -1;
+    const int off[3] = {0, qd, qd + kvd}, nrows[3] = {qd, kvd, kvd};
+    std::vector<float> sc(qd + 2 * kvd);
+    for (int s = 0; s < 3; s++) {
+        if (upload_packed_rows(L.qkv.w, L.qkv.ld, w[s]->w, nrows[s], K, nrows[s], 0, off[s], g->stream))
+            return -1;
+        memcpy(sc.data() + off[s], w[s]->scale, sizeof(float) * nrows[s]);
+    }
+    if (check_hip(hipMemcpyAsync(L.qkv.scale, sc.data(), sc.size() * 4, hipMemcpyHostToDevice, g->stream),
+                  "upload qkv scale") ||
+        hipStreamSynchronize(g->stream) != hipSuccess)
+        return -1;
+    // o, down
+    if (make(L.o, c.hidden, qd) || upload_packed_rows(L.o.w, L.o.ld, w[3]->w, c.hidden, qd, c.hidden, 0, 0, g->stream) ||
+        check_hip(hipMemcpyAsync(L.o.scale, w[3]->scale, (size_t)c.hidden * 4, hipMemcpyHostToDevice, g->stream), "o scale"))
+        return -1;
+    if (make(L.down, c.hidden, c.ffn) ||
+        upload_packed_rows(L.down.w, L.down.ld, w[6]->w, c.hidden, c.ffn, c.hidden, 0, 0, g->stream) ||
+        check_hip(hipMemcpyAsync(L.down.scale, w[6]->scale, (size_t)c.hidden * 4, hipMemcpyHostToDevice, g->stream), "down scale"))
+        return -1;
+    // gate|up interleaved per 128 rows: [gate 128 | up 128] blocks
+    if (make(L.gu, 2 * c.ffn, K) ||
+        upload_packed_rows(L.gu.w, L.gu.ld, w[4]->w, c.ffn, K, 128, 256, 0, g->stream) ||
+        upload_packed_rows(L.gu.w, L.gu.ld, w[5]->w, c.ffn, K, 128, 256, 128, g->stream))
+        return -1;
+    std::vector<float> gus(2 * c.ffn);
+    for (int n = 0; n < c.ffn; n++) {
+        gus[(n / 128) * 256 + n % 128] = w[4]->scale[n];
+        gus[(n / 128) * 256 + 128 + n % 128] = w[5]->scale[n];
+    }
+    if (check_hip(hipMemcpyAsync(L.gu.scale, gus.data(), gus.size() * 4, hipMemcpyHostToDevice, g->stream), "gu scale"))
+        return -1;
+    float **norms[6] = {&L.ln_in, &L.ln_attn, &L.ln_pre, &L.ln_ffn, &L.q_norm, &L.k_norm};
+    for (int s = 0; s < 6; s++) {
+        const size_t n = s < 4 ? (size_t)c.hidden : (size_t)c.head_dim;
+        if (upload_f32(g, norms[s], model_f32(m, layer_name(l, norm_suffix(s)), n), n)) return -1;
+    }
+    return check_hip(hipStreamSynchronize(g->stream), "layer upload sync");
+}
+
+// RoPE tables, text.c:483-506: inv = 1/theta^(2i/D), f = p * inv, duplicated over both halves
+static void rope_tables(const e2_config &c, std::vector<float> &cs, std::vector<float> &sn) {
+    const int D = c.head_dim, S = c.max_seq;
+    cs.resize((size_t)S * D);
+    sn.resize((size_t)S * D);
+    for (int p = 0; p < S; p++)
+        for (int i = 0; i < D / 2; i++) {
+            const float inv = 1.0f / powf(c.rope_theta, (float)(2 * i) / (float)D);
+            const float f = (float)p * inv;
+            cs[(size_t)p * D + i] = cs[(size_t)p * D + i + D / 2] = cosf(f);
+            sn[(size_t)p * D + i] = sn[(size_t)p * D + i + D / 2] = sinf(f);
+        }
+}
+
+// every kernel of one forward over B sequences of S tokens, on stream s; returns the launch count
+// or -1
+static int enqueue(e2mi_engine *g, int B, int S, hipStream_t s) {
+    const e2_config &c = g->cfg;
+    const int M = B * S, Dm = c.hidden, H = c.n_heads, KV = c.n_kv_heads, D = c.head_dim;
+    const int qd = H * D, F = c.ffn;
+    const int nl = g->layer_limit > 0 && g->layer_limit < c.n_layers ? g->layer_limit : c.n_layers;
+    const float eps = c.rms_eps;
+    int k = 0;
+#define RUN(call)                                                                                  \
+    do {                                                                                           \
+        if ((call) != 0) return -1;                                                                \
+        k++;                                                                                       \
+    } while (0)
+    RUN(e2mi_embed_norm_quant(s, g->embed, c.vocab, g->ids, c.embed_scale, g->layers[0].ln_in, eps, M, Dm,
+                              g->x, g->qa, g->as));
+    for (int l = 0; l < nl; l++) {
+        const LayerDev &L = g->layers[l];
+        RUN(e2mi_i8_gemm(s, g->qkv, qd + 2 * KV * D, g->qa, g->as, &L.qkv, M, 0, L.qkv.N));
+        RUN(e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, g->cos_tab,
+                               g->sin_tab, g->q16, g->k16, g->vt16, nullptr, nullptr, nullptr));
+        RUN(e2mi_attention(s, g->q16, g->k16, g->vt16, g->valid, B, S, H, KV, D, c.attn_scale,
+                           g->cq, g->cs, nullptr));
+        RUN(e2mi_i8_gemm(s, g->tmp, Dm, g->cq, g->cs, &L.o, M, 0, Dm));
+        RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_attn, L.ln_pre, eps, M, Dm, g->x, nullptr,
+                                g->qa, g->as));
+        RUN(e2mi_i8_gemm_geglu(s, g->qg, g->gs, nullptr, g->qa, g->as, &L.gu, M));
+        RUN(e2mi_i8_gemm(s, g->tmp, Dm, g->qg, g->gs, &L.down, M, 0, Dm));
+        const bool last = l + 1 == nl;
+        if (!last)
+            RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, g->layers[l + 1].ln_in, eps, M, Dm,
+                                    g->x, nullptr, g->qa, g->as));
+        else
+            RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, g->final_norm, eps, M, Dm, g->x,
+                                    g->xn, nullptr, nullptr));
+    }
+    RUN(e2mi_pool_l2(s, g->xn, g->valid, B, S, Dm, g->pool_ws, g->out));
+    (void)F;
+#undef RUN
+    return k + 1;  // the pool is two launches
+}
+
+static int run_shape(e2mi_engine *g, int B, int S, hipStream_t s) {
+    if (!g->use_graph) {
+        const int k = enqueue(g, B, S, s);
+        if (k < 0) return -1;
+        g->kernels_last = k;
+        return 0;
+    }
+    auto key = std::make_pair(B, S);
+    auto it = g->graphs.find(key);
+    if (it == g->graphs.end()) {
+        // the first call of a shape runs eagerly (kernel attributes get set outside any capture),
+        // then the sequence is recorded for every later call
+        const int k = enqueue(g, B, S, s);
+        if (k < 0) return -1;
+        g->kernels_last = k;
+        hipGraph_t graph = nullptr;
+        if (check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"))
+            return -1;
+        const int k2 = enqueue(g, B, S, s);
+        const hipError_t e = hipStreamEndCapture(s, &graph);
+        if (k2 < 0 || check_hip(e, "end capture")) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return -1;
+        }
+        hipGraphExec_t exec = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (check_hip(ei, "graph instantiate")) return -1;
+        g->graphs[key] = exec;
+        return 0;
+    }
+    return check_hip(hipGraphLaunch(it->second, s), "graph launch");
+}
+
+static int validate_batch(const e2mi_engine *g, const int32_t *ids, int batch, int seq_len, bool host_ids) {
+    if (batch <= 0 || seq_len <= 0 || seq_len > g->cfg.max_seq) {
+        set_error("bad batch geometry (batch=%d, seq_len=%d, max %d)", batch, seq_len, g->cfg.max_seq);
+        return -1;
+    }
+    if (!ids) {
+        set_error("token ids pointer is NULL");
+        return -1;
+    }
+    if (host_ids) {  // the whole request is validated before any output is written (text.c:1008-1013)
+        const size_t n = (size_t)batch * seq_len;
+        for (size_t i = 0; i < n; i++)
+            if (ids[i] < 0 || ids[i] >= g->cfg.vocab) {
+                set_error("token id %d at position %zu is out of range [0,%d)", ids[i], i, g->cfg.vocab);
+                return -1;
+            }
+    }
+    return 0;
+}
+
+}  // namespace e2mi
+
+// ------------------------------------------------------------------ C ABI (e2hip.h:34-64)
+extern "C" void e2mi_destroy(e2mi_engine *g) {
+    if (!g) return;
+    if (g->stream) (void)hipStreamSynchronize(g->stream);
+    for (auto &kv : g->graphs) (void)hipGraphExecDestroy(kv.second);
+    for (void *p : g->allocs) (void)hipFree(p);
+    if (g->h_ids) (void)hipHostFree(g->h_ids);
+    if (g->h_valid) (void)hipHostFree(g->h_valid);
+    if (g->h_out) (void)hipHostFree(g->h_out);
+    if (g->stream) (void)hipStreamDestroy(g->stream);
+    delete g;
+}
+
+extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
+    if (!m) {
+        set_error("create: null model");
+        return nullptr;
+    }
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) {
+        set_error("create: no HIP device");
+        return nullptr;
+    }
+    e2mi_engine *g = new (std::nothrow) e2mi_engine();
+    if (!g) {
+        set_error("oom: engine");
+        return nullptr;
+    }
+    e2_model_config(m, &g->cfg);
+    const e2_config &c = g->cfg;
+    g->R = max_rows > 0 ? max_rows : 32768;
+    if (g->R < c.max_seq) g->R = c.max_seq;
+    const char *ng = getenv("E2MI_NOGRAPH");
+    g->use_graph = !(ng && ng[0] && ng[0] != '0');
+    auto fail = [&]() -> e2mi_engine * {
+        e2mi_destroy(g);
+        return nullptr;
+    };
+    if (check_hip(hipGetDevice(&g->dev), "get device")) return fail();
+    hipDeviceProp_t prop;
+    if (check_hip(hipGetDeviceProperties(&prop, g->dev), "device properties")) return fail();
+    snprintf(g->devname, sizeof g->devname, "%s (%s, %d CUs)", prop.name, prop.gcnArchName,
+             prop.multiProcessorCount);
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_error("create: this backend is built for gfx950, the device is %s", prop.gcnArchName);
+        return fail();
+    }
+    // the attention precision comes from the selection surface (dispatch.c:180-197)
+    e2_attn_env_reload();
+    const e2_attn_kind ak = e2_attn_pick(E2_BK_HIP_GFX950, E2_TOWER_TEXT, E2_ATTN_ANY_KEYS);
+    if (ak != E2_ATTN_F16) {
+        set_error("create: attention kind %s requested; this backend implements f16 only",
+                  e2_attn_kind_name(ak));
+        return fail();
+    }
+    if (check_hip(hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking), "stream")) return fail();
+    // weights
+    g->layers.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; l++)
+        if (upload_layer(g, m, l, g->layers[l])) return fail();
+    if (upload_f32(g, &g->embed, model_f32(m, embed_name(), (size_t)c.vocab * c.hidden),
+                   (size_t)c.vocab * c.hidden) ||
+        upload_f32(g, &g->final_norm, model_f32(m, final_norm_name(), (size_t)c.hidden), (size_t)c.hidden))
+        return fail();
+    std::vector<float> cs, sn;
+    rope_tables(c, cs, sn);
+    if (upload_f32(g, &g->cos_tab, cs.data(), cs.size()) || upload_f32(g, &g->sin_tab, sn.data(), sn.size()))
+        return fail();
+    // workspace for R rows
+    const size_t R = (size_t)g->R;
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    const int kmax = c.hidden > c.ffn ? c.hidden : c.ffn;
+    g->bmax = g->R < 4096 ? g->R : 4096;
+    if (dalloc(g, &g->x, R * c.hidden) || dalloc(g, &g->tmp, R * c.hidden) ||
+        dalloc(g, &g->xn, R * c.hidden) || dalloc(g, &g->qkv, R * (qd + 2 * kvd)) ||
+        dalloc(g, &g->qa, R * kmax) || dalloc(g, &g->as, R * (kmax / 128)) ||
+        dalloc(g, &g->qg, R * c.ffn) || dalloc(g, &g->gs, R * (c.ffn / 128)) ||
+        dalloc(g, &g->cq, R * qd) || dalloc(g, &g->cs, R * (qd / 128)) ||
+        dalloc(g, &g->q16, R * qd) || dalloc(g, &g->k16, R * kvd) || dalloc(g, &g->vt16, R * kvd) ||
+        dalloc(g, &g->ids, R) || dalloc(g, &g->valid, R) || dalloc(g, &g->out, R * c.hidden) ||
+        dalloc(g, &g->pool_ws, (R / 64 + R + 64) * (size_t)(c.hidden + 1)))
+        return fail();
+    if (check_hip(hipHostMalloc((void **)&g->h_ids, R * 4), "pinned ids") ||
+        check_hip(hipHostMalloc((void **)&g->h_valid, R), "pinned valid") ||
+        check_hip(hipHostMalloc((void **)&g->h_out, (size_t)g->bmax * c.hidden * 4), "pinned out"))
+        return fail();
+    if (check_hip(hipStreamSynchronize(g->stream), "create sync")) return fail();
+    return g;
+}
+
+extern "C" e2mi_engine *e2mi_create(const e2_model *m) { return e2mi_create_rows(m, 0); }
+
+extern "C" const char *e2mi_device(e2mi_engine *g) { return g ? g->devname : ""; }
+
+extern "C" int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const uint8_t *valid, int batch,
+                                     int seq_len, float *out) {
+    if (!g || !out) {
+        set_error("text_embed_batch: null engine or output");
+        return -1;
+    }
+    if (validate_batch(g, ids, batch, seq_len, true)) return -1;
+    const double t0 = now_ms();
+    const int D = g->cfg.hidden;
+    int per = g->R / seq_len;
+    if (per > g->bmax) per = g->bmax;
+    for (int b0 = 0; b0 < batch;) {
+        const int n = batch - b0 < per ? batch - b0 : per;
+        const size_t rows = (size_t)n * seq_len, off = (size_t)b0 * seq_len;
+        memcpy(g->h_ids, ids + off, rows * 4);
+        for (size_t i = 0; i < rows; i++) g->h_valid[i] = valid ? (valid[off + i] != 0) : 1;
+        if (check_hip(hipMemcpyAsync(g->ids, g->h_ids, rows * 4, hipMemcpyHostToDevice, g->stream), "ids H2D") ||
+            check_hip(hipMemcpyAsync(g->valid, g->h_valid, rows, hipMemcpyHostToDevice, g->stream), "valid H2D") ||
+            run_shape(g, n, seq_len, g->stream) ||
+            check_hip(hipMemcpyAsync(g->h_out, g->out, (size_t)n * D * 4, hipMemcpyDeviceToHost, g->stream), "out D2H") ||
+            check_hip(hipStreamSynchronize(g->stream), "forward sync"))
+            return -1;
+        memcpy(out + (size_t)b0 * D, g->h_out, (size_t)n * D * 4);
+        b0 += n;
+    }
+    g->calls++;
+    g->last_ms = now_ms() - t0;
+    return 0;
+}
+
+extern "C" int e2mi_text_embed(e2mi_engine *g, const int32_t *ids, int n_ids, float *out) {
+    return e2mi_text_embed_batch(g, ids, nullptr, 1, n_ids, out);
+}
+
+extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, const uint8_t *valid,
+                                            int batch, int seq_len, float *out, e2mi_stream stream) {
+    if (!g || !out || !valid) {
+        set_error("text_embed_batch_device: null engine, mask or output");
+        return -1;
+    }
+    if (validate_batch(g, ids, batch, seq_len, false)) return -1;
+    if ((long)batch * seq_len > g->R) {
+        set_error("text_embed_batch_device: %d x %d rows exceed the engine's %d-row workspace",
+                  batch, seq_len, g->R);
+        return -1;
+    }
+    hipStream_t s = stream ? (hipStream_t)stream : g->stream;
+    const size_t rows = (size_t)batch * seq_len;
+    const double t0 = now_ms();
+    if (check_hip(hipMemcpyAsync(g->ids, ids, rows * 4, hipMemcpyDeviceToDevice, s), "ids D2D") ||
+        check_hip(hipMemcpyAsync(g->valid, valid, rows, hipMemcpyDeviceToDevice, s), "valid D2D") ||
+        run_shape(g, batch, seq_len, s) ||
+        check_hip(hipMemcpyAsync(out, g->out, (size_t)batch * g->cfg.hidden * 4, hipMemcpyDeviceToDevice, s),
+                  "out D2D"))
+        return -1;
+    if (!stream && check_hip(hipStreamSynchronize(s), "forward sync")) return -1;
+    g->calls++;
+    g->last_ms = now_ms() - t0;
+    return 0;
+}
+
+extern "C" int e2mi_stats(e2mi_engine *g, long *calls, long *kernels_last, double *last_ms) {
+    if (!g) {
+        set_error("stats: null engine");
+        return -1;
+    }
+    if (calls) *calls = g->calls;
+    if (kernels_last) *kernels_last = g->kernels_last;
+    if (last_ms) *last_ms = g->last_ms;
+    return 0;
+}
+
+extern "C" int e2mi_set_layer_limit(e2mi_engine *g, int n_layers) {
+    if (!g || n_layers < 0) {
+        set_error("set_layer_limit: null engine or negative limit");
+        return -1;
+    }
+    g->layer_limit = n_layers;
+    for (auto &kv : g->graphs) (void)hipGraphExecDestroy(kv.second);
+    g->graphs.clear();
+    return 0;
+}

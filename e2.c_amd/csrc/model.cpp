@@ -1,0 +1,524 @@
+// model.cpp — host-side model container: BASELINE geometry, seeded synthetic int8 weights, and
+// the E8CQ packed int8 cache (the reference's q8cache.c v1 on-disk format, restated).
+#include <fcntl.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <map>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/e2.h"
+#include "common.h"
+#include "model_internal.h"
+
+struct e2_model {
+    e2_config cfg;
+    std::map<std::string, e2mi::HostQ8W> q8;
+    std::map<std::string, e2mi::F32T> f32;
+    void *map = nullptr;
+    size_t map_size = 0;
+};
+
+namespace e2mi {
+
+// ------------------------------------------------------------------ names (e2.c:306-402)
+std::string layer_name(int l, const char *suffix) {
+    char b[128];
+    snprintf(b, sizeof b, "language_model.layers.%d.%s", l, suffix);
+    return b;
+}
+static const char *kEmbed = "language_model.embed_tokens.weight";
+static const char *kFinalNorm = "language_model.norm.weight";
+static const char *kQ8Suffix[7] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight",
+                                   "self_attn.v_proj.weight", "self_attn.o_proj.weight",
+                                   "mlp.gate_proj.weight", "mlp.up_proj.weight",
+                                   "mlp.down_proj.weight"};
+static const char *kNormSuffix[6] = {"input_layernorm.weight", "post_attention_layernorm.weight",
+                                     "pre_feedforward_layernorm.weight",
+                                     "post_feedforward_layernorm.weight", "self_attn.q_norm.weight",
+                                     "self_attn.k_norm.weight"};
+
+// (N, K) of weight s of a layer; norm s length
+static void q8_shape(const e2_config &c, int s, int *N, int *K) {
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    const int Ns[7] = {qd, kvd, kvd, c.hidden, c.ffn, c.ffn, c.hidden};
+    const int Ks[7] = {c.hidden, c.hidden, c.hidden, qd, c.hidden, c.hidden, c.ffn};
+    *N = Ns[s];
+    *K = Ks[s];
+}
+static int norm_len(const e2_config &c, int s) { return s < 4 ? c.hidden : c.head_dim; }
+
+// ------------------------------------------------------------------ packing (int8.h:14-22)
+static void pack_rows(const int8_t *rm, int N, int K, HostQ8W &q) {
+    q.N = N;
+    q.K = K;
+    q.nb = (K + kQBlock - 1) / kQBlock;
+    q.Npad = (N + 7) & ~7;
+    const int kq = (K + 3) / 4;
+    q.ow.assign((size_t)q.Npad * kq * 4, 0);
+    q.ob.assign((size_t)q.nb * q.Npad, 0);
+    for (int n = 0; n < N; n++)
+        for (int k = 0; k < K; k++) {
+            const int8_t v = rm[(size_t)n * K + k];
+            q.ow[(size_t)(n >> 3) * kq * 32 + (size_t)(k >> 2) * 32 + (n & 7) * 4 + (k & 3)] = v;
+            q.ob[(size_t)(k / kQBlock) * q.Npad + n] += v;
+        }
+    q.w = q.ow.data();
+    q.bsq = q.ob.data();
+}
+
+// ------------------------------------------------------------------ synthetic weights
+// The reference tests' LCG (test_scalar_kernels.c:26-28), one stream per (tensor, row).
+struct Lcg {
+    uint32_t s;
+    uint32_t next() { return s = s * 1664525u + 1013904223u; }
+    double unit() { return ((next() >> 8) + 0.5) * (1.0 / 16777216.0); }  // (0, 1)
+    int i8() { return (int)((next() >> 8) % 255u) - 127; }
+    float normal(double sd) {  // Box-Muller
+        const double u1 = unit(), u2 = unit();
+        return (float)(sd * sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
+    }
+};
+static uint32_t row_seed(uint64_t seed, int tensor, long row) {
+    uint64_t z = seed ^ ((uint64_t)(tensor + 1) << 40) ^ (uint64_t)row * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;  // splitmix64 finaliser
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return (uint32_t)(z ^ (z >> 31));
+}
+
+template <class F>
+static void parallel_rows(long n, F f) {
+    int nt = (int)std::thread::hardware_concurrency();
+    nt = nt < 1 ? 1 : (nt > 16 ? 16 : nt);
+    if (n < 4096) nt = 1;
+    std::vector<std::thread> th;
+    for (int t = 0; t < nt; t++)
+        th.emplace_back([=] {
+            for (long r = t; r < n; r += nt) f(r);
+        });
+    for (auto &x : th) x.join();
+}
+
+static void synth_q8(HostQ8W &q, int N, int K, uint64_t seed, int tensor) {
+    std::vector<int8_t> rm((size_t)N * K);
+    q.os.assign((size_t)((N + 7) & ~7), 0.f);
+    parallel_rows(N, [&](long n) {
+        Lcg g{row_seed(seed, tensor, n)};
+        for (int k = 0; k < K; k++) rm[(size_t)n * K + k] = (int8_t)g.i8();
+        q.os[n] = (float)(0.001 + 0.019 * g.unit());
+    });
+    pack_rows(rm.data(), N, K, q);
+    q.scale = q.os.data();
+}
+
+static void synth_f32(F32T &t, long rows, int cols, double mean, double sd, uint64_t seed,
+                      int tensor) {
+    t.own.resize((size_t)rows * cols);
+    t.ndim = rows > 1 ? 2 : 1;
+    t.dims[0] = rows > 1 ? rows : cols;
+    t.dims[1] = rows > 1 ? cols : 0;
+    float *p = t.own.data();
+    parallel_rows(rows, [&](long r) {
+        Lcg g{row_seed(seed, tensor, r)};
+        for (int c = 0; c < cols; c++) p[(size_t)r * cols + c] = (float)mean + g.normal(sd);
+    });
+    t.p = t.own.data();
+}
+
+static bool config_ok(const e2_config &c) {
+    if (c.n_layers < 1 || c.hidden <= 0 || c.hidden % 128 || c.ffn <= 0 || c.ffn % 128 ||
+        c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || c.head_dim != 256 ||
+        c.vocab <= 0 || c.max_seq <= 0 || c.max_seq > 2048 || c.hidden > 1280 ||
+        (c.n_heads * c.head_dim) % 128) {
+        set_error("config: unsupported geometry (hidden/ffn multiples of 128, hidden <= 1280, "
+                  "head_dim 256, H %% KV == 0, 1 <= max_seq <= 2048)");
+        return false;
+    }
+    return true;
+}
+
+// ------------------------------------------------------------------ E8CQ (q8cache.c:1-13)
+constexpr uint32_t kMagic = 0x51433845u;  // "E8CQ"
+constexpr uint32_t kVersion = 1u;
+enum { KIND_BF16 = 1, KIND_F32 = 2, KIND_Q8W = 3 };
+struct Entry {  // 152 bytes, the reference's q8c_entry
+    char name[96];
+    uint32_t kind, ndim;
+    int64_t dims[4];
+    uint64_t nbytes, off;
+};
+static_assert(sizeof(Entry) == 152, "E8CQ index entry is 152 bytes");
+
+static bool entry_ok(const Entry &e, uint64_t idx_off, const char *path) {
+    if (!memchr(e.name, 0, sizeof e.name) || !e.name[0]) {
+        set_error("%s: entry with an unterminated or empty name", path);
+        return false;
+    }
+    if (e.kind < KIND_BF16 || e.kind > KIND_Q8W || e.ndim > 4 || (e.kind == KIND_Q8W && e.ndim != 4)) {
+        set_error("%s: %.64s: bad kind/rank", path, e.name);
+        return false;
+    }
+    for (uint32_t d = 0; d < e.ndim; d++)
+        if (e.dims[d] < 0) {
+            set_error("%s: %.64s: negative dimension", path, e.name);
+            return false;
+        }
+    if (e.off < 16 || (e.off & 15) || e.off > idx_off || e.nbytes > idx_off - e.off) {
+        set_error("%s: %.64s: blob outside the data area", path, e.name);
+        return false;
+    }
+    if (e.kind != KIND_Q8W) {
+        uint64_t want = e.kind == KIND_BF16 ? 2 : 4;
+        for (uint32_t d = 0; d < e.ndim; d++) {
+            if (e.dims[d] == 0) { want = 0; continue; }
+            if (want > UINT64_MAX / (uint64_t)e.dims[d]) {
+                set_error("%s: %.64s: element count overflows", path, e.name);
+                return false;
+            }
+            want *= (uint64_t)e.dims[d];
+        }
+        if (e.nbytes != want) {
+            set_error("%s: %.64s: blob size is not its element count", path, e.name);
+            return false;
+        }
+        return true;
+    }
+    const int64_t N = e.dims[0], K = e.dims[1];
+    if (N <= 0 || K <= 0 || N > (1 << 30) || K > (1 << 30)) {
+        set_error("%s: %.64s: bad shape", path, e.name);
+        return false;
+    }
+    const int64_t nb = (K + kQBlock - 1) / kQBlock, Npad = (N + 7) & ~7ll;
+    if (e.dims[2] != nb || e.dims[3] != Npad) {
+        set_error("%s: %.64s: packed for another block size/Npad", path, e.name);
+        return false;
+    }
+    const uint64_t want = (uint64_t)Npad * ((K + 3) / 4) * 4 + (uint64_t)Npad * 4 + (uint64_t)nb * Npad * 4;
+    if (e.nbytes != want) {
+        set_error("%s: %.64s: blob size mismatch", path, e.name);
+        return false;
+    }
+    return true;
+}
+
+static bool write_all(int fd, const void *p, size_t n) {
+    const char *c = (const char *)p;
+    while (n) {
+        const ssize_t w = write(fd, c, n);
+        if (w <= 0) return false;
+        c += w;
+        n -= (size_t)w;
+    }
+    return true;
+}
+
+}  // namespace e2mi
+
+using namespace e2mi;
+
+extern "C" const char *e2_last_error(void) { return e2mi_last_error(); }
+
+extern "C" void e2_config_baseline(e2_config *c) {
+    if (!c) return;
+    c->n_layers = 24;
+    c->hidden = 768;
+    c->ffn = 1152;
+    c->n_heads = 3;
+    c->n_kv_heads = 1;
+    c->head_dim = 256;
+    c->vocab = 262144;
+    c->max_seq = 2048;
+    c->rms_eps = 1e-6f;
+    c->rope_theta = 10000.0f;
+    c->embed_scale = sqrtf(768.0f);
+    c->attn_scale = 1.0f;
+}
+
+extern "C" e2_model *e2_model_synthetic(const e2_config *c, uint64_t seed) {
+    if (!c || !config_ok(*c)) {
+        if (!c) set_error("model_synthetic: null config");
+        return nullptr;
+    }
+    e2_model *m = new (std::nothrow) e2_model();
+    if (!m) {
+        set_error("oom: model");
+        return nullptr;
+    }
+    m->cfg = *c;
+    try {
+        int t = 0;
+        synth_f32(m->f32[kEmbed], c->vocab, c->hidden, 0.0, 0.02, seed, t++);
+        synth_f32(m->f32[kFinalNorm], 1, c->hidden, 1.0, 0.05, seed, t++);
+        for (int l = 0; l < c->n_layers; l++) {
+            for (int s = 0; s < 7; s++) {
+                int N, K;
+                q8_shape(*c, s, &N, &K);
+                synth_q8(m->q8[layer_name(l, kQ8Suffix[s])], N, K, seed, t++);
+            }
+            for (int s = 0; s < 6; s++)
+                synth_f32(m->f32[layer_name(l, kNormSuffix[s])], 1, norm_len(*c, s), 1.0, 0.05, seed, t++);
+        }
+    } catch (...) {
+        delete m;
+        set_error("oom: synthetic weights");
+        return nullptr;
+    }
+    return m;
+}
+
+extern "C" void e2_free(e2_model *m) {
+    if (!m) return;
+    if (m->map) munmap(m->map, m->map_size);
+    delete m;
+}
+
+extern "C" int e2_model_config(const e2_model *m, e2_config *out) {
+    if (!m || !out) {
+        set_error("model_config: null argument");
+        return -1;
+    }
+    *out = m->cfg;
+    return 0;
+}
+
+extern "C" int e2_model_tensor(const e2_model *m, const char *name, e2_tensor_view *v) {
+    if (!m || !name || !v) {
+        set_error("model_tensor: null argument");
+        return -1;
+    }
+    memset(v, 0, sizeof *v);
+    auto q = m->q8.find(name);
+    if (q != m->q8.end()) {
+        const HostQ8W &w = q->second;
+        v->kind = KIND_Q8W;
+        v->ndim = 4;
+        v->dims[0] = w.N;
+        v->dims[1] = w.K;
+        v->dims[2] = w.nb;
+        v->dims[3] = w.Npad;
+        v->data = w.w;
+        v->scale = w.scale;
+        v->bsq = w.bsq;
+        v->nbytes = w.bytes();
+        return 0;
+    }
+    auto f = m->f32.find(name);
+    if (f != m->f32.end()) {
+        v->kind = KIND_F32;
+        v->ndim = f->second.ndim;
+        memcpy(v->dims, f->second.dims, sizeof v->dims);
+        v->data = f->second.p;
+        v->nbytes = f->second.count() * sizeof(float);
+        return 0;
+    }
+    set_error("model_tensor: %s: not in the model", name);
+    return -1;
+}
+
+extern "C" int e2_save_e8cq(const e2_model *m, const char *path) {
+    if (!m || !path) {
+        set_error("save_e8cq: null argument");
+        return -1;
+    }
+    std::string tmp = std::string(path) + ".tmp.XXXXXX";
+    std::vector<char> tb(tmp.begin(), tmp.end());
+    tb.push_back(0);
+    const int fd = mkstemp(tb.data());
+    if (fd < 0) {
+        set_error("save_e8cq: cannot create %s", tb.data());
+        return -1;
+    }
+    std::vector<Entry> idx;
+    uint64_t off = 16;
+    const uint32_t hdr0[4] = {kMagic, kVersion, 0, 0};
+    bool ok = write_all(fd, hdr0, sizeof hdr0);
+    auto pad = [&]() {
+        static const char z[16] = {0};
+        const size_t p = (16 - (off & 15)) & 15;
+        if (p) ok = ok && write_all(fd, z, p);
+        off += p;
+    };
+    auto begin = [&](const std::string &name, uint32_t kind, uint32_t ndim, const int64_t *dims) {
+        Entry e;
+        memset(&e, 0, sizeof e);
+        if (name.size() >= sizeof e.name) {
+            set_error("save_e8cq: tensor name too long: %s", name.c_str());
+            ok = false;
+        }
+        snprintf(e.name, sizeof e.name, "%s", name.c_str());
+        e.kind = kind;
+        e.ndim = ndim;
+        for (uint32_t i = 0; i < ndim; i++) e.dims[i] = dims[i];
+        e.off = off;
+        idx.push_back(e);
+    };
+    auto bytes = [&](const void *p, size_t n) {
+        ok = ok && write_all(fd, p, n);
+        off += n;
+        idx.back().nbytes += n;
+    };
+    for (auto &kv : m->q8) {  // q8c_put_q8w (q8cache.c:163-181): w | scale | bsq
+        const HostQ8W &w = kv.second;
+        const int64_t dims[4] = {w.N, w.K, w.nb, w.Npad};
+        begin(kv.first, KIND_Q8W, 4, dims);
+        bytes(w.w, w.bytes());
+        bytes(w.scale, (size_t)w.Npad * 4);
+        bytes(w.bsq, (size_t)w.nb * w.Npad * 4);
+        pad();
+    }
+    for (auto &kv : m->f32) {
+        begin(kv.first, KIND_F32, (uint32_t)kv.second.ndim, kv.second.dims);
+        bytes(kv.second.p, kv.second.count() * 4);
+        pad();
+    }
+    if (off > UINT32_MAX || idx.size() > UINT32_MAX) {
+        set_error("save_e8cq: the model exceeds the v1 32-bit index format");
+        ok = false;
+    }
+    const uint32_t hdr[4] = {kMagic, kVersion, (uint32_t)idx.size(), (uint32_t)off};
+    ok = ok && write_all(fd, idx.data(), idx.size() * sizeof(Entry));
+    ok = ok && lseek(fd, 0, SEEK_SET) == 0 && write_all(fd, hdr, sizeof hdr);
+    ok = ok && fsync(fd) == 0;
+    ok = (close(fd) == 0) && ok;
+    if (ok && rename(tb.data(), path) != 0) ok = false;
+    if (!ok) {
+        unlink(tb.data());
+        if (!strstr(e2mi_last_error(), "save_e8cq")) set_error("save_e8cq: write/commit of %s failed", path);
+        return -1;
+    }
+    return 0;
+}
+
+static float bf16f(uint16_t v) {
+    const uint32_t u = (uint32_t)v << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+extern "C" e2_model *e2_load_e8cq(const char *path, const e2_config *c) {
+    if (!path || !c || !config_ok(*c)) {
+        if (!path || !c) set_error("load_e8cq: null argument");
+        return nullptr;
+    }
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) {
+        set_error("%s: cannot open", path);
+        return nullptr;
+    }
+    struct stat st;
+    if (fstat(fd, &st) || st.st_size < 16) {
+        close(fd);
+        set_error("%s: too small", path);
+        return nullptr;
+    }
+    const size_t size = (size_t)st.st_size;
+    void *map = mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (map == MAP_FAILED) {
+        set_error("%s: mmap failed", path);
+        return nullptr;
+    }
+    e2_model *m = new (std::nothrow) e2_model();
+    if (!m) {
+        munmap(map, size);
+        set_error("oom: model");
+        return nullptr;
+    }
+    m->cfg = *c;
+    m->map = map;
+    m->map_size = size;
+    const uint8_t *base = (const uint8_t *)map;
+    const uint32_t *h = (const uint32_t *)base;
+    const uint64_t io = h[3];
+    const uint32_t n = h[2];
+    auto fail = [&](void) -> e2_model * {
+        e2_free(m);
+        return nullptr;
+    };
+    if (h[0] != kMagic || h[1] != kVersion) {
+        set_error("%s: bad magic/version", path);
+        return fail();
+    }
+    if (io < 16 || (io & 15) || io > size || (uint64_t)n > (size - io) / sizeof(Entry)) {
+        set_error("%s: truncated or misaligned index", path);
+        return fail();
+    }
+    const Entry *idx = (const Entry *)(base + io);
+    for (uint32_t i = 0; i < n; i++)
+        if (!entry_ok(idx[i], io, path)) return fail();
+    for (uint32_t i = 0; i < n; i++) {
+        const Entry &e = idx[i];
+        const uint8_t *p = base + e.off;
+        if (e.kind == KIND_Q8W) {
+            HostQ8W &w = m->q8[e.name];
+            w.N = (int)e.dims[0];
+            w.K = (int)e.dims[1];
+            w.nb = (int)e.dims[2];
+            w.Npad = (int)e.dims[3];
+            w.w = (const int8_t *)p;
+            w.scale = (const float *)(p + w.bytes());
+            w.bsq = (const int32_t *)(p + w.bytes() + (size_t)w.Npad * 4);
+        } else {
+            F32T &t = m->f32[e.name];
+            t.ndim = (int)e.ndim;
+            for (uint32_t d = 0; d < e.ndim; d++) t.dims[d] = e.dims[d];
+            if (e.kind == KIND_F32) {
+                t.p = (const float *)p;
+            } else {  // bf16 tensors (the reference keeps norm scales in bf16)
+                t.own.resize(e.nbytes / 2);
+                for (size_t j = 0; j < t.own.size(); j++) t.own[j] = bf16f(((const uint16_t *)p)[j]);
+                t.p = t.own.data();
+            }
+        }
+    }
+    // every tensor of the configured geometry must be present with its shape
+    const e2_config &cf = *c;
+    auto need_f32 = [&](const std::string &name, size_t count) {
+        auto it = m->f32.find(name);
+        if (it == m->f32.end() || it->second.count() != count) {
+            set_error("%s: %s missing or mis-shaped", path, name.c_str());
+            return false;
+        }
+        return true;
+    };
+    if (!need_f32(kEmbed, (size_t)cf.vocab * cf.hidden) || !need_f32(kFinalNorm, (size_t)cf.hidden))
+        return fail();
+    for (int l = 0; l < cf.n_layers; l++) {
+        for (int s = 0; s < 7; s++) {
+            int N, K;
+            q8_shape(cf, s, &N, &K);
+            auto it = m->q8.find(layer_name(l, kQ8Suffix[s]));
+            if (it == m->q8.end() || it->second.N != N || it->second.K != K) {
+                set_error("%s: %s missing or mis-shaped", path, layer_name(l, kQ8Suffix[s]).c_str());
+                return fail();
+            }
+        }
+        for (int s = 0; s < 6; s++)
+            if (!need_f32(layer_name(l, kNormSuffix[s]), (size_t)norm_len(cf, s))) return fail();
+    }
+    return m;
+}
+
+// ------------------------------------------------------------------ accessors for the engine
+namespace e2mi {
+const HostQ8W *model_q8(const e2_model *m, const std::string &name) {
+    auto it = m->q8.find(name);
+    return it == m->q8.end() ? nullptr : &it->second;
+}
+const float *model_f32(const e2_model *m, const std::string &name, size_t count) {
+    auto it = m->f32.find(name);
+    return (it == m->f32.end() || it->second.count() != count) ? nullptr : it->second.p;
+}
+const char *q8_suffix(int s) { return kQ8Suffix[s]; }
+const char *norm_suffix(int s) { return kNormSuffix[s]; }
+const char *embed_name() { return kEmbed; }
+const char *final_norm_name() { return kFinalNorm; }
+}  // namespace e2mi

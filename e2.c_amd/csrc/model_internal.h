@@ -1,0 +1,50 @@
+// model_internal.h — the host model's tensor records, shared by model.cpp and forward.cpp.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/e2.h"
+
+namespace e2mi {
+
+struct HostQ8W {  // the reference's e2_q8w (int8.h:79-92), owned or borrowed from a mapping
+    const int8_t *w = nullptr;
+    const float *scale = nullptr;
+    const int32_t *bsq = nullptr;
+    int N = 0, K = 0, nb = 0, Npad = 0;
+    std::vector<int8_t> ow;
+    std::vector<float> os;
+    std::vector<int32_t> ob;
+    size_t bytes() const { return (size_t)Npad * ((K + 3) / 4) * 4; }
+};
+
+struct F32T {
+    const float *p = nullptr;
+    std::vector<float> own;
+    int ndim = 1;
+    int64_t dims[4] = {0, 0, 0, 0};
+    size_t count() const {
+        size_t n = 1;
+        for (int i = 0; i < ndim; i++) n *= (size_t)dims[i];
+        return n;
+    }
+};
+
+std::string layer_name(int l, const char *suffix);
+const HostQ8W *model_q8(const e2_model *m, const std::string &name);
+const float *model_f32(const e2_model *m, const std::string &name, size_t count);
+const char *q8_suffix(int s);    // 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down
+const char *norm_suffix(int s);  // 0 input, 1 post_attn, 2 pre_ffn, 3 post_ffn, 4 q_norm, 5 k_norm
+const char *embed_name();
+const char *final_norm_name();
+
+// weights.hip: unpack a packed [Npad/8][K/4][8][4] blob into dst rows (n / grp) * gstride + goff +
+// n % grp of a row-major [*][ld] device matrix
+int upload_packed_rows(int8_t *dst, int ld, const int8_t *wq, int N, int K, int grp, int gstride,
+                       int goff, hipStream_t s);
+
+}  // namespace e2mi

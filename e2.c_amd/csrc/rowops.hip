@@ -24,7 +24,8 @@ struct RowArgs {
     const float *src;      // PLAIN/ADDNORM input rows [M][D] (ld = D)
     const float *res;      // ADDNORM residual [M][D]
     const float *table;    // EMBED table [vocab][D]
-    const int32_t *ids;    // EMBED token ids [M]
+    const int32_t *ids;    // EMBED token ids [M], clamped into [0, vocab)
+    int vocab;
     float embed_scale;
     const float *gamma_a;  // ADDNORM: gamma of the norm applied to src
     const float *gamma_n;  // gamma of the norm producing the quantized operand (NULL: no norm)
@@ -61,7 +62,8 @@ __global__ __launch_bounds__(256) void k_rows(RowArgs a) {
     const float *row;
     float escale = 1.f;
     if (MODE == ROW_EMBED) {
-        row = a.table + (size_t)a.ids[m] * D;
+        const int id = min(max(a.ids[m], 0), a.vocab - 1);
+        row = a.table + (size_t)id * D;
         escale = a.embed_scale;
     } else {
         row = a.src + (size_t)m * D;
@@ -336,15 +338,16 @@ extern "C" int e2mi_add_norm_quant(e2mi_stream stream, const float *src, const f
     return launch_rows((hipStream_t)stream, ROW_ADDNORM, a);
 }
 
-extern "C" int e2mi_embed_norm_quant(e2mi_stream stream, const float *table, const int32_t *ids,
-                                     float embed_scale, const float *gamma, float eps, int M, int D,
+extern "C" int e2mi_embed_norm_quant(e2mi_stream stream, const float *table, int vocab,
+                                     const int32_t *ids, float embed_scale, const float *gamma, float eps, int M, int D,
                                      float *x_out, int8_t *q, float *qs) {
-    if (!table || !ids || !gamma || !x_out || !al16(table) || !al16(x_out) || (!q) != (!qs)) {
+    if (!table || vocab <= 0 || !ids || !gamma || !x_out || !al16(table) || !al16(x_out) ||
+        (!q) != (!qs)) {
         set_error("embed_norm_quant: null/misaligned pointer");
         return -1;
     }
     RowArgs a = {};
-    a.table = table; a.ids = ids; a.embed_scale = embed_scale; a.gamma_n = gamma; a.eps = eps;
+    a.table = table; a.vocab = vocab; a.ids = ids; a.embed_scale = embed_scale; a.gamma_n = gamma; a.eps = eps;
     a.x_out = x_out; a.q = q; a.qs = qs; a.M = M; a.D = D;
     return launch_rows((hipStream_t)stream, ROW_EMBED, a);
 }

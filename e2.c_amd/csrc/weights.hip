@@ -9,17 +9,40 @@
 #include <string.h>
 
 #include "common.h"
+#include "model_internal.h"
 
 namespace e2mi {
 
+// row n of the packed blob lands in destination row (n / grp) * gstride + goff + n % grp: the
+// identity for a plain upload, an offset for q|k|v concatenation, and the per-128 gate|up
+// interleave the GeGLU epilogue reads
 __global__ void k_unpack_quads(int8_t *__restrict__ dst, int ld, const int8_t *__restrict__ src,
-                               int N, int K) {
+                               int N, int K, int grp, int gstride, int goff) {
     const int kq_n = (K + 3) / 4;
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)N * kq_n) return;
     const int n = (int)(i / kq_n), kq = (int)(i % kq_n);
     const uint32_t v = *(const uint32_t *)(src + ((size_t)(n >> 3) * kq_n + kq) * 32 + (n & 7) * 4);
-    *(uint32_t *)(dst + (size_t)n * ld + kq * 4) = v;
+    const size_t row = (size_t)(n / grp) * gstride + goff + n % grp;
+    *(uint32_t *)(dst + row * ld + kq * 4) = v;
+}
+
+int upload_packed_rows(int8_t *dst, int ld, const int8_t *wq, int N, int K, int grp, int gstride,
+                       int goff, hipStream_t s) {
+    const size_t bytes = (size_t)((N + 7) / 8) * ((K + 3) / 4) * 32;
+    int8_t *staging = nullptr;
+    if (check_hip(hipMalloc(&staging, bytes), "hipMalloc staging")) return -1;
+    int rc = check_hip(hipMemcpyAsync(staging, wq, bytes, hipMemcpyHostToDevice, s), "upload packed");
+    if (!rc) {
+        const long n = (long)N * ((K + 3) / 4);
+        hipLaunchKernelGGL(k_unpack_quads, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst,
+                           ld, staging, N, K, grp, gstride, goff);
+        rc = check_hip(hipGetLastError(), "unpack launch");
+    }
+    // the staging blob must outlive the kernel
+    if (!rc) rc = check_hip(hipStreamSynchronize(s), "unpack sync");
+    (void)hipFree(staging);
+    return rc;
 }
 
 static int alloc_q8w(e2mi_q8w *out, int N, int K, const float *scale, const float *bias,
@@ -32,13 +55,13 @@ static int alloc_q8w(e2mi_q8w *out, int N, int K, const float *scale, const floa
     out->out_max = 1e31f;
     E2MI_HIP(hipMalloc(&out->w, (size_t)N * out->ld));
     if (check_hip(hipMalloc(&out->scale, sizeof(float) * N), "hipMalloc scale")) {
-        hipFree(out->w);
+        (void)hipFree(out->w);
         memset(out, 0, sizeof *out);
         return -1;
     }
     if (bias && check_hip(hipMalloc(&out->bias, sizeof(float) * N), "hipMalloc bias")) {
-        hipFree(out->w);
-        hipFree(out->scale);
+        (void)hipFree(out->w);
+        (void)hipFree(out->scale);
         memset(out, 0, sizeof *out);
         return -1;
     }
@@ -71,21 +94,7 @@ extern "C" int e2mi_q8w_upload_packed(e2mi_q8w *out, const int8_t *wq, const flo
     if (!out || check_dims(N, K, wq, scale, "q8w_upload_packed")) return -1;
     hipStream_t s = (hipStream_t)stream;
     if (alloc_q8w(out, N, K, scale, bias, s)) return -1;
-    const size_t bytes = (size_t)((N + 7) / 8) * ((K + 3) / 4) * 32;
-    int8_t *staging = nullptr;
-    if (check_hip(hipMalloc(&staging, bytes), "hipMalloc staging") ||
-        check_hip(hipMemcpyAsync(staging, wq, bytes, hipMemcpyHostToDevice, s), "upload packed")) {
-        hipFree(staging);
-        e2mi_q8w_free(out);
-        return -1;
-    }
-    const long n = (long)N * ((K + 3) / 4);
-    hipLaunchKernelGGL(k_unpack_quads, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out->w,
-                       out->ld, staging, N, K);
-    int rc = check_hip(hipGetLastError(), "unpack launch");
-    // the staging blob must outlive the kernel: wait before freeing it
-    if (!rc) rc = check_hip(hipStreamSynchronize(s), "unpack sync");
-    hipFree(staging);
+    const int rc = upload_packed_rows(out->w, out->ld, wq, N, K, N, 0, 0, s);
     if (rc) e2mi_q8w_free(out);
     return rc;
 }
@@ -106,9 +115,9 @@ extern "C" int e2mi_q8w_upload_rowmajor(e2mi_q8w *out, const int8_t *w, const fl
 
 extern "C" void e2mi_q8w_free(e2mi_q8w *w) {
     if (!w) return;
-    if (w->w) hipFree(w->w);
-    if (w->scale) hipFree(w->scale);
-    if (w->bias) hipFree(w->bias);
+    if (w->w) (void)hipFree(w->w);
+    if (w->scale) (void)hipFree(w->scale);
+    if (w->bias) (void)hipFree(w->bias);
     memset(w, 0, sizeof *w);
 }
 

@@ -22,6 +22,19 @@ class Q8W(C.Structure):
                 ("out_min", _F), ("out_max", _F)]
 
 
+class E2Config(C.Structure):
+    """e2_config (include/e2.h)."""
+    _fields_ = [("n_layers", _I), ("hidden", _I), ("ffn", _I), ("n_heads", _I),
+                ("n_kv_heads", _I), ("head_dim", _I), ("vocab", _I), ("max_seq", _I),
+                ("rms_eps", _F), ("rope_theta", _F), ("embed_scale", _F), ("attn_scale", _F)]
+
+
+class TensorView(C.Structure):
+    """e2_tensor_view (include/e2.h)."""
+    _fields_ = [("kind", _I), ("ndim", _I), ("dims", C.c_int64 * 4), ("data", _P), ("scale", _P),
+                ("bsq", _P), ("nbytes", C.c_size_t)]
+
+
 # name -> (restype, argtypes); every symbol include/*.h declares appears here
 SIGNATURES = {
     "e2mi_last_error": (C.c_char_p, []),
@@ -37,12 +50,41 @@ SIGNATURES = {
     "e2mi_interleave_gate_up": (_I, [_P, _P, _P, _P, _P, _P, _I, _I]),
     "e2mi_norm_quant": (_I, [_P, _P, _P, _F, _I, _I, _P, _P, _P]),
     "e2mi_add_norm_quant": (_I, [_P, _P, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P]),
-    "e2mi_embed_norm_quant": (_I, [_P, _P, _P, _F, _P, _F, _I, _I, _P, _P, _P]),
+    "e2mi_embed_norm_quant": (_I, [_P, _P, _I, _P, _F, _P, _F, _I, _I, _P, _P, _P]),
     "e2mi_qkv_norm_rope": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P]),
     "e2mi_gelu_mul_quant": (_I, [_P, _P, _I, _P, _I, _I, _I, _P, _P, _I]),
     "e2mi_pool_l2": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
     "e2mi_pool_workspace_bytes": (C.c_size_t, [_I, _I, _I]),
     "e2mi_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
+    # backend-selection surface (include/e2_dispatch.h)
+    "e2_dispatch_set_cpu_backend": (None, [_I]),
+    "e2_cpu_backend": (_I, []),
+    "e2_backend_caps": (C.c_uint, [_I]),
+    "e2_attn_env_reload": (None, []),
+    "e2_attn_override": (None, [_I, _I]),
+    "e2_attn_stage_override": (_I, []),
+    "e2_attn_kind_name": (C.c_char_p, [_I]),
+    "e2_attn_min_keys": (_I, [_I, _I]),
+    "e2_attn_pick": (_I, [_I, _I, _I]),
+    # model container (include/e2.h)
+    "e2_config_baseline": (None, [C.POINTER(E2Config)]),
+    "e2_model_synthetic": (_P, [C.POINTER(E2Config), C.c_uint64]),
+    "e2_load_e8cq": (_P, [C.c_char_p, C.POINTER(E2Config)]),
+    "e2_save_e8cq": (_I, [_P, C.c_char_p]),
+    "e2_free": (None, [_P]),
+    "e2_last_error": (C.c_char_p, []),
+    "e2_model_config": (_I, [_P, C.POINTER(E2Config)]),
+    "e2_model_tensor": (_I, [_P, C.c_char_p, C.POINTER(TensorView)]),
+    # the encoder engine (include/e2mi.h)
+    "e2mi_create": (_P, [_P]),
+    "e2mi_create_rows": (_P, [_P, _I]),
+    "e2mi_destroy": (None, [_P]),
+    "e2mi_device": (C.c_char_p, [_P]),
+    "e2mi_text_embed": (_I, [_P, _P, _I, _P]),
+    "e2mi_text_embed_batch": (_I, [_P, _P, _P, _I, _I, _P]),
+    "e2mi_text_embed_batch_device": (_I, [_P, _P, _P, _I, _I, _P, _P]),
+    "e2mi_stats": (_I, [_P, C.POINTER(C.c_long), C.POINTER(C.c_long), C.POINTER(C.c_double)]),
+    "e2mi_set_layer_limit": (_I, [_P, _I]),
 }
 
 _lib = None
@@ -228,11 +270,11 @@ def add_norm_quant(src, res, gamma_add, gamma_next=None, eps=1e-6, x_out=None, w
 def embed_norm_quant(table, ids, embed_scale, gamma, eps=1e-6, stream=None):
     import torch
     M = ids.shape[0]
-    D = table.shape[1]
+    V, D = table.shape
     x = torch.empty((M, D), dtype=torch.float32, device=table.device)
     q = torch.empty((M, D), dtype=torch.int8, device=table.device)
     qs = torch.empty((M, D // 128), dtype=torch.float32, device=table.device)
-    check(load().e2mi_embed_norm_quant(stream_ptr(stream), ptr(table), ptr(ids), embed_scale,
+    check(load().e2mi_embed_norm_quant(stream_ptr(stream), ptr(table), V, ptr(ids), embed_scale,
                                        ptr(gamma), eps, M, D, ptr(x), ptr(q), ptr(qs)),
           "embed_norm_quant")
     return x, q, qs
@@ -291,3 +333,102 @@ def attention(q16, k16, vt16, valid, B, S, H, KV, scale=1.0, want_f32=True, stre
     check(load().e2mi_attention(stream_ptr(stream), ptr(q16), ptr(k16), ptr(vt16), ptr(valid), B, S,
                                 H, KV, D, scale, ptr(cq), ptr(cs), ptr(c32)), "attention")
     return cq, cs, c32
+
+
+# ---- model container and encoder engine
+def baseline_config(**over):
+    c = E2Config()
+    load().e2_config_baseline(C.byref(c))
+    for k, v in over.items():
+        setattr(c, k, v)
+    return c
+
+
+class Model:
+    """An e2_model (include/e2.h): synthetic or loaded from an E8CQ cache; freed with the object."""
+
+    def __init__(self, handle):
+        if not handle:
+            raise E2MIError(f"model: {last_error()}")
+        self.h = C.c_void_p(handle)
+
+    @classmethod
+    def synthetic(cls, cfg: E2Config, seed: int):
+        return cls(load().e2_model_synthetic(C.byref(cfg), seed))
+
+    @classmethod
+    def load_e8cq(cls, path: str, cfg: E2Config):
+        return cls(load().e2_load_e8cq(path.encode(), C.byref(cfg)))
+
+    def save_e8cq(self, path: str):
+        check(load().e2_save_e8cq(self.h, path.encode()), "save_e8cq")
+
+    @property
+    def config(self) -> E2Config:
+        c = E2Config()
+        check(load().e2_model_config(self.h, C.byref(c)), "model_config")
+        return c
+
+    def tensor(self, name: str):
+        """numpy copies: f32 tensors -> array; int8 weights -> (packed w, scale[N], bsq, N, K)."""
+        import numpy as np
+        v = TensorView()
+        check(load().e2_model_tensor(self.h, name.encode(), C.byref(v)), "model_tensor")
+        if v.kind == 2:
+            n = v.nbytes // 4
+            a = np.ctypeslib.as_array(C.cast(v.data, C.POINTER(C.c_float)), (n,)).copy()
+            return a.reshape([int(d) for d in v.dims[:v.ndim]])
+        N, K, nb, Npad = (int(d) for d in v.dims)
+        w = np.ctypeslib.as_array(C.cast(v.data, C.POINTER(C.c_int8)), (v.nbytes,)).copy()
+        sc = np.ctypeslib.as_array(C.cast(v.scale, C.POINTER(C.c_float)), (N,)).copy()
+        bsq = np.ctypeslib.as_array(C.cast(v.bsq, C.POINTER(C.c_int32)), (nb * Npad,)).copy()
+        return w, sc, bsq.reshape(nb, Npad), N, K
+
+    def __del__(self):
+        if _lib is not None and getattr(self, "h", None):
+            _lib.e2_free(self.h)
+            self.h = None
+
+
+class Engine:
+    """An e2mi_engine (include/e2mi.h) on the current device; destroyed with the object."""
+
+    def __init__(self, model: Model, max_rows: int = 0):
+        h = load().e2mi_create_rows(model.h, max_rows)
+        if not h:
+            raise E2MIError(f"create: {last_error()}")
+        self.h = C.c_void_p(h)
+        self.hidden = model.config.hidden
+
+    @property
+    def device(self) -> str:
+        return load().e2mi_device(self.h).decode()
+
+    def embed_batch(self, ids, valid=None):
+        import numpy as np
+        ids = np.ascontiguousarray(ids, np.int32)
+        B, S = ids.shape
+        v = None if valid is None else np.ascontiguousarray(valid, np.uint8)
+        out = np.empty((B, self.hidden), np.float32)
+        check(load().e2mi_text_embed_batch(self.h, ptr(ids), ptr(v), B, S, ptr(out)),
+              "text_embed_batch")
+        return out
+
+    def embed_batch_device(self, ids, valid, out, stream=None):
+        B, S = ids.shape
+        check(load().e2mi_text_embed_batch_device(self.h, ptr(ids), ptr(valid), B, S, ptr(out),
+                                                  stream_ptr(stream)), "text_embed_batch_device")
+        return out
+
+    def stats(self):
+        calls, kern, ms = C.c_long(), C.c_long(), C.c_double()
+        check(load().e2mi_stats(self.h, C.byref(calls), C.byref(kern), C.byref(ms)), "stats")
+        return calls.value, kern.value, ms.value
+
+    def set_layer_limit(self, n: int):
+        check(load().e2mi_set_layer_limit(self.h, n), "set_layer_limit")
+
+    def __del__(self):
+        if _lib is not None and getattr(self, "h", None):
+            _lib.e2mi_destroy(self.h)
+            self.h = None

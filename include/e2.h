@@ -1,0 +1,79 @@
+/* e2.h — the model container of the int8 encoder (host side).
+ *
+ * Mirrors the reference's include/e2.h handle (e2_model, e2_free, e2_last_error; e2.h:21-22,159)
+ * for the tier's geometry. The reference's e2_load reads its own checkpoint (hidden 512, PLE, ...,
+ * e2.c:254-434), which this tier does not run; a model here comes from
+ *   - e2_model_synthetic: seeded random-init int8 weights at a given geometry,
+ *   - e2_load_e8cq: an E8CQ packed int8 cache, the reference's q8cache.c v1 format (q8cache.c:1-13):
+ *     header "E8CQ" v1, 16-byte aligned blobs, 152-byte index entries; int8 weights as kind 3
+ *     (quad-interleaved w | per-row scale | per-block sums bsq), f32 tensors as kind 2.
+ * Tensor names follow the reference's safetensors names (e2.c:306-402), e.g.
+ * "language_model.layers.3.self_attn.q_proj.weight", "language_model.embed_tokens.weight".
+ *
+ * Weights are held in the reference's e2_q8w layout (int8.h:14-36): [Npad/8][K/4][8][4] int8,
+ * per-row f32 scale, bsq[nb][Npad]. The GPU engine (e2mi.h) re-lays them out on upload.
+ */
+#ifndef E2_H
+#define E2_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct e2_model e2_model;
+
+typedef struct {
+    int n_layers;      /* 24 */
+    int hidden;        /* 768 */
+    int ffn;           /* 1152 */
+    int n_heads;       /* 3 query heads */
+    int n_kv_heads;    /* 1 kv head (GQA 3:1) */
+    int head_dim;      /* 256 */
+    int vocab;         /* 262144 */
+    int max_seq;       /* 2048 (model.h:16) */
+    float rms_eps;     /* 1e-6 (e2.c:297) */
+    float rope_theta;  /* 10000 */
+    float embed_scale; /* sqrt(hidden) (e2.c:298) */
+    float attn_scale;  /* 1.0: the reference does not scale the logits (text.c:8-9) */
+} e2_config;
+
+/* The BASELINE config-4 geometry (values in the comments above). */
+void e2_config_baseline(e2_config *c);
+
+/* Random-init model: int8 weights uniform in [-127,127] with per-row scales U(0.001, 0.02), norm
+ * gammas ~N(1, 0.05), embedding table ~N(0, 0.02). Deterministic in `seed` (the reference tests'
+ * LCG s = s*1664525 + 1013904223, one stream per tensor row). NULL on error. */
+e2_model *e2_model_synthetic(const e2_config *c, uint64_t seed);
+
+/* Load an E8CQ cache written by e2_save_e8cq or by the reference's q8c writer (q8cache.c:61-222).
+ * The file is validated before any pointer into it is used (q8cache.c:242-280) and memory-mapped;
+ * int8 blobs are borrowed from the mapping, which lives until e2_free. NULL on error. */
+e2_model *e2_load_e8cq(const char *path, const e2_config *c);
+/* Write the model as an E8CQ cache (atomic: temp file + rename, q8cache.c:183-222). */
+int e2_save_e8cq(const e2_model *m, const char *path);
+
+void e2_free(e2_model *m);
+/* Last error of this process (e2.h:159). Never NULL. */
+const char *e2_last_error(void);
+
+int e2_model_config(const e2_model *m, e2_config *out);
+
+/* A read-only view of one tensor. kind: 2 = f32 (data), 3 = int8 weight (data = packed w,
+ * scale, bsq; dims = {N, K, nblocks, Npad}). */
+typedef struct {
+    int kind, ndim;
+    int64_t dims[4];
+    const void *data;
+    const float *scale;
+    const int32_t *bsq;
+    size_t nbytes;
+} e2_tensor_view;
+int e2_model_tensor(const e2_model *m, const char *name, e2_tensor_view *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* E2_H */

@@ -107,8 +107,10 @@ int e2mi_add_norm_quant(e2mi_stream stream, const float *src, const float *res,
                         float *x_out, float *xn_out, int8_t *q, float *qs);
 
 /* Embedding gather (text.c:917-921) fused with the first layer's norm_split + quantize:
- * x = table[ids[m]] * embed_scale -> x_out; rmsnorm(x)*gamma quantized into q/qs. */
-int e2mi_embed_norm_quant(e2mi_stream stream, const float *table, const int32_t *ids,
+ * x = table[ids[m]] * embed_scale -> x_out; rmsnorm(x)*gamma quantized into q/qs. Device-side ids
+ * cannot be validated before launch: they are clamped into [0, vocab) to keep every read in the
+ * table (the host entry points validate and reject, text.c:1008-1013). */
+int e2mi_embed_norm_quant(e2mi_stream stream, const float *table, int vocab, const int32_t *ids,
                           float embed_scale, const float *gamma, float eps, int M, int D,
                           float *x_out, int8_t *q, float *qs);
 
@@ -146,6 +148,41 @@ size_t e2mi_pool_workspace_bytes(int B, int S, int D);
 int e2mi_attention(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
                    const uint16_t *vt16, const uint8_t *valid, int B, int S, int H, int KV, int D,
                    float scale, int8_t *ctx_q, float *ctx_s, float *ctx32);
+
+/* ---- the encoder on the device (e2hip.h:34-64) */
+
+typedef struct e2_model e2_model; /* e2.h */
+typedef struct e2mi_engine e2mi_engine;
+
+/* Upload the model (int8 weights re-laid out for MFMA, q|k|v concatenated, gate|up interleaved)
+ * and allocate a workspace for 32768 token rows (e2_hip_create, hip.c:112-167). `m` may be freed
+ * afterwards. NULL (and e2mi_last_error) when there is no gfx950 device or the model is invalid. */
+e2mi_engine *e2mi_create(const e2_model *m);
+/* Same with an explicit workspace capacity in token rows (>= the model's max_seq). */
+e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows);
+void e2mi_destroy(e2mi_engine *g);
+/* Device name, architecture and CU count, for logging (e2_hip_device). */
+const char *e2mi_device(e2mi_engine *g);
+
+/* One sequence of n_ids tokens -> one unit vector of `hidden` floats (e2_hip_text_embed). */
+int e2mi_text_embed(e2mi_engine *g, const int32_t *ids, int n_ids, float *out);
+/* `batch` sequences of `seq_len` tokens, row-major; valid marks real tokens (NULL: all valid; any
+ * nonzero byte keeps a row). Positions restart per sequence; all-invalid sequences give an exact
+ * zero vector. Host buffers; the request is validated (ids in [0, vocab), 1 <= seq_len <=
+ * max_seq) before anything is written, then processed in chunks of whole sequences. Synchronous.
+ * (e2_hip_text_embed_batch, hip.c:308-342; e2_text_embed_batch, text.c:997-1027.) */
+int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const uint8_t *valid, int batch,
+                          int seq_len, float *out);
+/* The same forward with DEVICE buffers already resident in HBM: ids [batch*seq_len], valid
+ * [batch*seq_len], out [batch][hidden]; batch*seq_len must fit the workspace. Enqueued on `stream`
+ * (NULL: the engine's own stream, then synchronised). Ids are clamped, not validated. */
+int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, const uint8_t *valid,
+                                 int batch, int seq_len, float *out, e2mi_stream stream);
+/* Calls served, kernels launched by the last forward, wall time of the last call (e2_hip_stats). */
+int e2mi_stats(e2mi_engine *g, long *calls, long *kernels_last, double *last_ms);
+/* Run only the first n layers (0: all) before the final norm and pooling: the reference's
+ * E2_HIP_LAYERS bisection knob (forward.c:359-366), for parity checks layer by layer. */
+int e2mi_set_layer_limit(e2mi_engine *g, int n_layers);
 
 #ifdef __cplusplus
 }

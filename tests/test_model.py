@@ -1,0 +1,169 @@
+"""Model container: synthetic weights, tensor views, and the E8CQ packed cache format
+(q8cache.c v1) — round trip, cross-read with the reference's own writer/reader (oracle/_ref), and
+refusal of corrupted files (test_q8cache.c:113-248 style)."""
+import ctypes as C
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from model_util import NORMS, Q8, lname, small_config
+
+
+@pytest.fixture(scope="module")
+def e2mi_mod():
+    import e2mi
+    e2mi.load()
+    return e2mi
+
+
+@pytest.fixture(scope="module")
+def model(e2mi_mod):
+    return e2mi_mod.Model.synthetic(small_config(e2mi_mod), 1004)
+
+
+def test_baseline_config(e2mi_mod):
+    c = e2mi_mod.baseline_config()
+    assert (c.n_layers, c.hidden, c.ffn, c.n_heads, c.n_kv_heads, c.head_dim, c.vocab) == \
+        (24, 768, 1152, 3, 1, 256, 262144)
+    assert abs(c.embed_scale - np.sqrt(768)) < 1e-5 and c.attn_scale == 1.0 and c.rms_eps == np.float32(1e-6)
+
+
+def test_synthetic_is_deterministic_and_in_range(e2mi_mod, model, oracle):
+    m2 = e2mi_mod.Model.synthetic(small_config(e2mi_mod), 1004)
+    m3 = e2mi_mod.Model.synthetic(small_config(e2mi_mod), 1005)
+    wq, sc, bsq, N, K = model.tensor(lname(1, Q8[4]))
+    assert (N, K) == (1152, 768)
+    assert np.array_equal(wq, m2.tensor(lname(1, Q8[4]))[0])
+    assert not np.array_equal(wq, m3.tensor(lname(1, Q8[4]))[0])
+    w = oracle.q8w_unpack(wq, N, K)
+    assert w.min() >= -127 and w.max() <= 127 and abs(float(w.mean())) < 1
+    assert sc.min() >= 0.001 and sc.max() <= 0.02
+    # bsq is the per-128-block row sum (int8.c:57-61)
+    assert np.array_equal(bsq[:, :N], w.reshape(N, K // 128, 128).sum(-1).T.astype(np.int32))
+    g = model.tensor(lname(0, NORMS[0]))
+    assert g.shape == (768,) and abs(g.mean() - 1) < 0.02 and 0.03 < g.std() < 0.07
+    t = model.tensor("language_model.embed_tokens.weight")
+    assert t.shape == (1000, 768) and abs(t.std() - 0.02) < 0.001
+
+
+def test_e8cq_round_trip(e2mi_mod, model, tmp_path):
+    p = str(tmp_path / "m.e8cq")
+    model.save_e8cq(p)
+    m2 = e2mi_mod.Model.load_e8cq(p, small_config(e2mi_mod))
+    for l in range(2):
+        for s in Q8:
+            a, b = model.tensor(lname(l, s)), m2.tensor(lname(l, s))
+            assert all(np.array_equal(x, y) for x, y in zip(a[:3], b[:3]))
+        for s in NORMS:
+            assert np.array_equal(model.tensor(lname(l, s)), m2.tensor(lname(l, s)))
+    assert not [f for f in os.listdir(tmp_path) if ".tmp." in f]   # atomic commit leaves no temp
+
+
+def _ref_q8c(ref):
+    L = ref.lib
+    L.q8c_write_open.argtypes = [C.c_char_p]
+    L.q8c_put_q8w.argtypes = [C.c_char_p, C.c_void_p]
+    L.q8c_defer.argtypes = [C.c_char_p, C.c_int, C.c_int, C.POINTER(C.c_int64), C.c_void_p, C.c_size_t]
+    L.q8c_read_open.argtypes = [C.c_char_p]
+    L.q8c_get_q8w.argtypes = [C.c_char_p, C.c_void_p]
+    L.q8c_error.restype = C.c_char_p
+    return L
+
+
+def test_e8cq_cross_read_with_reference(e2mi_mod, model, ref, tmp_path):
+    from oracle.binding import Q8W
+    L = _ref_q8c(ref)
+    # ours -> the reference's validating reader (q8cache.c:242-385)
+    p1 = str(tmp_path / "ours.e8cq")
+    model.save_e8cq(p1)
+    assert L.q8c_read_open(p1.encode()) == 0, L.q8c_error()
+    try:
+        for l in range(2):
+            for s in Q8:
+                q = Q8W()
+                assert L.q8c_get_q8w(lname(l, s).encode(), C.byref(q)) == 0
+                wq, sc, bsq, N, K = model.tensor(lname(l, s))
+                assert (q.N, q.K, q.nblocks, q.Npad) == (N, K, K // 128, (N + 7) & ~7)
+                got = np.ctypeslib.as_array(C.cast(q.w, C.POINTER(C.c_int8)), (wq.size,))
+                assert np.array_equal(got, wq)
+                assert np.array_equal(np.ctypeslib.as_array(C.cast(q.scale, C.POINTER(C.c_float)), (N,)), sc)
+    finally:
+        L.q8c_read_close()
+    # the reference's writer (q8cache.c:61-222) -> our loader
+    p2 = str(tmp_path / "ref.e8cq")
+    assert L.q8c_write_open(p2.encode()) == 0
+    keep = []
+    for l in range(2):
+        for s in Q8:
+            wq, sc, bsq, N, K = model.tensor(lname(l, s))
+            keep += [wq, sc, bsq]
+            q = Q8W(wq.ctypes.data, bsq.ctypes.data, sc.ctypes.data, N, K, K // 128, (N + 7) & ~7,
+                    -1e31, 1e31, 0)
+            assert L.q8c_put_q8w(lname(l, s).encode(), C.byref(q)) == 0
+        for s in NORMS:
+            g = np.ascontiguousarray(model.tensor(lname(l, s)), np.float32)
+            keep.append(g)
+            dims = (C.c_int64 * 4)(g.size, 0, 0, 0)
+            assert L.q8c_defer(lname(l, s).encode(), 2, 1, dims, g.ctypes.data, g.nbytes) == 0
+    for name in ("language_model.embed_tokens.weight", "language_model.norm.weight"):
+        t = np.ascontiguousarray(model.tensor(name), np.float32)
+        keep.append(t)
+        dims = (C.c_int64 * 4)(*(list(t.shape) + [0] * (4 - t.ndim)))
+        assert L.q8c_defer(name.encode(), 2, t.ndim, dims, t.ctypes.data, t.nbytes) == 0
+    assert L.q8c_write_close() == 0
+    m2 = e2mi_mod.Model.load_e8cq(p2, small_config(e2mi_mod))
+    for l in range(2):
+        for s in Q8:
+            assert np.array_equal(model.tensor(lname(l, s))[0], m2.tensor(lname(l, s))[0])
+        for s in NORMS:
+            assert np.array_equal(model.tensor(lname(l, s)), m2.tensor(lname(l, s)))
+
+
+def _corrupt(src, dst, off, data):
+    b = bytearray(open(src, "rb").read())
+    b[off:off + len(data)] = data
+    open(dst, "wb").write(bytes(b))
+
+
+def test_e8cq_corruption_refused(e2mi_mod, model, tmp_path):
+    p = str(tmp_path / "good.e8cq")
+    model.save_e8cq(p)
+    raw = open(p, "rb").read()
+    magic, ver, n, io = struct.unpack_from("<4I", raw, 0)
+    first = io  # first index entry: name[96] kind ndim dims[4] nbytes off
+    kind_off, nb_off, off_off = first + 96, first + 136, first + 144
+    cases = {
+        "magic": (0, b"XXXX"),
+        "version": (4, struct.pack("<I", 2)),
+        "index misaligned": (12, struct.pack("<I", io + 4)),
+        "index past end": (12, struct.pack("<I", len(raw) + 16)),
+        "entry count": (8, struct.pack("<I", n + 10 ** 6)),
+        "unterminated name": (first, b"A" * 96),
+        "empty name": (first, b"\0"),
+        "kind": (kind_off, struct.pack("<I", 9)),
+        "blob misaligned": (off_off, struct.pack("<Q", struct.unpack_from("<Q", raw, off_off)[0] + 4)),
+        "blob outside": (off_off, struct.pack("<Q", io)),
+        "size mismatch": (nb_off, struct.pack("<Q", struct.unpack_from("<Q", raw, nb_off)[0] - 16)),
+        "truncated": None,
+    }
+    for name, mod in cases.items():
+        bad = str(tmp_path / f"bad_{name.replace(' ', '_')}.e8cq")
+        if mod is None:
+            open(bad, "wb").write(raw[: len(raw) // 2])
+        else:
+            _corrupt(p, bad, *mod)
+        with pytest.raises(e2mi_mod.E2MIError):
+            e2mi_mod.Model.load_e8cq(bad, small_config(e2mi_mod))
+    # a cache of another geometry is refused by shape
+    with pytest.raises(e2mi_mod.E2MIError, match="missing or mis-shaped"):
+        e2mi_mod.Model.load_e8cq(p, small_config(e2mi_mod, n_layers=3))
+    with pytest.raises(e2mi_mod.E2MIError, match="mis-shaped"):
+        e2mi_mod.Model.load_e8cq(p, small_config(e2mi_mod, vocab=999))
+
+
+def test_bad_configs_refused(e2mi_mod):
+    for over in (dict(head_dim=128), dict(hidden=700), dict(n_heads=3, n_kv_heads=2), dict(max_seq=4096)):
+        with pytest.raises(e2mi_mod.E2MIError):
+            e2mi_mod.Model.synthetic(e2mi_mod.baseline_config(n_layers=1, vocab=10, **over), 1)
