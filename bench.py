@@ -180,6 +180,76 @@ def cpu_baseline(budget_s=12.0):
     }
 
 
+# ------------------------------------------------------------------ encoder (config 4)
+ENC_B, ENC_S = 64, 512
+
+
+def encoder_bench(torch, e2mi, steps, warmup, cpu_sample=4):
+    """the 24-layer encoder (d=768, FFN 1152, 3q/1kv heads of 256) with
+    random-init int8 weights, token ids uniform over the 262144 vocabulary, f32 table ~N(0,0.02)
+    scaled by sqrt(768), batch 64 x seq 512 with random lengths in [64, 512], mean pooling, L2.
+    Ids, mask and output stay in HBM (e2mi_text_embed_batch_device)."""
+    cfg = e2mi.baseline_config()
+    t0 = time.perf_counter()
+    model = e2mi.Model.synthetic(cfg, 1004)
+    t_model = time.perf_counter() - t0
+    eng = e2mi.Engine(model, max_rows=ENC_B * ENC_S)
+    rng = np.random.default_rng(1004)
+    ids = rng.integers(0, cfg.vocab, (ENC_B, ENC_S)).astype(np.int32)
+    lens = rng.integers(64, ENC_S + 1, ENC_B)
+    valid = (np.arange(ENC_S)[None, :] < lens[:, None]).astype(np.uint8)
+    dev = torch.device("cuda:0")
+    ids_d, valid_d = torch.from_numpy(ids).to(dev), torch.from_numpy(valid).to(dev)
+    out = torch.empty((ENC_B, cfg.hidden), device=dev)
+    stream = torch.cuda.current_stream()
+    for _ in range(max(2, warmup)):  # the first call records the shape's graph
+        eng.embed_batch_device(ids_d, valid_d, out, stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.embed_batch_device(ids_d, valid_d, out, stream)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    # the host-buffer entry point (PCIe-inclusive), for reference
+    h_t = []
+    for _ in range(3):
+        t1 = time.perf_counter()
+        host_out = eng.embed_batch(ids, valid)
+        h_t.append(time.perf_counter() - t1)
+    o = out.cpu().numpy()
+    res = {
+        "embeddings_per_s": round(ENC_B / dt, 2),
+        "ms_per_batch": round(dt * 1e3, 3),
+        "tokens_per_s_valid": round(float(valid.sum()) / dt, 1),
+        "host_buffers_embeddings_per_s": round(ENC_B / min(h_t), 2),
+        "unit_norm_ok": bool(np.allclose(np.linalg.norm(o, axis=1), 1, atol=1e-4)),
+        "host_matches_device": bool(np.array_equal(host_out, o)),
+        "config": f"24 layers, B={ENC_B}, S={ENC_S}, lengths U[64,512] (mean {lens.mean():.0f}), vocab {cfg.vocab}",
+        "model_build_s": round(t_model, 2),
+        "kernels_per_forward": eng.stats()[1],
+    }
+    res["_model"] = model
+    res["_batch"] = (ids, valid)
+    return res
+
+
+def encoder_cpu_baseline(model, ids, valid, nseq=4):
+    """The oracle's text recipe (oracle/e2_oracle_model.c, a C port: VNNI int8 GEMMs, fp32 row-wise
+    attention) on the host cores, over the first nseq sequences of the benchmark batch."""
+    sys.path.insert(0, ROOT)
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle.binding import Oracle
+    from model_util import oracle_model
+    threads = physical_cores()
+    om = oracle_model(Oracle(), model)
+    t0 = time.perf_counter()
+    om.encode(np.ascontiguousarray(ids[:nseq]), np.ascontiguousarray(valid[:nseq]), nthreads=threads)
+    dt = time.perf_counter() - t0
+    return {"value": round(nseq / dt, 4), "unit": "embeddings/s", "cores": threads, "kind": "port",
+            "sample": f"{nseq} of the {ENC_B} benchmark sequences (lengths {valid[:nseq].sum(1).tolist()}), "
+                      f"24 layers, {dt:.1f} s"}
+
+
 # ------------------------------------------------------------------ HBM traffic from PMC runs
 COPY_BYTES = 256 << 20
 
@@ -224,6 +294,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-encoder", action="store_true", help="skip the config-4 encoder leg")
+    ap.add_argument("--encoder-only", action="store_true",
+                    help="only the config-4 encoder leg (for profiling; prints its own line)")
     ap.add_argument("--probe", action="store_true",
                     help="one calibration copy + one launch per GEMM (for rocprofv3 --pmc runs)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -242,6 +315,11 @@ def main():
     import torch
     import e2mi
     e2mi.load()
+    if args.encoder_only:
+        enc = encoder_bench(torch, e2mi, args.steps, args.warmup)
+        enc.pop("_model"), enc.pop("_batch")
+        print(json.dumps({"encoder": enc}))
+        return
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(1005)
@@ -357,6 +435,14 @@ def main():
                      "algorithmic_bytes": algo_bytes, "ops": ops[dom],
                      "note": "int8 ops counted as TFLOP/s; bound by the algorithmic roofline max(t_mfma, t_hbm)"},
     }
+    if not args.no_encoder:
+        enc = encoder_bench(torch, e2mi, max(5, args.steps // 2), args.warmup)
+        model, (eids, evalid) = enc.pop("_model"), enc.pop("_batch")
+        out["encoder"] = enc
+        out["embeddings_per_s"] = enc["embeddings_per_s"]
+        if not args.no_cpu_baseline:
+            out["encoder_cpu_baseline"] = encoder_cpu_baseline(model, eids, evalid)
+        del model
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))

@@ -55,6 +55,17 @@ __device__ inline int qbyte(float x, float inv) {
     r = fminf(fmaxf(r, -128.f), 127.f);
     return (int)r;
 }
+// q = rne(x * inv) via the 1.5*2^23 trick: x*inv is rounded to f32 first (as the reference's
+// mulps does), then adding 12582912 rounds it to an integer with ties to even; |x*inv| <= 127.00002
+// for |x| <= amax, so the integer lands in [-127, 127] and is the low byte of the sum's bits.
+__device__ inline uint32_t qbits(float x, float inv) {
+    return __builtin_bit_cast(uint32_t, __fadd_rn(__fmul_rn(x, inv), 12582912.0f));
+}
+__device__ inline uint32_t pack4_magic(float a, float b, float c, float d, float inv) {
+    const uint32_t lo = __builtin_amdgcn_perm(qbits(b, inv), qbits(a, inv), 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(qbits(d, inv), qbits(c, inv), 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
 __device__ inline uint32_t pack4(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
            ((uint32_t)(d & 0xff) << 24);

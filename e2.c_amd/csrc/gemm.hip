@@ -15,6 +15,9 @@
 // with a 144-byte row pitch (16 B of padding: the ds_read_b128 fragment loads of 16 consecutive
 // lanes then hit 16 distinct 4-bank groups), double-buffered so the next step's global loads are in
 // flight while the MFMAs run. Each wave owns a WM x WN sub-tile of 32x32 MFMA tiles.
+#include <stdlib.h>
+#include <string.h>
+
 #include "common.h"
 
 namespace e2mi {
@@ -37,9 +40,13 @@ struct GemmArgs {
 };
 
 
+// GELU-tanh through the identity 0.5 v (1 + tanh z) = v / (1 + e^(-2z)): one v_exp_f32 and one
+// reciprocal instead of the library tanhf, with no cancellation for negative v (1 + tanh z is never
+// formed); e^(-2z) -> inf gives exactly 0 and -> 0 gives v
 __device__ inline float gelu_tanh(float v) {
     const float c = 0.7978845608028654f;
-    return 0.5f * v * (1.f + tanhf(c * (v + 0.044715f * v * v * v)));
+    const float z = c * (v + 0.044715f * v * v * v);
+    return __fdividef(v, 1.f + __expf(-2.f * z));
 }
 
 // LDS tiles hold 128-byte K slices of consecutive rows with no padding; the 16-byte chunk c of row
@@ -50,7 +57,7 @@ __device__ inline int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4);
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP>
+template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP, bool FAST>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 128 * 128) ? 1 : 2) void k_gemm(GemmArgs p) {
     constexpr int NWN = BN / WN, NWAVE = (BM / WM) * NWN, NT = NWAVE * 64;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -131,40 +138,46 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 12
         if (kb + NS - 1 < nb) issue(kb + NS - 1, (kb + NS - 1) % NS);
         const int cur = kb % NS;
         const unsigned char *sb0 = smem + cur * STAGE;
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const int cc = kk * 2 + (lane >> 5);
-            v4i af[TM], bf[TN];
-#pragma unroll
-            for (int tm = 0; tm < TM; tm++)
-                af[tm] = *(const v4i *)(sb0 + swz(wm * WM + tm * 32 + (lane & 31), cc));
-#pragma unroll
-            for (int tn = 0; tn < TN; tn++)
-                bf[tn] = *(const v4i *)(sb0 + BM * 128 + swz(wn * WN + tn * 32 + (lane & 31), cc));
-#pragma unroll
-            for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-                for (int tn = 0; tn < TN; tn++)
-                    acc[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                        af[tm], bf[tn], kk == 0 ? zero : acc[tm][tn], 0, 0, 0);
-        }
-        // fold this block: f = fma((float)acc, RN(as*ws), f), the reference's order
         const float *asb = (const float *)(sb0 + (BM + BN) * 128) + wm * WM + (lane >> 5) * 4;
+        {
 #pragma unroll
-        for (int tm = 0; tm < TM; tm++)
+            for (int kk = 0; kk < 4; kk++) {
+                const int cc = kk * 2 + (lane >> 5);
+                v4i af[TM], bf[TN];
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const float4 a4 = *(const float4 *)(asb + tm * 32 + g * 8);
-                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+                for (int tm = 0; tm < TM; tm++)
+                    af[tm] = *(const v4i *)(sb0 + swz(wm * WM + tm * 32 + (lane & 31), cc));
 #pragma unroll
                 for (int tn = 0; tn < TN; tn++)
+                    bf[tn] = *(const v4i *)(sb0 + BM * 128 + swz(wn * WN + tn * 32 + (lane & 31), cc));
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int r = g * 4 + j;
-                        f[tm][tn][r] = __builtin_fmaf((float)acc[tm][tn][r], __fmul_rn(av[j], wsr[tn]),
-                                                      f[tm][tn][r]);
-                    }
+                for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+                    for (int tn = 0; tn < TN; tn++)
+                        acc[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                            af[tm], bf[tn], kk == 0 ? zero : acc[tm][tn], 0, 0, 0);
             }
+            // fold this block: f = fma((float)acc, RN(as*ws), f), the reference's order
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 a4 = *(const float4 *)(asb + tm * 32 + g * 8);
+                    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+                    for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int r = g * 4 + j;
+                            // FAST folds only the activation scale per block and applies ws[n] once
+                            // at the end (2 VALU ops per element and block instead of 3; f32 result
+                            // within a few ulp of the reference's order instead of bit-exact)
+                            f[tm][tn][r] = __builtin_fmaf((float)acc[tm][tn][r],
+                                                          FAST ? av[j] : __fmul_rn(av[j], wsr[tn]),
+                                                          f[tm][tn][r]);
+                        }
+                }
+        }
         if constexpr (DUMP) {
 #pragma unroll
             for (int tm = 0; tm < TM; tm++)
@@ -181,23 +194,33 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 12
     }
     __syncthreads();  // the epilogue may reuse the staging buffers
 
+    // bias / saturation are per-launch uniform: skip their VALU work when neither is set
+    const bool post = p.bias != nullptr || p.lo > -1e30f || p.hi < 1e30f;
     if constexpr (EPI == EPI_F32) {
+        // buffer stores: the lane's byte offset is computed once, every (tile, register) row step
+        // is a wave-uniform SGPR offset; rows past M fall outside the descriptor's range and are
+        // dropped by the hardware, columns past N are masked per lane
+        const __amdgpu_buffer_rsrc_t ry =
+            __builtin_amdgcn_make_buffer_rsrc(p.Y, 0, (int)min((long)p.M * p.ldy * 4, 0x7fffffffL), 0x00020000);
+        const int vrow = wm * WM + (lane >> 5) * 4, vcol = wn * WN + (lane & 31);
+        const int voff = ((m0 + vrow) * p.ldy + n0 + vcol) * 4;
 #pragma unroll
         for (int tn = 0; tn < TN; tn++) {
-            const int n = n0 + wn * WN + tn * 32 + (lane & 31);
+            const int n = n0 + vcol + tn * 32;
             if (n >= p.N) continue;
             const float b = p.bias ? p.bias[n] : 0.f;
 #pragma unroll
             for (int tm = 0; tm < TM; tm++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int m = m0 + wm * WM + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                    if (m < p.M) {
-                        float v = f[tm][tn][r];
+                    float v = FAST ? __fmul_rn(f[tm][tn][r], wsr[tn]) : f[tm][tn][r];
+                    if (post) {
                         if (p.bias) v = v + b;
                         v = fminf(fmaxf(v, p.lo), p.hi);
-                        p.Y[(size_t)m * p.ldy + n] = v;
                     }
+                    const int srow = __builtin_amdgcn_readfirstlane((tm * 32 + (r >> 2) * 8 + (r & 3)) * p.ldy * 4);
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
+                                                          voff + tn * 128, srow, 0);
                 }
         }
     } else {
@@ -206,19 +229,23 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 12
         constexpr int FP = BN + 4;  // f32 row pitch
         static_assert(BM * FP * 4 <= NS * STAGE, "epilogue tile does not fit");
         float *sf = (float *)smem;
+        {
+            float *sl = sf + (wm * WM + (lane >> 5) * 4) * FP + wn * WN + (lane & 31);
 #pragma unroll
-        for (int tn = 0; tn < TN; tn++) {
-            const int nl = wn * WN + tn * 32 + (lane & 31);
-            const float b = p.bias ? p.bias[min(n0 + nl, p.N - 1)] : 0.f;
+            for (int tn = 0; tn < TN; tn++) {
+                const float b = p.bias ? p.bias[min(n0 + wn * WN + tn * 32 + (lane & 31), p.N - 1)] : 0.f;
 #pragma unroll
-            for (int tm = 0; tm < TM; tm++)
+                for (int tm = 0; tm < TM; tm++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int ml = wm * WM + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                    float v = f[tm][tn][r];
-                    if (p.bias) v = v + b;
-                    sf[ml * FP + nl] = fminf(fmaxf(v, p.lo), p.hi);
-                }
+                    for (int r = 0; r < 16; r++) {
+                        float v = FAST ? __fmul_rn(f[tm][tn][r], wsr[tn]) : f[tm][tn][r];
+                        if (post) {
+                            if (p.bias) v = v + b;
+                            v = fminf(fmaxf(v, p.lo), p.hi);
+                        }
+                        sl[(tm * 32 + (r >> 2) * 8 + (r & 3)) * FP + tn * 32] = v;
+                    }
+            }
         }
         __syncthreads();
         // output columns per tile and per thread: I8Q keeps BN columns, GEGLU halves them
@@ -232,16 +259,26 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 12
         for (int rr = 0; rr < BM; rr += RPP) {
             const int ml = rr + t_r, m = m0 + ml;
             float v[16];
+            if constexpr (EPI == EPI_GEGLU) {
+                // W rows are interleaved per 256: [128 gate | 128 up] for each output block
+                const int blk = (t_c * 16) >> 7, w = (t_c * 16) & 127;
+                const float *gp = sf + ml * FP + blk * 256 + w;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int oc = t_c * 16 + i;  // output column within the tile
-                if constexpr (EPI == EPI_GEGLU) {
-                    // W rows are interleaved per 256: [128 gate | 128 up] for output block oc/128
-                    const int blk = oc >> 7, w = oc & 127;
-                    const float g = sf[ml * FP + blk * 256 + w], u = sf[ml * FP + blk * 256 + 128 + w];
-                    v[i] = gelu_tanh(g) * u;
-                } else {
-                    v[i] = sf[ml * FP + oc];
+                for (int i = 0; i < 16; i += 4) {
+                    const float4 g = *(const float4 *)(gp + i), u = *(const float4 *)(gp + 128 + i);
+                    v[i] = gelu_tanh(g.x) * u.x;
+                    v[i + 1] = gelu_tanh(g.y) * u.y;
+                    v[i + 2] = gelu_tanh(g.z) * u.z;
+                    v[i + 3] = gelu_tanh(g.w) * u.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i += 4) {
+                    const float4 x = *(const float4 *)(sf + ml * FP + t_c * 16 + i);
+                    v[i] = x.x;
+                    v[i + 1] = x.y;
+                    v[i + 2] = x.z;
+                    v[i + 3] = x.w;
                 }
             }
             float a = 0.f;
@@ -254,8 +291,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 12
                 uint32_t w4[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    w4[i] = pack4(qbyte(v[4 * i], s.inv), qbyte(v[4 * i + 1], s.inv),
-                                  qbyte(v[4 * i + 2], s.inv), qbyte(v[4 * i + 3], s.inv));
+                    w4[i] = pack4_magic(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3], s.inv);
                 *(uint4 *)(p.Yq + (size_t)m * p.ldyq + oc) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
                 if ((t_c & 7) == 0) p.ys[(size_t)m * p.ldys + (oc >> 7)] = s.sc;
                 if (EPI == EPI_GEGLU && p.Y) {
@@ -269,13 +305,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 12
     }
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP>
-static int launch_tile(hipStream_t s, const GemmArgs &p) {
+template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP, bool FAST>
+static int launch_tile1(hipStream_t s, const GemmArgs &p) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
     constexpr int NWAVE = (BM / WM) * (BN / WN);
     constexpr size_t lds = NS * ((size_t)(BM + BN) * 128 + 64 * NWAVE * 4);
     static_assert(NS >= 2 && NS <= 4 && lds <= 160 * 1024, "LDS budget");
-    auto kern = k_gemm<BM, BN, WM, WN, NS, EPI, DUMP>;
+    auto kern = k_gemm<BM, BN, WM, WN, NS, EPI, DUMP, FAST>;
     static bool attr = false;
     if (!attr) {
         if (check_hip(hipFuncSetAttribute((const void *)kern,
@@ -287,6 +323,23 @@ static int launch_tile(hipStream_t s, const GemmArgs &p) {
     const long tiles = (long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NT), lds, s, p);
     return check_hip(hipGetLastError(), "gemm launch");
+}
+
+// E2MI_GEMM_FOLD=fast selects the 2-op fold for the whole process (read once); the default is
+// the reference's bit-exact fold order
+static bool fold_fast() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("E2MI_GEMM_FOLD");
+        v = (e && strcmp(e, "fast") == 0) ? 1 : 0;
+    }
+    return v == 1;
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP>
+static int launch_tile(hipStream_t s, const GemmArgs &p) {
+    if (!DUMP && fold_fast()) return launch_tile1<BM, BN, WM, WN, NS, EPI, DUMP, true>(s, p);
+    return launch_tile1<BM, BN, WM, WN, NS, EPI, DUMP, false>(s, p);
 }
 
 static int check_args(const GemmArgs &p, const char *who) {
@@ -301,7 +354,7 @@ static int check_args(const GemmArgs &p, const char *who) {
         return -1;
     }
     if ((long)p.M * (long)p.N > (1L << 31) || (long)p.M * p.lda >= (1L << 32) ||
-        (long)p.N * p.ldw >= (1L << 32)) {
+        (long)p.N * p.ldw >= (1L << 32) || (long)p.M * p.ldy * 4 >= (1L << 31)) {
         set_error("%s: problem too large", who);
         return -1;
     }

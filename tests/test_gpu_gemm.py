@@ -142,7 +142,9 @@ def test_gemm_geglu_epilogue(gpu, oracle, rng, M):
     up = oracle.i8_gemm(qa, as_, wu, su)
     go, qo, so = oracle.gelu_mul_quant(gate, up)
     g = _np(g)
-    assert_f32_close(g, go, rtol=1e-4, atol=1e-6, what="gelu*up")
+    # the reference's own bar for this stage: |got - want| / (1 + |want|) < 1e-4 (test_gpu_ffn.c:104);
+    # for very negative gate values both reference formulas cancel in 1 + tanh, the kernel does not
+    assert_f32_close(g, go, rtol=1e-4, atol=1e-4, what="gelu*up")
     # bytes: exact for the kernel's own f32 values; within one step of the oracle's only where the
     # scaled value sits at a rounding boundary (test_gpu_ffn.c:114-120 rule)
     qg, sgk = oracle.quantize(g)
