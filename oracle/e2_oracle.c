@@ -9,7 +9,7 @@
  *
  * Parity status (how each function is pinned; the tests named are under tests/):
  *   or_q8w_from_f32/pack/unpack  — bit-exact vs oracle/_ref e2_q8w_from_f32 + layout closed form
- *                                   (test_oracle_ref.py), golden vectors (test_oracle_golden.py)
+ *                                   (test_oracle_ref.py), golden vectors (test_golden.py)
  *   or_quantize                  — bit-exact vs _ref e2_quantize_blocks_avx512 and _scalar on random,
  *                                   outlier, zero and tie-breaking rows; golden vectors
  *   or_i8_gemm / _acc / _mt      — int32: brute-force integer dot (order independent); f32: bit-exact
@@ -22,10 +22,13 @@
  *                                   table builder (text.c rope_init is static): table pinned by
  *                                   the formula test
  *   or_softmax / or_attention    — softmax within 3e-7 of double (test_softmax.c:33); attention vs
- *                                   a float64 brute force (test_oracle_attention.py)
+ *                                   a float64 brute force (test_oracle_math.py)
  *   or_meanpool / or_l2norm      — within 1e-6 of _ref e2_meanpool_f32 / e2_l2norm_f32
  *   or_embed                     — closed form
- *   text recipe (e2_oracle_model.c) — composed of the above; layer order restated from text.c:939-984
+ *   text recipe (e2_oracle_model.c) — layer order restated from text.c:817-984, pinned by special
+ *                                   cases: zero-weight layer = identity, W_q = W_k = 0 gives the
+ *                                   closed-form uniform attention, padding/batch independence and
+ *                                   the no-layer closed form (test_oracle_recipe.py)
  */
 #define _GNU_SOURCE
 #include "e2_oracle.h"
