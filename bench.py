@@ -281,6 +281,16 @@ def summarize_pmc(fetch_csv, write_csv):
         d["hbm_bytes"] = d.get("fetch_bytes", 0) + d.get("write_bytes", 0)
     res = {k: round(v["hbm_bytes"]) for k, v in out.items()}
     res["detail"] = out
+    res["commands"] = [
+        "timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch "
+        "-o f -- python3 bench.py --probe",
+        "timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write "
+        "-o w -- python3 bench.py --probe",
+        "python3 bench.py --summarize-pmc gpurun_out/pmc_fetch/f_counter_collection.csv "
+        "gpurun_out/pmc_write/w_counter_collection.csv",
+    ]
+    res["calibration"] = (f"a plain {COPY_BYTES >> 20} MiB device copy in the same run: bytes / "
+                          "counter reading gives the per-counter scale")
     os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
     with open(os.path.join(ROOT, "profiles", "gemm_q_traffic.json"), "w") as f:
         json.dump(res, f, indent=1)
