@@ -72,6 +72,34 @@ __device__ inline void lds_load4(__amdgpu_buffer_rsrc_t r, void *lds, uint32_t v
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, voff, soff, 0, 0);
 }
 
+// The same direct-to-LDS loads as inline assembly, for the pipelined kernel. The compiler's
+// wait-count pass cannot tell which LDS bytes a builtin direct-to-LDS load writes, so after one it
+// waits for all of them (s_waitcnt vmcnt(0)) before the next LDS read, draining a multi-stage load
+// pipeline every K step. Loads issued here are invisible to that pass: the kernel orders them
+// itself (explicit vmcnt waits + barriers), and issues no other vector-memory load the compiler
+// would wait for inside the loop. M0 carries the LDS destination (no other code in the kernel uses
+// M0); one wait state separates its write from the load.
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+__device__ inline v4u rsrc_words(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    v4u r;
+    r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
+    r.z = __builtin_amdgcn_readfirstlane(bytes);
+    r.w = 0x00020000u;
+    return r;
+}
+__device__ inline void dma16(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory");
+}
+__device__ inline void dma4(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                 ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory");
+}
+
 // The fused epilogues over a finished BM x BN tile: f holds each wave's WM x WN f32 results in the
 // MFMA C layout (lane column lane % 32, rows 8 (r / 4) + 4 (lane / 32) + r % 4 of each 32x32 tile).
 // POST: bit 0 adds the bias, bit 1 clamps to [lo, hi] (compile-time, so the common case of
@@ -346,180 +374,440 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 12
     store_tile<BM, BN, WM, WN, NS * STAGE, EPI, FAST>(p, f, wsr, m0, n0, wm, wn, tid, smem);
 }
 
-// LDS of the double-buffered kernel: NS stages of A|W, NS+1 scale slots, and at least the f32
-// tile the requantizing epilogues stage (row pitch BN+4 floats)
-constexpr int db_lds_bytes(int BM, int BN, int NWAVE, int NS, int EPI) {
-    const int loop = NS * (BM + BN) * 128 + (NS + 1) * 64 * NWAVE * 4;
-    const int epi = EPI == EPI_F32 ? 0 : BM * (BN + 4) * 4;
-    return loop > epi ? loop : epi;
+// fold order of all GEMM launches (e2mi_gemm_set_fold); E2MI_GEMM_FOLD=fast sets the fast one
+// at the first launch
+static int g_fold = -1;
+static bool fold_fast() {
+    if (g_fold < 0) {
+        const char *e = getenv("E2MI_GEMM_FOLD");
+        g_fold = (e && strcmp(e, "fast") == 0) ? 1 : 0;
+    }
+    return g_fold == 1;
 }
 
-// Kernel with double-buffered int32 accumulators: the MFMAs of K step kb accumulate into one set
-// while the other set, holding step kb-1, is folded into f on the VALU, one 32x32 tile after each
-// of the 4 MFMA rounds. The fold of a step therefore overlaps the next step's MFMAs instead of
-// waiting for them (the fold costs as many VALU cycles per element as the MFMAs take). The loads
-// run NS-1 steps ahead; the activation scales of a step live in a ring of NS+1 slots so the fold
-// of step kb-1 can still read them while step kb+NS-1 is being loaded.
-template <int BM, int BN, int WM, int WN, int NS, int EPI, bool FAST, int OCC>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_db(GemmArgs p) {
-    constexpr int NWN = BN / WN, NWAVE = (BM / WM) * NWN;
-    constexpr int TM = WM / 32, TN = WN / 32, NTILE = TM * TN;
-    constexpr int TPK = (NTILE + 3) / 4;                      // tiles folded per MFMA round
-    constexpr int AI = BM / 8 / NWAVE, BI = BN / 8 / NWAVE;  // 1-KB loads per wave per step
-    static_assert(AI * NWAVE * 8 == BM && BI * NWAVE * 8 == BN, "tile/threads mismatch");
-    static_assert(BM <= 64 * NWAVE, "one scale per lane");
-    constexpr int TILE = (BM + BN) * 128;  // A | W of one step
-    constexpr int SSLOT = 64 * NWAVE * 4;  // one step's activation scales (one per lane)
-    constexpr int RS = NS + 1;
-    extern __shared__ __align__(16) unsigned char smem[];
-    unsigned char *const sscale = smem + NS * TILE;
+// ---------------------------------------------------------------------------------------------
+// Persistent pipelined kernel (the production path). One 512-thread workgroup per CU walks a list
+// of BM x BN output tiles; the 128-deep K steps of consecutive tiles form one flat pipeline:
+//   - A, W and the step's activation scales go HBM/L2 -> LDS by direct buffer loads two steps
+//     ahead (3 A|W stages, a ring of 4 scale slots);
+//   - 8 waves of 64x64 each; the int32 accumulators are double-buffered: the MFMAs of step g
+//     accumulate into one set while the other set (step g-1) is folded into f on the VALU, the
+//     fold cut into 4-element units spread evenly between the step's 16 MFMAs
+//     (sched_group_barrier), since the fold costs about as many VALU cycles as the MFMAs take;
+//   - a tile's last step is folded during the next tile's first step, then the tile's epilogue
+//     runs; requantizing epilogues stage f through the one A|W stage free at that point, in 4
+//     chunks of rows.
+// The tile list (M-major) is cut into one contiguous chunk per XCD (workgroups are dispatched
+// round-robin over the 8 XCDs), so the N tiles of an M block run on one XCD and share its L2.
+constexpr int kPStages = 3, kPSlots = 4;
 
-    const int tiles_n = (p.N + BN - 1) / BN;
-    const int pid = xcd_swizzle(blockIdx.x, gridDim.x);
-    const int m0 = (pid / tiles_n) * BM, n0 = (pid % tiles_n) * BN;
+// a slot holds one step's activation scales and its tile's weight scales, one float per lane each
+template <int BM, int BN, int NWAVE>
+constexpr int p_lds_bytes() {
+    return kPStages * (BM + BN) * 128 + kPSlots * 2 * 64 * NWAVE * 4;
+}
+
+// requantizing epilogue of one tile through LDS scratch `scr` (>= NWM*16 rows x (BN+4) floats):
+// chunk c holds accumulator registers 4c..4c+3 of every wave, i.e. rows 8c..8c+7 of each 32-row
+// tile; every thread then owns CPT consecutive output columns of one row
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
+__device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArgs &p, float (&f)[2][2][16], const float (&wsr)[2],
+                                    int m0, int n0, int wm, int wn, int tid, float *scr) {
+    constexpr int NT = NWM * NWN * 64;
+    constexpr int CR = NWM * 16;  // rows per chunk
+    constexpr int FP = BN + 4;    // f32 row pitch in LDS
+    constexpr int OUTC = (EPI == EPI_GEGLU) ? BN / 2 : BN;
+    constexpr int CPT = OUTC * CR / NT;  // output columns per thread
+    constexpr int TPR = OUTC / CPT;      // threads per row
+    constexpr int TPB = 128 / CPT;       // threads per 128-column quantization block
+    static_assert(CPT % 4 == 0 && CPT >= 4 && TPB <= 64 && OUTC % 128 == 0, "epilogue geometry");
+    const int lane = tid & 63;
+    float b[2] = {0.f, 0.f};
+    if constexpr (POST & 1) {
+        if (p.bias) {
+#pragma unroll
+            for (int tn = 0; tn < 2; tn++) b[tn] = p.bias[min(n0 + wn * 64 + tn * 32 + (lane & 31), p.N - 1)];
+        }
+    }
+    const int oc0 = (EPI == EPI_GEGLU) ? n0 / 2 : n0;
+    const int ldo = (EPI == EPI_GEGLU) ? p.N / 2 : p.N;
+    const int t_r = tid / TPR, t_c = tid % TPR;
+    // the chunk-local row t_r -> tile row: t_r = wm*16 + tm*8 + h*4 + j -> wm*64 + tm*32 + 8c + h*4 + j
+    const int rbase = (t_r >> 4) * 64 + ((t_r >> 3) & 1) * 32 + (t_r & 7);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        {
+            float *sl = scr + (wm * 16 + (lane >> 5) * 4) * FP + wn * 64 + (lane & 31);
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                for (int tn = 0; tn < 2; tn++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        float v = f[tm][tn][4 * c + j];
+                        if constexpr (FAST) v = __fmul_rn(v, wsr[tn]);
+                        if constexpr (POST & 1) v = v + b[tn];
+                        if constexpr (POST & 2) v = fminf(fmaxf(v, p.lo), p.hi);
+                        sl[(tm * 8 + j) * FP + tn * 32] = v;
+                    }
+        }
+        __syncthreads();
+        const int m = m0 + rbase + 8 * c;
+        float v[CPT];
+        if constexpr (EPI == EPI_GEGLU) {
+            // W rows are interleaved per 256: [128 gate | 128 up] for each output block
+            const int blk = (t_c * CPT) >> 7, w = (t_c * CPT) & 127;
+            const float *gp = scr + t_r * FP + blk * 256 + w;
+#pragma unroll
+            for (int i = 0; i < CPT; i += 4) {
+                const float4 g = *(const float4 *)(gp + i), u = *(const float4 *)(gp + 128 + i);
+                v[i] = gelu_tanh(g.x) * u.x;
+                v[i + 1] = gelu_tanh(g.y) * u.y;
+                v[i + 2] = gelu_tanh(g.z) * u.z;
+                v[i + 3] = gelu_tanh(g.w) * u.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPT; i += 4) {
+                const float4 x = *(const float4 *)(scr + t_r * FP + t_c * CPT + i);
+                v[i] = x.x;
+                v[i + 1] = x.y;
+                v[i + 2] = x.z;
+                v[i + 3] = x.w;
+            }
+        }
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < CPT; i++) a = fmaxf(a, fabsf(v[i]));
+        a = group_max<TPB>(a);
+        const QScale s = qscale(a);
+        const int oc = oc0 + t_c * CPT;
+        if (m < p.M && oc < ldo) {
+            uint32_t w4[CPT / 4];
+#pragma unroll
+            for (int i = 0; i < CPT / 4; i++)
+                w4[i] = pack4_magic(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3], s.inv);
+            int8_t *dst = p.Yq + (size_t)m * p.ldyq + oc;
+            if constexpr (CPT == 16) *(uint4 *)dst = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+            else if constexpr (CPT == 8) *(uint2 *)dst = make_uint2(w4[0], w4[1]);
+            else *(uint32_t *)dst = w4[0];
+            if (t_c % TPB == 0) p.ys[(size_t)m * p.ldys + (oc >> 7)] = s.sc;
+            if (EPI == EPI_GEGLU && p.Y) {
+#pragma unroll
+                for (int i = 0; i < CPT; i += 4)
+                    *(float4 *)(p.Y + (size_t)m * p.ldy + oc + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// f32 epilogue straight from the accumulator registers: buffer stores whose row step is a scalar
+// offset; rows past M fall outside the descriptor's range and are dropped, columns past N masked
+template <int POST, bool FAST>
+__device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmArgs &p, float (&f)[2][2][16], const float (&wsr)[2],
+                                      int m0, int n0, int wm, int wn, int lane) {
+    const __amdgpu_buffer_rsrc_t ry =
+        __builtin_amdgcn_make_buffer_rsrc(p.Y, 0, (int)min((long)p.M * p.ldy * 4, 0x7fffffffL), 0x00020000);
+    const int vrow = wm * 64 + (lane >> 5) * 4, vcol = wn * 64 + (lane & 31);
+    const int voff = ((m0 + vrow) * p.ldy + n0 + vcol) * 4;
+#pragma unroll
+    for (int tn = 0; tn < 2; tn++) {
+        const int n = n0 + vcol + tn * 32;
+        if (n >= p.N) continue;
+        const float b = ((POST & 1) && p.bias) ? p.bias[n] : 0.f;
+#pragma unroll
+        for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float v = f[tm][tn][r];
+                if constexpr (FAST) v = __fmul_rn(v, wsr[tn]);
+                if constexpr (POST & 1) v = v + b;
+                if constexpr (POST & 2) v = fminf(fmaxf(v, p.lo), p.hi);
+                const int srow = __builtin_amdgcn_readfirstlane((tm * 32 + (r >> 2) * 8 + (r & 3)) * p.ldy * 4);
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry, voff + tn * 128, srow, 0);
+            }
+    }
+}
+
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
+__global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int tiles_n, int tiles) {
+    constexpr int NWAVE = NWM * NWN;
+    static_assert(BM == 64 * NWM && BN == 64 * NWN && NWAVE == 8, "8 waves of 64x64");
+    constexpr int AI = BM / 8 / NWAVE, BI = BN / 8 / NWAVE;  // 1-KB loads per wave per step
+    constexpr int L = AI + BI + 2;                           // loads per wave per step
+    constexpr int TILE = (BM + BN) * 128;                    // A | W of one step
+    constexpr int SHALF = 64 * NWAVE * 4;                    // as of one step (one per lane)
+    constexpr int SSLOT = 2 * SHALF;                         // as | ws
+    constexpr bool XACT = !FAST;
+    extern __shared__ __align__(16) unsigned char smem[];
+    unsigned char *const sscale = smem + kPStages * TILE;
+
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / NWN, wn = wave % NWN;
     const int nb = p.K / kQBlock;
 
-    uint32_t oa[AI], ob[BI];
-#pragma unroll
-    for (int i = 0; i < AI; i++) {
-        const int r = (i * NWAVE + wave) * 8 + (lane >> 3);
-        oa[i] = (uint32_t)min(m0 + r, p.M - 1) * (uint32_t)p.lda + (((lane & 7) ^ swzk(r)) << 4);
-    }
-#pragma unroll
-    for (int i = 0; i < BI; i++) {
-        const int r = (i * NWAVE + wave) * 8 + (lane >> 3);
-        ob[i] = (uint32_t)min(n0 + r, p.N - 1) * (uint32_t)p.ldw + (((lane & 7) ^ swzk(r)) << 4);
-    }
-    const uint32_t os = (uint32_t)min(m0 + wave * 64 + lane, p.M - 1) * (uint32_t)nb * 4;
-    // buffer descriptors: per-lane offsets stay in VGPRs, the K step's offset is a scalar
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)p.A, 0, (int)(uint32_t)((size_t)p.M * p.lda), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)p.W, 0, (int)(uint32_t)((size_t)p.N * p.ldw), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)p.as, 0, (int)(uint32_t)((size_t)p.M * nb * 4), 0x00020000);
+    // this workgroup's tiles: chunk [c0, c1) of the tile list, every per-th tile from c0 + li
+    const int nx = (gridDim.x % 8 == 0) ? 8 : 1;
+    const int grp = blockIdx.x % nx, li = blockIdx.x / nx, per = gridDim.x / nx;
+    const int c0 = (int)((long)tiles * grp / nx), c1 = (int)((long)tiles * (grp + 1) / nx);
+    const int ntile = (c1 - c0 > li) ? (c1 - c0 - li + per - 1) / per : 0;
+    const int G = ntile * nb;  // K steps of this workgroup
+    auto tile_m0 = [&](int j) { return ((c0 + li + j * per) / tiles_n) * BM; };
+    auto tile_n0 = [&](int j) { return ((c0 + li + j * per) % tiles_n) * BN; };
 
-    auto issue = [&](int kb) {
-        unsigned char *st = smem + (kb % NS) * TILE;
-        const int ko = kb * kQBlock;
+    const v4u rA = rsrc_words(p.A, (uint32_t)((size_t)p.M * p.lda));
+    const v4u rW = rsrc_words(p.W, (uint32_t)((size_t)p.N * p.ldw));
+    const v4u rS = rsrc_words(p.as, (uint32_t)((size_t)p.M * nb * 4));
+    const v4u rV = rsrc_words(p.ws, (uint32_t)((size_t)p.N * 4));
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)smem);
+
+    // loads of flat step g (tile j, block kb) into stage g % 3 and slot g % 4. Load i of a wave
+    // fills rows (i * 8 + wave) * 8 + lane / 8 of the tile, 16-byte chunk (lane % 8) ^ swzk(row);
+    // with 8 waves swzk(row) = (wave % 2) * 4 + (lane / 16) % 4 for every i, so one per-lane offset
+    // per operand serves all loads and the row base is a scalar. Rows past M (N) lie past the
+    // buffer's range and read as zero; their outputs are never stored. The slot gets the step's
+    // activation scales and its tile's ws (waves past BM/64 or BN/64 fetch a copy of the last 64).
+    const int swl = ((lane & 7) ^ ((wave & 1) * 4 + ((lane >> 4) & 3))) << 4;
+    const uint32_t vla = (uint32_t)(lane >> 3) * (uint32_t)p.lda + swl;
+    const uint32_t vlb = (uint32_t)(lane >> 3) * (uint32_t)p.ldw + swl;
+    const uint32_t vls = (uint32_t)lane * (uint32_t)nb * 4;
+    int ij = 0, ikb = 0;  // next step to issue
+    // a step's 8 loads per wave (AI of A, BI of W, as, ws) in 4 parts of 2, so that issuing them is
+    // spread over the step's MFMAs: issuing all at once stalls the wave on the vector-memory path
+    struct Issue {
+        uint32_t st, sl, ko, ks;
+        int m0, n0;
+    };
+    auto issue_prep = [&](int g) {
+        Issue is;
+        is.m0 = tile_m0(ij);
+        is.n0 = tile_n0(ij);
+        is.st = lds0 + (uint32_t)((g % kPStages) * TILE);
+        is.sl = lds0 + (uint32_t)(kPStages * TILE + (g % kPSlots) * SSLOT + wave * 256);
+        is.ko = (uint32_t)(ikb * kQBlock);
+        is.ks = (uint32_t)(ikb * 4);
+        if (++ikb == nb) {
+            ikb = 0;
+            ++ij;
+        }
+        return is;
+    };
+    static_assert(AI + BI + 2 == 8, "4 parts of 2 loads");
+    auto issue_load = [&](const Issue &is, int i) {
+        if (i < AI)
+            dma16(rA, is.st + (i * NWAVE + wave) * 1024,
+                  vla + (uint32_t)(is.m0 + (i * NWAVE + wave) * 8) * (uint32_t)p.lda, is.ko);
+        else if (i < AI + BI)
+            dma16(rW, is.st + BM * 128 + ((i - AI) * NWAVE + wave) * 1024,
+                  vlb + (uint32_t)(is.n0 + ((i - AI) * NWAVE + wave) * 8) * (uint32_t)p.ldw, is.ko);
+        else if (i == AI + BI)
+            dma4(rS, is.sl, vls + (uint32_t)(is.m0 + min(wave * 64, BM - 64)) * (uint32_t)nb * 4, is.ks);
+        else
+            dma4(rV, is.sl + SHALF, (uint32_t)(is.n0 + min(wave * 64, BN - 64) + lane) * 4, 0);
+    };
+    auto issue_part = [&](const Issue &is, int part) {
+        issue_load(is, 2 * part);
+        issue_load(is, 2 * part + 1);
+    };
+    auto issue_next = [&](int g) {
+        const Issue is = issue_prep(g);
 #pragma unroll
-        for (int i = 0; i < AI; i++)
-            lds_load16(rA, st + (i * NWAVE + wave) * 1024, oa[i], ko);
-#pragma unroll
-        for (int i = 0; i < BI; i++)
-            lds_load16(rW, st + BM * 128 + (i * NWAVE + wave) * 1024, ob[i], ko);
-        lds_load4(rS, sscale + (kb % RS) * SSLOT + wave * 256, os, kb * 4);
+        for (int q = 0; q < 4; q++) issue_part(is, q);
     };
 
-    float wsr[TN];
-#pragma unroll
-    for (int tn = 0; tn < TN; tn++)
-        wsr[tn] = p.ws[min(n0 + wn * WN + tn * 32 + (lane & 31), p.N - 1)];
+    // the fold of "step -1" (zero accumulators) reads slot 3, which must hold finite scales; it is
+    // not loaded before step 1, after that fold (the barrier of step 0 publishes the zeros)
+    for (int i = tid; i < SSLOT / 16; i += NWAVE * 64)
+        ((uint4 *)(sscale + (kPSlots - 1) * SSLOT))[i] = make_uint4(0, 0, 0, 0);
+    if (G > 0) issue_next(0);
+    if (G > 1) issue_next(1);
 
-    float f[TM][TN][16];
+    // ws of this lane's two columns, read from a slot's ws half
+    float wsr[2];
+    auto read_ws = [&](const unsigned char *slot) {
 #pragma unroll
-    for (int tm = 0; tm < TM; tm++)
+        for (int tn = 0; tn < 2; tn++)
+            wsr[tn] = *(const float *)(slot + SHALF + (wn * 64 + tn * 32 + (lane & 31)) * 4);
+    };
+
+    float f[2][2][16];
 #pragma unroll
-        for (int tn = 0; tn < TN; tn++)
+    for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+        for (int tn = 0; tn < 2; tn++)
 #pragma unroll
             for (int r = 0; r < 16; r++) f[tm][tn][r] = 0.f;
-    v16i acc0[TM][TN], acc1[TM][TN];
+    v16i acc0[2][2], acc1[2][2];
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+        for (int tn = 0; tn < 2; tn++) acc1[tm][tn] = (v16i){};
 
-    // fold one 32x32 tile of step kb: f = fma((float)acc, RN(as*ws), f), the reference's order
-    auto fold = [&](const v16i (&acc)[TM][TN], int t, int kb) {
-        const int tm = t / TN, tn = t % TN;
-        const float *asb = (const float *)(sscale + (kb % RS) * SSLOT) + wm * WM + tm * 32 + (lane >> 5) * 4;
+    // per-lane fragment offsets inside a stage: row (lane % 32) of a 32-row tile, 16-byte chunk
+    // 2 kk + lane / 32; the XOR swizzle depends only on the row within 16, so one offset per kk
+    // serves all four tiles (tile t adds t * 4096 as an immediate)
+    int offa[4], offb[4];
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const float4 a4 = *(const float4 *)(asb + g * 8);
-            const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+    for (int kk = 0; kk < 4; kk++) {
+        const int o = swz(lane & 31, kk * 2 + (lane >> 5));
+        offa[kk] = wm * 64 * 128 + o;
+        offb[kk] = BM * 128 + wn * 64 * 128 + o;
+    }
+    const int offs = (wm * 64 + (lane >> 5) * 4) * 4;
+
+    // fold unit u (4 elements): tile (tm = u / 8, tn = u % 2), registers 4q..4q+3, q = (u / 2) % 4
+    auto fold_unit = [&](const v16i (&acc)[2][2], int u, const float *sslot, const float (&w)[2]) {
+        const int tn = u % 2, q = (u / 2) % 4, tm = u / 8;
+        const float4 a4 = *(const float4 *)((const unsigned char *)sslot + offs + (tm * 32 + q * 8) * 4);
+        const float av[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int r = g * 4 + j;
-                f[tm][tn][r] = __builtin_fmaf((float)acc[tm][tn][r],
-                                              FAST ? av[j] : __fmul_rn(av[j], wsr[tn]), f[tm][tn][r]);
-            }
+        for (int j = 0; j < 4; j++) {
+            const int r = q * 4 + j;
+            // the reference's order: f = fma((float)acc, RN(as * ws), f); FAST folds as only and
+            // multiplies by ws once in the epilogue
+            f[tm][tn][r] = __builtin_fmaf((float)acc[tm][tn][r], XACT ? __fmul_rn(av[j], w[tn]) : av[j],
+                                          f[tm][tn][r]);
         }
     };
-
-#pragma unroll
-    for (int st = 0; st < NS - 1; st++)
-        if (st < nb) issue(st);
-    constexpr int L = AI + BI + 1;  // loads per wave per step
     const v16i zero = {};
-    // one K step into `cur`, folding `prev` (step kb-1) tile by tile when FOLD
-    auto step = [&](auto fold_prev, int kb, v16i (&cur)[TM][TN], const v16i (&prev)[TM][TN]) {
-        const int rem = min(nb - 1 - kb, NS - 2);
-        if (rem <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        else if (rem == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
-        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * L) : "memory");
+    int cj = 0, ckb = 0;  // tile / block of the step being computed
+    // one K step: MFMAs of step g into cur, interleaved with the fold of prev (step g-1), and the
+    // loads of step g + 2 issued 2 per K sub-step (past the end of the list they fetch rows beyond
+    // the operands' range into stages no longer read, which is harmless)
+    auto step = [&](int g, v16i (&cur)[2][2], const v16i (&prev)[2][2]) {
+        if (g + 1 < G) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (kb + NS - 1 < nb) issue(kb + NS - 1);
-        const unsigned char *sb = smem + (kb % NS) * TILE;
+        const bool tile_start = ckb == 0 && g > 0;  // prev is the previous tile's last step
+        const Issue is_next = issue_prep(g + 2);
+        const unsigned char *sb = smem + (g % kPStages) * TILE;
+        const unsigned char *spb = sscale + ((g + kPSlots - 1) % kPSlots) * SSLOT;
+        const float *sp = (const float *)spb;
+        read_ws(spb);  // the folded step's tile
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
-            const int cc = kk * 2 + (lane >> 5);
-            v4i af[TM], bf[TN];
+            issue_part(is_next, kk);
+            v4i af[2], bf[2];
 #pragma unroll
-            for (int tm = 0; tm < TM; tm++)
-                af[tm] = *(const v4i *)(sb + swz(wm * WM + tm * 32 + (lane & 31), cc));
+            for (int t = 0; t < 2; t++) {
+                af[t] = *(const v4i *)(sb + offa[kk] + t * 4096);
+                bf[t] = *(const v4i *)(sb + offb[kk] + t * 4096);
+            }
 #pragma unroll
-            for (int tn = 0; tn < TN; tn++)
-                bf[tn] = *(const v4i *)(sb + BM * 128 + swz(wn * WN + tn * 32 + (lane & 31), cc));
+            for (int tm = 0; tm < 2; tm++)
 #pragma unroll
-            for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-                for (int tn = 0; tn < TN; tn++)
+                for (int tn = 0; tn < 2; tn++)
                     cur[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[tm], bf[tn],
                                                                         kk == 0 ? zero : cur[tm][tn], 0, 0, 0);
-            if constexpr (decltype(fold_prev)::value) {
 #pragma unroll
-                for (int t = kk * TPK; t < (kk + 1) * TPK; t++)
-                    if (t < NTILE) fold(prev, t, kb - 1);
+            for (int u = kk * 4; u < kk * 4 + 4; u++) fold_unit(prev, u, sp, wsr);
+            // 4 fragment reads + 2 scale reads, then 1 MFMA : 1 fold unit
+            __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, XACT ? 12 : 8, 0);
             }
         }
+        if (tile_start) {
+            // the previous tile is complete: its epilogue, then a fresh f. A requantizing epilogue
+            // stages through this step's A|W stage once every wave is done with it; the stage is
+            // refilled only by the next step's loads, issued after that step's barrier.
+            const int pm0 = tile_m0(cj - 1), pn0 = tile_n0(cj - 1);
+            if constexpr (EPI == EPI_F32) {
+                p_epilogue_f32<POST, FAST>(p, f, wsr, pm0, pn0, wm, wn, lane);
+            } else {
+                __syncthreads();
+                p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST>(p, f, wsr, pm0, pn0, wm, wn, tid,
+                                                                (float *)(smem + (g % kPStages) * TILE));
+            }
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                for (int tn = 0; tn < 2; tn++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) f[tm][tn][r] = 0.f;
+        }
+        if (++ckb == nb) {
+            ckb = 0;
+            ++cj;
+        }
     };
-    using no_fold = std::integral_constant<bool, false>;
-    using do_fold = std::integral_constant<bool, true>;
-    step(no_fold{}, 0, acc0, acc1);
-    int kb = 1;
-    for (; kb + 1 < nb; kb += 2) {
-        step(do_fold{}, kb, acc1, acc0);
-        step(do_fold{}, kb + 1, acc0, acc1);
+    int g = 0;
+    for (; g + 1 < G; g += 2) {
+        step(g, acc0, acc1);
+        step(g + 1, acc1, acc0);
     }
-    if (kb < nb) {  // nb even: the last step (odd) lands in acc1
-        step(do_fold{}, kb, acc1, acc0);
+    if (g < G) step(g, acc0, acc1);
+    if (G > 0) {
+        // fold the last step (acc0 when G is odd) and write the last tile
+        __syncthreads();
+        const float *sp = (const float *)(sscale + ((G - 1) % kPSlots) * SSLOT);
+        read_ws((const unsigned char *)sp);
+        // (two branches: selecting one of the register arrays at run time would put it in memory)
+        if (G & 1) {
 #pragma unroll
-        for (int t = 0; t < NTILE; t++) fold(acc1, t, kb);
-    } else {
+            for (int u = 0; u < 16; u++) fold_unit(acc0, u, sp, wsr);
+        } else {
 #pragma unroll
-        for (int t = 0; t < NTILE; t++) fold(acc0, t, nb - 1);
+            for (int u = 0; u < 16; u++) fold_unit(acc1, u, sp, wsr);
+        }
+        const int pm0 = tile_m0(ntile - 1), pn0 = tile_n0(ntile - 1);
+        if constexpr (EPI == EPI_F32)
+            p_epilogue_f32<POST, FAST>(p, f, wsr, pm0, pn0, wm, wn, lane);
+        else
+            p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST>(p, f, wsr, pm0, pn0, wm, wn, tid,
+                                                            (float *)(smem + ((G - 1) % kPStages) * TILE));
     }
-    __syncthreads();  // the epilogue may reuse the staging buffers
-    store_tile<BM, BN, WM, WN, db_lds_bytes(BM, BN, NWAVE, NS, EPI), EPI, FAST>(p, f, wsr, m0, n0, wm, wn,
-                                                                             tid, smem);
+    // the last steps issued loads past the end of the list: they must land before the workgroup's
+    // LDS is released
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int EPI, bool FAST, int OCC>
-static int launch_db1(hipStream_t s, const GemmArgs &p) {
-    constexpr int NWAVE = (BM / WM) * (BN / WN);
-    constexpr size_t lds = db_lds_bytes(BM, BN, NWAVE, NS, EPI);
-    static_assert(NS >= 2 && NS <= 4 && lds <= 160 * 1024, "LDS budget");
-    auto kern = k_gemm_db<BM, BN, WM, WN, NS, EPI, FAST, OCC>;
+static int num_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return cus;
+}
+
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
+static int launch_p1(hipStream_t s, const GemmArgs &p) {
+    constexpr size_t lds = p_lds_bytes<BM, BN, NWM * NWN>();
+    static_assert(lds <= 160 * 1024, "LDS budget");
+    static_assert(EPI == EPI_F32 || (NWM * 16) * (BN + 4) * 4 <= (BM + BN) * 128, "epilogue chunk fits a stage");
+    auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST>;
     static bool attr = false;
     if (!attr) {
-        if (check_hip(hipFuncSetAttribute((const void *)kern,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+        if (check_hip(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                       "gemm lds attribute"))
             return -1;
         attr = true;
     }
-    const long tiles = (long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NWAVE * 64), lds, s, p);
+    const int tiles_n = (p.N + BN - 1) / BN;
+    const long tiles = (long)((p.M + BM - 1) / BM) * tiles_n;
+    if (tiles > (1L << 30)) {
+        set_error("gemm: too many tiles");
+        return -1;
+    }
+    const int grid = (int)min(tiles, (long)num_cus());
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NWM * NWN * 64), lds, s, p, tiles_n, (int)tiles);
     return check_hip(hipGetLastError(), "gemm launch");
+}
+
+// POST: bit 0 adds a bias, bit 1 clamps to [lo, hi]; only "none" and "both" are instantiated (the
+// bias pointer may be null and an absent clamp is +-1e31)
+template <int BM, int BN, int NWM, int NWN, int EPI>
+static int launch_p(hipStream_t s, const GemmArgs &p) {
+    const bool post = p.bias != nullptr || p.lo > -1e30f || p.hi < 1e30f;
+    if (fold_fast())
+        return post ? launch_p1<BM, BN, NWM, NWN, EPI, true, 3>(s, p) : launch_p1<BM, BN, NWM, NWN, EPI, true, 0>(s, p);
+    return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3>(s, p) : launch_p1<BM, BN, NWM, NWN, EPI, false, 0>(s, p);
 }
 
 template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP, bool FAST>
@@ -540,17 +828,6 @@ static int launch_tile1(hipStream_t s, const GemmArgs &p) {
     const long tiles = (long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NT), lds, s, p);
     return check_hip(hipGetLastError(), "gemm launch");
-}
-
-// E2MI_GEMM_FOLD=fast selects the 2-op fold for the whole process (read once); the default is
-// the reference's bit-exact fold order
-static bool fold_fast() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("E2MI_GEMM_FOLD");
-        v = (e && strcmp(e, "fast") == 0) ? 1 : 0;
-    }
-    return v == 1;
 }
 
 template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP>
@@ -591,7 +868,7 @@ int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump) {
         }
         return launch_tile<128, 128, 64, 64, 2, EPI_F32, true>(s, p);
     }
-    return launch_tile<128, 128, 64, 64, 2, EPI_F32, false>(s, p);
+    return launch_p<256, 128, 4, 2, EPI_F32>(s, p);
 }
 
 int launch_gemm_i8q(hipStream_t s, GemmArgs p) {
@@ -601,7 +878,7 @@ int launch_gemm_i8q(hipStream_t s, GemmArgs p) {
         set_error("i8_gemm_q: N must be a multiple of 128 with a 16-byte aligned int8 output");
         return -1;
     }
-    return launch_tile<128, 128, 64, 64, 2, EPI_I8Q, false>(s, p);
+    return launch_p<256, 128, 4, 2, EPI_I8Q>(s, p);
 }
 
 int launch_gemm_geglu(hipStream_t s, GemmArgs p) {
@@ -611,10 +888,8 @@ int launch_gemm_geglu(hipStream_t s, GemmArgs p) {
         set_error("i8_gemm_geglu: N (gate|up interleaved) must be a multiple of 256, outputs aligned");
         return -1;
     }
-    // 8 waves of 64x64 over a 128x256 tile (64 output columns per wave pair), accumulators
-    // double-buffered so the fold overlaps the next step's MFMAs
-    if (fold_fast()) return launch_db1<128, 256, 64, 64, 2, EPI_GEGLU, true, 2>(s, p);
-    return launch_db1<128, 256, 64, 64, 2, EPI_GEGLU, false, 2>(s, p);
+    // 128 x 256 tiles: a tile holds the interleaved gate|up columns of two output blocks
+    return launch_p<128, 256, 2, 4, EPI_GEGLU>(s, p);
 }
 
 }  // namespace e2mi
@@ -647,6 +922,16 @@ static GemmArgs make_args(const int8_t *qa, const float *as, const e2mi_q8w *w, 
     p.lo = w->out_min;
     p.hi = w->out_max;
     return p;
+}
+
+extern "C" int e2mi_gemm_set_fold(int mode) {
+    if (mode != 0 && mode != 1) {
+        set_error("gemm_set_fold: mode must be 0 (exact) or 1 (fast), got %d", mode);
+        return -1;
+    }
+    const int prev = fold_fast() ? 1 : 0;
+    g_fold = mode;
+    return prev;
 }
 
 extern "C" int e2mi_i8_gemm(e2mi_stream stream, float *y, int ldy, const int8_t *qa,

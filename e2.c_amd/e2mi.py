@@ -47,6 +47,7 @@ SIGNATURES = {
     "e2mi_i8_gemm_acc": (_I, [_P, _P, _I, _P, _P, _P, C.POINTER(Q8W), _I, _I, _I]),
     "e2mi_i8_gemm_q": (_I, [_P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
     "e2mi_i8_gemm_geglu": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
+    "e2mi_gemm_set_fold": (_I, [_I]),
     "e2mi_interleave_gate_up": (_I, [_P, _P, _P, _P, _P, _P, _I, _I]),
     "e2mi_norm_quant": (_I, [_P, _P, _P, _F, _I, _I, _P, _P, _P]),
     "e2mi_add_norm_quant": (_I, [_P, _P, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P]),
@@ -183,6 +184,15 @@ def interleave_gate_up(gate, sgate, up, sup):
     check(load().e2mi_interleave_gate_up(ptr(w), ptr(s), ptr(args[0]), ptr(args[1]), ptr(args[2]),
                                          ptr(args[3]), F, K), "interleave_gate_up")
     return w, s
+
+
+def set_gemm_fold(mode: str) -> str:
+    """Select the GEMM fold order ("exact": the reference's, bit-exact; "fast": as-only fold and
+    one ws multiply per output). Returns the previous mode."""
+    prev = load().e2mi_gemm_set_fold({"exact": 0, "fast": 1}[mode])
+    if prev < 0:
+        raise RuntimeError(last_error())
+    return "fast" if prev == 1 else "exact"
 
 
 # ---- kernel wrappers over torch device tensors

@@ -87,6 +87,16 @@ int e2mi_i8_gemm_q(e2mi_stream stream, int8_t *yq, float *ys, const int8_t *qa,
 int e2mi_i8_gemm_geglu(e2mi_stream stream, int8_t *q, float *qs, float *g, const int8_t *qa,
                        const float *a_scales, const e2mi_q8w *w_gate_up, int M);
 
+/* Fold order of every GEMM above (process-wide; no counterpart in the reference, which has one):
+ *   0 (default) the reference's per-block f = fma((float)acc_b, RN(as[m,b]*ws[n]), f), bit-exact;
+ *   1 f = fma((float)acc_b, as[m,b], f) per block and one multiply by ws[n] at the end: two VALU
+ *     operations per element and block instead of three, int32 accumulators still exact, f32
+ *     results within a few ulp (not bit-exact) of the reference's order.
+ * The environment variable E2MI_GEMM_FOLD=fast sets 1 at load. Returns the previous mode, or -1
+ * for a mode other than 0 or 1. Kernel-level entry points only; not safe against concurrent
+ * launches from other threads. */
+int e2mi_gemm_set_fold(int mode);
+
 /* Host helper: interleave row-major gate [F][K] and up [F][K] int8 (and their scales) into the
  * [F/128][gate 128 | up 128] row order e2mi_i8_gemm_geglu consumes. F % 128 == 0. */
 int e2mi_interleave_gate_up(int8_t *w_out, float *s_out, const int8_t *gate, const float *sgate,
