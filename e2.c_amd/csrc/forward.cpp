@@ -139,15 +139,15 @@ static int upload_layer(e2mi_engine *g, const e2_model *m, int l, LayerDev &L) {
         upload_packed_rows(L.down.w, L.down.ld, w[6]->w, c.hidden, c.ffn, c.hidden, 0, 0, g->stream) ||
         check_hip(hipMemcpyAsync(L.down.scale, w[6]->scale, (size_t)c.hidden * 4, hipMemcpyHostToDevice, g->stream), "down scale"))
         return -1;
-    // gate|up interleaved per 128 rows: [gate 128 | up 128] blocks
+    // gate|up interleaved per 32 rows: [gate 32 | up 32] blocks (the GeGLU epilogue's layout)
     if (make(L.gu, 2 * c.ffn, K) ||
-        upload_packed_rows(L.gu.w, L.gu.ld, w[4]->w, c.ffn, K, 128, 256, 0, g->stream) ||
-        upload_packed_rows(L.gu.w, L.gu.ld, w[5]->w, c.ffn, K, 128, 256, 128, g->stream))
+        upload_packed_rows(L.gu.w, L.gu.ld, w[4]->w, c.ffn, K, 32, 64, 0, g->stream) ||
+        upload_packed_rows(L.gu.w, L.gu.ld, w[5]->w, c.ffn, K, 32, 64, 32, g->stream))
         return -1;
     std::vector<float> gus(2 * c.ffn);
     for (int n = 0; n < c.ffn; n++) {
-        gus[(n / 128) * 256 + n % 128] = w[4]->scale[n];
-        gus[(n / 128) * 256 + 128 + n % 128] = w[5]->scale[n];
+        gus[(n / 32) * 64 + n % 32] = w[4]->scale[n];
+        gus[(n / 32) * 64 + 32 + n % 32] = w[5]->scale[n];
     }
     if (check_hip(hipMemcpyAsync(L.gu.scale, gus.data(), gus.size() * 4, hipMemcpyHostToDevice, g->stream), "gu scale"))
         return -1;

@@ -7,15 +7,15 @@
 // then one of the fused epilogues:
 //   EPI_F32   y (+bias), clamped to [lo,hi], stored f32 (the reference contract)
 //   EPI_I8Q   y (+bias) requantized per (row, 128 output columns) for the next GEMM: int8 + scale
-//   EPI_GEGLU W rows interleaved per 256 as [128 gate | 128 up]; g = gelu_tanh(gate) * up is
+//   EPI_GEGLU W rows interleaved per 64 as [32 gate | 32 up]; g = gelu_tanh(gate) * up is
 //             quantized per 128 (text.c:424-468 fused into the producing GEMM), g optionally kept
 //
-// Tiling: BM x BN workgroup tile of 64x64 wave tiles, K walked in 128-deep steps (one quantization
-// block per step, so the int32 accumulators are folded into f32 once per step). A, W and the
-// step's activation scales go HBM -> LDS with buffer loads that write LDS directly (no VGPR round
-// trip), NS-1 steps ahead of the MFMAs; the fragment reads are conflict-free on the 64-bank LDS
-// (see swz). Two kernels share the epilogues: k_gemm folds each step after its MFMAs, k_gemm_db
-// double-buffers the int32 accumulators so one step's fold overlaps the next step's MFMAs.
+// The production kernel is k_gemm_p (a persistent, software-pipelined kernel; its design is
+// described above it); k_gemm_dump is a plain kernel that also writes every K block's int32
+// accumulators, the parity hook for the integer part. K is walked in 128-deep steps, one
+// quantization block per step, so the int32 accumulators are folded into f32 once per step.
+// A and W tiles live in LDS as 128-byte K slices of consecutive rows whose fragment reads are
+// conflict-free on the 64-bank LDS (see swz).
 #include <stdlib.h>
 #include <type_traits>
 #include <string.h>
@@ -100,145 +100,13 @@ __device__ inline void dma4(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
                  : "memory");
 }
 
-// The fused epilogues over a finished BM x BN tile: f holds each wave's WM x WN f32 results in the
-// MFMA C layout (lane column lane % 32, rows 8 (r / 4) + 4 (lane / 32) + r % 4 of each 32x32 tile).
-// POST: bit 0 adds the bias, bit 1 clamps to [lo, hi] (compile-time, so the common case of
-// neither costs no VALU work per element)
-template <int BM, int BN, int WM, int WN, int LDSB, int EPI, bool FAST, int POST>
-__device__ inline void store_tile_impl(const GemmArgs &p, float (&f)[WM / 32][WN / 32][16],
-                                       const float (&wsr)[WN / 32], int m0, int n0, int wm, int wn,
-                                       int tid, unsigned char *smem) {
-    constexpr int TM = WM / 32, TN = WN / 32;
-    constexpr int NT = (BM / WM) * (BN / WN) * 64;
-    const int lane = tid & 63;
-    auto post = [&](float v, float b) {
-        if constexpr (POST & 1) v = v + b;
-        if constexpr (POST & 2) v = fminf(fmaxf(v, p.lo), p.hi);
-        return v;
-    };
-    if constexpr (EPI == EPI_F32) {
-        // buffer stores: the lane's byte offset is computed once, every (tile, register) row step
-        // is a wave-uniform SGPR offset; rows past M fall outside the descriptor's range and are
-        // dropped by the hardware, columns past N are masked per lane
-        const __amdgpu_buffer_rsrc_t ry =
-            __builtin_amdgcn_make_buffer_rsrc(p.Y, 0, (int)min((long)p.M * p.ldy * 4, 0x7fffffffL), 0x00020000);
-        const int vrow = wm * WM + (lane >> 5) * 4, vcol = wn * WN + (lane & 31);
-        const int voff = ((m0 + vrow) * p.ldy + n0 + vcol) * 4;
-#pragma unroll
-        for (int tn = 0; tn < TN; tn++) {
-            const int n = n0 + vcol + tn * 32;
-            if (n >= p.N) continue;
-            const float b = (POST & 1) ? p.bias[n] : 0.f;
-#pragma unroll
-            for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const float v = post(FAST ? __fmul_rn(f[tm][tn][r], wsr[tn]) : f[tm][tn][r], b);
-                    const int srow = __builtin_amdgcn_readfirstlane((tm * 32 + (r >> 2) * 8 + (r & 3)) * p.ldy * 4);
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
-                                                          voff + tn * 128, srow, 0);
-                }
-        }
-    } else {
-        // Stage the f32 tile through LDS (the A/W staging buffers are free now), then each group of
-        // threads owns whole 128-column quantization blocks of a row.
-        constexpr int FP = BN + 4;  // f32 row pitch
-        static_assert(BM * FP * 4 <= LDSB, "epilogue tile does not fit");
-        float *sf = (float *)smem;
-        {
-            float *sl = sf + (wm * WM + (lane >> 5) * 4) * FP + wn * WN + (lane & 31);
-#pragma unroll
-            for (int tn = 0; tn < TN; tn++) {
-                const float b = (POST & 1) ? p.bias[min(n0 + wn * WN + tn * 32 + (lane & 31), p.N - 1)] : 0.f;
-#pragma unroll
-                for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const float v = post(FAST ? __fmul_rn(f[tm][tn][r], wsr[tn]) : f[tm][tn][r], b);
-                        sl[(tm * 32 + (r >> 2) * 8 + (r & 3)) * FP + tn * 32] = v;
-                    }
-            }
-        }
-        __syncthreads();
-        // output columns per tile and per thread: I8Q keeps BN columns, GEGLU halves them
-        constexpr int OUTC = (EPI == EPI_GEGLU) ? BN / 2 : BN;
-        constexpr int TPR = OUTC / 16;  // threads per row, 16 columns each
-        constexpr int RPP = NT / TPR;   // rows per pass
-        static_assert(OUTC % 128 == 0 && TPR <= 64, "quantization block must be tile-local");
-        const int oc0 = (EPI == EPI_GEGLU) ? n0 / 2 : n0;  // first output column of this tile
-        const int ldo = (EPI == EPI_GEGLU) ? p.N / 2 : p.N;
-        const int t_r = tid / TPR, t_c = tid % TPR;
-        for (int rr = 0; rr < BM; rr += RPP) {
-            const int ml = rr + t_r, m = m0 + ml;
-            float v[16];
-            if constexpr (EPI == EPI_GEGLU) {
-                // W rows are interleaved per 256: [128 gate | 128 up] for each output block
-                const int blk = (t_c * 16) >> 7, w = (t_c * 16) & 127;
-                const float *gp = sf + ml * FP + blk * 256 + w;
-#pragma unroll
-                for (int i = 0; i < 16; i += 4) {
-                    const float4 g = *(const float4 *)(gp + i), u = *(const float4 *)(gp + 128 + i);
-                    v[i] = gelu_tanh(g.x) * u.x;
-                    v[i + 1] = gelu_tanh(g.y) * u.y;
-                    v[i + 2] = gelu_tanh(g.z) * u.z;
-                    v[i + 3] = gelu_tanh(g.w) * u.w;
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; i += 4) {
-                    const float4 x = *(const float4 *)(sf + ml * FP + t_c * 16 + i);
-                    v[i] = x.x;
-                    v[i + 1] = x.y;
-                    v[i + 2] = x.z;
-                    v[i + 3] = x.w;
-                }
-            }
-            float a = 0.f;
-#pragma unroll
-            for (int i = 0; i < 16; i++) a = fmaxf(a, fabsf(v[i]));
-            a = group_max<8>(a);  // 8 threads x 16 columns = one 128-column block
-            const QScale s = qscale(a);
-            const int oc = oc0 + t_c * 16;
-            if (m < p.M && oc < ldo) {
-                uint32_t w4[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    w4[i] = pack4_magic(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3], s.inv);
-                *(uint4 *)(p.Yq + (size_t)m * p.ldyq + oc) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-                if ((t_c & 7) == 0) p.ys[(size_t)m * p.ldys + (oc >> 7)] = s.sc;
-                if (EPI == EPI_GEGLU && p.Y) {
-#pragma unroll
-                    for (int i = 0; i < 16; i += 4)
-                        *(float4 *)(p.Y + (size_t)m * p.ldy + oc + i) =
-                            make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
-                }
-            }
-        }
-    }
-}
-
-template <int BM, int BN, int WM, int WN, int LDSB, int EPI, bool FAST>
-__device__ inline void store_tile(const GemmArgs &p, float (&f)[WM / 32][WN / 32][16],
-                                  const float (&wsr)[WN / 32], int m0, int n0, int wm, int wn,
-                                  int tid, unsigned char *smem) {
-    const int post = (p.bias != nullptr ? 1 : 0) | ((p.lo > -1e30f || p.hi < 1e30f) ? 2 : 0);
-    if (post == 0)
-        store_tile_impl<BM, BN, WM, WN, LDSB, EPI, FAST, 0>(p, f, wsr, m0, n0, wm, wn, tid, smem);
-    else if (post == 1)
-        store_tile_impl<BM, BN, WM, WN, LDSB, EPI, FAST, 1>(p, f, wsr, m0, n0, wm, wn, tid, smem);
-    else if (post == 2)
-        store_tile_impl<BM, BN, WM, WN, LDSB, EPI, FAST, 2>(p, f, wsr, m0, n0, wm, wn, tid, smem);
-    else
-        store_tile_impl<BM, BN, WM, WN, LDSB, EPI, FAST, 3>(p, f, wsr, m0, n0, wm, wn, tid, smem);
-}
-
-template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP, bool FAST>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 128 * 128) ? 1 : 2) void k_gemm(GemmArgs p) {
-    constexpr int NWN = BN / WN, NWAVE = (BM / WM) * NWN, NT = NWAVE * 64;
-    constexpr int TM = WM / 32, TN = WN / 32;
+// The accumulator-dump kernel (e2mi_i8_gemm_acc, the parity hook for "bit-exact int32
+// accumulators"): 128 x 128 tiles of 4 waves of 64 x 64, two direct-to-LDS stages, the exact fold
+// after each step's MFMAs, every step's int32 accumulators written to accd [nb][M][N], f32 output
+// with the optional bias and clamp. Not a throughput path.
+__global__ __launch_bounds__(256, 2) void k_gemm_dump(GemmArgs p) {
+    constexpr int BM = 128, BN = 128, WM = 64, WN = 64, NWN = 2, NWAVE = 4, TM = 2, TN = 2;
     constexpr int AI = BM / 8 / NWAVE, BI = BN / 8 / NWAVE;  // 1-KB loads per wave per step
-    static_assert(AI * NWAVE * 8 == BM && BI * NWAVE * 8 == BN, "tile/threads mismatch");
-    static_assert(BM <= 64 * NWAVE, "one scale per lane");
     constexpr int STAGE = (BM + BN) * 128 + 64 * NWAVE * 4;  // A | W | scales (one per lane)
     extern __shared__ __align__(16) unsigned char smem[];
 
@@ -263,34 +131,26 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 12
         const int r = (i * NWAVE + wave) * 8 + (lane >> 3);
         ob[i] = (uint32_t)min(n0 + r, p.N - 1) * (uint32_t)p.ldw + (((lane & 7) ^ swzk(r)) << 4);
     }
-    // scales: lane (wave, lane) fetches row wave*64+lane (waves past BM/64 fetch a clamped copy
-    // into their own slot, so every wave issues the same number of loads per step)
     const uint32_t os = (uint32_t)min(m0 + wave * 64 + lane, p.M - 1) * (uint32_t)nb * 4;
-    // buffer descriptors: per-lane offsets stay in VGPRs, the K step's offset is a scalar
     const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
         (void *)p.A, 0, (int)(uint32_t)((size_t)p.M * p.lda), 0x00020000);
     const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
         (void *)p.W, 0, (int)(uint32_t)((size_t)p.N * p.ldw), 0x00020000);
     const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
         (void *)p.as, 0, (int)(uint32_t)((size_t)p.M * nb * 4), 0x00020000);
-
-    auto issue = [&](int kb, int st) {
-        unsigned char *s = smem + st * STAGE;
+    auto issue = [&](int kb) {
+        unsigned char *s = smem + (kb & 1) * STAGE;
         const int ko = kb * kQBlock;
 #pragma unroll
-        for (int i = 0; i < AI; i++)
-            lds_load16(rA, s + (i * NWAVE + wave) * 1024, oa[i], ko);
+        for (int i = 0; i < AI; i++) lds_load16(rA, s + (i * NWAVE + wave) * 1024, oa[i], ko);
 #pragma unroll
-        for (int i = 0; i < BI; i++)
-            lds_load16(rW, s + BM * 128 + (i * NWAVE + wave) * 1024, ob[i], ko);
+        for (int i = 0; i < BI; i++) lds_load16(rW, s + BM * 128 + (i * NWAVE + wave) * 1024, ob[i], ko);
         lds_load4(rS, s + (BM + BN) * 128 + wave * 256, os, kb * 4);
     };
 
     float wsr[TN];
 #pragma unroll
-    for (int tn = 0; tn < TN; tn++)
-        wsr[tn] = p.ws[min(n0 + wn * WN + tn * 32 + (lane & 31), p.N - 1)];
-
+    for (int tn = 0; tn < TN; tn++) wsr[tn] = p.ws[min(n0 + wn * WN + tn * 32 + (lane & 31), p.N - 1)];
     v16i acc[TM][TN];
     float f[TM][TN][16];
 #pragma unroll
@@ -299,79 +159,67 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (NS > 2 || BM * BN > 12
         for (int tn = 0; tn < TN; tn++)
 #pragma unroll
             for (int r = 0; r < 16; r++) f[tm][tn][r] = 0.f;
-
-#pragma unroll
-    for (int st = 0; st < NS - 1; st++)
-        if (st < nb) issue(st, st);
+    issue(0);
     const v16i zero = {};
-    constexpr int L = AI + BI + 1;  // loads per wave per step
     for (int kb = 0; kb < nb; kb++) {
-        // wait for this step's tiles (later steps may stay in flight), then the barrier both
-        // publishes them and retires every wave's reads of the buffer refilled next
-        const int rem = min(nb - 1 - kb, NS - 2);
-        if (rem <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        else if (rem == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
-        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * L) : "memory");
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (kb + NS - 1 < nb) issue(kb + NS - 1, (kb + NS - 1) % NS);
-        const int cur = kb % NS;
-        const unsigned char *sb0 = smem + cur * STAGE;
+        if (kb + 1 < nb) issue(kb + 1);
+        const unsigned char *sb0 = smem + (kb & 1) * STAGE;
         const float *asb = (const float *)(sb0 + (BM + BN) * 128) + wm * WM + (lane >> 5) * 4;
-        {
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const int cc = kk * 2 + (lane >> 5);
-                v4i af[TM], bf[TN];
+        for (int kk = 0; kk < 4; kk++) {
+            const int cc = kk * 2 + (lane >> 5);
+            v4i af[TM], bf[TN];
 #pragma unroll
-                for (int tm = 0; tm < TM; tm++)
-                    af[tm] = *(const v4i *)(sb0 + swz(wm * WM + tm * 32 + (lane & 31), cc));
+            for (int tm = 0; tm < TM; tm++) af[tm] = *(const v4i *)(sb0 + swz(wm * WM + tm * 32 + (lane & 31), cc));
 #pragma unroll
-                for (int tn = 0; tn < TN; tn++)
-                    bf[tn] = *(const v4i *)(sb0 + BM * 128 + swz(wn * WN + tn * 32 + (lane & 31), cc));
-#pragma unroll
-                for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-                    for (int tn = 0; tn < TN; tn++)
-                        acc[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                            af[tm], bf[tn], kk == 0 ? zero : acc[tm][tn], 0, 0, 0);
-            }
-            // fold this block: f = fma((float)acc, RN(as*ws), f), the reference's order
+            for (int tn = 0; tn < TN; tn++) bf[tn] = *(const v4i *)(sb0 + BM * 128 + swz(wn * WN + tn * 32 + (lane & 31), cc));
 #pragma unroll
             for (int tm = 0; tm < TM; tm++)
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const float4 a4 = *(const float4 *)(asb + tm * 32 + g * 8);
-                    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-#pragma unroll
-                    for (int tn = 0; tn < TN; tn++)
-#pragma unroll
-                        for (int j = 0; j < 4; j++) {
-                            const int r = g * 4 + j;
-                            // FAST folds only the activation scale per block and applies ws[n] once
-                            // at the end (2 VALU ops per element and block instead of 3; f32 result
-                            // within a few ulp of the reference's order instead of bit-exact)
-                            f[tm][tn][r] = __builtin_fmaf((float)acc[tm][tn][r],
-                                                          FAST ? av[j] : __fmul_rn(av[j], wsr[tn]),
-                                                          f[tm][tn][r]);
-                        }
-                }
+                for (int tn = 0; tn < TN; tn++)
+                    acc[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[tm], bf[tn], kk == 0 ? zero : acc[tm][tn], 0, 0, 0);
         }
-        if constexpr (DUMP) {
+        // fold this block: f = fma((float)acc, RN(as*ws), f), the reference's order
 #pragma unroll
-            for (int tm = 0; tm < TM; tm++)
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 a4 = *(const float4 *)(asb + tm * 32 + g * 8);
+                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
                 for (int tn = 0; tn < TN; tn++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int m = m0 + wm * WM + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                        const int n = n0 + wn * WN + tn * 32 + (lane & 31);
-                        if (m < p.M && n < p.N)
-                            p.accd[((size_t)kb * p.M + m) * p.N + n] = acc[tm][tn][r];
+                    for (int j = 0; j < 4; j++) {
+                        const int r = g * 4 + j;
+                        f[tm][tn][r] = __builtin_fmaf((float)acc[tm][tn][r], __fmul_rn(av[j], wsr[tn]), f[tm][tn][r]);
                     }
-        }
+            }
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int m = m0 + wm * WM + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                    const int n = n0 + wn * WN + tn * 32 + (lane & 31);
+                    if (m < p.M && n < p.N) p.accd[((size_t)kb * p.M + m) * p.N + n] = acc[tm][tn][r];
+                }
     }
-    __syncthreads();  // the epilogue may reuse the staging buffers
-    store_tile<BM, BN, WM, WN, NS * STAGE, EPI, FAST>(p, f, wsr, m0, n0, wm, wn, tid, smem);
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+        const int n = n0 + wn * WN + tn * 32 + (lane & 31);
+        if (n >= p.N) continue;
+        const float b = p.bias ? p.bias[n] : 0.f;
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * WM + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                if (m < p.M) p.Y[(size_t)m * p.ldy + n] = fminf(fmaxf(f[tm][tn][r] + b, p.lo), p.hi);
+            }
+    }
 }
 
 // fold order of all GEMM launches (e2mi_gemm_set_fold); E2MI_GEMM_FOLD=fast sets the fast one
@@ -388,15 +236,16 @@ static bool fold_fast() {
 // ---------------------------------------------------------------------------------------------
 // Persistent pipelined kernel (the production path). One 512-thread workgroup per CU walks a list
 // of BM x BN output tiles; the 128-deep K steps of consecutive tiles form one flat pipeline:
-//   - A, W and the step's activation scales go HBM/L2 -> LDS by direct buffer loads two steps
-//     ahead (3 A|W stages, a ring of 4 scale slots);
-//   - 8 waves of 64x64 each; the int32 accumulators are double-buffered: the MFMAs of step g
+//   - A, W, the step's activation scales and its tile's weight scales go HBM/L2 -> LDS by direct
+//     buffer loads two steps ahead (3 A|W stages, a ring of 4 scale slots), issued two at a time
+//     between the step's MFMAs;
+//   - 8 waves of 32 x 128 each; the int32 accumulators are double-buffered: the MFMAs of step g
 //     accumulate into one set while the other set (step g-1) is folded into f on the VALU, the
-//     fold cut into 4-element units spread evenly between the step's 16 MFMAs
-//     (sched_group_barrier), since the fold costs about as many VALU cycles as the MFMAs take;
+//     fold cut into 4-element units placed between the step's 16 MFMAs (sched_group_barrier),
+//     since the fold costs more VALU cycles than the MFMAs take;
 //   - a tile's last step is folded during the next tile's first step, then the tile's epilogue
-//     runs; requantizing epilogues stage f through the one A|W stage free at that point, in 4
-//     chunks of rows.
+//     runs; requantizing epilogues transpose f through wave-private rows of the step's consumed
+//     A|W stage.
 // The tile list (M-major) is cut into one contiguous chunk per XCD (workgroups are dispatched
 // round-robin over the 8 XCDs), so the N tiles of an M block run on one XCD and share its L2.
 constexpr int kPStages = 3, kPSlots = 4;
@@ -407,133 +256,139 @@ constexpr int p_lds_bytes() {
     return kPStages * (BM + BN) * 128 + kPSlots * 2 * 64 * NWAVE * 4;
 }
 
-// requantizing epilogue of one tile through LDS scratch `scr` (>= NWM*16 rows x (BN+4) floats):
-// chunk c holds accumulator registers 4c..4c+3 of every wave, i.e. rows 8c..8c+7 of each 32-row
-// tile; every thread then owns CPT consecutive output columns of one row
+// requantizing epilogue of one tile. Every wave owns whole rows of each 128-column quantization
+// block (I8Q: its 32 x 128 tile; GEGLU: 32 rows x 64 of a block's 128 output columns, the other
+// 64 in wave wn ^ 1), so the transpose from the MFMA layout to row-contiguous columns goes through
+// a wave-private LDS area (8 rows at a time) with no workgroup barrier; GEGLU exchanges only the
+// per-row partial maxima between the two waves of a block (one barrier). scr: 8 waves x 8 rows x
+// (RW + 4) floats, then GEGLU's exchange area of 8 waves x 32 floats.
 template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
-__device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArgs &p, float (&f)[2][2][16], const float (&wsr)[2],
-                                    int m0, int n0, int wm, int wn, int tid, float *scr) {
-    constexpr int NT = NWM * NWN * 64;
-    constexpr int CR = NWM * 16;  // rows per chunk
-    constexpr int FP = BN + 4;    // f32 row pitch in LDS
-    constexpr int OUTC = (EPI == EPI_GEGLU) ? BN / 2 : BN;
-    constexpr int CPT = OUTC * CR / NT;  // output columns per thread
-    constexpr int TPR = OUTC / CPT;      // threads per row
-    constexpr int TPB = 128 / CPT;       // threads per 128-column quantization block
-    static_assert(CPT % 4 == 0 && CPT >= 4 && TPB <= 64 && OUTC % 128 == 0, "epilogue geometry");
-    const int lane = tid & 63;
-    float b[2] = {0.f, 0.f};
+__device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArgs &p, float (&f)[4][16],
+                                                                   const float (&wsr)[4], int m0, int n0,
+                                                                   int wave, int wm, int wn, int lane,
+                                                                   float *scr) {
+    constexpr bool GG = EPI == EPI_GEGLU;
+    constexpr int RW = GG ? 64 : 128;  // output columns per wave row
+    constexpr int FP = RW + 4;          // f32 pitch of the wave-private rows
+    constexpr int CPL = RW / 8;         // output columns per lane in the transposed chunk (16 | 8)
+    float *ws_ = scr + wave * 8 * FP;   // this wave's 8 rows
+    float b[4] = {0.f, 0.f, 0.f, 0.f};
     if constexpr (POST & 1) {
         if (p.bias) {
 #pragma unroll
-            for (int tn = 0; tn < 2; tn++) b[tn] = p.bias[min(n0 + wn * 64 + tn * 32 + (lane & 31), p.N - 1)];
+            for (int tn = 0; tn < 4; tn++) b[tn] = p.bias[min(n0 + wn * 128 + tn * 32 + (lane & 31), p.N - 1)];
         }
     }
-    const int oc0 = (EPI == EPI_GEGLU) ? n0 / 2 : n0;
-    const int ldo = (EPI == EPI_GEGLU) ? p.N / 2 : p.N;
-    const int t_r = tid / TPR, t_c = tid % TPR;
-    // the chunk-local row t_r -> tile row: t_r = wm*16 + tm*8 + h*4 + j -> wm*64 + tm*32 + 8c + h*4 + j
-    const int rbase = (t_r >> 4) * 64 + ((t_r >> 3) & 1) * 32 + (t_r & 7);
+    auto post = [&](float v, int tn) {
+        if constexpr (FAST) v = __fmul_rn(v, wsr[tn]);
+        if constexpr (POST & 1) v = v + b[tn];
+        if constexpr (POST & 2) v = fminf(fmaxf(v, p.lo), p.hi);
+        return v;
+    };
+    const int cr = lane >> 3, cc = (lane & 7) * CPL;  // transposed chunk: row, first column
+    // output column of this lane's transposed values and the row stride
+    const int oc = (GG ? n0 / 2 + wn * 64 : n0) + cc;
+    const int ldo = GG ? p.N / 2 : p.N;
+    float v[4][CPL];  // per chunk, the lane's CPL output values of row 8c + cr
+    float amax[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        {
-            float *sl = scr + (wm * 16 + (lane >> 5) * 4) * FP + wn * 64 + (lane & 31);
+        // registers 4c..4c+3 hold rows 8c + 4 (lane / 32) + j; column (lane % 32) of each 32-wide tile
+        float *sl = ws_ + ((lane >> 5) * 4) * FP + (lane & 31);
 #pragma unroll
-            for (int tm = 0; tm < 2; tm++)
+        for (int j = 0; j < 4; j++) {
+            if constexpr (GG) {
+                // W columns of the wave: [gate 32 | up 32 | gate 32 | up 32]
 #pragma unroll
-                for (int tn = 0; tn < 2; tn++)
+                for (int t = 0; t < 2; t++)
+                    sl[j * FP + t * 32] = gelu_tanh(post(f[2 * t][4 * c + j], 2 * t)) * post(f[2 * t + 1][4 * c + j], 2 * t + 1);
+            } else {
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        float v = f[tm][tn][4 * c + j];
-                        if constexpr (FAST) v = __fmul_rn(v, wsr[tn]);
-                        if constexpr (POST & 1) v = v + b[tn];
-                        if constexpr (POST & 2) v = fminf(fmaxf(v, p.lo), p.hi);
-                        sl[(tm * 8 + j) * FP + tn * 32] = v;
-                    }
+                for (int tn = 0; tn < 4; tn++) sl[j * FP + tn * 32] = post(f[tn][4 * c + j], tn);
+            }
         }
-        __syncthreads();
-        const int m = m0 + rbase + 8 * c;
-        float v[CPT];
-        if constexpr (EPI == EPI_GEGLU) {
-            // W rows are interleaved per 256: [128 gate | 128 up] for each output block
-            const int blk = (t_c * CPT) >> 7, w = (t_c * CPT) & 127;
-            const float *gp = scr + t_r * FP + blk * 256 + w;
+        // (LDS operations of one wave complete in order: no barrier, the reads see the writes)
+        const float *rp = ws_ + cr * FP + cc;
 #pragma unroll
-            for (int i = 0; i < CPT; i += 4) {
-                const float4 g = *(const float4 *)(gp + i), u = *(const float4 *)(gp + 128 + i);
-                v[i] = gelu_tanh(g.x) * u.x;
-                v[i + 1] = gelu_tanh(g.y) * u.y;
-                v[i + 2] = gelu_tanh(g.z) * u.z;
-                v[i + 3] = gelu_tanh(g.w) * u.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < CPT; i += 4) {
-                const float4 x = *(const float4 *)(scr + t_r * FP + t_c * CPT + i);
-                v[i] = x.x;
-                v[i + 1] = x.y;
-                v[i + 2] = x.z;
-                v[i + 3] = x.w;
-            }
+        for (int i = 0; i < CPL; i += 4) {
+            const float4 x = *(const float4 *)(rp + i);
+            v[c][i] = x.x;
+            v[c][i + 1] = x.y;
+            v[c][i + 2] = x.z;
+            v[c][i + 3] = x.w;
         }
         float a = 0.f;
 #pragma unroll
-        for (int i = 0; i < CPT; i++) a = fmaxf(a, fabsf(v[i]));
-        a = group_max<TPB>(a);
-        const QScale s = qscale(a);
-        const int oc = oc0 + t_c * CPT;
-        if (m < p.M && oc < ldo) {
-            uint32_t w4[CPT / 4];
+        for (int i = 0; i < CPL; i++) a = fmaxf(a, fabsf(v[c][i]));
+        amax[c] = group_max<8>(a);  // the 8 lanes of a row hold its RW columns
+    }
+    if constexpr (GG) {
+        // the other 64 columns of each block live in wave wn ^ 1: exchange per-row maxima
+        float *xch = scr + 8 * 8 * FP;
+        if ((lane & 7) == 0) {
 #pragma unroll
-            for (int i = 0; i < CPT / 4; i++)
-                w4[i] = pack4_magic(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3], s.inv);
-            int8_t *dst = p.Yq + (size_t)m * p.ldyq + oc;
-            if constexpr (CPT == 16) *(uint4 *)dst = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-            else if constexpr (CPT == 8) *(uint2 *)dst = make_uint2(w4[0], w4[1]);
-            else *(uint32_t *)dst = w4[0];
-            if (t_c % TPB == 0) p.ys[(size_t)m * p.ldys + (oc >> 7)] = s.sc;
-            if (EPI == EPI_GEGLU && p.Y) {
-#pragma unroll
-                for (int i = 0; i < CPT; i += 4)
-                    *(float4 *)(p.Y + (size_t)m * p.ldy + oc + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
-            }
+            for (int c = 0; c < 4; c++) xch[wave * 32 + 8 * c + cr] = amax[c];
         }
         __syncthreads();
+        const int other = wm * NWN + (wn ^ 1);
+#pragma unroll
+        for (int c = 0; c < 4; c++) amax[c] = fmaxf(amax[c], xch[other * 32 + 8 * c + cr]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const QScale s = qscale(amax[c]);
+        const int m = m0 + wm * 32 + 8 * c + cr;
+        if (m < p.M && oc < ldo) {
+            uint32_t w4[CPL / 4];
+#pragma unroll
+            for (int i = 0; i < CPL / 4; i++)
+                w4[i] = pack4_magic(v[c][4 * i], v[c][4 * i + 1], v[c][4 * i + 2], v[c][4 * i + 3], s.inv);
+            int8_t *dst = p.Yq + (size_t)m * p.ldyq + oc;
+            if constexpr (CPL == 16) *(uint4 *)dst = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+            else *(uint2 *)dst = make_uint2(w4[0], w4[1]);
+            if ((lane & 7) == 0 && (!GG || (wn & 1) == 0)) p.ys[(size_t)m * p.ldys + (oc >> 7)] = s.sc;
+            if (GG && p.Y) {
+#pragma unroll
+                for (int i = 0; i < CPL; i += 4)
+                    *(float4 *)(p.Y + (size_t)m * p.ldy + oc + i) = make_float4(v[c][i], v[c][i + 1], v[c][i + 2], v[c][i + 3]);
+            }
+        }
     }
 }
 
 // f32 epilogue straight from the accumulator registers: buffer stores whose row step is a scalar
 // offset; rows past M fall outside the descriptor's range and are dropped, columns past N masked
 template <int POST, bool FAST>
-__device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmArgs &p, float (&f)[2][2][16], const float (&wsr)[2],
-                                      int m0, int n0, int wm, int wn, int lane) {
+__device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmArgs &p, float (&f)[4][16],
+                                                                     const float (&wsr)[4], int m0, int n0,
+                                                                     int wm, int wn, int lane) {
     const __amdgpu_buffer_rsrc_t ry =
         __builtin_amdgcn_make_buffer_rsrc(p.Y, 0, (int)min((long)p.M * p.ldy * 4, 0x7fffffffL), 0x00020000);
-    const int vrow = wm * 64 + (lane >> 5) * 4, vcol = wn * 64 + (lane & 31);
+    const int vrow = wm * 32 + (lane >> 5) * 4, vcol = wn * 128 + (lane & 31);
     const int voff = ((m0 + vrow) * p.ldy + n0 + vcol) * 4;
 #pragma unroll
-    for (int tn = 0; tn < 2; tn++) {
+    for (int tn = 0; tn < 4; tn++) {
         const int n = n0 + vcol + tn * 32;
         if (n >= p.N) continue;
         const float b = ((POST & 1) && p.bias) ? p.bias[n] : 0.f;
 #pragma unroll
-        for (int tm = 0; tm < 2; tm++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float v = f[tm][tn][r];
-                if constexpr (FAST) v = __fmul_rn(v, wsr[tn]);
-                if constexpr (POST & 1) v = v + b;
-                if constexpr (POST & 2) v = fminf(fmaxf(v, p.lo), p.hi);
-                const int srow = __builtin_amdgcn_readfirstlane((tm * 32 + (r >> 2) * 8 + (r & 3)) * p.ldy * 4);
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry, voff + tn * 128, srow, 0);
-            }
+        for (int r = 0; r < 16; r++) {
+            float v = f[tn][r];
+            if constexpr (FAST) v = __fmul_rn(v, wsr[tn]);
+            if constexpr (POST & 1) v = v + b;
+            if constexpr (POST & 2) v = fminf(fmaxf(v, p.lo), p.hi);
+            const int srow = __builtin_amdgcn_readfirstlane(((r >> 2) * 8 + (r & 3)) * p.ldy * 4);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry, voff + tn * 128, srow, 0);
+        }
     }
 }
 
+// 8 waves of 32 x 128 (one 32-row MFMA tile by four 32-column ones): NWM x NWN waves, BM = 32 NWM,
+// BN = 128 NWN
 template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
 __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int tiles_n, int tiles) {
     constexpr int NWAVE = NWM * NWN;
-    static_assert(BM == 64 * NWM && BN == 64 * NWN && NWAVE == 8, "8 waves of 64x64");
+    static_assert(BM == 32 * NWM && BN == 128 * NWN && NWAVE == 8, "8 waves of 32x128");
     constexpr int AI = BM / 8 / NWAVE, BI = BN / 8 / NWAVE;  // 1-KB loads per wave per step
     constexpr int L = AI + BI + 2;                           // loads per wave per step
     constexpr int TILE = (BM + BN) * 128;                    // A | W of one step
@@ -624,51 +479,46 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
     if (G > 0) issue_next(0);
     if (G > 1) issue_next(1);
 
-    // ws of this lane's two columns, read from a slot's ws half
-    float wsr[2];
+    // ws of this lane's four columns, read from a slot's ws half
+    float wsr[4];
     auto read_ws = [&](const unsigned char *slot) {
 #pragma unroll
-        for (int tn = 0; tn < 2; tn++)
-            wsr[tn] = *(const float *)(slot + SHALF + (wn * 64 + tn * 32 + (lane & 31)) * 4);
+        for (int tn = 0; tn < 4; tn++)
+            wsr[tn] = *(const float *)(slot + SHALF + (wn * 128 + tn * 32 + (lane & 31)) * 4);
     };
 
-    float f[2][2][16];
+    float f[4][16];
 #pragma unroll
-    for (int tm = 0; tm < 2; tm++)
+    for (int tn = 0; tn < 4; tn++)
 #pragma unroll
-        for (int tn = 0; tn < 2; tn++)
+        for (int r = 0; r < 16; r++) f[tn][r] = 0.f;
+    v16i acc0[4], acc1[4];
 #pragma unroll
-            for (int r = 0; r < 16; r++) f[tm][tn][r] = 0.f;
-    v16i acc0[2][2], acc1[2][2];
-#pragma unroll
-    for (int tm = 0; tm < 2; tm++)
-#pragma unroll
-        for (int tn = 0; tn < 2; tn++) acc1[tm][tn] = (v16i){};
+    for (int tn = 0; tn < 4; tn++) acc1[tn] = (v16i){};
 
     // per-lane fragment offsets inside a stage: row (lane % 32) of a 32-row tile, 16-byte chunk
     // 2 kk + lane / 32; the XOR swizzle depends only on the row within 16, so one offset per kk
-    // serves all four tiles (tile t adds t * 4096 as an immediate)
+    // serves every tile (W tile t adds t * 4096 as an immediate)
     int offa[4], offb[4];
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) {
         const int o = swz(lane & 31, kk * 2 + (lane >> 5));
-        offa[kk] = wm * 64 * 128 + o;
-        offb[kk] = BM * 128 + wn * 64 * 128 + o;
+        offa[kk] = wm * 32 * 128 + o;
+        offb[kk] = BM * 128 + wn * 128 * 128 + o;
     }
-    const int offs = (wm * 64 + (lane >> 5) * 4) * 4;
+    const int offs = (wm * 32 + (lane >> 5) * 4) * 4;
 
-    // fold unit u (4 elements): tile (tm = u / 8, tn = u % 2), registers 4q..4q+3, q = (u / 2) % 4
-    auto fold_unit = [&](const v16i (&acc)[2][2], int u, const float *sslot, const float (&w)[2]) {
-        const int tn = u % 2, q = (u / 2) % 4, tm = u / 8;
-        const float4 a4 = *(const float4 *)((const unsigned char *)sslot + offs + (tm * 32 + q * 8) * 4);
+    // fold unit u (4 elements): tile tn = u % 4, registers 4q..4q+3 with q = u / 4
+    auto fold_unit = [&](const v16i (&acc)[4], int u, const float *sslot) {
+        const int tn = u % 4, q = u / 4;
+        const float4 a4 = *(const float4 *)((const unsigned char *)sslot + offs + q * 32);
         const float av[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int r = q * 4 + j;
             // the reference's order: f = fma((float)acc, RN(as * ws), f); FAST folds as only and
             // multiplies by ws once in the epilogue
-            f[tm][tn][r] = __builtin_fmaf((float)acc[tm][tn][r], XACT ? __fmul_rn(av[j], w[tn]) : av[j],
-                                          f[tm][tn][r]);
+            f[tn][r] = __builtin_fmaf((float)acc[tn][r], XACT ? __fmul_rn(av[j], wsr[tn]) : av[j], f[tn][r]);
         }
     };
     const v16i zero = {};
@@ -676,7 +526,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
     // one K step: MFMAs of step g into cur, interleaved with the fold of prev (step g-1), and the
     // loads of step g + 2 issued 2 per K sub-step (past the end of the list they fetch rows beyond
     // the operands' range into stages no longer read, which is harmless)
-    auto step = [&](int g, v16i (&cur)[2][2], const v16i (&prev)[2][2]) {
+    auto step = [&](int g, v16i (&cur)[4], const v16i (&prev)[4]) {
         if (g + 1 < G) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -689,21 +539,16 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             issue_part(is_next, kk);
-            v4i af[2], bf[2];
+            const v4i af = *(const v4i *)(sb + offa[kk]);
+            v4i bf[4];
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                af[t] = *(const v4i *)(sb + offa[kk] + t * 4096);
-                bf[t] = *(const v4i *)(sb + offb[kk] + t * 4096);
-            }
+            for (int t = 0; t < 4; t++) bf[t] = *(const v4i *)(sb + offb[kk] + t * 4096);
 #pragma unroll
-            for (int tm = 0; tm < 2; tm++)
+            for (int tn = 0; tn < 4; tn++)
+                cur[tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[tn], kk == 0 ? zero : cur[tn], 0, 0, 0);
 #pragma unroll
-                for (int tn = 0; tn < 2; tn++)
-                    cur[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[tm], bf[tn],
-                                                                        kk == 0 ? zero : cur[tm][tn], 0, 0, 0);
-#pragma unroll
-            for (int u = kk * 4; u < kk * 4 + 4; u++) fold_unit(prev, u, sp, wsr);
-            // 4 fragment reads + 2 scale reads, then 1 MFMA : 1 fold unit
+            for (int u = kk * 4; u < kk * 4 + 4; u++) fold_unit(prev, u, sp);
+            // 5 fragment reads + 1 scale read, then 1 MFMA : 1 fold unit
             __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -720,15 +565,13 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
                 p_epilogue_f32<POST, FAST>(p, f, wsr, pm0, pn0, wm, wn, lane);
             } else {
                 __syncthreads();
-                p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST>(p, f, wsr, pm0, pn0, wm, wn, tid,
+                p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
                                                                 (float *)(smem + (g % kPStages) * TILE));
             }
 #pragma unroll
-            for (int tm = 0; tm < 2; tm++)
+            for (int tn = 0; tn < 4; tn++)
 #pragma unroll
-                for (int tn = 0; tn < 2; tn++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) f[tm][tn][r] = 0.f;
+                for (int r = 0; r < 16; r++) f[tn][r] = 0.f;
         }
         if (++ckb == nb) {
             ckb = 0;
@@ -749,16 +592,16 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
         // (two branches: selecting one of the register arrays at run time would put it in memory)
         if (G & 1) {
 #pragma unroll
-            for (int u = 0; u < 16; u++) fold_unit(acc0, u, sp, wsr);
+            for (int u = 0; u < 16; u++) fold_unit(acc0, u, sp);
         } else {
 #pragma unroll
-            for (int u = 0; u < 16; u++) fold_unit(acc1, u, sp, wsr);
+            for (int u = 0; u < 16; u++) fold_unit(acc1, u, sp);
         }
         const int pm0 = tile_m0(ntile - 1), pn0 = tile_n0(ntile - 1);
         if constexpr (EPI == EPI_F32)
             p_epilogue_f32<POST, FAST>(p, f, wsr, pm0, pn0, wm, wn, lane);
         else
-            p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST>(p, f, wsr, pm0, pn0, wm, wn, tid,
+            p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
                                                             (float *)(smem + ((G - 1) % kPStages) * TILE));
     }
     // the last steps issued loads past the end of the list: they must land before the workgroup's
@@ -780,7 +623,8 @@ template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
 static int launch_p1(hipStream_t s, const GemmArgs &p) {
     constexpr size_t lds = p_lds_bytes<BM, BN, NWM * NWN>();
     static_assert(lds <= 160 * 1024, "LDS budget");
-    static_assert(EPI == EPI_F32 || (NWM * 16) * (BN + 4) * 4 <= (BM + BN) * 128, "epilogue chunk fits a stage");
+    static_assert(EPI == EPI_F32 || (8 * 8 * ((EPI == EPI_GEGLU ? 64 : 128) + 4) + 8 * 32) * 4 <= (BM + BN) * 128,
+                  "epilogue scratch fits a stage");
     auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST>;
     static bool attr = false;
     if (!attr) {
@@ -810,30 +654,19 @@ static int launch_p(hipStream_t s, const GemmArgs &p) {
     return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3>(s, p) : launch_p1<BM, BN, NWM, NWN, EPI, false, 0>(s, p);
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP, bool FAST>
-static int launch_tile1(hipStream_t s, const GemmArgs &p) {
-    constexpr int NT = (BM / WM) * (BN / WN) * 64;
-    constexpr int NWAVE = (BM / WM) * (BN / WN);
-    constexpr size_t lds = NS * ((size_t)(BM + BN) * 128 + 64 * NWAVE * 4);
-    static_assert(NS >= 2 && NS <= 4 && lds <= 160 * 1024, "LDS budget");
-    auto kern = k_gemm<BM, BN, WM, WN, NS, EPI, DUMP, FAST>;
+static int launch_dump(hipStream_t s, const GemmArgs &p) {
+    constexpr size_t lds = 2 * ((size_t)(128 + 128) * 128 + 64 * 4 * 4);
     static bool attr = false;
     if (!attr) {
-        if (check_hip(hipFuncSetAttribute((const void *)kern,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+        if (check_hip(hipFuncSetAttribute((const void *)k_gemm_dump, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)lds),
                       "gemm lds attribute"))
             return -1;
         attr = true;
     }
-    const long tiles = (long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NT), lds, s, p);
+    const long tiles = (long)((p.M + 127) / 128) * ((p.N + 127) / 128);
+    hipLaunchKernelGGL(k_gemm_dump, dim3((unsigned)tiles), dim3(256), lds, s, p);
     return check_hip(hipGetLastError(), "gemm launch");
-}
-
-template <int BM, int BN, int WM, int WN, int NS, int EPI, bool DUMP>
-static int launch_tile(hipStream_t s, const GemmArgs &p) {
-    if (!DUMP && fold_fast()) return launch_tile1<BM, BN, WM, WN, NS, EPI, DUMP, true>(s, p);
-    return launch_tile1<BM, BN, WM, WN, NS, EPI, DUMP, false>(s, p);
 }
 
 static int check_args(const GemmArgs &p, const char *who) {
@@ -866,9 +699,9 @@ int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump) {
             set_error("i8_gemm: null accumulator dump");
             return -1;
         }
-        return launch_tile<128, 128, 64, 64, 2, EPI_F32, true>(s, p);
+        return launch_dump(s, p);
     }
-    return launch_p<256, 128, 4, 2, EPI_F32>(s, p);
+    return launch_p<256, 128, 8, 1, EPI_F32>(s, p);
 }
 
 int launch_gemm_i8q(hipStream_t s, GemmArgs p) {
@@ -878,7 +711,7 @@ int launch_gemm_i8q(hipStream_t s, GemmArgs p) {
         set_error("i8_gemm_q: N must be a multiple of 128 with a 16-byte aligned int8 output");
         return -1;
     }
-    return launch_p<256, 128, 4, 2, EPI_I8Q>(s, p);
+    return launch_p<256, 128, 8, 1, EPI_I8Q>(s, p);
 }
 
 int launch_gemm_geglu(hipStream_t s, GemmArgs p) {
@@ -888,8 +721,8 @@ int launch_gemm_geglu(hipStream_t s, GemmArgs p) {
         set_error("i8_gemm_geglu: N (gate|up interleaved) must be a multiple of 256, outputs aligned");
         return -1;
     }
-    // 128 x 256 tiles: a tile holds the interleaved gate|up columns of two output blocks
-    return launch_p<128, 256, 2, 4, EPI_GEGLU>(s, p);
+    // 128 x 256 tiles: a tile holds the interleaved gate|up columns of one output block
+    return launch_p<128, 256, 4, 2, EPI_GEGLU>(s, p);
 }
 
 }  // namespace e2mi

@@ -14,7 +14,7 @@
 namespace e2mi {
 
 // row n of the packed blob lands in destination row (n / grp) * gstride + goff + n % grp: the
-// identity for a plain upload, an offset for q|k|v concatenation, and the per-128 gate|up
+// identity for a plain upload, an offset for q|k|v concatenation, and the per-32 gate|up
 // interleave the GeGLU epilogue reads
 __global__ void k_unpack_quads(int8_t *__restrict__ dst, int ld, const int8_t *__restrict__ src,
                                int N, int K, int grp, int gstride, int goff) {
@@ -128,13 +128,13 @@ extern "C" int e2mi_interleave_gate_up(int8_t *w_out, float *s_out, const int8_t
         set_error("interleave_gate_up: null pointer or F not a positive multiple of 128 (F=%d)", F);
         return -1;
     }
-    for (int b = 0; b < F / 128; b++)
-        for (int i = 0; i < 128; i++) {
-            const int src = b * 128 + i;
-            memcpy(w_out + (size_t)(b * 256 + i) * K, gate + (size_t)src * K, (size_t)K);
-            memcpy(w_out + (size_t)(b * 256 + 128 + i) * K, up + (size_t)src * K, (size_t)K);
-            s_out[b * 256 + i] = sgate[src];
-            s_out[b * 256 + 128 + i] = sup[src];
+    for (int b = 0; b < F / 32; b++)
+        for (int i = 0; i < 32; i++) {
+            const int src = b * 32 + i;
+            memcpy(w_out + (size_t)(b * 64 + i) * K, gate + (size_t)src * K, (size_t)K);
+            memcpy(w_out + (size_t)(b * 64 + 32 + i) * K, up + (size_t)src * K, (size_t)K);
+            s_out[b * 64 + i] = sgate[src];
+            s_out[b * 64 + 32 + i] = sup[src];
         }
     return 0;
 }

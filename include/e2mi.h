@@ -81,8 +81,8 @@ int e2mi_i8_gemm_q(e2mi_stream stream, int8_t *yq, float *ys, const int8_t *qa,
                    const float *a_scales, const e2mi_q8w *w, int M);
 
 /* gate|up GEMM with the GeGLU product and its quantization fused in the epilogue (text.c:424-468
- * gate_quant, fused into the producing GEMM). w holds 2*F rows interleaved per 256 as
- * [128 gate rows | 128 up rows] (see e2mi_interleave_gate_up). Writes q [M][F] int8, qs [M][F/128]
+ * gate_quant, fused into the producing GEMM). w holds 2*F rows interleaved per 64 as
+ * [32 gate rows | 32 up rows] (see e2mi_interleave_gate_up). Writes q [M][F] int8, qs [M][F/128]
  * and, when g != NULL, the f32 product g [M][F] (the reference writes it back into gate). */
 int e2mi_i8_gemm_geglu(e2mi_stream stream, int8_t *q, float *qs, float *g, const int8_t *qa,
                        const float *a_scales, const e2mi_q8w *w_gate_up, int M);
@@ -98,7 +98,7 @@ int e2mi_i8_gemm_geglu(e2mi_stream stream, int8_t *q, float *qs, float *g, const
 int e2mi_gemm_set_fold(int mode);
 
 /* Host helper: interleave row-major gate [F][K] and up [F][K] int8 (and their scales) into the
- * [F/128][gate 128 | up 128] row order e2mi_i8_gemm_geglu consumes. F % 128 == 0. */
+ * [F/32][gate 32 | up 32] row order e2mi_i8_gemm_geglu consumes. F % 128 == 0. */
 int e2mi_interleave_gate_up(int8_t *w_out, float *s_out, const int8_t *gate, const float *sgate,
                             const int8_t *up, const float *sup, int F, int K);
 
