@@ -2,16 +2,19 @@
 """Benchmark of the int8 encoder hot path on one MI355X (BASELINE.json metric).
 
 Step (the timed unit): the BASELINE config-5 sweep — four int8 GEMMs at M = 65536 tokens,
-(K, N) in {(768,1152), (1152,768), (768,1280), (768,768)}, each consuming int8 activations +
-per-128 scales already resident in HBM and producing the next GEMM's int8 activations + scales
-(the requantizing epilogue the encoder feeds forward). `value` is the aggregate int8 TOPS over the
-step. Reported beside it on the same line: the same sweep with the reference's f32-output
-contract, the activation quantizer's HBM rate, the `roofline` object for the dominant kernel, and
-the CPU baseline (the reference's own AVX512-VNNI kernel built from its sources, on the host).
+(K, N) in {(768,1152), (1152,768), (768,1280), (768,768)}, each consuming int8 activations with
+per-token scales (config 5's dynamic per-token quantization) already resident in HBM and writing
+the f32 output of the reference's e2_i8_gemm contract (dequantized int32 accumulators, bit-exact
+with the reference built with E2_I8_BLOCK = K). `value` is the aggregate int8 TOPS over the step.
+Reported beside it on the same line: the per-token sweep with the fused requantizing epilogue, the
+per-(token, 128) sweep the encoder runs (the reference's default block; exact and fast fold, f32
+and requant), the vendor int8 GEMM (torch._int_mm) on the same shapes, the activation quantizer's
+HBM rate, the `roofline` object for the dominant kernel, and the CPU baseline (the reference's own
+AVX512-VNNI kernel built from its sources with per-row blocks, on the host).
 
 Inputs are synthetic, as BASELINE config 5 specifies: Student-t(nu=3) activations with 0.1 % of
-the channels scaled x50, quantized per (token, 128 block); int8 weights uniform in [-127,127] with
-per-row scales U(0.001, 0.02), handed over as the reference's packed (E8CQ-style) blobs and
+the channels scaled x50, quantized per token (and per (token, 128 block) for the per-128 legs);
+int8 weights uniform in [-127,127] with per-row scales U(0.001, 0.02), handed over as the reference's packed (E8CQ-style) blobs and
 re-laid out on the device at load.
 """
 from __future__ import annotations
@@ -99,29 +102,35 @@ def physical_cores():
 
 
 def cpu_baseline(budget_s=12.0):
-    """The reference's e2_i8_gemm_avx512 (oracle/_ref, built from its sources) on the host cores,
-    N-split across threads like text.c's gemm_segs, over a bounded sample of the same sweep:
-    M_s = 2048 rows of each shape."""
+    """The reference's e2_i8_gemm_avx512 (oracle/_ref, built from its sources with one activation
+    block per row, E2_I8_BLOCK = K, int8.h:61-70: per-token scales, like the timed sweep) on the
+    host cores, N-split across threads like text.c's gemm_segs, over a bounded sample of the same
+    sweep: M_s = 2048 rows of each shape, f32 output."""
     sys.path.insert(0, ROOT)
     from oracle.binding import Oracle, Ref, Q8W
     flags = cpu_flags()
     threads = physical_cores()
     Ms = 2048
     rng = np.random.default_rng(7)
-    use_ref = Ref.available() and {"avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512_vnni"} <= flags
+    have_ref = all(os.path.exists(Ref.per_row_path(K)) for K, _ in SHAPES)
+    use_ref = have_ref and {"avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512_vnni"} <= flags
     kind, which = ("reference", "avx512") if use_ref else ("port", None)
-    if not use_ref and Ref.available() and "avx_vnni" in flags:
+    if not use_ref and have_ref and "avx_vnni" in flags:
         kind, which = "reference", "vnni_range"
-    ref = Ref() if kind == "reference" else None
-    orc = Oracle() if ref is None else None
+    refs = {K: Ref.per_row(K) for K in {k for k, _ in SHAPES}} if kind == "reference" else None
+    orc = Oracle() if refs is None else None
     work = []
     for K, N in SHAPES:
         qa = rng.integers(-127, 128, (Ms, K), dtype=np.int8)
         qb = (qa.view(np.uint8) ^ 0x80).view(np.int8).copy()
-        as_ = rng.uniform(0.001, 0.05, (Ms, K // 128)).astype(np.float32)
         w, ws, wq = packed_weight(rng, N, K)
-        bsq = np.zeros((K // 128 * N + 32,), np.int32)
-        bsq[: K // 128 * N] = w.reshape(N, K // 128, 128).sum(-1).T.astype(np.int32).reshape(-1)
+        if refs is None:  # the threaded port has per-128 blocks only
+            as_ = rng.uniform(0.001, 0.05, (Ms, K // 128)).astype(np.float32)
+            bsq = np.zeros(1, np.int32)
+        else:
+            as_ = rng.uniform(0.001, 0.05, (Ms, 1)).astype(np.float32)
+            bsq = np.zeros((N + 32,), np.int32)
+            bsq[:N] = w.astype(np.int32).sum(1)
         wsp = np.zeros(N + 32, np.float32)
         wsp[:N] = ws
         wqp = np.concatenate([wq, np.zeros(4 * K * 8, np.int8)])
@@ -130,11 +139,11 @@ def cpu_baseline(budget_s=12.0):
 
     def run_shape(item):
         K, N, qa, qb, as_, w, ws, wqp, wsp, bsq, y = item
-        if ref is None:
+        if refs is None:
             orc.i8_gemm_mt(qa, as_, w, ws, nthreads=threads)
             return
-        q = Q8W(wqp.ctypes.data, bsq.ctypes.data, wsp.ctypes.data, N, K, K // 128, N, -1e31, 1e31, 1)
-        fn = getattr(ref.lib, f"e2_i8_gemm_{which}")
+        q = Q8W(wqp.ctypes.data, bsq.ctypes.data, wsp.ctypes.data, N, K, 1, N, -1e31, 1e31, 1)
+        fn = getattr(refs[K].lib, f"e2_i8_gemm_{which}")
         tile = max(16, (N // (threads * 2)) // 16 * 16)
         ranges = [(a, min(N, a + tile)) for a in range(0, N, tile)]
         nxt = [0]
@@ -172,8 +181,10 @@ def cpu_baseline(budget_s=12.0):
         "unit": "TOPS",
         "cores": threads,
         "kind": kind,
-        "sample": (f"the config-5 sweep on M={Ms} rows per shape (of 65536), f32 output "
-                   f"(e2_i8_gemm_{which or 'port'} N-split over {threads} threads); best of "
+        "sample": (f"the config-5 sweep on M={Ms} rows per shape (of 65536), f32 output, "
+                   + ("per-token scales (the reference built with E2_I8_BLOCK=K) " if refs else
+                      "per-128 scales (the threaded port; no AVX-512 VNNI per-row build here) ")
+                   + f"(e2_i8_gemm_{which or 'port'} N-split over {threads} threads); best of "
                    f"{len(times)} passes; median {ops_per_pass / float(np.median(times)) / 1e12:.4f} TOPS"),
         "kernel": f"e2_i8_gemm_{which}" if which else "or_i8_gemm_mt",
         "cpu_avx512_vnni": "avx512_vnni" in flags,
@@ -292,7 +303,7 @@ def summarize_pmc(fetch_csv, write_csv):
     res["calibration"] = (f"a plain {COPY_BYTES >> 20} MiB device copy in the same run: bytes / "
                           "counter reading gives the per-counter scale")
     os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
-    with open(os.path.join(ROOT, "profiles", "gemm_q_traffic.json"), "w") as f:
+    with open(os.path.join(ROOT, "profiles", "gemm_tok_traffic.json"), "w") as f:
         json.dump(res, f, indent=1)
     print(json.dumps(res, indent=1))
 
@@ -311,7 +322,7 @@ def main():
                     help="one calibration copy + one launch per GEMM (for rocprofv3 --pmc runs)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn FETCH_SIZE / WRITE_SIZE counter CSVs of a --probe run into "
-                         "profiles/gemm_q_traffic.json")
+                         "profiles/gemm_tok_traffic.json")
     args = ap.parse_args()
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
@@ -338,18 +349,28 @@ def main():
     cases = []
     for K, N in SHAPES:
         x = student_t_acts(torch, K, gen, dev)
-        qa, as_ = e2mi.quantize(x)
+        qt, st = e2mi.quantize(x, block=K)   # per-token scales (config 5)
+        qa, as_ = e2mi.quantize(x)           # per (token, 128) scales, the reference's default
         w, ws, wq = packed_weight(rng, N, K)
         W = e2mi.DeviceWeight.from_packed(wq, ws, N, K)
         yq = torch.empty((M, N), dtype=torch.int8, device=dev)
         ys = torch.empty((M, N // 128), dtype=torch.float32, device=dev)
         yf = torch.empty((M, N), dtype=torch.float32, device=dev)
-        cases.append(dict(K=K, N=N, x=x, qa=qa, as_=as_, W=W, yq=yq, ys=ys, yf=yf))
+        wt = torch.from_numpy(w).to(dev)
+        cases.append(dict(K=K, N=N, x=x, qt=qt, st=st, qa=qa, as_=as_, W=W, yq=yq, ys=ys, yf=yf, wt=wt))
     torch.cuda.synchronize()
 
     lib = e2mi.load()
     stream = torch.cuda.current_stream()
     sp = e2mi.stream_ptr(stream)
+
+    def gemm_tok(c):
+        e2mi.check(lib.e2mi_i8_gemm_tok(sp, e2mi.ptr(c["yf"]), c["N"], e2mi.ptr(c["qt"]),
+                                        e2mi.ptr(c["st"]), c["W"].ref, M, 0, c["N"]), "i8_gemm_tok")
+
+    def gemm_tok_q(c):
+        e2mi.check(lib.e2mi_i8_gemm_tok_q(sp, e2mi.ptr(c["yq"]), e2mi.ptr(c["ys"]), e2mi.ptr(c["qt"]),
+                                          e2mi.ptr(c["st"]), c["W"].ref, M), "i8_gemm_tok_q")
 
     def gemm_q(c):
         e2mi.check(lib.e2mi_i8_gemm_q(sp, e2mi.ptr(c["yq"]), e2mi.ptr(c["ys"]), e2mi.ptr(c["qa"]),
@@ -361,7 +382,7 @@ def main():
 
     def step():
         for c in cases:
-            gemm_q(c)
+            gemm_tok(c)
 
     if args.probe:
         # calibration: a plain copy of COPY_BYTES (read COPY_BYTES, write COPY_BYTES), then one
@@ -388,7 +409,7 @@ def main():
     for s in range(args.steps):
         for i, c in enumerate(cases):
             ev[s][i][0].record(stream)
-            gemm_q(c)
+            gemm_tok(c)
             ev[s][i][1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -398,13 +419,29 @@ def main():
     ms_per_step = wall / args.steps * 1e3
     value = sum(ops) / (wall / args.steps) / 1e12
 
-    # the reference contract (f32 output) on the same inputs, and the quantizer
-    f32_t = [time_calls(torch, lambda c=c: gemm_f32(c), max(3, args.steps // 2)) for c in cases]
-    # the fast fold (int32 accumulators still exact; f32 within a few ulp of the reference's order)
+    # the other contracts on the same activations: per-token with the fused requantizing epilogue;
+    # per-128 scales (exact and fast fold, f32 and requant); the vendor int8 GEMM for scale
+    reps = max(3, args.steps // 2)
+
+    def sweep(fn):
+        for c in cases:  # first calls (library heuristics, attribute set-up) stay untimed
+            fn(c)
+        torch.cuda.synchronize()
+        t = [time_calls(torch, lambda c=c: fn(c), reps) for c in cases]
+        return {"tops": round(sum(ops) / sum(t) / 1e12, 2),
+                "pct_of_int8_mfma_peak": round(100 * sum(ops) / sum(t) / 1e12 / PEAK_INT8_TOPS, 2),
+                "per_shape_us": {f"{c['K']}x{c['N']}": round(x * 1e6, 2) for c, x in zip(cases, t)}}
+
+    tok_q = sweep(gemm_tok_q)
+    b128_q, b128_f32 = sweep(gemm_q), sweep(gemm_f32)
     prev_fold = e2mi.set_gemm_fold("fast")
-    fast_t = [time_calls(torch, lambda c=c: gemm_q(c), max(3, args.steps // 2)) for c in cases]
-    fast_f32_t = [time_calls(torch, lambda c=c: gemm_f32(c), max(3, args.steps // 2)) for c in cases]
+    fast_q, fast_f32 = sweep(gemm_q), sweep(gemm_f32)
     e2mi.set_gemm_fold(prev_fold)
+    try:
+        vendor = sweep(lambda c: torch._int_mm(c["qa"], c["wt"].t()))
+        vendor["note"] = "torch._int_mm (hipBLASLt), int32 output, no scales or epilogue"
+    except (RuntimeError, AttributeError) as e:  # pragma: no cover - depends on the torch build
+        vendor = {"error": str(e)[:200]}
     q_t = time_calls(torch, lambda: e2mi.quantize(cases[0]["x"], q=cases[0]["qa"],
                                                   scales=cases[0]["as_"]), 10)
     q_bytes = M * 768 * (4 + 1) + M * 6 * 4
@@ -412,10 +449,10 @@ def main():
     # roofline: the dominant launch of the step (longest average duration)
     dom = int(np.argmax(per_launch))
     c = cases[dom]
-    algo_bytes = M * c["K"] + 4 * M * c["K"] // 128 + c["N"] * c["K"] + 4 * c["N"] + M * c["N"] + 4 * M * c["N"] // 128
+    algo_bytes = M * c["K"] + 4 * M + c["N"] * c["K"] + 4 * c["N"] + 4 * M * c["N"]
     ach = ops[dom] / per_launch[dom] / 1e12
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "gemm_q_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "gemm_tok_traffic.json")
     if os.path.exists(tpath):
         try:
             tj = json.load(open(tpath))
@@ -435,24 +472,25 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (BASELINE config 5: Student-t nu=3 activations, 0.1% outlier channels x50; uniform int8 weights from packed blobs)",
+        "data": "synthetic (BASELINE config 5: Student-t nu=3 activations, 0.1% outlier channels x50, "
+                "quantized per token; uniform int8 weights from packed blobs)",
         "config": {"workload": "config-5 int8 GEMM sweep, M=65536, (K,N) in " + str(SHAPES)
-                   + ", int8-requant epilogue", "global_batch": M, "seq_len": 512,
-                   "parallelism": "none (1 GPU)"},
+                   + ", per-token activation scales, f32 output (e2_i8_gemm's contract)",
+                   "global_batch": M, "seq_len": 512, "parallelism": "none (1 GPU)"},
         "pct_of_int8_mfma_peak": round(100 * value / PEAK_INT8_TOPS, 2),
         "per_shape_us": {f"{c['K']}x{c['N']}": round(t * 1e6, 2) for c, t in zip(cases, per_launch)},
-        "f32_out": {"tops": round(sum(ops) / sum(f32_t) / 1e12, 2),
-                    "per_shape_us": {f"{c['K']}x{c['N']}": round(t * 1e6, 2) for c, t in zip(cases, f32_t)}},
-        "fast_fold": {"tops": round(sum(ops) / sum(fast_t) / 1e12, 2),
-                      "pct_of_int8_mfma_peak": round(100 * sum(ops) / sum(fast_t) / 1e12 / PEAK_INT8_TOPS, 2),
-                      "per_shape_us": {f"{c['K']}x{c['N']}": round(t * 1e6, 2) for c, t in zip(cases, fast_t)},
-                      "f32_out_tops": round(sum(ops) / sum(fast_f32_t) / 1e12, 2),
-                      "note": "E2MI_GEMM_FOLD=fast / e2mi_gemm_set_fold(1): fold by as per block, ws once; "
-                              "int32 accumulators exact, f32 within 1e-4 rel of the reference order"},
+        "per_token_requant": tok_q,
+        "per128_exact_requant": b128_q,
+        "per128_exact_f32": b128_f32,
+        "per128_fast_requant": fast_q,
+        "per128_fast_f32": fast_f32,
+        "fast_fold_note": "E2MI_GEMM_FOLD=fast / e2mi_gemm_set_fold(1): fold by as per block, ws "
+                          "once; int32 accumulators exact, f32 within 1e-4 rel of the reference order",
+        "vendor_int_mm": vendor,
         "quantize_65536x768": {"us": round(q_t * 1e6, 2), "GB/s": round(q_bytes / q_t / 1e9, 1)},
         "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic,
-                     "kernel": f"k_gemm requant epilogue {c['K']}x{c['N']}",
+                     "kernel": f"k_gemm_p per-token f32 {c['K']}x{c['N']}",
                      "algorithmic_bytes": algo_bytes, "ops": ops[dom],
                      "note": "int8 ops counted as TFLOP/s; bound by the algorithmic roofline max(t_mfma, t_hbm)"},
     }

@@ -100,6 +100,16 @@ __device__ inline void dma4(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
                  : "memory");
 }
 
+// 16-byte buffer store. A VALU write of the store's data registers right after it needs a wait
+// state (the store reads its data late: without it the last lanes of each 16 store the new
+// values); the compiler does not insert one after the buffer-store builtin, so the store is
+// issued here with its own s_nop. The compiler does not count it: waits are explicit.
+__device__ inline void bstore16(v4u r, v4u d, uint32_t voff, uint32_t soff) {
+    asm volatile("buffer_store_dwordx4 %0, %1, %2, %3 offen\n\ts_nop 1"
+                 ::"v"(d), "v"(voff), "s"(r), "s"(soff)
+                 : "memory");
+}
+
 // The accumulator-dump kernel (e2mi_i8_gemm_acc, the parity hook for "bit-exact int32
 // accumulators"): 128 x 128 tiles of 4 waves of 64 x 64, two direct-to-LDS stages, the exact fold
 // after each step's MFMAs, every step's int32 accumulators written to accd [nb][M][N], f32 output
@@ -385,8 +395,36 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmA
 
 // 8 waves of 32 x 128 (one 32-row MFMA tile by four 32-column ones): NWM x NWN waves, BM = 32 NWM,
 // BN = 128 NWN
-template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
+// 4 x 4 transpose inside each quad of lanes (DPP quad permutes): lane 4q + i enters with
+// v[j] = X[j][i] and leaves with v[j] = X[i][j]. Two exchange stages, one per index bit: where a
+// lane's bit differs from a register's, the value trades places with the partner lane's.
+template <int CTRL>
+__device__ inline float quad_read(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ inline void quad_xpose(float (&v)[4], int lane) {
+    constexpr int kXor2 = 0x4E, kXor1 = 0xB1;  // quad_perm [2,3,0,1], [1,0,3,2]
+    const bool b1 = (lane & 2) != 0, b0 = (lane & 1) != 0;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const float r = quad_read<kXor2>(b1 ? v[j] : v[j + 2]);
+        v[j] = b1 ? r : v[j];
+        v[j + 2] = b1 ? v[j + 2] : r;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j += 2) {
+        const float r = quad_read<kXor1>(b0 ? v[j] : v[j + 1]);
+        v[j] = b0 ? r : v[j];
+        v[j + 1] = b0 ? v[j + 1] : r;
+    }
+}
+
+// TOKM: 0 per-(row, 128) activation scales; 1 per-token scales; 2 per-token scales with 16-byte
+// f32 output stores (EPI_F32 without bias or clamp; N, ldy and the output 16-byte aligned)
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, int TOKM>
 __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int tiles_n, int tiles) {
+    constexpr bool TOK = TOKM > 0;
+    static_assert(TOKM < 2 || (EPI == EPI_F32 && POST == 0), "16-byte stores: f32 epilogue, no bias or clamp");
     constexpr int NWAVE = NWM * NWN;
     static_assert(BM == 32 * NWM && BN == 128 * NWN && NWAVE == 8, "8 waves of 32x128");
     constexpr int AI = BM / 8 / NWAVE, BI = BN / 8 / NWAVE;  // 1-KB loads per wave per step
@@ -394,14 +432,15 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
     constexpr int TILE = (BM + BN) * 128;                    // A | W of one step
     constexpr int SHALF = 64 * NWAVE * 4;                    // as of one step (one per lane)
     constexpr int SSLOT = 2 * SHALF;                         // as | ws
-    constexpr bool XACT = !FAST;
+    constexpr bool XACT = TOK || !FAST;
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned char *const sscale = smem + kPStages * TILE;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / NWN, wn = wave % NWN;
-    const int nb = p.K / kQBlock;
+    const int nb = p.K / kQBlock;   // K steps per tile
+    const int nsb = TOK ? 1 : nb;   // activation scales per row
 
     // this workgroup's tiles: chunk [c0, c1) of the tile list, every per-th tile from c0 + li
     const int nx = (gridDim.x % 8 == 0) ? 8 : 1;
@@ -414,7 +453,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
 
     const v4u rA = rsrc_words(p.A, (uint32_t)((size_t)p.M * p.lda));
     const v4u rW = rsrc_words(p.W, (uint32_t)((size_t)p.N * p.ldw));
-    const v4u rS = rsrc_words(p.as, (uint32_t)((size_t)p.M * nb * 4));
+    const v4u rS = rsrc_words(p.as, (uint32_t)((size_t)p.M * nsb * 4));
     const v4u rV = rsrc_words(p.ws, (uint32_t)((size_t)p.N * 4));
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)smem);
 
@@ -427,7 +466,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
     const int swl = ((lane & 7) ^ ((wave & 1) * 4 + ((lane >> 4) & 3))) << 4;
     const uint32_t vla = (uint32_t)(lane >> 3) * (uint32_t)p.lda + swl;
     const uint32_t vlb = (uint32_t)(lane >> 3) * (uint32_t)p.ldw + swl;
-    const uint32_t vls = (uint32_t)lane * (uint32_t)nb * 4;
+    const uint32_t vls = (uint32_t)lane * (uint32_t)nsb * 4;
     int ij = 0, ikb = 0;  // next step to issue
     // a step's 8 loads per wave (AI of A, BI of W, as, ws) in 4 parts of 2, so that issuing them is
     // spread over the step's MFMAs: issuing all at once stalls the wave on the vector-memory path
@@ -442,7 +481,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
         is.st = lds0 + (uint32_t)((g % kPStages) * TILE);
         is.sl = lds0 + (uint32_t)(kPStages * TILE + (g % kPSlots) * SSLOT + wave * 256);
         is.ko = (uint32_t)(ikb * kQBlock);
-        is.ks = (uint32_t)(ikb * 4);
+        is.ks = TOK ? 0u : (uint32_t)(ikb * 4);
         if (++ikb == nb) {
             ikb = 0;
             ++ij;
@@ -458,7 +497,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
             dma16(rW, is.st + BM * 128 + ((i - AI) * NWAVE + wave) * 1024,
                   vlb + (uint32_t)(is.n0 + ((i - AI) * NWAVE + wave) * 8) * (uint32_t)p.ldw, is.ko);
         else if (i == AI + BI)
-            dma4(rS, is.sl, vls + (uint32_t)(is.m0 + min(wave * 64, BM - 64)) * (uint32_t)nb * 4, is.ks);
+            dma4(rS, is.sl, vls + (uint32_t)(is.m0 + min(wave * 64, BM - 64)) * (uint32_t)nsb * 4, is.ks);
         else
             dma4(rV, is.sl + SHALF, (uint32_t)(is.n0 + min(wave * 64, BN - 64) + lane) * 4, 0);
     };
@@ -578,6 +617,91 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
             ++cj;
         }
     };
+    // per-token scales (the reference built with a per-row block, E2_I8_BLOCK = K): the int32
+    // accumulators run over the whole K of a tile and are folded once, f = fma((float)acc,
+    // RN(as[m] * ws[n]), 0), at the tile's last step, followed by its epilogue.
+    // TOKM 2 (f32 output): each 4 x 4 block of a lane quad's registers is transposed across the
+    // quad (DPP), so a lane holds 4 consecutive columns of one row and writes them with one 16-byte
+    // store: exactly 16 stores per lane per tile (columns past N are sent past the descriptor's
+    // range rather than skipped). Vector-memory operations complete in issue order and the 16
+    // stores follow the loads of the next two steps, so those two steps' waits for their stage
+    // allow 8 + 16 operations outstanding: the stores drain while they compute instead of before.
+    int last_epi = -8;  // step of the last 16-byte-store epilogue
+    // after the transpose lane (h = lane / 32, i = lane % 4) holds row 8 g + 4 h + i of register
+    // group g and columns (lane % 32) & ~3 .. + 3 of each 32-column slice
+    const int fcol4 = wn * 128 + (lane & 28);
+    const uint32_t vst4 = (uint32_t)((wm * 32 + (lane >> 5) * 4 + (lane & 3)) * p.ldy + fcol4) * 4u;
+    const int ldy4 = p.ldy * 4;
+    const v4u ry = rsrc_words(p.Y, (uint32_t)min((long)p.M * p.ldy * 4, 0x7fffffffL));
+    // register group g of a 32-column slice (rows past M fall past the descriptor's range)
+    auto store_group4 = [&](const float (&fs)[16], int g, uint32_t base, int col0) {
+        float v[4] = {fs[4 * g], fs[4 * g + 1], fs[4 * g + 2], fs[4 * g + 3]};
+        quad_xpose(v, lane);
+        const uint32_t vso = (col0 + fcol4 < p.N) ? vst4 : 0x80000000u;
+        const uint32_t so = __builtin_amdgcn_readfirstlane(base + (uint32_t)(g * 8 * ldy4));
+        const v4u d = {__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                       __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])};
+        bstore16(ry, d, vso, so);
+    };
+    auto step_tok = [&](int g) {
+        if (g + 1 >= G) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else if (TOKM == 2 && g - last_epi <= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L + 16) : "memory");
+        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
+        __syncthreads();
+        const Issue is_next = issue_prep(g + 2);
+        const unsigned char *sb = smem + (g % kPStages) * TILE;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            issue_part(is_next, kk);
+            const v4i af = *(const v4i *)(sb + offa[kk]);
+            v4i bf[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) bf[t] = *(const v4i *)(sb + offb[kk] + t * 4096);
+#pragma unroll
+            for (int tn = 0; tn < 4; tn++) acc0[tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[tn], acc0[tn], 0, 0, 0);
+        }
+        if (++ckb == nb) {
+            const unsigned char *slot = sscale + (g % kPSlots) * SSLOT;
+            read_ws(slot);
+            const float *sp = (const float *)slot;
+            const int pm0 = tile_m0(cj), pn0 = tile_n0(cj);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 a4 = *(const float4 *)((const unsigned char *)sp + offs + q * 32);
+                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+                for (int tn = 0; tn < 4; tn++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        f[tn][q * 4 + j] = __builtin_fmaf((float)acc0[tn][q * 4 + j], __fmul_rn(av[j], wsr[tn]), 0.f);
+            }
+#pragma unroll
+            for (int tn = 0; tn < 4; tn++) acc0[tn] = zero;
+            if constexpr (TOKM == 2) {
+                const uint32_t tb = (uint32_t)(pm0 * p.ldy + pn0) * 4u;
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int gg = 0; gg < 4; gg++) store_group4(f[t], gg, tb + t * 128, pn0 + t * 32);
+                last_epi = g;
+            } else if constexpr (EPI == EPI_F32) {
+                p_epilogue_f32<POST, false>(p, f, wsr, pm0, pn0, wm, wn, lane);
+            } else {
+                __syncthreads();
+                p_epilogue_q<BM, BN, NWM, NWN, EPI, false, POST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
+                                                                 (float *)(smem + (g % kPStages) * TILE));
+            }
+            ckb = 0;
+            ++cj;
+        }
+    };
+    if constexpr (TOK) {
+#pragma unroll
+        for (int tn = 0; tn < 4; tn++) acc0[tn] = zero;
+        for (int g = 0; g < G; g++) step_tok(g);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
+    }
     int g = 0;
     for (; g + 1 < G; g += 2) {
         step(g, acc0, acc1);
@@ -619,13 +743,13 @@ static int num_cus() {
     return cus;
 }
 
-template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, int TOKM>
 static int launch_p1(hipStream_t s, const GemmArgs &p) {
     constexpr size_t lds = p_lds_bytes<BM, BN, NWM * NWN>();
     static_assert(lds <= 160 * 1024, "LDS budget");
     static_assert(EPI == EPI_F32 || (8 * 8 * ((EPI == EPI_GEGLU ? 64 : 128) + 4) + 8 * 32) * 4 <= (BM + BN) * 128,
                   "epilogue scratch fits a stage");
-    auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST>;
+    auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST, TOKM>;
     static bool attr = false;
     if (!attr) {
         if (check_hip(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
@@ -647,11 +771,25 @@ static int launch_p1(hipStream_t s, const GemmArgs &p) {
 // POST: bit 0 adds a bias, bit 1 clamps to [lo, hi]; only "none" and "both" are instantiated (the
 // bias pointer may be null and an absent clamp is +-1e31)
 template <int BM, int BN, int NWM, int NWN, int EPI>
-static int launch_p(hipStream_t s, const GemmArgs &p) {
+static int launch_p(hipStream_t s, const GemmArgs &p, bool tok = false) {
     const bool post = p.bias != nullptr || p.lo > -1e30f || p.hi < 1e30f;
+    if constexpr (EPI != EPI_GEGLU) {
+        if (tok) {  // one fold per output: the fast fold has nothing to save
+            if constexpr (EPI == EPI_F32) {
+                // 16-byte stores of 4-column groups (N, ldy, the output 16-byte aligned); no bias
+                // or clamp
+                if (!post && p.N % 4 == 0 && p.ldy % 4 == 0 && aligned16(p.Y))
+                    return launch_p1<BM, BN, NWM, NWN, EPI, false, 0, 2>(s, p);
+            }
+            return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3, 1>(s, p)
+                        : launch_p1<BM, BN, NWM, NWN, EPI, false, 0, 1>(s, p);
+        }
+    }
     if (fold_fast())
-        return post ? launch_p1<BM, BN, NWM, NWN, EPI, true, 3>(s, p) : launch_p1<BM, BN, NWM, NWN, EPI, true, 0>(s, p);
-    return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3>(s, p) : launch_p1<BM, BN, NWM, NWN, EPI, false, 0>(s, p);
+        return post ? launch_p1<BM, BN, NWM, NWN, EPI, true, 3, 0>(s, p)
+                    : launch_p1<BM, BN, NWM, NWN, EPI, true, 0, 0>(s, p);
+    return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3, 0>(s, p)
+                : launch_p1<BM, BN, NWM, NWN, EPI, false, 0, 0>(s, p);
 }
 
 static int launch_dump(hipStream_t s, const GemmArgs &p) {
@@ -688,7 +826,7 @@ static int check_args(const GemmArgs &p, const char *who) {
     return 0;
 }
 
-int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump) {
+int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump, bool tok = false) {
     if (check_args(p, "i8_gemm")) return -1;
     if (!p.Y || p.ldy < p.N) {
         set_error("i8_gemm: null output or ldy < N");
@@ -701,17 +839,17 @@ int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump) {
         }
         return launch_dump(s, p);
     }
-    return launch_p<256, 128, 8, 1, EPI_F32>(s, p);
+    return launch_p<256, 128, 8, 1, EPI_F32>(s, p, tok);
 }
 
-int launch_gemm_i8q(hipStream_t s, GemmArgs p) {
+int launch_gemm_i8q(hipStream_t s, GemmArgs p, bool tok = false) {
     if (check_args(p, "i8_gemm_q")) return -1;
     if (p.N % 128 || !p.Yq || !p.ys || p.ldyq < p.N || p.ldyq % 16 || !aligned16(p.Yq) ||
         p.ldys < p.N / 128) {
         set_error("i8_gemm_q: N must be a multiple of 128 with a 16-byte aligned int8 output");
         return -1;
     }
-    return launch_p<256, 128, 8, 1, EPI_I8Q>(s, p);
+    return launch_p<256, 128, 8, 1, EPI_I8Q>(s, p, tok);
 }
 
 int launch_gemm_geglu(hipStream_t s, GemmArgs p) {
@@ -804,6 +942,32 @@ extern "C" int e2mi_i8_gemm_q(e2mi_stream stream, int8_t *yq, float *ys, const i
     p.ys = ys;
     p.ldys = w->N / 128;
     return launch_gemm_i8q((hipStream_t)stream, p);
+}
+
+// per-token activation scales (a_scales [M], the reference's int8 path built with one block per
+// row, int8.h:61-70 E2_I8_BLOCK = K)
+extern "C" int e2mi_i8_gemm_tok(e2mi_stream stream, float *y, int ldy, const int8_t *qa,
+                                const float *a_scales, const e2mi_q8w *w, int M, int n0, int n1) {
+    if (!weight_ok(w, "i8_gemm_tok")) return -1;
+    if (n0 < 0 || n1 > w->N || n0 >= n1 || !y) {
+        set_error("i8_gemm_tok: bad column range [%d,%d) for N=%d", n0, n1, w ? w->N : 0);
+        return -1;
+    }
+    GemmArgs p = make_args(qa, a_scales, w, M, n0, n1);
+    p.Y = y + n0;
+    p.ldy = ldy;
+    return launch_gemm_f32((hipStream_t)stream, p, false, true);
+}
+
+extern "C" int e2mi_i8_gemm_tok_q(e2mi_stream stream, int8_t *yq, float *ys, const int8_t *qa,
+                                  const float *a_scales, const e2mi_q8w *w, int M) {
+    if (!weight_ok(w, "i8_gemm_tok_q")) return -1;
+    GemmArgs p = make_args(qa, a_scales, w, M, 0, w->N);
+    p.Yq = yq;
+    p.ldyq = w->N;
+    p.ys = ys;
+    p.ldys = w->N / 128;
+    return launch_gemm_i8q((hipStream_t)stream, p, true);
 }
 
 extern "C" int e2mi_i8_gemm_geglu(e2mi_stream stream, int8_t *q, float *qs, float *g,

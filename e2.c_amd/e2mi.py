@@ -46,6 +46,8 @@ SIGNATURES = {
     "e2mi_i8_gemm": (_I, [_P, _P, _I, _P, _P, C.POINTER(Q8W), _I, _I, _I]),
     "e2mi_i8_gemm_acc": (_I, [_P, _P, _I, _P, _P, _P, C.POINTER(Q8W), _I, _I, _I]),
     "e2mi_i8_gemm_q": (_I, [_P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
+    "e2mi_i8_gemm_tok": (_I, [_P, _P, _I, _P, _P, C.POINTER(Q8W), _I, _I, _I]),
+    "e2mi_i8_gemm_tok_q": (_I, [_P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
     "e2mi_i8_gemm_geglu": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
     "e2mi_gemm_set_fold": (_I, [_I]),
     "e2mi_interleave_gate_up": (_I, [_P, _P, _P, _P, _P, _P, _I, _I]),
@@ -235,6 +237,27 @@ def i8_gemm_q(qa, as_, w: DeviceWeight, stream=None):
     ys = torch.empty((M, w.q.N // 128), dtype=torch.float32, device=qa.device)
     check(load().e2mi_i8_gemm_q(stream_ptr(stream), ptr(yq), ptr(ys), ptr(qa), ptr(as_), w.ref, M),
           "i8_gemm_q")
+    return yq, ys
+
+
+def i8_gemm_tok(qa, as_, w: DeviceWeight, n0=0, n1=None, y=None, stream=None):
+    """GEMM over per-token activation scales as_ [M] (or [M, 1])."""
+    import torch
+    M = qa.shape[0]
+    n1 = w.q.N if n1 is None else n1
+    y = torch.zeros((M, w.q.N), dtype=torch.float32, device=qa.device) if y is None else y
+    check(load().e2mi_i8_gemm_tok(stream_ptr(stream), ptr(y), y.stride(0), ptr(qa), ptr(as_), w.ref,
+                                  M, n0, n1), "i8_gemm_tok")
+    return y
+
+
+def i8_gemm_tok_q(qa, as_, w: DeviceWeight, stream=None):
+    import torch
+    M = qa.shape[0]
+    yq = torch.empty((M, w.q.N), dtype=torch.int8, device=qa.device)
+    ys = torch.empty((M, w.q.N // 128), dtype=torch.float32, device=qa.device)
+    check(load().e2mi_i8_gemm_tok_q(stream_ptr(stream), ptr(yq), ptr(ys), ptr(qa), ptr(as_), w.ref, M),
+          "i8_gemm_tok_q")
     return yq, ys
 
 

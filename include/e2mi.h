@@ -80,6 +80,16 @@ int e2mi_i8_gemm_acc(e2mi_stream stream, float *y, int ldy, int32_t *acc, const 
 int e2mi_i8_gemm_q(e2mi_stream stream, int8_t *yq, float *ys, const int8_t *qa,
                    const float *a_scales, const e2mi_q8w *w, int M);
 
+/* The same two GEMMs for per-token activation scales: a_scales is [M] (one scale per row, the
+ * reference's int8 path built with a single block per row, int8.h:61-70 E2_I8_BLOCK = K; the
+ * activations come from e2mi_quantize with block = K). The int32 accumulators run over the whole
+ * K and are folded once: y = fma((float)acc, RN(as[m]*ws[n]), 0) (+bias), clamped. _tok_q
+ * requantizes the output per (row, 128 columns) like e2mi_i8_gemm_q. */
+int e2mi_i8_gemm_tok(e2mi_stream stream, float *y, int ldy, const int8_t *qa, const float *a_scales,
+                     const e2mi_q8w *w, int M, int n0, int n1);
+int e2mi_i8_gemm_tok_q(e2mi_stream stream, int8_t *yq, float *ys, const int8_t *qa,
+                       const float *a_scales, const e2mi_q8w *w, int M);
+
 /* gate|up GEMM with the GeGLU product and its quantization fused in the epilogue (text.c:424-468
  * gate_quant, fused into the producing GEMM). w holds 2*F rows interleaved per 64 as
  * [32 gate rows | 32 up rows] (see e2mi_interleave_gate_up). Writes q [M][F] int8, qs [M][F/128]

@@ -290,9 +290,12 @@ class Q8W(C.Structure):
 class Ref:
     """The reference's own kernels, compiled from /root/reference/src by oracle/Makefile."""
 
-    def __init__(self, path=REF_SO):
+    def __init__(self, path=REF_SO, block=128):
+        """block: the build's E2_I8_BLOCK (int8.h:61-70); the per-row builds under _ref/b<K>/ set
+        it to K, so activation scales are one per row and weight block sums one per row."""
         if not os.path.exists(path):
             raise FileNotFoundError(path)
+        self.block = block
         L = self.lib = C.CDLL(path)
         L.e2_cpu_init.restype = None
         L.e2_cpu_init()
@@ -314,10 +317,19 @@ class Ref:
     def available(path=REF_SO):
         return os.path.exists(path)
 
+    @staticmethod
+    def per_row_path(K):
+        """The reference built with E2_I8_BLOCK = K (oracle/Makefile ROWK)."""
+        return os.path.join(HERE, "_ref", f"b{K}", "libe2ref.so")
+
+    @classmethod
+    def per_row(cls, K):
+        return cls(cls.per_row_path(K), block=K)
+
     def quantize(self, x, which="avx512"):
         x = _need(np.ascontiguousarray(x, np.float32), np.float32)
         M, K = x.shape
-        nb = (K + 127) // 128
+        nb = (K + self.block - 1) // self.block
         q = np.empty((M, K), np.int8)
         s = np.empty((M, nb), np.float32)
         getattr(self.lib, f"e2_quantize_blocks_{which}")(_ptr(q), _ptr(s), _ptr(x), M, K,
@@ -349,12 +361,15 @@ class Ref:
         # zero-padded copies with the leading dimension Npad they index with
         wsp = np.zeros(Npad + 32, np.float32)
         wsp[:N] = ws[:N]
-        bs_flat = np.zeros(bsq.shape[0] * Npad + 32, np.int32)
-        bs_flat[: bsq.shape[0] * Npad] = bsq[:, :Npad].reshape(-1)
+        nbq = bsq.shape[0]
+        bs_pad = np.zeros((nbq, Npad), np.int32)
+        bs_pad[:, : min(Npad, bsq.shape[1])] = bsq[:, :Npad]
+        bs_flat = np.zeros(nbq * Npad + 32, np.int32)
+        bs_flat[: nbq * Npad] = bs_pad.reshape(-1)
         wq_pad = np.zeros(wq.size + 4 * kq * 32, np.int8)
         wq_pad[: wq.size] = wq
-        q = Q8W(wq_pad.ctypes.data, bs_flat.ctypes.data, wsp.ctypes.data, N, K, (K + 127) // 128,
-                Npad, -1e31, 1e31, 1)
+        q = Q8W(wq_pad.ctypes.data, bs_flat.ctypes.data, wsp.ctypes.data, N, K,
+                (K + self.block - 1) // self.block, Npad, -1e31, 1e31, 1)
         y = np.zeros((M, N), np.float32)
         getattr(self.lib, f"e2_i8_gemm_{which}")(_ptr(y), _ptr(qb), _ptr(as_), C.byref(q), M, N,
                                                  n0, n1)

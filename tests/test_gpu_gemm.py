@@ -155,3 +155,83 @@ def test_gemm_geglu_epilogue(gpu, oracle, rng, M):
     near = np.abs(scaled - (np.floor(scaled) + 0.5)) < 0.002
     assert np.all((d == 0) | ((d == 1) & near))
     assert_f32_close(_np(qs), so, rtol=1e-4, what="scales")
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 1152, 768), (77, 200, 384), (300, 768, 1152), (1, 8, 128)])
+def test_gemm_per_token_bit_exact(gpu, oracle, rng, M, N, K):
+    """Per-token activation scales (BASELINE configs 1 and 5; the reference built with one block per
+    row, int8.h:61-70 E2_I8_BLOCK = K): int32 over the whole K, one fold, bit-exact."""
+    import e2mi
+    qa = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    as_ = rng.uniform(0.001, 0.05, (M, 1)).astype(np.float32)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    bias = (0.01 * rng.standard_normal(N)).astype(np.float32)
+    W = e2mi.DeviceWeight.from_rowmajor(w, ws, bias=bias)
+    y = e2mi.i8_gemm_tok(_t(qa, gpu), _t(as_, gpu), W)
+    yo = oracle.i8_gemm(qa, as_, w, ws, bias=bias, block=K)
+    assert np.array_equal(_np(y).view(np.uint32), yo.view(np.uint32))
+
+
+def test_gemm_per_token_config1_quantized(gpu, oracle, rng):
+    """BASELINE config 1 as written: A f32 [128 x 768] ~N(0,1) quantized per token, W uniform int8,
+    ws ~U(0.001,0.02), bias ~N(0,0.01); quantizer and GEMM bit-exact, and close to the fp32 product."""
+    import e2mi
+    M, N, K = 128, 1152, 768
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    bias = (0.01 * rng.standard_normal(N)).astype(np.float32)
+    W = e2mi.DeviceWeight.from_rowmajor(w, ws, bias=bias)
+    q, s = e2mi.quantize(_t(a, gpu), block=K)
+    y = e2mi.i8_gemm_tok(q, s, W)
+    qo, so = oracle.quantize(a, block=K)
+    assert np.array_equal(_np(q), qo) and np.array_equal(_np(s).view(np.uint32), so.view(np.uint32))
+    yo = oracle.i8_gemm(qo, so, w, ws, bias=bias, block=K)
+    assert np.array_equal(_np(y).view(np.uint32), yo.view(np.uint32))
+    yf = a @ (w.astype(np.float32) * ws[:, None]).T + bias
+    cos = float((_np(y) * yf).sum() / np.linalg.norm(_np(y)) / np.linalg.norm(yf))
+    assert cos > 0.999
+
+
+def test_gemm_per_token_column_range_clamp_and_requant(gpu, oracle, rng):
+    import e2mi
+    import torch
+    M, N, K = 40, 256, 256
+    qa = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    as_ = rng.uniform(0.001, 0.05, (M, 1)).astype(np.float32)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    W = e2mi.DeviceWeight.from_rowmajor(w, ws)
+    yq, ys = e2mi.i8_gemm_tok_q(_t(qa, gpu), _t(as_, gpu), W)
+    qo, so = oracle.quantize(oracle.i8_gemm(qa, as_, w, ws, block=K))
+    assert np.array_equal(_np(yq), qo) and np.array_equal(_np(ys).view(np.uint32), so.view(np.uint32))
+    W.set_clamp(-0.5, 0.5)
+    y = torch.full((M, N), 7.0, device=gpu)
+    e2mi.i8_gemm_tok(_t(qa, gpu), _t(as_, gpu), W, n0=24, n1=200, y=y)
+    yo = oracle.i8_gemm(qa, as_, w, ws, block=K, lo=-0.5, hi=0.5)
+    got = _np(y)
+    assert np.all(got[:, :24] == 7.0) and np.all(got[:, 200:] == 7.0)
+    assert np.array_equal(got[:, 24:200].view(np.uint32), yo[:, 24:200].view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,K,n0,n1", [(300, 1152, 768, 0, 1152), (77, 200, 512, 0, 200),
+                                         (515, 384, 1152, 4, 380), (130, 77, 768, 0, 77),
+                                         (64, 256, 768, 3, 250), (257, 1280, 640, 128, 1280)])
+def test_gemm_per_token_no_post_bit_exact(gpu, oracle, rng, M, N, K, n0, n1):
+    """Per-token GEMM without bias or clamp: the 16-byte-store epilogue (rows of 4 columns formed by
+    a transpose across lane quads) where N, the column offset and the pitch allow it, the 4-byte
+    one otherwise; columns outside [n0, n1) untouched."""
+    import e2mi
+    import torch
+    qa = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    as_ = rng.uniform(0.001, 0.05, (M, 1)).astype(np.float32)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    W = e2mi.DeviceWeight.from_rowmajor(w, ws)
+    y = torch.full((M, N), 7.0, device=gpu)
+    e2mi.i8_gemm_tok(_t(qa, gpu), _t(as_, gpu), W, n0=n0, n1=n1, y=y)
+    yo = oracle.i8_gemm(qa, as_, w, ws, block=K)
+    got = _np(y)
+    assert np.all(got[:, :n0] == 7.0) and np.all(got[:, n1:] == 7.0)
+    assert np.array_equal(got[:, n0:n1].view(np.uint32), yo[:, n0:n1].view(np.uint32))

@@ -125,3 +125,25 @@ def test_gemm_fast_fold_within_bar(gpu, oracle, rng, fast_fold, K, N):
     d = np.abs(yq.cpu().numpy()[rows].astype(int) - qo.astype(int))
     assert d.max() <= 1
     assert (d > 0).mean() < 0.01
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+def test_gemm_per_token_large_bit_exact(gpu, oracle, rng, K, N):
+    """BASELINE config 5 as written: per-token activation scales, M = 65536 (minus a partial
+    tile); f32 output and the requantizing epilogue, bit-exact on sampled rows."""
+    import e2mi
+    M = 65536 - 5
+    qa = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    as_ = rng.uniform(0.001, 0.05, (M, 1)).astype(np.float32)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    W = e2mi.DeviceWeight.from_rowmajor(w, ws)
+    qd, sd = _t(qa, gpu), _t(as_, gpu)
+    y = e2mi.i8_gemm_tok(qd, sd, W).cpu().numpy()
+    yq, ys = e2mi.i8_gemm_tok_q(qd, sd, W)
+    rows = _rows(rng, M)
+    yo = oracle.i8_gemm(qa[rows], as_[rows], w, ws, block=K)
+    assert np.array_equal(y[rows].view(np.uint32), yo.view(np.uint32))
+    qo, so = oracle.quantize(yo)
+    assert np.array_equal(yq.cpu().numpy()[rows], qo)
+    assert np.array_equal(ys.cpu().numpy()[rows].view(np.uint32), so.view(np.uint32))

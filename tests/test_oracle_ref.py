@@ -4,6 +4,8 @@ Bit-exact: the per-block quantizer (AVX-512, AVX-VNNI and scalar builds), the we
 packer, the int8 GEMM with the AVX-512 fold order, and the scalar GEMM's mul+add fold.
 Tolerance: the fp32 helpers, which the reference builds with rsqrt/rcp approximations.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -123,3 +125,31 @@ def test_fp32_helpers_match_reference(oracle, ref, rng):
     xm = rng.standard_normal((50, 768)).astype(np.float32)
     assert_f32_close(oracle.meanpool_l2(xm, valid), ref.meanpool_l2(xm, valid), rtol=1e-6,
                      atol=1e-7, what="pool")
+
+
+@pytest.mark.parametrize("K", [768, 1152])
+def test_per_row_build_bit_exact(oracle, rng, K):
+    """The reference built with one activation block per row (E2_I8_BLOCK = K, int8.h:61-70):
+    its quantizer and GEMM against the oracle's block = K restatement, bit for bit. These builds
+    are the CPU baseline of the per-token GEMM sweep."""
+    from oracle.binding import Ref
+    if not os.path.exists(Ref.per_row_path(K)):
+        pytest.skip("oracle/_ref per-row builds absent (the reference tree is absent on this host)")
+    ref = Ref.per_row(K)
+    M, N = 37, 77
+    x = _acts(rng, M, K)
+    q1, s1 = oracle.quantize(x, block=K)
+    q2, s2 = ref.quantize(x)
+    assert s2.shape == (M, 1)
+    assert np.array_equal(q1, q2)
+    assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    wq, _ = oracle.q8w_pack(w)
+    bsq = w.astype(np.int32).sum(1)[None, :]
+    y_ref = ref.gemm(q1, s1, wq, ws, bsq, N, K, "avx512")
+    y_or = oracle.i8_gemm(q1, s1, w, ws, block=K)
+    assert np.array_equal(y_or.view(np.uint32), y_ref.view(np.uint32))
+    # and it differs from the per-128 build's result (the block is really K)
+    y128 = oracle.i8_gemm(*oracle.quantize(x), w, ws)
+    assert not np.array_equal(y128, y_or)
