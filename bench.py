@@ -199,7 +199,9 @@ def encoder_bench(torch, e2mi, steps, warmup, cpu_sample=4):
     """the 24-layer encoder (d=768, FFN 1152, 3q/1kv heads of 256) with
     random-init int8 weights, token ids uniform over the 262144 vocabulary, f32 table ~N(0,0.02)
     scaled by sqrt(768), batch 64 x seq 512 with random lengths in [64, 512], mean pooling, L2.
-    Ids, mask and output stay in HBM (e2mi_text_embed_batch_device)."""
+    Ids, mask and output stay in HBM (e2mi_text_embed_batch_device). The engine computes only the
+    valid tokens (packed batches); the same batch with every padded row computed is timed beside
+    it, and its embeddings must be bit-identical (right-padded masks)."""
     cfg = e2mi.baseline_config()
     t0 = time.perf_counter()
     model = e2mi.Model.synthetic(cfg, 1004)
@@ -221,6 +223,20 @@ def encoder_bench(torch, e2mi, steps, warmup, cpu_sample=4):
         eng.embed_batch_device(ids_d, valid_d, out, stream)
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / steps
+    # the same batch with every padded row computed (the reference's way), for comparison
+    eng.set_packing(False)
+    try:
+        for _ in range(2):
+            eng.embed_batch_device(ids_d, valid_d, out, stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(max(3, steps // 2)):
+            eng.embed_batch_device(ids_d, valid_d, out, stream)
+        torch.cuda.synchronize()
+        dt_pad = (time.perf_counter() - t1) / max(3, steps // 2)
+        o_pad = out.cpu().numpy()
+    finally:
+        eng.set_packing(True)
     # the host-buffer entry point (PCIe-inclusive), for reference
     h_t = []
     for _ in range(3):
@@ -235,6 +251,10 @@ def encoder_bench(torch, e2mi, steps, warmup, cpu_sample=4):
         "host_buffers_embeddings_per_s": round(ENC_B / min(h_t), 2),
         "unit_norm_ok": bool(np.allclose(np.linalg.norm(o, axis=1), 1, atol=1e-4)),
         "host_matches_device": bool(np.array_equal(host_out, o)),
+        "padded_rows_embeddings_per_s": round(ENC_B / dt_pad, 2),
+        "padded_matches_packed": bool(np.array_equal(o_pad, o)),
+        "rows_computed": {"packed": int(sum(((int(n) + 7) & ~7) for n in valid.sum(1))),
+                          "padded": ENC_B * ENC_S},
         "config": f"24 layers, B={ENC_B}, S={ENC_S}, lengths U[64,512] (mean {lens.mean():.0f}), vocab {cfg.vocab}",
         "model_build_s": round(t_model, 2),
         "kernels_per_forward": eng.stats()[1],

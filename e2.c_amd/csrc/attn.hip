@@ -29,11 +29,13 @@ constexpr int kVP = kKT + 4;     // V^T row pitch in halves (72 B)
 struct AttnArgs {
     const uint16_t *q;      // [M][H*D] f16
     const uint16_t *k;      // [M][KV*D] f16
-    const uint16_t *vt;     // [B][KV][D][S] f16
-    const uint8_t *valid;   // [M]
+    const uint16_t *vt;     // padded: [B][KV][D][S]; packed: [KV][D][S] with S = M
+    const uint8_t *valid;   // padded: [M]
     int8_t *cq;             // [M][H*D] int8 context
     float *cs;              // [M][H*D/128] scales
     float *c32;             // optional [M][H*D] f32 context
+    // packed batches: sequence b is rows [seq_start[b], seq_start[b] + seq_len[b]), all valid
+    const int32_t *seq_start, *seq_len;
     int B, S, H, KV;
     float scale;
 };
@@ -47,20 +49,29 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5;
     const int S = a.S, HD = a.H * kD, kvh = h / (a.H / a.KV);
-    const size_t row0 = (size_t)b * S;
-    const uint8_t *valid = a.valid + row0;
+    const bool packed = a.seq_start != nullptr;
+    // padded: the sequence's rows b*S .. b*S+S-1 with a mask; packed: its own rows, all valid.
+    // Sk: keys (and rows) of the sequence that can be read
+    const size_t row0 = packed ? (size_t)a.seq_start[b] : (size_t)b * S;
+    const int Sk = packed ? a.seq_len[b] : S;
+    const uint8_t *valid = packed ? nullptr : a.valid + row0;
 
     // the sequence's last valid row + 1 (trailing padding is trimmed, text.c:849-852)
-    if (tid == 0) s_len = 0;
-    __syncthreads();
-    for (int i = tid; i < S; i += 256)
-        if (valid[i]) atomicMax(&s_len, i + 1);
+    if (packed) {
+        if (tid == 0) s_len = Sk;
+    } else {
+        if (tid == 0) s_len = 0;
+        __syncthreads();
+        for (int i = tid; i < S; i += 256)
+            if (valid[i]) atomicMax(&s_len, i + 1);
+    }
     __syncthreads();
     const int Sb = s_len;
+    if (packed && qb * 128 >= Sb) return;  // no rows of this sequence in the block
 
     const int qi = qb * 128 + w * 32 + (lane & 31);  // this lane's query
-    const bool qvalid = qi < Sb && valid[qi];
-    const int qc = min(qi, S - 1);
+    const bool qvalid = qi < Sb && (packed || valid[qi]);
+    const int qc = min(qi, Sk - 1);
 
     // Q fragments: B operand of S^T = K Q^T, lane holds Q[qi][16 s + 8 half .. +8]
     h8 qf[16];
@@ -77,8 +88,8 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     const bool block_live = qb * 128 < Sb;
     const int ntiles = block_live ? (Sb + kKT - 1) / kKT : 0;
     const uint16_t *kbase = a.k + row0 * a.KV * kD + kvh * kD;
-    const uint16_t *vbase = a.vt + ((size_t)(b * a.KV + kvh) * kD) * S;
-    const bool vfast = (S % 8) == 0;
+    const uint16_t *vbase = packed ? a.vt + (size_t)kvh * kD * S + row0 : a.vt + ((size_t)(b * a.KV + kvh) * kD) * S;
+    const bool vfast = (S % 8) == 0 && (row0 % 8) == 0;
 
     for (int kt = 0; kt < ntiles; kt++) {
         const int k0 = kt * kKT;
@@ -88,23 +99,23 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
         for (int p = 0; p < 4; p++) {
             const int key = tid / 32 + 8 * p, ch = tid % 32;
             uint4 val = make_uint4(0, 0, 0, 0);
-            if (k0 + key < S) val = *(const uint4 *)(kbase + (size_t)(k0 + key) * a.KV * kD + ch * 8);
+            if (k0 + key < Sk) val = *(const uint4 *)(kbase + (size_t)(k0 + key) * a.KV * kD + ch * 8);
             *(uint4 *)(Ks + key * kKP + ch * 8) = val;
         }
         // V^T tile: row d = tid, keys k0 .. k0+31
         {
             const uint16_t *vr = vbase + (size_t)tid * S + k0;
             _Float16 *dst = Vs + tid * kVP;
-            if (vfast && k0 + kKT <= S) {
+            if (vfast && k0 + kKT <= Sk) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) *(uint2 *)(dst + 8 * c) = *(const uint2 *)(vr + 8 * c),
                                             *(uint2 *)(dst + 8 * c + 4) = *(const uint2 *)(vr + 8 * c + 4);
             } else {
                 for (int j = 0; j < kKT; j++)
-                    dst[j] = k0 + j < S ? __builtin_bit_cast(_Float16, vr[j]) : (_Float16)0.f;
+                    dst[j] = k0 + j < Sk ? __builtin_bit_cast(_Float16, vr[j]) : (_Float16)0.f;
             }
         }
-        if (tid < kKT) vk[tid] = (k0 + tid < Sb) ? valid[k0 + tid] : 0;
+        if (tid < kKT) vk[tid] = (k0 + tid < Sb) ? (packed ? 1 : valid[k0 + tid]) : 0;
         __syncthreads();
 
         // S^T tile (32 keys x 32 queries): A = K rows (lane%32 = key), B = Q
@@ -173,7 +184,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     const float inv = (qvalid && ltot > 0.f) ? __fdiv_rn(1.0f, ltot) : 0.f;
 #pragma unroll
     for (int t = 0; t < 8; t++) o[t] *= inv;
-    if (qi >= S) return;
+    if (qi >= Sk) return;  // packed: rows past the sequence belong to the next one
     const size_t orow = (row0 + qi);
 #pragma unroll
     for (int blk = 0; blk < 2; blk++) {
@@ -218,7 +229,27 @@ extern "C" int e2mi_attention(e2mi_stream stream, const uint16_t *q16, const uin
         set_error("attention: null or misaligned pointer");
         return -1;
     }
-    AttnArgs a = {q16, k16, vt16, valid, ctx_q, ctx_s, ctx32, B, S, H, KV, scale};
+    AttnArgs a = {q16, k16, vt16, valid, ctx_q, ctx_s, ctx32, nullptr, nullptr, B, S, H, KV, scale};
     hipLaunchKernelGGL(k_attn, dim3((S + 127) / 128, H, B), dim3(256), 0, (hipStream_t)stream, a);
+    return check_hip(hipGetLastError(), "attention launch");
+}
+
+extern "C" int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
+                                     const uint16_t *vt16, int M, const int32_t *seq_start,
+                                     const int32_t *seq_len, int B, int max_len, int H, int KV, int D,
+                                     float scale, int8_t *ctx_q, float *ctx_s, float *ctx32) {
+    if (D != kD || B <= 0 || M <= 0 || max_len <= 0 || H <= 0 || KV <= 0 || H % KV) {
+        set_error("attention_packed: needs head_dim 256 and H %% KV == 0 (B=%d M=%d H=%d KV=%d D=%d)", B,
+                  M, H, KV, D);
+        return -1;
+    }
+    if (!q16 || !k16 || !vt16 || !seq_start || !seq_len || !ctx_q || !ctx_s || !aligned16(q16) ||
+        !aligned16(k16) || ((uintptr_t)vt16 & 7) || ((uintptr_t)ctx_q & 3) ||
+        (ctx32 && !aligned16(ctx32))) {
+        set_error("attention_packed: null or misaligned pointer");
+        return -1;
+    }
+    AttnArgs a = {q16, k16, vt16, nullptr, ctx_q, ctx_s, ctx32, seq_start, seq_len, B, M, H, KV, scale};
+    hipLaunchKernelGGL(k_attn, dim3((max_len + 127) / 128, H, B), dim3(256), 0, (hipStream_t)stream, a);
     return check_hip(hipGetLastError(), "attention launch");
 }

@@ -13,6 +13,13 @@
 // and after the last layer norm_add(post_ffn) + final RMSNorm, masked mean pool, L2
 // (text.c:963-981). The recorded graph is replayed for every later call of the same shape, like
 // the reference's HIP backend (forward.c:553-579).
+//
+// Packed batches (the default): only valid tokens are computed. Each sequence's valid tokens are
+// laid out in order from a row that is a multiple of 8, the total rounded up to a multiple of 256
+// (filler rows carry token 0 and belong to no sequence). Every row kernel and GEMM is row-local,
+// attention and pooling take each sequence's row range, and RoPE positions come from a per-row
+// table, so the embeddings are those of the padded batch (bit-identical for right-padded masks,
+// where the attention key tiles and the pooling chunks fall the same way).
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -21,6 +28,7 @@
 
 #include <map>
 #include <string>
+#include <tuple>
 #include <utility>
 #include <vector>
 
@@ -67,7 +75,15 @@ struct e2mi_engine {
     int32_t *h_ids = nullptr;
     uint8_t *h_valid = nullptr;
     float *h_out = nullptr;
-    std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+    // packed batches: per packed row its source index in the chunk (-1 filler) and RoPE position,
+    // per sequence its first row and length (device copies at fixed addresses for the graphs)
+    int32_t *rowmap = nullptr, *pos = nullptr, *seq_start = nullptr, *seq_len = nullptr;
+    int32_t *h_rowmap = nullptr, *h_pos = nullptr, *h_start = nullptr, *h_len = nullptr;
+    uint8_t *h_mask = nullptr;  // device-entry mask copy
+    size_t mask_cap = 0;
+    hipStream_t last_stream = nullptr;
+    bool packed = true;
+    std::map<std::tuple<int, int, int>, hipGraphExec_t> graphs;  // (sequences, seq_len, rows)
     bool use_graph = true;
     int layer_limit = 0;
     long calls = 0, kernels_last = 0;
@@ -173,11 +189,12 @@ static void rope_tables(const e2_config &c, std::vector<float> &cs, std::vector<
         }
 }
 
-// every kernel of one forward over B sequences of S tokens, on stream s; returns the launch count
-// or -1
-static int enqueue(e2mi_engine *g, int B, int S, hipStream_t s) {
+// every kernel of one forward over B sequences of S tokens (M rows: B * S padded, or the packed
+// row count), on stream s; returns the launch count or -1
+static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
     const e2_config &c = g->cfg;
-    const int M = B * S, Dm = c.hidden, H = c.n_heads, KV = c.n_kv_heads, D = c.head_dim;
+    const bool pk = Mp > 0;
+    const int M = pk ? Mp : B * S, Dm = c.hidden, H = c.n_heads, KV = c.n_kv_heads, D = c.head_dim;
     const int qd = H * D, F = c.ffn;
     const int nl = g->layer_limit > 0 && g->layer_limit < c.n_layers ? g->layer_limit : c.n_layers;
     const float eps = c.rms_eps;
@@ -192,10 +209,18 @@ static int enqueue(e2mi_engine *g, int B, int S, hipStream_t s) {
     for (int l = 0; l < nl; l++) {
         const LayerDev &L = g->layers[l];
         RUN(e2mi_i8_gemm(s, g->qkv, qd + 2 * KV * D, g->qa, g->as, &L.qkv, M, 0, L.qkv.N));
-        RUN(e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, g->cos_tab,
-                               g->sin_tab, g->q16, g->k16, g->vt16, nullptr, nullptr, nullptr));
-        RUN(e2mi_attention(s, g->q16, g->k16, g->vt16, g->valid, B, S, H, KV, D, c.attn_scale,
-                           g->cq, g->cs, nullptr));
+        if (pk) {
+            RUN(e2mi_qkv_norm_rope_packed(s, g->qkv, M, g->pos, H, KV, D, L.q_norm, L.k_norm, eps,
+                                          g->cos_tab, g->sin_tab, g->q16, g->k16, g->vt16, nullptr,
+                                          nullptr, nullptr));
+            RUN(e2mi_attention_packed(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len, B, S, H,
+                                      KV, D, c.attn_scale, g->cq, g->cs, nullptr));
+        } else {
+            RUN(e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, g->cos_tab,
+                                   g->sin_tab, g->q16, g->k16, g->vt16, nullptr, nullptr, nullptr));
+            RUN(e2mi_attention(s, g->q16, g->k16, g->vt16, g->valid, B, S, H, KV, D, c.attn_scale,
+                               g->cq, g->cs, nullptr));
+        }
         RUN(e2mi_i8_gemm(s, g->tmp, Dm, g->cq, g->cs, &L.o, M, 0, Dm));
         RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_attn, L.ln_pre, eps, M, Dm, g->x, nullptr,
                                 g->qa, g->as));
@@ -209,31 +234,34 @@ static int enqueue(e2mi_engine *g, int B, int S, hipStream_t s) {
             RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, g->final_norm, eps, M, Dm, g->x,
                                     g->xn, nullptr, nullptr));
     }
-    RUN(e2mi_pool_l2(s, g->xn, g->valid, B, S, Dm, g->pool_ws, g->out));
+    if (pk)
+        RUN(e2mi_pool_l2_packed(s, g->xn, g->seq_start, g->seq_len, B, S, Dm, g->pool_ws, g->out));
+    else
+        RUN(e2mi_pool_l2(s, g->xn, g->valid, B, S, Dm, g->pool_ws, g->out));
     (void)F;
 #undef RUN
     return k + 1;  // the pool is two launches
 }
 
-static int run_shape(e2mi_engine *g, int B, int S, hipStream_t s) {
+static int run_shape(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
     if (!g->use_graph) {
-        const int k = enqueue(g, B, S, s);
+        const int k = enqueue(g, B, S, Mp, s);
         if (k < 0) return -1;
         g->kernels_last = k;
         return 0;
     }
-    auto key = std::make_pair(B, S);
+    auto key = std::make_tuple(B, S, Mp);
     auto it = g->graphs.find(key);
     if (it == g->graphs.end()) {
         // the first call of a shape runs eagerly (kernel attributes get set outside any capture),
         // then the sequence is recorded for every later call
-        const int k = enqueue(g, B, S, s);
+        const int k = enqueue(g, B, S, Mp, s);
         if (k < 0) return -1;
         g->kernels_last = k;
         hipGraph_t graph = nullptr;
         if (check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"))
             return -1;
-        const int k2 = enqueue(g, B, S, s);
+        const int k2 = enqueue(g, B, S, Mp, s);
         const hipError_t e = hipStreamEndCapture(s, &graph);
         if (k2 < 0 || check_hip(e, "end capture")) {
             if (graph) (void)hipGraphDestroy(graph);
@@ -269,6 +297,69 @@ static int validate_batch(const e2mi_engine *g, const int32_t *ids, int batch, i
     return 0;
 }
 
+// rows one sequence takes in a packed chunk: its valid tokens, rounded up to a multiple of 8
+static int seq_rows(const uint8_t *valid, int S) {
+    int len = 0;
+    for (int i = 0; i < S; i++) len += valid ? (valid[i] != 0) : 1;
+    return (len + 7) & ~7;
+}
+
+// the packed layout of n sequences of S tokens (valid: host mask, null = all valid) into the
+// engine's host staging arrays; returns the row count
+static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
+    int r = 0;
+    for (int b = 0; b < n; b++) {
+        g->h_start[b] = r;
+        int len = 0;
+        for (int i = 0; i < S; i++)
+            if (!valid || valid[(size_t)b * S + i]) {
+                g->h_rowmap[r + len] = b * S + i;
+                g->h_pos[r + len] = i;
+                len++;
+            }
+        g->h_len[b] = len;
+        const int end = (r + len + 7) & ~7;
+        for (int i = r + len; i < end; i++) g->h_rowmap[i] = -1, g->h_pos[i] = 0;
+        r = end;
+    }
+    const int Mp = (r + 255) & ~255;
+    for (int i = r; i < Mp; i++) g->h_rowmap[i] = -1, g->h_pos[i] = 0;
+    return Mp;
+}
+
+// sequences of the next chunk starting at b0: as many as fit the workspace rows (packed: rounded
+// up to 256), the staging arrays and the pooling workspace; at least one
+static int chunk_size(const e2mi_engine *g, const uint8_t *valid, int b0, int batch, int S) {
+    if (!g->packed) {
+        int per = g->R / S;
+        if (per > g->bmax) per = g->bmax;
+        return batch - b0 < per ? batch - b0 : per;
+    }
+    const long pool_cap = (long)g->R / 64 + g->R + 64, chunks = (S + 63) / 64;
+    int n = 0;
+    long rows = 0;
+    while (b0 + n < batch && n < g->bmax && (long)(n + 1) * chunks <= pool_cap) {
+        const long r = seq_rows(valid ? valid + (size_t)n * S : nullptr, S);
+        if (n > 0 && ((rows + r + 255) & ~255L) > g->R) break;
+        rows += r;
+        n++;
+    }
+    return n;
+}
+
+// upload the chunk's packing tables (and, from host ids, its packed ids) on stream s
+static int upload_pack(e2mi_engine *g, int n, int Mp, const int32_t *host_ids, hipStream_t s) {
+    if (host_ids)
+        for (int r = 0; r < Mp; r++) g->h_ids[r] = g->h_rowmap[r] >= 0 ? host_ids[g->h_rowmap[r]] : 0;
+    if ((host_ids && check_hip(hipMemcpyAsync(g->ids, g->h_ids, (size_t)Mp * 4, hipMemcpyHostToDevice, s), "ids H2D")) ||
+        (!host_ids && check_hip(hipMemcpyAsync(g->rowmap, g->h_rowmap, (size_t)Mp * 4, hipMemcpyHostToDevice, s), "rowmap H2D")) ||
+        check_hip(hipMemcpyAsync(g->pos, g->h_pos, (size_t)Mp * 4, hipMemcpyHostToDevice, s), "pos H2D") ||
+        check_hip(hipMemcpyAsync(g->seq_start, g->h_start, (size_t)n * 4, hipMemcpyHostToDevice, s), "start H2D") ||
+        check_hip(hipMemcpyAsync(g->seq_len, g->h_len, (size_t)n * 4, hipMemcpyHostToDevice, s), "len H2D"))
+        return -1;
+    return 0;
+}
+
 }  // namespace e2mi
 
 // ------------------------------------------------------------------ C ABI (e2hip.h:34-64)
@@ -280,6 +371,10 @@ extern "C" void e2mi_destroy(e2mi_engine *g) {
     if (g->h_ids) (void)hipHostFree(g->h_ids);
     if (g->h_valid) (void)hipHostFree(g->h_valid);
     if (g->h_out) (void)hipHostFree(g->h_out);
+    for (int32_t *p : {g->h_rowmap, g->h_pos, g->h_start, g->h_len})
+        if (p) (void)hipHostFree(p);
+    if (g->h_mask) (void)hipHostFree(g->h_mask);
+    if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
     if (g->stream) (void)hipStreamDestroy(g->stream);
     delete g;
 }
@@ -303,6 +398,7 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
     const e2_config &c = g->cfg;
     g->R = max_rows > 0 ? max_rows : 32768;
     if (g->R < c.max_seq) g->R = c.max_seq;
+    g->R = (g->R + 255) & ~255;  // a packed chunk of one full sequence fits
     const char *ng = getenv("E2MI_NOGRAPH");
     g->use_graph = !(ng && ng[0] && ng[0] != '0');
     auto fail = [&]() -> e2mi_engine * {
@@ -351,12 +447,24 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         dalloc(g, &g->cq, R * qd) || dalloc(g, &g->cs, R * (qd / 128)) ||
         dalloc(g, &g->q16, R * qd) || dalloc(g, &g->k16, R * kvd) || dalloc(g, &g->vt16, R * kvd) ||
         dalloc(g, &g->ids, R) || dalloc(g, &g->valid, R) || dalloc(g, &g->out, R * c.hidden) ||
-        dalloc(g, &g->pool_ws, (R / 64 + R + 64) * (size_t)(c.hidden + 1)))
+        dalloc(g, &g->pool_ws, (R / 64 + R + 64) * (size_t)(c.hidden + 1)) ||
+        dalloc(g, &g->rowmap, R) || dalloc(g, &g->pos, R) || dalloc(g, &g->seq_start, (size_t)g->bmax) ||
+        dalloc(g, &g->seq_len, (size_t)g->bmax))
         return fail();
     if (check_hip(hipHostMalloc((void **)&g->h_ids, R * 4), "pinned ids") ||
         check_hip(hipHostMalloc((void **)&g->h_valid, R), "pinned valid") ||
-        check_hip(hipHostMalloc((void **)&g->h_out, (size_t)g->bmax * c.hidden * 4), "pinned out"))
+        check_hip(hipHostMalloc((void **)&g->h_out, (size_t)g->bmax * c.hidden * 4), "pinned out") ||
+        check_hip(hipHostMalloc((void **)&g->h_rowmap, R * 4), "pinned rowmap") ||
+        check_hip(hipHostMalloc((void **)&g->h_pos, R * 4), "pinned pos") ||
+        check_hip(hipHostMalloc((void **)&g->h_start, (size_t)g->bmax * 4), "pinned start") ||
+        check_hip(hipHostMalloc((void **)&g->h_len, (size_t)g->bmax * 4), "pinned len"))
         return fail();
+    // filler rows of packed batches read contexts that no attention writes: start them at zero
+    if (check_hip(hipMemsetAsync(g->cq, 0, R * qd, g->stream), "clear ctx") ||
+        check_hip(hipMemsetAsync(g->cs, 0, R * (qd / 128) * 4, g->stream), "clear ctx scales"))
+        return fail();
+    const char *np = getenv("E2MI_NOPACK");
+    g->packed = !(np && np[0] && np[0] != '0');
     if (check_hip(hipStreamSynchronize(g->stream), "create sync")) return fail();
     return g;
 }
@@ -374,16 +482,23 @@ extern "C" int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const u
     if (validate_batch(g, ids, batch, seq_len, true)) return -1;
     const double t0 = now_ms();
     const int D = g->cfg.hidden;
-    int per = g->R / seq_len;
-    if (per > g->bmax) per = g->bmax;
     for (int b0 = 0; b0 < batch;) {
-        const int n = batch - b0 < per ? batch - b0 : per;
-        const size_t rows = (size_t)n * seq_len, off = (size_t)b0 * seq_len;
-        memcpy(g->h_ids, ids + off, rows * 4);
-        for (size_t i = 0; i < rows; i++) g->h_valid[i] = valid ? (valid[off + i] != 0) : 1;
-        if (check_hip(hipMemcpyAsync(g->ids, g->h_ids, rows * 4, hipMemcpyHostToDevice, g->stream), "ids H2D") ||
-            check_hip(hipMemcpyAsync(g->valid, g->h_valid, rows, hipMemcpyHostToDevice, g->stream), "valid H2D") ||
-            run_shape(g, n, seq_len, g->stream) ||
+        const size_t off = (size_t)b0 * seq_len;
+        const uint8_t *vchunk = valid ? valid + off : nullptr;
+        const int n = chunk_size(g, vchunk, b0, batch, seq_len);
+        const size_t rows = (size_t)n * seq_len;
+        int Mp = 0;
+        if (g->packed) {
+            Mp = plan_pack(g, vchunk, n, seq_len);
+            if (upload_pack(g, n, Mp, ids + off, g->stream)) return -1;
+        } else {
+            memcpy(g->h_ids, ids + off, rows * 4);
+            for (size_t i = 0; i < rows; i++) g->h_valid[i] = valid ? (valid[off + i] != 0) : 1;
+            if (check_hip(hipMemcpyAsync(g->ids, g->h_ids, rows * 4, hipMemcpyHostToDevice, g->stream), "ids H2D") ||
+                check_hip(hipMemcpyAsync(g->valid, g->h_valid, rows, hipMemcpyHostToDevice, g->stream), "valid H2D"))
+                return -1;
+        }
+        if (run_shape(g, n, seq_len, Mp, g->stream) ||
             check_hip(hipMemcpyAsync(g->h_out, g->out, (size_t)n * D * 4, hipMemcpyDeviceToHost, g->stream), "out D2H") ||
             check_hip(hipStreamSynchronize(g->stream), "forward sync"))
             return -1;
@@ -406,23 +521,65 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
         return -1;
     }
     if (validate_batch(g, ids, batch, seq_len, false)) return -1;
-    if ((long)batch * seq_len > g->R) {
-        set_error("text_embed_batch_device: %d x %d rows exceed the engine's %d-row workspace",
-                  batch, seq_len, g->R);
-        return -1;
-    }
     hipStream_t s = stream ? (hipStream_t)stream : g->stream;
     const size_t rows = (size_t)batch * seq_len;
     const double t0 = now_ms();
-    if (check_hip(hipMemcpyAsync(g->ids, ids, rows * 4, hipMemcpyDeviceToDevice, s), "ids D2D") ||
-        check_hip(hipMemcpyAsync(g->valid, valid, rows, hipMemcpyDeviceToDevice, s), "valid D2D") ||
-        run_shape(g, batch, seq_len, s) ||
-        check_hip(hipMemcpyAsync(out, g->out, (size_t)batch * g->cfg.hidden * 4, hipMemcpyDeviceToDevice, s),
-                  "out D2D"))
-        return -1;
+    if (!g->packed) {
+        if ((long)batch * seq_len > g->R) {
+            set_error("text_embed_batch_device: %d x %d rows exceed the engine's %d-row workspace",
+                      batch, seq_len, g->R);
+            return -1;
+        }
+        if (check_hip(hipMemcpyAsync(g->ids, ids, rows * 4, hipMemcpyDeviceToDevice, s), "ids D2D") ||
+            check_hip(hipMemcpyAsync(g->valid, valid, rows, hipMemcpyDeviceToDevice, s), "valid D2D") ||
+            run_shape(g, batch, seq_len, 0, s) ||
+            check_hip(hipMemcpyAsync(out, g->out, (size_t)batch * g->cfg.hidden * 4, hipMemcpyDeviceToDevice, s),
+                      "out D2D"))
+            return -1;
+    } else {
+        // the packing is planned on the host from the mask: one synchronous copy of B*S bytes
+        // (which also drains earlier work on the stream that used the staging arrays)
+        if (rows > g->mask_cap) {
+            uint8_t *m = nullptr;
+            if (check_hip(hipHostMalloc((void **)&m, rows), "pinned mask")) return -1;
+            if (g->h_mask) (void)hipHostFree(g->h_mask);
+            g->h_mask = m;
+            g->mask_cap = rows;
+        }
+        if ((g->last_stream && g->last_stream != s && check_hip(hipStreamSynchronize(g->last_stream), "sync")) ||
+            check_hip(hipMemcpyAsync(g->h_mask, valid, rows, hipMemcpyDeviceToHost, s), "mask D2H") ||
+            check_hip(hipStreamSynchronize(s), "mask sync"))
+            return -1;
+        g->last_stream = s;
+        for (int b0 = 0; b0 < batch;) {
+            const size_t off = (size_t)b0 * seq_len;
+            const int n = chunk_size(g, g->h_mask + off, b0, batch, seq_len);
+            const int Mp = plan_pack(g, g->h_mask + off, n, seq_len);
+            if (upload_pack(g, n, Mp, nullptr, s) ||
+                e2mi_gather_ids(s, ids + off, g->rowmap, Mp, g->ids) ||
+                run_shape(g, n, seq_len, Mp, s) ||
+                check_hip(hipMemcpyAsync(out + (size_t)b0 * g->cfg.hidden, g->out, (size_t)n * g->cfg.hidden * 4,
+                                         hipMemcpyDeviceToDevice, s), "out D2D"))
+                return -1;
+            b0 += n;
+            // the staging arrays are reused by the next chunk
+            if (b0 < batch && check_hip(hipStreamSynchronize(s), "chunk sync")) return -1;
+        }
+    }
     if (!stream && check_hip(hipStreamSynchronize(s), "forward sync")) return -1;
     g->calls++;
     g->last_ms = now_ms() - t0;
+    return 0;
+}
+
+extern "C" int e2mi_set_packing(e2mi_engine *g, int on) {
+    if (!g) {
+        set_error("set_packing: null engine");
+        return -1;
+    }
+    if (g->stream) (void)hipStreamSynchronize(g->stream);
+    if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
+    g->packed = on != 0;
     return 0;
 }
 

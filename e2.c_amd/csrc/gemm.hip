@@ -100,16 +100,6 @@ __device__ inline void dma4(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
                  : "memory");
 }
 
-// 16-byte buffer store. A VALU write of the store's data registers right after it needs a wait
-// state (the store reads its data late: without it the last lanes of each 16 store the new
-// values); the compiler does not insert one after the buffer-store builtin, so the store is
-// issued here with its own s_nop. The compiler does not count it: waits are explicit.
-__device__ inline void bstore16(v4u r, v4u d, uint32_t voff, uint32_t soff) {
-    asm volatile("buffer_store_dwordx4 %0, %1, %2, %3 offen\n\ts_nop 1"
-                 ::"v"(d), "v"(voff), "s"(r), "s"(soff)
-                 : "memory");
-}
-
 // The accumulator-dump kernel (e2mi_i8_gemm_acc, the parity hook for "bit-exact int32
 // accumulators"): 128 x 128 tiles of 4 waves of 64 x 64, two direct-to-LDS stages, the exact fold
 // after each step's MFMAs, every step's int32 accumulators written to accd [nb][M][N], f32 output
@@ -395,36 +385,9 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmA
 
 // 8 waves of 32 x 128 (one 32-row MFMA tile by four 32-column ones): NWM x NWN waves, BM = 32 NWM,
 // BN = 128 NWN
-// 4 x 4 transpose inside each quad of lanes (DPP quad permutes): lane 4q + i enters with
-// v[j] = X[j][i] and leaves with v[j] = X[i][j]. Two exchange stages, one per index bit: where a
-// lane's bit differs from a register's, the value trades places with the partner lane's.
-template <int CTRL>
-__device__ inline float quad_read(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ inline void quad_xpose(float (&v)[4], int lane) {
-    constexpr int kXor2 = 0x4E, kXor1 = 0xB1;  // quad_perm [2,3,0,1], [1,0,3,2]
-    const bool b1 = (lane & 2) != 0, b0 = (lane & 1) != 0;
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const float r = quad_read<kXor2>(b1 ? v[j] : v[j + 2]);
-        v[j] = b1 ? r : v[j];
-        v[j + 2] = b1 ? v[j + 2] : r;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j += 2) {
-        const float r = quad_read<kXor1>(b0 ? v[j] : v[j + 1]);
-        v[j] = b0 ? r : v[j];
-        v[j + 1] = b0 ? v[j + 1] : r;
-    }
-}
-
-// TOKM: 0 per-(row, 128) activation scales; 1 per-token scales; 2 per-token scales with 16-byte
-// f32 output stores (EPI_F32 without bias or clamp; N, ldy and the output 16-byte aligned)
-template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, int TOKM>
+// TOK: per-token activation scales (one per row) instead of one per (row, 128-element block)
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, bool TOK>
 __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int tiles_n, int tiles) {
-    constexpr bool TOK = TOKM > 0;
-    static_assert(TOKM < 2 || (EPI == EPI_F32 && POST == 0), "16-byte stores: f32 epilogue, no bias or clamp");
     constexpr int NWAVE = NWM * NWN;
     static_assert(BM == 32 * NWM && BN == 128 * NWN && NWAVE == 8, "8 waves of 32x128");
     constexpr int AI = BM / 8 / NWAVE, BI = BN / 8 / NWAVE;  // 1-KB loads per wave per step
@@ -620,32 +583,8 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
     // per-token scales (the reference built with a per-row block, E2_I8_BLOCK = K): the int32
     // accumulators run over the whole K of a tile and are folded once, f = fma((float)acc,
     // RN(as[m] * ws[n]), 0), at the tile's last step, followed by its epilogue.
-    // TOKM 2 (f32 output): each 4 x 4 block of a lane quad's registers is transposed across the
-    // quad (DPP), so a lane holds 4 consecutive columns of one row and writes them with one 16-byte
-    // store: exactly 16 stores per lane per tile (columns past N are sent past the descriptor's
-    // range rather than skipped). Vector-memory operations complete in issue order and the 16
-    // stores follow the loads of the next two steps, so those two steps' waits for their stage
-    // allow 8 + 16 operations outstanding: the stores drain while they compute instead of before.
-    int last_epi = -8;  // step of the last 16-byte-store epilogue
-    // after the transpose lane (h = lane / 32, i = lane % 4) holds row 8 g + 4 h + i of register
-    // group g and columns (lane % 32) & ~3 .. + 3 of each 32-column slice
-    const int fcol4 = wn * 128 + (lane & 28);
-    const uint32_t vst4 = (uint32_t)((wm * 32 + (lane >> 5) * 4 + (lane & 3)) * p.ldy + fcol4) * 4u;
-    const int ldy4 = p.ldy * 4;
-    const v4u ry = rsrc_words(p.Y, (uint32_t)min((long)p.M * p.ldy * 4, 0x7fffffffL));
-    // register group g of a 32-column slice (rows past M fall past the descriptor's range)
-    auto store_group4 = [&](const float (&fs)[16], int g, uint32_t base, int col0) {
-        float v[4] = {fs[4 * g], fs[4 * g + 1], fs[4 * g + 2], fs[4 * g + 3]};
-        quad_xpose(v, lane);
-        const uint32_t vso = (col0 + fcol4 < p.N) ? vst4 : 0x80000000u;
-        const uint32_t so = __builtin_amdgcn_readfirstlane(base + (uint32_t)(g * 8 * ldy4));
-        const v4u d = {__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
-                       __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])};
-        bstore16(ry, d, vso, so);
-    };
     auto step_tok = [&](int g) {
         if (g + 1 >= G) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        else if (TOKM == 2 && g - last_epi <= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L + 16) : "memory");
         else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
         __syncthreads();
         const Issue is_next = issue_prep(g + 2);
@@ -677,14 +616,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
             }
 #pragma unroll
             for (int tn = 0; tn < 4; tn++) acc0[tn] = zero;
-            if constexpr (TOKM == 2) {
-                const uint32_t tb = (uint32_t)(pm0 * p.ldy + pn0) * 4u;
-#pragma unroll
-                for (int t = 0; t < 4; t++)
-#pragma unroll
-                    for (int gg = 0; gg < 4; gg++) store_group4(f[t], gg, tb + t * 128, pn0 + t * 32);
-                last_epi = g;
-            } else if constexpr (EPI == EPI_F32) {
+            if constexpr (EPI == EPI_F32) {
                 p_epilogue_f32<POST, false>(p, f, wsr, pm0, pn0, wm, wn, lane);
             } else {
                 __syncthreads();
@@ -743,13 +675,13 @@ static int num_cus() {
     return cus;
 }
 
-template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, int TOKM>
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, bool TOK>
 static int launch_p1(hipStream_t s, const GemmArgs &p) {
     constexpr size_t lds = p_lds_bytes<BM, BN, NWM * NWN>();
     static_assert(lds <= 160 * 1024, "LDS budget");
     static_assert(EPI == EPI_F32 || (8 * 8 * ((EPI == EPI_GEGLU ? 64 : 128) + 4) + 8 * 32) * 4 <= (BM + BN) * 128,
                   "epilogue scratch fits a stage");
-    auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST, TOKM>;
+    auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST, TOK>;
     static bool attr = false;
     if (!attr) {
         if (check_hip(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
@@ -774,22 +706,15 @@ template <int BM, int BN, int NWM, int NWN, int EPI>
 static int launch_p(hipStream_t s, const GemmArgs &p, bool tok = false) {
     const bool post = p.bias != nullptr || p.lo > -1e30f || p.hi < 1e30f;
     if constexpr (EPI != EPI_GEGLU) {
-        if (tok) {  // one fold per output: the fast fold has nothing to save
-            if constexpr (EPI == EPI_F32) {
-                // 16-byte stores of 4-column groups (N, ldy, the output 16-byte aligned); no bias
-                // or clamp
-                if (!post && p.N % 4 == 0 && p.ldy % 4 == 0 && aligned16(p.Y))
-                    return launch_p1<BM, BN, NWM, NWN, EPI, false, 0, 2>(s, p);
-            }
-            return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3, 1>(s, p)
-                        : launch_p1<BM, BN, NWM, NWN, EPI, false, 0, 1>(s, p);
-        }
+        if (tok)  // one fold per output: the fast fold has nothing to save
+            return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3, true>(s, p)
+                        : launch_p1<BM, BN, NWM, NWN, EPI, false, 0, true>(s, p);
     }
     if (fold_fast())
-        return post ? launch_p1<BM, BN, NWM, NWN, EPI, true, 3, 0>(s, p)
-                    : launch_p1<BM, BN, NWM, NWN, EPI, true, 0, 0>(s, p);
-    return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3, 0>(s, p)
-                : launch_p1<BM, BN, NWM, NWN, EPI, false, 0, 0>(s, p);
+        return post ? launch_p1<BM, BN, NWM, NWN, EPI, true, 3, false>(s, p)
+                    : launch_p1<BM, BN, NWM, NWN, EPI, true, 0, false>(s, p);
+    return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3, false>(s, p)
+                : launch_p1<BM, BN, NWM, NWN, EPI, false, 0, false>(s, p);
 }
 
 static int launch_dump(hipStream_t s, const GemmArgs &p) {

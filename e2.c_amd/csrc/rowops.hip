@@ -134,6 +134,7 @@ struct QkvArgs {
     uint16_t *k16;             // [M][KV*D] f16
     uint16_t *vt16;            // [B][KV][D][S] f16 (V transposed per sequence)
     float *q32, *k32, *v32;    // optional f32 copies (parity tests), same layouts as q16/k16/[M][KV*D]
+    const int32_t *pos;        // packed batches: RoPE position of each row (then S = M, B = 1)
     int M, S, H, KV;
 };
 
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a) {
     } else {
         v = scale4(v, inv, ld4((kind == 0 ? a.q_gamma : a.k_gamma) + 4 * l));
         // rotate-half: lane l < 32 holds a = x[i], lane l + 32 holds y = x[i + 128]
-        const int pos = m % a.S;
+        const int pos = a.pos ? a.pos[m] : m % a.S;
         const float4 c = ld4(a.cs + (size_t)pos * D + 4 * l), s = ld4(a.sn + (size_t)pos * D + 4 * l);
         const float4 o = make_float4(__shfl_xor(v.x, 32), __shfl_xor(v.y, 32), __shfl_xor(v.z, 32),
                                      __shfl_xor(v.w, 32));
@@ -237,6 +238,27 @@ __global__ __launch_bounds__(256) void k_pool_partial(const float *__restrict__ 
     }
 }
 
+// packed batches: sequence b is rows [start[b], start[b] + len[b]), all valid; chunk ch covers its
+// rows 64 ch .. 64 ch + 63, so a right-padded batch sums in the same order as the masked kernel
+__global__ __launch_bounds__(256) void k_pool_partial_packed(const float *__restrict__ x,
+                                                             const int32_t *__restrict__ start,
+                                                             const int32_t *__restrict__ len, int D,
+                                                             int chunks, float *__restrict__ part,
+                                                             int *__restrict__ cnt) {
+    const int b = blockIdx.x / chunks, ch = blockIdx.x % chunks;
+    const int r0 = ch * 64, r1 = min(len[b], r0 + 64);
+    const size_t base = (size_t)start[b];
+    for (int c = threadIdx.x; c < D / 4; c += blockDim.x) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int r = r0; r < r1; r++) {
+            const float4 v = ld4(x + (base + r) * D + 4 * c);
+            acc = make_float4(acc.x + v.x, acc.y + v.y, acc.z + v.z, acc.w + v.w);
+        }
+        st4(part + ((size_t)b * chunks + ch) * D + 4 * c, acc);
+    }
+    if (threadIdx.x == 0) cnt[b * chunks + ch] = max(0, r1 - r0);
+}
+
 __global__ __launch_bounds__(256) void k_pool_finish(const float *__restrict__ part,
                                                      const int *__restrict__ cnt, int chunks,
                                                      int D, float *__restrict__ out) {
@@ -264,6 +286,17 @@ __global__ __launch_bounds__(256) void k_pool_finish(const float *__restrict__ p
     k = 0;
     for (int d = threadIdx.x; d < D && k < 4; d += blockDim.x, k++)
         out[(size_t)b * D + d] = n > 0 ? __fmul_rn(vals[k], inv) : 0.f;
+}
+
+// ---- packed batches: token ids of the packed rows (filler rows, rowmap < 0, get token 0)
+__global__ __launch_bounds__(256) void k_gather_ids(const int32_t *__restrict__ ids,
+                                                    const int32_t *__restrict__ rowmap, int M,
+                                                    int32_t *__restrict__ out) {
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r < M) {
+        const int src = rowmap[r];
+        out[r] = src >= 0 ? ids[src] : 0;
+    }
 }
 
 // ------------------------------------------------------------------ launchers
@@ -295,6 +328,15 @@ int launch_qkv_norm_rope(hipStream_t s, const QkvArgs &a) {
     const long items = (long)a.M * (a.H + 2 * a.KV);
     hipLaunchKernelGGL(k_qkv_norm_rope, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
     return check_hip(hipGetLastError(), "qkv_norm_rope launch");
+}
+
+int launch_pool_packed(hipStream_t s, const float *x, const int32_t *start, const int32_t *len,
+                       int B, int max_len, int D, float *part, int *cnt, float *out) {
+    const int chunks = (max_len + 63) / 64;
+    hipLaunchKernelGGL(k_pool_partial_packed, dim3(B * chunks), dim3(256), 0, s, x, start, len, D,
+                       chunks, part, cnt);
+    hipLaunchKernelGGL(k_pool_finish, dim3(B), dim3(256), 0, s, part, cnt, chunks, D, out);
+    return check_hip(hipGetLastError(), "pool launch");
 }
 
 int launch_pool(hipStream_t s, const float *x, const uint8_t *valid, int B, int S, int D,
@@ -367,7 +409,27 @@ extern "C" int e2mi_qkv_norm_rope(e2mi_stream stream, const float *qkv, int M, i
         set_error("qkv_norm_rope: null/misaligned pointer");
         return -1;
     }
-    QkvArgs a = {qkv, q_gamma, k_gamma, cos_tab, sin_tab, eps, q16, k16, vt16, q32, k32, v32, M, S, H, KV};
+    QkvArgs a = {qkv, q_gamma, k_gamma, cos_tab, sin_tab, eps, q16, k16, vt16, q32, k32, v32, nullptr, M, S, H, KV};
+    return launch_qkv_norm_rope((hipStream_t)stream, a);
+}
+
+extern "C" int e2mi_qkv_norm_rope_packed(e2mi_stream stream, const float *qkv, int M, const int32_t *pos,
+                                         int H, int KV, int D, const float *q_gamma, const float *k_gamma,
+                                         float eps, const float *cos_tab, const float *sin_tab,
+                                         uint16_t *q16, uint16_t *k16, uint16_t *vt16, float *q32,
+                                         float *k32, float *v32) {
+    if (D != 256 || H <= 0 || KV <= 0 || H % KV || M <= 0) {
+        set_error("qkv_norm_rope_packed: needs head_dim 256 and H %% KV == 0 (M=%d H=%d KV=%d D=%d)", M, H,
+                  KV, D);
+        return -1;
+    }
+    if (!qkv || !pos || !q_gamma || !k_gamma || !cos_tab || !sin_tab || !q16 || !k16 || !vt16 ||
+        !aligned16(qkv) || !al16(q32) || !al16(k32) || !al16(v32) || ((uintptr_t)q16 & 7) ||
+        ((uintptr_t)k16 & 7)) {
+        set_error("qkv_norm_rope_packed: null/misaligned pointer");
+        return -1;
+    }
+    QkvArgs a = {qkv, q_gamma, k_gamma, cos_tab, sin_tab, eps, q16, k16, vt16, q32, k32, v32, pos, M, M, H, KV};
     return launch_qkv_norm_rope((hipStream_t)stream, a);
 }
 
@@ -397,7 +459,32 @@ extern "C" int e2mi_pool_l2(e2mi_stream stream, const float *x, const uint8_t *v
     return launch_pool((hipStream_t)stream, x, valid, B, S, D, part, cnt, out);
 }
 
+extern "C" int e2mi_pool_l2_packed(e2mi_stream stream, const float *x, const int32_t *seq_start,
+                                   const int32_t *seq_len, int B, int max_len, int D, float *workspace,
+                                   float *out) {
+    if (!x || !seq_start || !seq_len || !workspace || !out || B <= 0 || max_len <= 0 || D <= 0 ||
+        D % 4 || D > 1024 || !aligned16(x) || !aligned16(workspace)) {
+        set_error("pool_l2_packed: bad geometry or pointers");
+        return -1;
+    }
+    const int chunks = (max_len + 63) / 64;
+    float *part = workspace;
+    int *cnt = (int *)(workspace + (size_t)B * chunks * D);
+    return launch_pool_packed((hipStream_t)stream, x, seq_start, seq_len, B, max_len, D, part, cnt, out);
+}
+
 extern "C" size_t e2mi_pool_workspace_bytes(int B, int S, int D) {
     const size_t chunks = (size_t)(S + 63) / 64;
     return (size_t)B * chunks * (D + 1) * sizeof(float);
+}
+
+extern "C" int e2mi_gather_ids(e2mi_stream stream, const int32_t *ids, const int32_t *rowmap, int M,
+                               int32_t *out) {
+    if (!ids || !rowmap || !out || M <= 0) {
+        set_error("gather_ids: null pointer or M <= 0");
+        return -1;
+    }
+    hipLaunchKernelGGL(k_gather_ids, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       ids, rowmap, M, out);
+    return check_hip(hipGetLastError(), "gather_ids launch");
 }

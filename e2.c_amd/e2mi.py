@@ -59,6 +59,10 @@ SIGNATURES = {
     "e2mi_pool_l2": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
     "e2mi_pool_workspace_bytes": (C.c_size_t, [_I, _I, _I]),
     "e2mi_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
+    "e2mi_qkv_norm_rope_packed": (_I, [_P, _P, _I, _P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "e2mi_attention_packed": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
+    "e2mi_pool_l2_packed": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
+    "e2mi_gather_ids": (_I, [_P, _P, _P, _I, _P]),
     # backend-selection surface (include/e2_dispatch.h)
     "e2_dispatch_set_cpu_backend": (None, [_I]),
     "e2_cpu_backend": (_I, []),
@@ -88,6 +92,7 @@ SIGNATURES = {
     "e2mi_text_embed_batch_device": (_I, [_P, _P, _P, _I, _I, _P, _P]),
     "e2mi_stats": (_I, [_P, C.POINTER(C.c_long), C.POINTER(C.c_long), C.POINTER(C.c_double)]),
     "e2mi_set_layer_limit": (_I, [_P, _I]),
+    "e2mi_set_packing": (_I, [_P, _I]),
 }
 
 _lib = None
@@ -368,6 +373,86 @@ def attention(q16, k16, vt16, valid, B, S, H, KV, scale=1.0, want_f32=True, stre
     return cq, cs, c32
 
 
+# ---- packed batches (valid tokens only, sequence b in rows [start[b], start[b] + len[b]))
+def pack_plan(valid):
+    """The engine's packed layout of a [B, S] mask: each sequence's valid tokens in order from a
+    row that is a multiple of 8, the total rounded up to 256. Returns (rowmap, pos, start, len, M):
+    rowmap[r] = b * S + s of packed row r (-1 for filler rows), pos[r] = s."""
+    import numpy as np
+    valid = np.asarray(valid).astype(bool)
+    B, S = valid.shape
+    rowmap, pos, start, lens = [], [], [], []
+    for b in range(B):
+        idx = np.nonzero(valid[b])[0]
+        start.append(len(rowmap))
+        lens.append(len(idx))
+        rowmap += list(b * S + idx)
+        pos += list(idx)
+        pad = (-len(rowmap)) % 8
+        rowmap += [-1] * pad
+        pos += [0] * pad
+    pad = (-len(rowmap)) % 256
+    rowmap += [-1] * pad
+    pos += [0] * pad
+    i32 = lambda v: np.asarray(v, np.int32)
+    return i32(rowmap), i32(pos), i32(start), i32(lens), len(rowmap)
+
+
+def qkv_norm_rope_packed(qkv, pos, H, KV, q_gamma, k_gamma, cos_tab, sin_tab, eps=1e-6,
+                         want_f32=True, stream=None):
+    import torch
+    M = qkv.shape[0]
+    D = 256
+    dev = qkv.device
+    q16 = torch.empty((M, H * D), dtype=torch.float16, device=dev)
+    k16 = torch.empty((M, KV * D), dtype=torch.float16, device=dev)
+    vt16 = torch.empty((KV, D, M), dtype=torch.float16, device=dev)
+    f = (lambda *s: torch.empty(s, dtype=torch.float32, device=dev)) if want_f32 else (lambda *s: None)
+    q32, k32, v32 = f(M, H * D), f(M, KV * D), f(M, KV * D)
+    check(load().e2mi_qkv_norm_rope_packed(stream_ptr(stream), ptr(qkv), M, ptr(pos), H, KV, D,
+                                           ptr(q_gamma), ptr(k_gamma), eps, ptr(cos_tab),
+                                           ptr(sin_tab), ptr(q16), ptr(k16), ptr(vt16), ptr(q32),
+                                           ptr(k32), ptr(v32)), "qkv_norm_rope_packed")
+    return q16, k16, vt16, q32, k32, v32
+
+
+def attention_packed(q16, k16, vt16, start, lens, max_len, H, KV, scale=1.0, want_f32=True,
+                     cq=None, cs=None, c32=None, stream=None):
+    import torch
+    M = q16.shape[0]
+    D = 256
+    dev = q16.device
+    cq = torch.zeros((M, H * D), dtype=torch.int8, device=dev) if cq is None else cq
+    cs = torch.zeros((M, H * D // 128), dtype=torch.float32, device=dev) if cs is None else cs
+    if want_f32 and c32 is None:
+        c32 = torch.zeros((M, H * D), dtype=torch.float32, device=dev)
+    check(load().e2mi_attention_packed(stream_ptr(stream), ptr(q16), ptr(k16), ptr(vt16), M,
+                                       ptr(start), ptr(lens), start.shape[0], max_len, H, KV, D,
+                                       scale, ptr(cq), ptr(cs), ptr(c32)), "attention_packed")
+    return cq, cs, c32
+
+
+def pool_l2_packed(x, start, lens, max_len, stream=None):
+    import torch
+    D = x.shape[1]
+    B = start.shape[0]
+    lib = load()
+    ws = torch.empty(lib.e2mi_pool_workspace_bytes(B, max_len, D) // 4 + 64, dtype=torch.float32,
+                     device=x.device)
+    out = torch.empty((B, D), dtype=torch.float32, device=x.device)
+    check(lib.e2mi_pool_l2_packed(stream_ptr(stream), ptr(x), ptr(start), ptr(lens), B, max_len, D,
+                                  ptr(ws), ptr(out)), "pool_l2_packed")
+    return out
+
+
+def gather_ids(ids, rowmap, stream=None):
+    import torch
+    M = rowmap.shape[0]
+    out = torch.empty(M, dtype=torch.int32, device=rowmap.device)
+    check(load().e2mi_gather_ids(stream_ptr(stream), ptr(ids), ptr(rowmap), M, ptr(out)), "gather_ids")
+    return out
+
+
 # ---- model container and encoder engine
 def baseline_config(**over):
     c = E2Config()
@@ -460,6 +545,10 @@ class Engine:
 
     def set_layer_limit(self, n: int):
         check(load().e2mi_set_layer_limit(self.h, n), "set_layer_limit")
+
+    def set_packing(self, on: bool):
+        """Packed batches (valid tokens only) on or off; off computes every padded row."""
+        check(load().e2mi_set_packing(self.h, 1 if on else 0), "set_packing")
 
     def __del__(self):
         if _lib is not None and getattr(self, "h", None):

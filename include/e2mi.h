@@ -157,6 +157,30 @@ int e2mi_pool_l2(e2mi_stream stream, const float *x, const uint8_t *valid, int B
                  float *workspace, float *out);
 size_t e2mi_pool_workspace_bytes(int B, int S, int D);
 
+/* Packed batches (no counterpart in the reference, which computes padding rows): the valid tokens
+ * of B sequences laid out back to back, sequence b in rows [seq_start[b], seq_start[b] +
+ * seq_len[b]). Row kernels and GEMMs are row-local and take the packed rows as they are; these
+ * three take the per-row RoPE position or the per-sequence row ranges instead of a padded mask.
+ * qkv_norm_rope_packed: as e2mi_qkv_norm_rope with positions pos [M] and V transposed over all
+ * rows, vt16 [KV][D][M]. */
+int e2mi_qkv_norm_rope_packed(e2mi_stream stream, const float *qkv, int M, const int32_t *pos,
+                              int H, int KV, int D, const float *q_gamma, const float *k_gamma,
+                              float eps, const float *cos_tab, const float *sin_tab, uint16_t *q16,
+                              uint16_t *k16, uint16_t *vt16, float *q32, float *k32, float *v32);
+/* attention of each packed sequence over its own rows (all valid); vt16 [KV][D][M] from
+ * e2mi_qkv_norm_rope_packed, seq_len[b] <= max_len; rows outside every sequence are not written */
+int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
+                          const uint16_t *vt16, int M, const int32_t *seq_start,
+                          const int32_t *seq_len, int B, int max_len, int H, int KV, int D,
+                          float scale, int8_t *ctx_q, float *ctx_s, float *ctx32);
+/* mean pool + L2 of each packed sequence's rows (workspace: e2mi_pool_workspace_bytes(B, max_len, D)) */
+int e2mi_pool_l2_packed(e2mi_stream stream, const float *x, const int32_t *seq_start,
+                        const int32_t *seq_len, int B, int max_len, int D, float *workspace,
+                        float *out);
+/* out[r] = rowmap[r] >= 0 ? ids[rowmap[r]] : 0 for r < M (the packed rows' token ids) */
+int e2mi_gather_ids(e2mi_stream stream, const int32_t *ids, const int32_t *rowmap, int M,
+                    int32_t *out);
+
 /* ---- attention */
 
 /* Fused bidirectional GQA attention (text.c:534-572,817-891): per sequence b, head h (kv head
@@ -194,8 +218,10 @@ int e2mi_text_embed(e2mi_engine *g, const int32_t *ids, int n_ids, float *out);
 int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const uint8_t *valid, int batch,
                           int seq_len, float *out);
 /* The same forward with DEVICE buffers already resident in HBM: ids [batch*seq_len], valid
- * [batch*seq_len], out [batch][hidden]; batch*seq_len must fit the workspace. Enqueued on `stream`
- * (NULL: the engine's own stream, then synchronised). Ids are clamped, not validated. */
+ * [batch*seq_len], out [batch][hidden]. Enqueued on `stream` (NULL: the engine's own stream, then
+ * synchronised). Ids are clamped, not validated. With packed batches the mask is first copied to
+ * the host (one synchronous copy of batch*seq_len bytes) to plan the packing, and batches larger
+ * than the workspace run in chunks; unpacked, batch*seq_len must fit the workspace. */
 int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, const uint8_t *valid,
                                  int batch, int seq_len, float *out, e2mi_stream stream);
 /* Calls served, kernels launched by the last forward, wall time of the last call (e2_hip_stats). */
@@ -203,6 +229,9 @@ int e2mi_stats(e2mi_engine *g, long *calls, long *kernels_last, double *last_ms)
 /* Run only the first n layers (0: all) before the final norm and pooling: the reference's
  * E2_HIP_LAYERS bisection knob (forward.c:359-366), for parity checks layer by layer. */
 int e2mi_set_layer_limit(e2mi_engine *g, int n_layers);
+/* Packed batches on (1, the default; E2MI_NOPACK=1 turns it off at creation) or off (0: every
+ * row of the padded batch is computed, as the reference does). No counterpart in the reference. */
+int e2mi_set_packing(e2mi_engine *g, int on);
 
 #ifdef __cplusplus
 }

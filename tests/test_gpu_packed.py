@@ -1,0 +1,181 @@
+"""Packed batches: only the valid tokens of each sequence are computed, laid out back to back.
+
+The packed kernels are checked against their padded counterparts on the same data (bit-exact for
+right-padded masks, where attention key tiles and pooling chunks fall the same way) and against the
+oracle (masks with holes, where the packed attention sees only the valid keys, as the masked one
+does). The engine's packed forward must give the padded forward's embeddings: bit-exact for
+right-padded batches, within the north star's cosine bar for masks with holes; the device entry
+point, including its chunking of batches larger than the workspace, must match the host one.
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_f32_close
+from model_util import random_batch, small_config
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+
+
+def _t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _np(t):
+    return t.cpu().numpy()
+
+
+def _mask(rng, B, S, lengths=None, holes=False):
+    valid = np.zeros((B, S), np.uint8)
+    for b in range(B):
+        L = int(rng.integers(1, S + 1)) if lengths is None else lengths[b]
+        valid[b, :L] = 1
+    if holes:
+        valid[rng.random((B, S)) < 0.1] = 0
+    return valid
+
+
+def test_pack_plan_layout(rng):
+    import e2mi
+    valid = _mask(rng, 5, 37, lengths=[37, 1, 0, 20, 9], holes=True)
+    rowmap, pos, start, lens, M = e2mi.pack_plan(valid)
+    assert M % 256 == 0 and np.all(start % 8 == 0)
+    for b in range(5):
+        idx = np.nonzero(valid[b])[0]
+        assert lens[b] == len(idx)
+        assert np.array_equal(rowmap[start[b]:start[b] + lens[b]], b * 37 + idx)
+        assert np.array_equal(pos[start[b]:start[b] + lens[b]], idx)
+    covered = np.zeros(M, bool)
+    for b in range(5):
+        covered[start[b]:start[b] + lens[b]] = True
+    assert np.all(rowmap[~covered] == -1)
+
+
+def test_gather_ids(gpu, rng):
+    import e2mi
+    ids = rng.integers(0, 1000, (3, 50)).astype(np.int32)
+    valid = _mask(rng, 3, 50, holes=True)
+    rowmap, _, _, _, M = e2mi.pack_plan(valid)
+    got = _np(e2mi.gather_ids(_t(ids.reshape(-1), gpu), _t(rowmap, gpu)))
+    want = np.where(rowmap >= 0, ids.reshape(-1)[np.maximum(rowmap, 0)], 0)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("B,S,lengths,holes", [
+    (3, 512, [512, 300, 33], False),
+    (4, 100, [100, 37, 1, 0], False),
+    (3, 77, None, True),
+])
+def test_packed_qkv_attention_pool_vs_padded(gpu, oracle, rng, B, S, lengths, holes):
+    import e2mi
+    import torch
+    H, KV, D = 3, 1, 256
+    valid = _mask(rng, B, S, lengths, holes)
+    rowmap, pos, start, lens, M = e2mi.pack_plan(valid)
+    qkv = (rng.standard_normal((B * S, (H + 2 * KV) * D)) * 15).astype(np.float32)
+    gq = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
+    gk = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
+    cs, sn = oracle.rope_table(S, D, 10000.0)
+    args = (_t(gq, gpu), _t(gk, gpu), _t(cs, gpu), _t(sn, gpu), EPS)
+    # padded
+    q16, k16, vt16, q32, _, _ = e2mi.qkv_norm_rope(_t(qkv, gpu), S, H, KV, *args)
+    cq, cs_, c32 = e2mi.attention(q16, k16, vt16, _t(valid.reshape(-1), gpu), B, S, H, KV)
+    # packed: the valid rows gathered (filler rows get arbitrary finite values)
+    qkv_p = qkv[np.maximum(rowmap, 0)]
+    p16, pk16, pvt16, p32, _, _ = e2mi.qkv_norm_rope_packed(_t(qkv_p, gpu), _t(pos, gpu), H, KV, *args)
+    sd, ld = _t(start, gpu), _t(lens, gpu)
+    pq, ps, p32c = e2mi.attention_packed(p16, pk16, pvt16, sd, ld, S, H, KV)
+    live = rowmap >= 0
+    src = rowmap[live]
+    # q/k/v stages are row-local: identical on the packed rows
+    assert torch.equal(p16[_t(np.nonzero(live)[0], gpu)], q16[_t(src, gpu)])
+    vt_pad = _np(vt16.float())                        # [B][KV][D][S]
+    vt_pk = _np(pvt16.float())                        # [KV][D][M]
+    for b in range(B):
+        idx = np.nonzero(valid[b])[0]
+        assert np.array_equal(vt_pk[:, :, start[b]:start[b] + lens[b]], vt_pad[b][:, :, idx])
+    # filler rows: not written by the packed attention (zero-initialised here)
+    assert np.all(_np(pq)[~live] == 0) and np.all(_np(ps)[~live] == 0)
+    got = _np(p32c)[live]
+    if not holes:
+        assert np.array_equal(got, _np(c32)[src])
+        assert np.array_equal(_np(pq)[live], _np(cq)[src]) and np.array_equal(_np(ps)[live], _np(cs_)[src])
+    qf, kf = _np(p16.float()), _np(pk16.float())
+    v32 = np.ascontiguousarray(vt_pk.transpose(2, 0, 1).reshape(M, KV * D))  # [M][KV*D]
+    for b in range(B):
+        if lens[b] == 0:
+            continue
+        r = slice(start[b], start[b] + lens[b])
+        want = oracle.attention(np.ascontiguousarray(qf[r]), np.ascontiguousarray(kf[r]),
+                                np.ascontiguousarray(v32[r]), np.ones(lens[b], np.uint8), H, KV, D)
+        g = _np(p32c)[r].astype(np.float64).reshape(-1, D)
+        w = want.astype(np.float64).reshape(-1, D)
+        cos = (g * w).sum(1) / (np.linalg.norm(g, axis=1) * np.linalg.norm(w, axis=1))
+        assert cos.min() >= 0.9999
+    # pooling of the packed rows == masked pooling of the padded rows
+    x = rng.standard_normal((B * S, 768)).astype(np.float32)
+    pool_pad = _np(e2mi.pool_l2(_t(x, gpu), _t(valid.reshape(-1), gpu), B, S))
+    pool_pk = _np(e2mi.pool_l2_packed(_t(x[np.maximum(rowmap, 0)], gpu), sd, ld, S))
+    if not holes:
+        assert np.array_equal(pool_pk, pool_pad)
+    else:
+        assert_f32_close(pool_pk, pool_pad, rtol=1e-5, atol=1e-7, what="pool")
+    assert np.all(pool_pk[lens == 0] == 0)
+
+
+@pytest.fixture(scope="module")
+def engine(gpu):
+    import e2mi
+    m = e2mi.Model.synthetic(small_config(e2mi, n_layers=2), 77)
+    return e2mi, m, e2mi.Engine(m, max_rows=1024)
+
+
+def test_engine_packed_equals_padded(engine, rng):
+    e2mi, m, eng = engine
+    ids, valid = random_batch(rng, 6, 160, 1000, min_len=1)
+    valid[4] = 0                                       # an all-padding sequence
+    eng.set_packing(False)
+    try:
+        pad = eng.embed_batch(ids, valid)
+    finally:
+        eng.set_packing(True)
+    pk = eng.embed_batch(ids, valid)
+    assert np.array_equal(pk, pad)
+    assert np.all(pk[4] == 0)
+    # holes inside sequences: the packed attention sees the same valid keys, but its 32-key tiles
+    # group them differently (the padded tiles hold masked positions), so the online softmax
+    # rounds its f16 probabilities against other running maxima; the pooling's chunks differ too.
+    # Two random-init layers at logit scale 1.0 amplify such roundings (a 1-ulp change of the
+    # embedding table alone moves embeddings to ~0.9998): the north star's cosine bar applies
+    ids2, valid2 = random_batch(rng, 4, 96, 1000, min_len=20, holes=True)
+    eng.set_packing(False)
+    try:
+        pad2 = eng.embed_batch(ids2, valid2)
+    finally:
+        eng.set_packing(True)
+    pk2 = eng.embed_batch(ids2, valid2)
+    cos = (pk2 * pad2).sum(1) / (np.linalg.norm(pk2, axis=1) * np.linalg.norm(pad2, axis=1))
+    assert cos.min() >= 0.9999, cos
+
+
+def test_engine_packed_chunks_and_device_path(engine, rng):
+    """Batches larger than the 1024-row workspace run in chunks, on the host and device paths."""
+    import torch
+    e2mi, m, eng = engine
+    ids, valid = random_batch(rng, 13, 200, 1000, min_len=1)
+    host = eng.embed_batch(ids, valid)
+    eng.set_packing(False)
+    try:
+        pad = eng.embed_batch(ids, valid)
+    finally:
+        eng.set_packing(True)
+    assert np.array_equal(host, pad)
+    dev = torch.device("cuda:0")
+    out = torch.empty((13, 768), device=dev)
+    for _ in range(3):                                  # eager, record, replay
+        out.zero_()
+        eng.embed_batch_device(_t(ids, dev), _t(valid, dev), out)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), host)
