@@ -13,7 +13,9 @@
 // over d = 256) so that every lane holds 16 logits of ONE query: the running max/sum of the online
 // softmax need only one exchange with the partner lane (lane ^ 32). P^T then feeds O^T += V^T P^T
 // (16 more MFMAs) straight from registers: the 16 logits a lane holds are exactly the keys its
-// B-operand slots must carry, once the A operand (V^T) is read in the same key order.
+// B-operand slots must carry, once the A operand (V^T) is read in the same key order. K tile rows
+// are stored with bits 2 and 3 of the key index exchanged, which makes those keys consecutive
+// (16 j + 8 half + 0..7 for MFMA j), so a lane's V^T operand is 8 consecutive keys of one row.
 #include "common.h"
 
 namespace e2mi {
@@ -100,7 +102,9 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
             const int key = tid / 32 + 8 * p, ch = tid % 32;
             uint4 val = make_uint4(0, 0, 0, 0);
             if (k0 + key < Sk) val = *(const uint4 *)(kbase + (size_t)(k0 + key) * a.KV * kD + ch * 8);
-            *(uint4 *)(Ks + key * kKP + ch * 8) = val;
+            // row swap23(key): see the S^T register layout below
+            const int row = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+            *(uint4 *)(Ks + row * kKP + ch * 8) = val;
         }
         // V^T tile: row d = tid, keys k0 .. k0+31
         {
@@ -128,12 +132,15 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
                 st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
             }
         }
-        // online softmax for this lane's query over the 16 keys it holds (+ the partner's 16)
+        // online softmax for this lane's query over the 16 keys it holds (+ the partner's 16).
+        // K row i holds key swap23(i), so register r (row 8 (r / 4) + 4 half + r % 4) holds key
+        // 16 (r / 8) + 8 half + 4 ((r / 4) % 2) + r % 4: registers 8 j .. 8 j + 7 hold the
+        // consecutive keys 16 j + 8 half .. + 7, the PV MFMA's k order
         float tv[16];
         float mloc = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int key = 8 * (r >> 2) + 4 * half + (r & 3);
+            const int key = 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
             tv[r] = vk[key] ? st[r] * a.scale : -INFINITY;
             mloc = fmaxf(mloc, tv[r]);
         }
@@ -159,7 +166,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
 #pragma unroll
         for (int t = 0; t < 8; t++) o[t] *= alpha;
         // O^T += V^T P^T: MFMA #j covers the keys of registers 8j..8j+7, i.e. keys
-        // 16j + {4 half + 0..3, 8 + 4 half + 0..3}; V^T is read in that order
+        // 16 j + 8 half + 0..7; V^T is read in that order
         h8 pb[2];
 #pragma unroll
         for (int j = 0; j < 2; j++)
@@ -167,11 +174,11 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
             for (int e = 0; e < 8; e++) pb[j][e] = ph[8 * j + e];
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            const _Float16 *vp = Vs + (32 * t + (lane & 31)) * kVP + 4 * half;
+            const _Float16 *vp = Vs + (32 * t + (lane & 31)) * kVP + 8 * half;
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 h8 vf;
-                const uint2 lo = *(const uint2 *)(vp + 16 * j), hi = *(const uint2 *)(vp + 16 * j + 8);
+                const uint2 lo = *(const uint2 *)(vp + 16 * j), hi = *(const uint2 *)(vp + 16 * j + 4);
                 *(uint2 *)&vf = lo;
                 *((uint2 *)&vf + 1) = hi;
                 o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[j], o[t], 0, 0, 0);
@@ -209,6 +216,205 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
             }
         if (half == 0) a.cs[orow * (HD / kQBlock) + h * 2 + blk] = qs.sc;
     }
+}
+
+// ---- packed batches: the same attention with K/V tiles fetched straight into LDS one tile ahead.
+// Every key of a packed sequence is valid, so no mask is read; the per-sequence work is the
+// arithmetic of k_attn bit for bit (same MFMA order, same softmax; masked keys read as zero here
+// and contribute p = 0 in both).
+//
+// LDS per workgroup: 2 buffers of [K tile 32 keys x 512 B | V^T tile 256 d x 64 B] = 64 KB.
+//   K tile row i holds key swap23(i) (bits 2 and 3 of the index exchanged). The S^T MFMA then
+//     leaves in a lane's registers 8 j + e (e = 0..7) the keys 16 j + 8 half + e: consecutive keys,
+//     so the PV MFMA's A operand is one 16-byte chunk of a V^T row in natural key order.
+//   K rows are 512 B; 16-byte chunk x of row i sits at position x ^ (i & 7), so the eight lanes of
+//     a read group (rows i..i+7, one chunk) hit eight bank groups.
+//   V^T rows (one d, 32 keys) are 64 B; chunk c of row d sits at position c ^ ((d >> 2) & 3)
+//     (conflict-free for rows d..d+7).
+// The tile loads are 16-byte direct-to-LDS buffer loads, 4 per wave for K (two rows each) and 4
+// for V^T (16 rows each), whose lanes fetch the permuted, swizzled source chunks. Keys past the
+// sequence read as zero (K: past the descriptor's range; V^T: 8-key chunks past the sequence get an
+// offset past it, and the sequence's rows end on an 8-row boundary of the slab).
+constexpr int kPKTile = kKT * 512, kPVTile = kD * 64, kPBuf = kPKTile + kPVTile;
+constexpr size_t kAttnPackedLds = 2 * (size_t)kPBuf;
+
+__global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
+    extern __shared__ __align__(16) unsigned char pk_smem[];
+    const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5;
+    const int S = a.S, HD = a.H * kD, kvh = h / (a.H / a.KV);
+    const size_t row0 = (size_t)a.seq_start[b];
+    const int Sk = a.seq_len[b];
+    if (qb * 128 >= Sk) return;  // no rows of this sequence in the block
+
+    const int qi = qb * 128 + w * 32 + (lane & 31);  // this lane's query
+    const bool qvalid = qi < Sk;
+    const int qc = min(qi, Sk - 1);
+    h8 qf[16];
+    {
+        const uint16_t *qp = a.q + (row0 + qc) * HD + h * kD + 8 * half;
+#pragma unroll
+        for (int s = 0; s < 16; s++) qf[s] = *(const h8 *)(qp + 16 * s);
+    }
+    // wait for the Q loads here, with a wait the compiler's wait-count pass sees: otherwise it
+    // waits for them inside the tile loop, where the count would also cover the tile loads in
+    // flight (s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15))
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    f16v o[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) o[t] = (f16v){};
+    float mrun = -INFINITY, lrun = 0.f;
+    const int ntiles = (Sk + kKT - 1) / kKT;
+
+    // sources: K rows of this kv head (row pitch KV*D halves), V^T slab [D][S] of this kv head
+    const uint32_t rowB = (uint32_t)a.KV * kD * 2;
+    const v4u rK = rsrc_words(a.k + row0 * a.KV * kD + kvh * kD, (uint32_t)Sk * rowB);
+    const uint16_t *vslab = a.vt + (size_t)kvh * kD * S + row0;
+    const v4u rV = rsrc_words(vslab, (uint32_t)((size_t)kD * S * 2));
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)pk_smem);
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    const int lh = lane >> 5, lc = lane & 31;
+    // K: instruction i of wave w fills LDS rows 8 w + 2 i + lane / 32, i.e. keys swap23 of that
+    // (the scalar part goes to the scalar offset); lane's chunk position lane % 32 holds source
+    // chunk (lane % 32) ^ (row & 7), row & 7 = (2 i + lane / 32) & 7.
+    // V^T: instruction i of wave w fills rows d = 64 w + 16 i + lane / 4, chunk position lane % 4,
+    // which holds source chunk (lane % 4) ^ ((d >> 2) & 3) = (lane % 4) ^ ((lane >> 4) & 3).
+    const uint32_t vlane = (uint32_t)(lane >> 2) * (uint32_t)S * 2;
+    const int vchunk = (lane & 3) ^ ((lane >> 4) & 3);
+    auto issue_tile = [&](int kt) {
+        const int k0 = kt * kKT;
+        const uint32_t base = lds0 + (uint32_t)((kt & 1) * kPBuf);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int ks = 16 * (wu >> 1) + 8 * ((i >> 1) & 1) + 4 * (wu & 1) + 2 * (i & 1);  // swap23(row) - lane / 32
+            const uint32_t voff = (uint32_t)lh * rowB + (uint32_t)((lc ^ ((2 * i + lh) & 7)) << 4);
+            dma16(rK, __builtin_amdgcn_readfirstlane(base + (4 * wu + i) * 1024), voff,
+                  __builtin_amdgcn_readfirstlane((uint32_t)(ks + k0) * rowB));
+        }
+        const uint32_t vo = (k0 + 8 * vchunk < Sk) ? vlane + (uint32_t)vchunk * 16 : 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            dma16(rV, __builtin_amdgcn_readfirstlane(base + kPKTile + (64 * wu + 16 * i) * 64), vo,
+                  __builtin_amdgcn_readfirstlane((uint32_t)((64 * wu + 16 * i) * S + k0) * 2));
+    };
+
+    // per-lane LDS read offsets. K (S^T A operand): row lane % 32, chunk 2 s + half at position
+    // (2 s + half) ^ (row & 7): for s = 4 t + u the position is 8 t + ((2 u + half) ^ (row & 7)).
+    const int kkey = lane & 31;
+    uint32_t krd[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) krd[u] = (uint32_t)(kkey * 512 + (((2 * u + half) ^ (kkey & 7)) << 4));
+    // V^T (PV A operand): row d = 32 t + lane % 32, chunk 2 j + half at position ^ ((d >> 2) & 3)
+    uint32_t vrd[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+        vrd[j] = (uint32_t)(kPKTile + (lane & 31) * 64 + (((2 * j + half) ^ (((lane & 31) >> 2) & 3)) << 4));
+
+    if (ntiles > 0) issue_tile(0);
+    for (int kt = 0; kt < ntiles; kt++) {
+        const int k0 = kt * kKT;
+        // this wave's loads of tile kt have landed; the barrier makes every wave's visible and
+        // ends every wave's reads of tile kt - 1, whose buffer the next loads refill
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (kt + 1 < ntiles) issue_tile(kt + 1);
+        const unsigned char *sb = pk_smem + (kt & 1) * kPBuf;
+
+        f16v st = (f16v){};
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const h8 kf = *(const h8 *)(sb + krd[s & 3] + (s >> 2) * 128);
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
+        }
+        float tv[16];
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            // S^T row 8 (r / 4) + 4 half + r % 4 of this register holds key swap23(row)
+            const int key = 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
+            tv[r] = (k0 + key < Sk) ? st[r] * a.scale : -INFINITY;
+            mloc = fmaxf(mloc, tv[r]);
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        const float mnew = fmaxf(mrun, mloc);
+        float alpha = 1.f;
+        float psum = 0.f;
+        _Float16 ph[16];
+        if (mnew == -INFINITY) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) ph[r] = (_Float16)0.f;
+        } else {
+            alpha = __expf(mrun - mnew);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float pr = tv[r] == -INFINITY ? 0.f : __expf(tv[r] - mnew);
+                psum += pr;
+                ph[r] = (_Float16)pr;
+            }
+        }
+        lrun = lrun * alpha + psum;
+        mrun = mnew;
+        // the running max rarely moves after the first tiles: skip the rescale when no lane's did
+        if (__any(alpha != 1.f)) {
+#pragma unroll
+            for (int t = 0; t < 8; t++) o[t] *= alpha;
+        }
+        h8 pb[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) pb[j][e] = ph[8 * j + e];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const h8 vf = *(const h8 *)(sb + vrd[j] + t * 32 * 64);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[j], o[t], 0, 0, 0);
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    const float ltot = lrun + __shfl_xor(lrun, 32);
+    const float inv = (qvalid && ltot > 0.f) ? __fdiv_rn(1.0f, ltot) : 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; t++) o[t] *= inv;
+    if (qi >= Sk) return;  // rows past the sequence belong to the next one
+    const size_t orow = (row0 + qi);
+#pragma unroll
+    for (int blk = 0; blk < 2; blk++) {
+        float am = 0.f;
+#pragma unroll
+        for (int t = 4 * blk; t < 4 * blk + 4; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) am = fmaxf(am, fabsf(o[t][r]));
+        am = fmaxf(am, __shfl_xor(am, 32));
+        const QScale qs = qscale(am);
+#pragma unroll
+        for (int t = 4 * blk; t < 4 * blk + 4; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int d = 32 * t + 8 * g + 4 * half;
+                *(uint32_t *)(a.cq + orow * HD + h * kD + d) =
+                    pack4(qbyte(o[t][4 * g], qs.inv), qbyte(o[t][4 * g + 1], qs.inv),
+                          qbyte(o[t][4 * g + 2], qs.inv), qbyte(o[t][4 * g + 3], qs.inv));
+                if (a.c32)
+                    *(float4 *)(a.c32 + orow * HD + h * kD + d) =
+                        make_float4(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]);
+            }
+        if (half == 0) a.cs[orow * (HD / kQBlock) + h * 2 + blk] = qs.sc;
+    }
+}
+
+static int attn_packed_attr() {
+    static bool done = false;
+    if (!done) {
+        if (check_hip(hipFuncSetAttribute((const void *)k_attn_packed, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)kAttnPackedLds), "attention lds attribute"))
+            return -1;
+        done = true;
+    }
+    return 0;
 }
 
 }  // namespace e2mi
@@ -250,6 +456,16 @@ extern "C" int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, co
         return -1;
     }
     AttnArgs a = {q16, k16, vt16, nullptr, ctx_q, ctx_s, ctx32, seq_start, seq_len, B, M, H, KV, scale};
-    hipLaunchKernelGGL(k_attn, dim3((max_len + 127) / 128, H, B), dim3(256), 0, (hipStream_t)stream, a);
+    // the direct-to-LDS kernel needs 4-byte-aligned V^T rows and 32-bit offsets into the V^T slab
+    // and the K rows; every sequence must start on an even row (the engine starts them on
+    // multiples of 8)
+    if (M % 2 == 0 && (size_t)KV * kD * M * 2 < 0x7fffffffu && (size_t)M * KV * kD * 2 < 0x7fffffffu &&
+        ((uintptr_t)vt16 & 3) == 0) {
+        if (attn_packed_attr()) return -1;
+        hipLaunchKernelGGL(k_attn_packed, dim3((max_len + 127) / 128, H, B), dim3(256), kAttnPackedLds,
+                           (hipStream_t)stream, a);
+    } else {
+        hipLaunchKernelGGL(k_attn, dim3((max_len + 127) / 128, H, B), dim3(256), 0, (hipStream_t)stream, a);
+    }
     return check_hip(hipGetLastError(), "attention launch");
 }

@@ -93,5 +93,34 @@ __device__ inline int xcd_swizzle(int pid, int total) {
     return (pid % kXcd) * (total / kXcd) + pid / kXcd;
 }
 
+// The same direct-to-LDS loads as inline assembly, for the pipelined kernels (GEMM, attention). The compiler's
+// wait-count pass cannot tell which LDS bytes a builtin direct-to-LDS load writes, so after one it
+// waits for all of them (s_waitcnt vmcnt(0)) before the next LDS read, draining a multi-stage load
+// pipeline every K step. Loads issued here are invisible to that pass: the kernel orders them
+// itself (explicit vmcnt waits + barriers), and issues no other vector-memory load the compiler
+// would wait for inside the loop. M0 carries the LDS destination (no other code in the kernel uses
+// M0); one wait state separates its write from the load.
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ inline v4u rsrc_words(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    v4u r;
+    r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
+    r.z = __builtin_amdgcn_readfirstlane(bytes);
+    r.w = 0x00020000u;
+    return r;
+}
+__device__ inline void dma16(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory");
+}
+__device__ inline void dma4(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                 ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory");
+}
+
 }  // namespace e2mi
 #endif

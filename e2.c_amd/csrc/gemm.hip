@@ -60,8 +60,6 @@ __device__ inline float gelu_tanh(float v) {
 __device__ inline int swzk(int r) { return (r >> 1) & 7; }
 __device__ inline int swz(int r, int c) { return r * 128 + ((c ^ swzk(r)) << 4); }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // Buffer loads straight into LDS: the per-lane offset is a VGPR fixed for the whole K loop and the
 // K step's offset a scalar, so a step costs no VALU address arithmetic. (Device functions rather
 // than lambdas: the builtin is only known to the device pass.)
@@ -72,33 +70,7 @@ __device__ inline void lds_load4(__amdgpu_buffer_rsrc_t r, void *lds, uint32_t v
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, voff, soff, 0, 0);
 }
 
-// The same direct-to-LDS loads as inline assembly, for the pipelined kernel. The compiler's
-// wait-count pass cannot tell which LDS bytes a builtin direct-to-LDS load writes, so after one it
-// waits for all of them (s_waitcnt vmcnt(0)) before the next LDS read, draining a multi-stage load
-// pipeline every K step. Loads issued here are invisible to that pass: the kernel orders them
-// itself (explicit vmcnt waits + barriers), and issues no other vector-memory load the compiler
-// would wait for inside the loop. M0 carries the LDS destination (no other code in the kernel uses
-// M0); one wait state separates its write from the load.
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-__device__ inline v4u rsrc_words(const void *base, uint32_t bytes) {
-    const uint64_t a = (uint64_t)base;
-    v4u r;
-    r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
-    r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
-    r.z = __builtin_amdgcn_readfirstlane(bytes);
-    r.w = 0x00020000u;
-    return r;
-}
-__device__ inline void dma16(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
-                 : "memory");
-}
-__device__ inline void dma4(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-                 ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
-                 : "memory");
-}
+// The direct-to-LDS loads of the pipelined kernel (dma16, dma4, rsrc_words) are in common.h.
 
 // The accumulator-dump kernel (e2mi_i8_gemm_acc, the parity hook for "bit-exact int32
 // accumulators"): 128 x 128 tiles of 4 waves of 64 x 64, two direct-to-LDS stages, the exact fold
