@@ -138,21 +138,76 @@ struct QkvArgs {
     int M, S, H, KV;
 };
 
-__device__ inline uint16_t f2h(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+// f16 of an f32 value that is already rounded: the register barrier keeps the compiler from folding
+// the multiply that produced x into the conversion (v_fma_mix rounds the exact product to f16
+// once, which differs from rounding it to f32 first)
+__device__ inline uint16_t f2h(float x) {
+    asm volatile("" : "+v"(x));
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
 
-__global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a) {
-    constexpr int D = 256;
+// The first nv blocks take the v heads, 32 rows each (one block per kv head and row block), and
+// write V^T through LDS so that each d row of V^T gets 64 contiguous bytes instead of one 2-byte
+// store per (row, d); they come first so that their longer chains overlap the q/k blocks. The other
+// blocks take the q and k heads, one wave per (row, head).
+__global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a, int nv) {
+    constexpr int D = 256, VR = 32;
     const int heads = a.H + 2 * a.KV;
-    const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= (long)a.M * heads) return;
-    const int m = (int)(item / heads), h = (int)(item % heads), l = threadIdx.x & 63;
-    const int kind = h < a.H ? 0 : (h < a.H + a.KV ? 1 : 2);  // q, k, v
+    const int l = threadIdx.x & 63;
+    if ((int)blockIdx.x < nv) {
+        __shared__ __align__(16) uint16_t vbuf[VR * D];
+        const int vb = (int)blockIdx.x, nrb = (a.M + VR - 1) / VR;
+        const int vh = vb / nrb, m0 = (vb % nrb) * VR, w = threadIdx.x >> 6;
+        const int h = a.H + a.KV + vh;
+        // wave w: rows 8 w .. 8 w + 7, four at a time (independent loads in flight)
+#pragma unroll
+        for (int r0 = 8 * w; r0 < 8 * w + 8; r0 += 4) {
+            float4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                v[j] = m0 + r0 + j < a.M ? ld4(a.qkv + (size_t)(m0 + r0 + j) * heads * D + h * D + 4 * l)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float inv = rms_inv(group_sum<64>(sumsq4(v[j])), D, a.eps);
+                const float4 x = make_float4(__fmul_rn(v[j].x, inv), __fmul_rn(v[j].y, inv),
+                                             __fmul_rn(v[j].z, inv), __fmul_rn(v[j].w, inv));
+                const uint32_t lo = (uint32_t)f2h(x.x) | ((uint32_t)f2h(x.y) << 16);
+                const uint32_t hi = (uint32_t)f2h(x.z) | ((uint32_t)f2h(x.w) << 16);
+                *(uint2 *)(vbuf + (r0 + j) * D + 4 * l) = make_uint2(lo, hi);
+                if (a.v32 && m0 + r0 + j < a.M) st4(a.v32 + (size_t)(m0 + r0 + j) * a.KV * D + vh * D + 4 * l, x);
+            }
+        }
+        __syncthreads();
+        // thread d writes V^T row d for the block's rows: [B][KV][D][S], row m at (m / S, m % S)
+        const int d = threadIdx.x, nr = min(VR, a.M - m0);
+        const int b0 = m0 / a.S, p0 = m0 % a.S;
+        uint16_t *dst = a.vt16 + ((size_t)(b0 * a.KV + vh) * D + d) * a.S + p0;
+        if (nr == VR && p0 + VR <= a.S && ((uintptr_t)dst & 15) == 0) {
+#pragma unroll
+            for (int c = 0; c < VR / 8; c++) {
+                uint32_t wv[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    wv[k] = (uint32_t)vbuf[(8 * c + 2 * k) * D + d] | ((uint32_t)vbuf[(8 * c + 2 * k + 1) * D + d] << 16);
+                *(uint4 *)(dst + 8 * c) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+            }
+        } else {
+            for (int r = 0; r < nr; r++) {
+                const int m = m0 + r, b = m / a.S, p = m % a.S;
+                a.vt16[((size_t)(b * a.KV + vh) * D + d) * a.S + p] = vbuf[r * D + d];
+            }
+        }
+        return;
+    }
+    const int qkh = a.H + a.KV;
+    const long item = (long)(blockIdx.x - nv) * 4 + (threadIdx.x >> 6);
+    if (item >= (long)a.M * qkh) return;
+    const int m = (int)(item / qkh), h = (int)(item % qkh);
+    const int kind = h < a.H ? 0 : 1;  // q, k
     float4 v = ld4(a.qkv + (size_t)m * heads * D + h * D + 4 * l);
     const float inv = rms_inv(group_sum<64>(sumsq4(v)), D, a.eps);
-    if (kind == 2) {
-        v = make_float4(__fmul_rn(v.x, inv), __fmul_rn(v.y, inv), __fmul_rn(v.z, inv),
-                        __fmul_rn(v.w, inv));
-    } else {
+    {
         v = scale4(v, inv, ld4((kind == 0 ? a.q_gamma : a.k_gamma) + 4 * l));
         // rotate-half: lane l < 32 holds a = x[i], lane l + 32 holds y = x[i + 128]
         const int pos = a.pos ? a.pos[m] : m % a.S;
@@ -172,18 +227,10 @@ __global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a) {
     if (kind == 0) {
         *(uint2 *)(a.q16 + (size_t)m * a.H * D + h * D + 4 * l) = make_uint2(lo, hi);
         if (a.q32) st4(a.q32 + (size_t)m * a.H * D + h * D + 4 * l, v);
-    } else if (kind == 1) {
+    } else {
         const int kh = h - a.H;
         *(uint2 *)(a.k16 + (size_t)m * a.KV * D + kh * D + 4 * l) = make_uint2(lo, hi);
         if (a.k32) st4(a.k32 + (size_t)m * a.KV * D + kh * D + 4 * l, v);
-    } else {
-        const int vh = h - a.H - a.KV, b = m / a.S, p = m % a.S;
-        uint16_t *dst = a.vt16 + ((size_t)(b * a.KV + vh) * D + 4 * l) * a.S + p;
-        dst[0] = (uint16_t)lo;
-        dst[a.S] = (uint16_t)(lo >> 16);
-        dst[2 * a.S] = (uint16_t)hi;
-        dst[3 * a.S] = (uint16_t)(hi >> 16);
-        if (a.v32) st4(a.v32 + (size_t)m * a.KV * D + vh * D + 4 * l, v);
     }
 }
 
@@ -325,8 +372,13 @@ static int row_launch(hipStream_t s, int mode, const RowArgs &a) {
 int launch_rows(hipStream_t s, int mode, const RowArgs &a) { return row_launch(s, mode, a); }
 
 int launch_qkv_norm_rope(hipStream_t s, const QkvArgs &a) {
-    const long items = (long)a.M * (a.H + 2 * a.KV);
-    hipLaunchKernelGGL(k_qkv_norm_rope, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
+    const long nqk = ((long)a.M * (a.H + a.KV) + 3) / 4;
+    const long nv = (long)a.KV * ((a.M + 31) / 32);
+    if (nqk + nv > 0x7fffffffL) {
+        set_error("qkv_norm_rope: too many rows");
+        return -1;
+    }
+    hipLaunchKernelGGL(k_qkv_norm_rope, dim3((unsigned)(nqk + nv)), dim3(256), 0, s, a, (int)nv);
     return check_hip(hipGetLastError(), "qkv_norm_rope launch");
 }
 
