@@ -236,6 +236,14 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
 // sequence read as zero (K: past the descriptor's range; V^T: 8-key chunks past the sequence get an
 // offset past it, and the sequence's rows end on an 8-row boundary of the slab).
 constexpr int kPKTile = kKT * 512, kPVTile = kD * 64, kPBuf = kPKTile + kPVTile;
+
+// dma16 without a compiler memory clobber: the loads of tile kt + 1 fill the LDS buffer that no
+// read of tile kt touches, so LDS reads and MFMAs may be scheduled across them; the loop-top wait
+// and barrier order them with the reads of tile kt + 1
+__device__ inline void dma16_nc(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 ::"s"(lds), "v"(voff), "s"(r), "s"(soff));
+}
 constexpr size_t kAttnPackedLds = 2 * (size_t)kPBuf;
 
 __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
@@ -281,21 +289,22 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
     // which holds source chunk (lane % 4) ^ ((d >> 2) & 3) = (lane % 4) ^ ((lane >> 4) & 3).
     const uint32_t vlane = (uint32_t)(lane >> 2) * (uint32_t)S * 2;
     const int vchunk = (lane & 3) ^ ((lane >> 4) & 3);
-    auto issue_tile = [&](int kt) {
+    // load j (0-3: K, 4-7: V^T) of tile kt; issued one per two S^T MFMAs of the previous tile
+    auto issue_load = [&](int kt, int j) {
         const int k0 = kt * kKT;
         const uint32_t base = lds0 + (uint32_t)((kt & 1) * kPBuf);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
+        if (j < 4) {
+            const int i = j;
             const int ks = 16 * (wu >> 1) + 8 * ((i >> 1) & 1) + 4 * (wu & 1) + 2 * (i & 1);  // swap23(row) - lane / 32
             const uint32_t voff = (uint32_t)lh * rowB + (uint32_t)((lc ^ ((2 * i + lh) & 7)) << 4);
-            dma16(rK, __builtin_amdgcn_readfirstlane(base + (4 * wu + i) * 1024), voff,
-                  __builtin_amdgcn_readfirstlane((uint32_t)(ks + k0) * rowB));
+            dma16_nc(rK, __builtin_amdgcn_readfirstlane(base + (4 * wu + i) * 1024), voff,
+                     __builtin_amdgcn_readfirstlane((uint32_t)(ks + k0) * rowB));
+        } else {
+            const int i = j - 4;
+            const uint32_t vo = (k0 + 8 * vchunk < Sk) ? vlane + (uint32_t)vchunk * 16 : 0x80000000u;
+            dma16_nc(rV, __builtin_amdgcn_readfirstlane(base + kPKTile + (64 * wu + 16 * i) * 64), vo,
+                     __builtin_amdgcn_readfirstlane((uint32_t)((64 * wu + 16 * i) * S + k0) * 2));
         }
-        const uint32_t vo = (k0 + 8 * vchunk < Sk) ? vlane + (uint32_t)vchunk * 16 : 0x80000000u;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            dma16(rV, __builtin_amdgcn_readfirstlane(base + kPKTile + (64 * wu + 16 * i) * 64), vo,
-                  __builtin_amdgcn_readfirstlane((uint32_t)((64 * wu + 16 * i) * S + k0) * 2));
     };
 
     // per-lane LDS read offsets. K (S^T A operand): row lane % 32, chunk 2 s + half at position
@@ -310,14 +319,16 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
     for (int j = 0; j < 2; j++)
         vrd[j] = (uint32_t)(kPKTile + (lane & 31) * 64 + (((2 * j + half) ^ (((lane & 31) >> 2) & 3)) << 4));
 
-    if (ntiles > 0) issue_tile(0);
+    if (ntiles > 0)
+#pragma unroll
+        for (int j = 0; j < 8; j++) issue_load(0, j);
     for (int kt = 0; kt < ntiles; kt++) {
         const int k0 = kt * kKT;
         // this wave's loads of tile kt have landed; the barrier makes every wave's visible and
         // ends every wave's reads of tile kt - 1, whose buffer the next loads refill
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (kt + 1 < ntiles) issue_tile(kt + 1);
+        const bool next = kt + 1 < ntiles;
         const unsigned char *sb = pk_smem + (kt & 1) * kPBuf;
 
         f16v st = (f16v){};
@@ -325,6 +336,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
         for (int s = 0; s < 16; s++) {
             const h8 kf = *(const h8 *)(sb + krd[s & 3] + (s >> 2) * 128);
             st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
+            if ((s & 1) && next) issue_load(kt + 1, s >> 1);
         }
         float tv[16];
         float mloc = -INFINITY;
