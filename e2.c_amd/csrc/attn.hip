@@ -38,6 +38,9 @@ struct AttnArgs {
     float *c32;             // optional [M][H*D] f32 context
     // packed batches: sequence b is rows [seq_start[b], seq_start[b] + seq_len[b]), all valid
     const int32_t *seq_start, *seq_len;
+    // packed batches, optional: one (sequence | head << 16 | query block << 24) per workgroup of a
+    // 1-D grid, longest sequences first; negative entries are no work
+    const int32_t *work;
     int B, S, H, KV;
     float scale;
 };
@@ -248,7 +251,14 @@ constexpr size_t kAttnPackedLds = 2 * (size_t)kPBuf;
 
 __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
     extern __shared__ __align__(16) unsigned char pk_smem[];
-    const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    if (a.work) {
+        const int item = a.work[blockIdx.x];
+        if (item < 0) return;
+        b = item & 0xffff;
+        h = (item >> 16) & 0xff;
+        qb = item >> 24;
+    }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5;
     const int S = a.S, HD = a.H * kD, kvh = h / (a.H / a.KV);
     const size_t row0 = (size_t)a.seq_start[b];
@@ -447,7 +457,7 @@ extern "C" int e2mi_attention(e2mi_stream stream, const uint16_t *q16, const uin
         set_error("attention: null or misaligned pointer");
         return -1;
     }
-    AttnArgs a = {q16, k16, vt16, valid, ctx_q, ctx_s, ctx32, nullptr, nullptr, B, S, H, KV, scale};
+    AttnArgs a = {q16, k16, vt16, valid, ctx_q, ctx_s, ctx32, nullptr, nullptr, nullptr, B, S, H, KV, scale};
     hipLaunchKernelGGL(k_attn, dim3((S + 127) / 128, H, B), dim3(256), 0, (hipStream_t)stream, a);
     return check_hip(hipGetLastError(), "attention launch");
 }
@@ -455,7 +465,8 @@ extern "C" int e2mi_attention(e2mi_stream stream, const uint16_t *q16, const uin
 extern "C" int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
                                      const uint16_t *vt16, int M, const int32_t *seq_start,
                                      const int32_t *seq_len, int B, int max_len, int H, int KV, int D,
-                                     float scale, int8_t *ctx_q, float *ctx_s, float *ctx32) {
+                                     float scale, int8_t *ctx_q, float *ctx_s, float *ctx32,
+                                     const int32_t *work, int n_work) {
     if (D != kD || B <= 0 || M <= 0 || max_len <= 0 || H <= 0 || KV <= 0 || H % KV) {
         set_error("attention_packed: needs head_dim 256 and H %% KV == 0 (B=%d M=%d H=%d KV=%d D=%d)", B,
                   M, H, KV, D);
@@ -467,16 +478,21 @@ extern "C" int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, co
         set_error("attention_packed: null or misaligned pointer");
         return -1;
     }
-    AttnArgs a = {q16, k16, vt16, nullptr, ctx_q, ctx_s, ctx32, seq_start, seq_len, B, M, H, KV, scale};
+    if (work && (n_work <= 0 || B > 0xffff || H > 0xff || (max_len + 127) / 128 > 127)) {
+        set_error("attention_packed: work list needs n_work > 0, B < 65536, H < 256, max_len < 16257");
+        return -1;
+    }
+    AttnArgs a = {q16, k16, vt16, nullptr, ctx_q, ctx_s, ctx32, seq_start, seq_len, work, B, M, H, KV, scale};
     // the direct-to-LDS kernel needs 4-byte-aligned V^T rows and 32-bit offsets into the V^T slab
     // and the K rows; every sequence must start on an even row (the engine starts them on
     // multiples of 8)
     if (M % 2 == 0 && (size_t)KV * kD * M * 2 < 0x7fffffffu && (size_t)M * KV * kD * 2 < 0x7fffffffu &&
         ((uintptr_t)vt16 & 3) == 0) {
         if (attn_packed_attr()) return -1;
-        hipLaunchKernelGGL(k_attn_packed, dim3((max_len + 127) / 128, H, B), dim3(256), kAttnPackedLds,
-                           (hipStream_t)stream, a);
+        const dim3 grid = work ? dim3(n_work) : dim3((max_len + 127) / 128, H, B);
+        hipLaunchKernelGGL(k_attn_packed, grid, dim3(256), kAttnPackedLds, (hipStream_t)stream, a);
     } else {
+        a.work = nullptr;
         hipLaunchKernelGGL(k_attn, dim3((max_len + 127) / 128, H, B), dim3(256), 0, (hipStream_t)stream, a);
     }
     return check_hip(hipGetLastError(), "attention launch");

@@ -26,6 +26,7 @@
 #include <string.h>
 #include <time.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <tuple>
@@ -79,6 +80,8 @@ struct e2mi_engine {
     // per sequence its first row and length (device copies at fixed addresses for the graphs)
     int32_t *rowmap = nullptr, *pos = nullptr, *seq_start = nullptr, *seq_len = nullptr;
     int32_t *h_rowmap = nullptr, *h_pos = nullptr, *h_start = nullptr, *h_len = nullptr;
+    // attention work list (longest sequences first), a fixed number of slots per (sequences, rows)
+    int32_t *work = nullptr, *h_work = nullptr;
     uint8_t *h_mask = nullptr;  // device-entry mask copy
     size_t mask_cap = 0;
     hipStream_t last_stream = nullptr;
@@ -189,6 +192,9 @@ static void rope_tables(const e2_config &c, std::vector<float> &cs, std::vector<
         }
 }
 
+// attention workgroups of a packed chunk of n sequences in M rows: at most H (M / 128 + n)
+static int work_slots(const e2mi_engine *g, int n, int M) { return g->cfg.n_heads * (M / 128 + n); }
+
 // every kernel of one forward over B sequences of S tokens (M rows: B * S padded, or the packed
 // row count), on stream s; returns the launch count or -1
 static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
@@ -214,7 +220,8 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
                                           g->cos_tab, g->sin_tab, g->q16, g->k16, g->vt16, nullptr,
                                           nullptr, nullptr));
             RUN(e2mi_attention_packed(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len, B, S, H,
-                                      KV, D, c.attn_scale, g->cq, g->cs, nullptr));
+                                      KV, D, c.attn_scale, g->cq, g->cs, nullptr, g->work,
+                                      work_slots(g, B, M)));
         } else {
             RUN(e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, g->cos_tab,
                                    g->sin_tab, g->q16, g->k16, g->vt16, nullptr, nullptr, nullptr));
@@ -324,6 +331,17 @@ static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
     }
     const int Mp = (r + 255) & ~255;
     for (int i = r; i < Mp; i++) g->h_rowmap[i] = -1, g->h_pos[i] = 0;
+    // attention work, longest sequences first: the grid holds more workgroups than the CUs can run
+    // at once, and the last to start should be the short ones
+    std::vector<int> order(n);
+    for (int b = 0; b < n; b++) order[b] = b;
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return g->h_len[x] > g->h_len[y]; });
+    const int H = g->cfg.n_heads, slots = work_slots(g, n, Mp);
+    int k = 0;
+    for (int b : order)
+        for (int h = 0; h < H; h++)
+            for (int q = 0; q < (g->h_len[b] + 127) / 128; q++) g->h_work[k++] = b | (h << 16) | (q << 24);
+    while (k < slots) g->h_work[k++] = -1;
     return Mp;
 }
 
@@ -355,7 +373,9 @@ static int upload_pack(e2mi_engine *g, int n, int Mp, const int32_t *host_ids, h
         (!host_ids && check_hip(hipMemcpyAsync(g->rowmap, g->h_rowmap, (size_t)Mp * 4, hipMemcpyHostToDevice, s), "rowmap H2D")) ||
         check_hip(hipMemcpyAsync(g->pos, g->h_pos, (size_t)Mp * 4, hipMemcpyHostToDevice, s), "pos H2D") ||
         check_hip(hipMemcpyAsync(g->seq_start, g->h_start, (size_t)n * 4, hipMemcpyHostToDevice, s), "start H2D") ||
-        check_hip(hipMemcpyAsync(g->seq_len, g->h_len, (size_t)n * 4, hipMemcpyHostToDevice, s), "len H2D"))
+        check_hip(hipMemcpyAsync(g->seq_len, g->h_len, (size_t)n * 4, hipMemcpyHostToDevice, s), "len H2D") ||
+        check_hip(hipMemcpyAsync(g->work, g->h_work, (size_t)work_slots(g, n, Mp) * 4, hipMemcpyHostToDevice, s),
+                  "work H2D"))
         return -1;
     return 0;
 }
@@ -371,7 +391,7 @@ extern "C" void e2mi_destroy(e2mi_engine *g) {
     if (g->h_ids) (void)hipHostFree(g->h_ids);
     if (g->h_valid) (void)hipHostFree(g->h_valid);
     if (g->h_out) (void)hipHostFree(g->h_out);
-    for (int32_t *p : {g->h_rowmap, g->h_pos, g->h_start, g->h_len})
+    for (int32_t *p : {g->h_rowmap, g->h_pos, g->h_start, g->h_len, g->h_work})
         if (p) (void)hipHostFree(p);
     if (g->h_mask) (void)hipHostFree(g->h_mask);
     if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
@@ -449,7 +469,8 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         dalloc(g, &g->ids, R) || dalloc(g, &g->valid, R) || dalloc(g, &g->out, R * c.hidden) ||
         dalloc(g, &g->pool_ws, (R / 64 + R + 64) * (size_t)(c.hidden + 1)) ||
         dalloc(g, &g->rowmap, R) || dalloc(g, &g->pos, R) || dalloc(g, &g->seq_start, (size_t)g->bmax) ||
-        dalloc(g, &g->seq_len, (size_t)g->bmax))
+        dalloc(g, &g->seq_len, (size_t)g->bmax) ||
+        dalloc(g, &g->work, (size_t)c.n_heads * (R / 128 + g->bmax)))
         return fail();
     if (check_hip(hipHostMalloc((void **)&g->h_ids, R * 4), "pinned ids") ||
         check_hip(hipHostMalloc((void **)&g->h_valid, R), "pinned valid") ||
@@ -457,7 +478,8 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         check_hip(hipHostMalloc((void **)&g->h_rowmap, R * 4), "pinned rowmap") ||
         check_hip(hipHostMalloc((void **)&g->h_pos, R * 4), "pinned pos") ||
         check_hip(hipHostMalloc((void **)&g->h_start, (size_t)g->bmax * 4), "pinned start") ||
-        check_hip(hipHostMalloc((void **)&g->h_len, (size_t)g->bmax * 4), "pinned len"))
+        check_hip(hipHostMalloc((void **)&g->h_len, (size_t)g->bmax * 4), "pinned len") ||
+        check_hip(hipHostMalloc((void **)&g->h_work, (size_t)c.n_heads * (R / 128 + g->bmax) * 4), "pinned work"))
         return fail();
     // filler rows of packed batches read contexts that no attention writes: start them at zero
     if (check_hip(hipMemsetAsync(g->cq, 0, R * qd, g->stream), "clear ctx") ||

@@ -60,7 +60,7 @@ SIGNATURES = {
     "e2mi_pool_workspace_bytes": (C.c_size_t, [_I, _I, _I]),
     "e2mi_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
     "e2mi_qkv_norm_rope_packed": (_I, [_P, _P, _I, _P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P]),
-    "e2mi_attention_packed": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
+    "e2mi_attention_packed": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _I]),
     "e2mi_pool_l2_packed": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "e2mi_gather_ids": (_I, [_P, _P, _P, _I, _P]),
     # backend-selection surface (include/e2_dispatch.h)
@@ -416,8 +416,17 @@ def qkv_norm_rope_packed(qkv, pos, H, KV, q_gamma, k_gamma, cos_tab, sin_tab, ep
     return q16, k16, vt16, q32, k32, v32
 
 
+def attention_work(lens, H):
+    """The engine's attention work list for packed sequences of these lengths: (b | h << 16 |
+    query_block << 24) per 128-query block, longest sequences first."""
+    import numpy as np
+    order = sorted(range(len(lens)), key=lambda b: -int(lens[b]))
+    return np.asarray([b | (h << 16) | (q << 24) for b in order for h in range(H)
+                       for q in range((int(lens[b]) + 127) // 128)], np.int32)
+
+
 def attention_packed(q16, k16, vt16, start, lens, max_len, H, KV, scale=1.0, want_f32=True,
-                     cq=None, cs=None, c32=None, stream=None):
+                     cq=None, cs=None, c32=None, work=None, stream=None):
     import torch
     M = q16.shape[0]
     D = 256
@@ -428,7 +437,8 @@ def attention_packed(q16, k16, vt16, start, lens, max_len, H, KV, scale=1.0, wan
         c32 = torch.zeros((M, H * D), dtype=torch.float32, device=dev)
     check(load().e2mi_attention_packed(stream_ptr(stream), ptr(q16), ptr(k16), ptr(vt16), M,
                                        ptr(start), ptr(lens), start.shape[0], max_len, H, KV, D,
-                                       scale, ptr(cq), ptr(cs), ptr(c32)), "attention_packed")
+                                       scale, ptr(cq), ptr(cs), ptr(c32), ptr(work),
+                                       0 if work is None else work.shape[0]), "attention_packed")
     return cq, cs, c32
 
 

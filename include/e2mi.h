@@ -168,11 +168,16 @@ int e2mi_qkv_norm_rope_packed(e2mi_stream stream, const float *qkv, int M, const
                               float eps, const float *cos_tab, const float *sin_tab, uint16_t *q16,
                               uint16_t *k16, uint16_t *vt16, float *q32, float *k32, float *v32);
 /* attention of each packed sequence over its own rows (all valid); vt16 [KV][D][M] from
- * e2mi_qkv_norm_rope_packed, seq_len[b] <= max_len; rows outside every sequence are not written */
+ * e2mi_qkv_norm_rope_packed, seq_len[b] <= max_len, every seq_start a multiple of 8 (the
+ * e2mi.pack_plan layout); rows outside every sequence are not written. work (optional, device):
+ * n_work entries b | h << 16 | query_block << 24 (128 queries per block), one workgroup each, in
+ * the order given (longest sequences first balances the grid), negative entries idle; NULL runs a
+ * (query block, head, sequence) grid over max_len. */
 int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
                           const uint16_t *vt16, int M, const int32_t *seq_start,
                           const int32_t *seq_len, int B, int max_len, int H, int KV, int D,
-                          float scale, int8_t *ctx_q, float *ctx_s, float *ctx32);
+                          float scale, int8_t *ctx_q, float *ctx_s, float *ctx32,
+                          const int32_t *work, int n_work);
 /* mean pool + L2 of each packed sequence's rows (workspace: e2mi_pool_workspace_bytes(B, max_len, D)) */
 int e2mi_pool_l2_packed(e2mi_stream stream, const float *x, const int32_t *seq_start,
                         const int32_t *seq_len, int B, int max_len, int D, float *workspace,

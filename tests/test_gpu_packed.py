@@ -87,6 +87,10 @@ def test_packed_qkv_attention_pool_vs_padded(gpu, oracle, rng, B, S, lengths, ho
     p16, pk16, pvt16, p32, _, _ = e2mi.qkv_norm_rope_packed(_t(qkv_p, gpu), _t(pos, gpu), H, KV, *args)
     sd, ld = _t(start, gpu), _t(lens, gpu)
     pq, ps, p32c = e2mi.attention_packed(p16, pk16, pvt16, sd, ld, S, H, KV)
+    # the same through a longest-first work list (with idle slots), bit for bit
+    work = np.concatenate([e2mi.attention_work(lens, H), np.full(5, -1, np.int32)])
+    wq, ws_, w32 = e2mi.attention_packed(p16, pk16, pvt16, sd, ld, S, H, KV, work=_t(work, gpu))
+    assert torch.equal(wq, pq) and torch.equal(ws_, ps) and torch.equal(w32, p32c)
     live = rowmap >= 0
     src = rowmap[live]
     # q/k/v stages are row-local: identical on the packed rows
