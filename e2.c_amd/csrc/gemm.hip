@@ -220,12 +220,16 @@ static bool fold_fast() {
 //     A|W stage.
 // The tile list (M-major) is cut into one contiguous chunk per XCD (workgroups are dispatched
 // round-robin over the 8 XCDs), so the N tiles of an M block run on one XCD and share its L2.
-constexpr int kPStages = 3, kPSlots = 4;
+// 8-wave workgroups (one per CU) keep 3 A|W stages (loads two steps ahead); 4-wave workgroups
+// (two per CU) keep 2 (one step ahead)
+constexpr int kPSlots = 4;
+template <int NWAVE>
+constexpr int p_stages() { return NWAVE == 8 ? 3 : 2; }
 
 // a slot holds one step's activation scales and its tile's weight scales, one float per lane each
 template <int BM, int BN, int NWAVE>
 constexpr int p_lds_bytes() {
-    return kPStages * (BM + BN) * 128 + kPSlots * 2 * 64 * NWAVE * 4;
+    return p_stages<NWAVE>() * (BM + BN) * 128 + kPSlots * 2 * 64 * NWAVE * 4;
 }
 
 // requantizing epilogue of one tile. Every wave owns whole rows of each 128-column quantization
@@ -296,7 +300,7 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArg
     }
     if constexpr (GG) {
         // the other 64 columns of each block live in wave wn ^ 1: exchange per-row maxima
-        float *xch = scr + 8 * 8 * FP;
+        float *xch = scr + NWM * NWN * 8 * FP;
         if ((lane & 7) == 0) {
 #pragma unroll
             for (int c = 0; c < 4; c++) xch[wave * 32 + 8 * c + cr] = amax[c];
@@ -359,9 +363,10 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmA
 // BN = 128 NWN
 // TOK: per-token activation scales (one per row) instead of one per (row, 128-element block)
 template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, bool TOK>
-__global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int tiles_n, int tiles) {
+__global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(GemmArgs p, int tiles_n, int tiles) {
     constexpr int NWAVE = NWM * NWN;
-    static_assert(BM == 32 * NWM && BN == 128 * NWN && NWAVE == 8, "8 waves of 32x128");
+    static_assert(BM == 32 * NWM && BN == 128 * NWN && (NWAVE == 8 || NWAVE == 4), "8 or 4 waves of 32x128");
+    constexpr int kPStages = p_stages<NWAVE>(), AHEAD = kPStages - 1;  // loads AHEAD steps ahead
     constexpr int AI = BM / 8 / NWAVE, BI = BN / 8 / NWAVE;  // 1-KB loads per wave per step
     constexpr int L = AI + BI + 2;                           // loads per wave per step
     constexpr int TILE = (BM + BN) * 128;                    // A | W of one step
@@ -392,9 +397,9 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
     const v4u rV = rsrc_words(p.ws, (uint32_t)((size_t)p.N * 4));
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)smem);
 
-    // loads of flat step g (tile j, block kb) into stage g % 3 and slot g % 4. Load i of a wave
-    // fills rows (i * 8 + wave) * 8 + lane / 8 of the tile, 16-byte chunk (lane % 8) ^ swzk(row);
-    // with 8 waves swzk(row) = (wave % 2) * 4 + (lane / 16) % 4 for every i, so one per-lane offset
+    // loads of flat step g (tile j, block kb) into stage g % stages and slot g % 4. Load i of a wave
+    // fills rows (i * NWAVE + wave) * 8 + lane / 8 of the tile, 16-byte chunk (lane % 8) ^ swzk(row);
+    // with 8 or 4 waves swzk(row) = (wave % 2) * 4 + (lane / 16) % 4 for every i, so one per-lane offset
     // per operand serves all loads and the row base is a scalar. Rows past M (N) lie past the
     // buffer's range and read as zero; their outputs are never stored. The slot gets the step's
     // activation scales and its tile's ws (waves past BM/64 or BN/64 fetch a copy of the last 64).
@@ -423,7 +428,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
         }
         return is;
     };
-    static_assert(AI + BI + 2 == 8, "4 parts of 2 loads");
+    constexpr int WAITN = (AHEAD - 1) * L;  // loads issued after a step's own, when it starts
     auto issue_load = [&](const Issue &is, int i) {
         if (i < AI)
             dma16(rA, is.st + (i * NWAVE + wave) * 1024,
@@ -437,8 +442,8 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
             dma4(rV, is.sl + SHALF, (uint32_t)(is.n0 + min(wave * 64, BN - 64) + lane) * 4, 0);
     };
     auto issue_part = [&](const Issue &is, int part) {
-        issue_load(is, 2 * part);
-        issue_load(is, 2 * part + 1);
+#pragma unroll
+        for (int i = part * L / 4; i < (part + 1) * L / 4; i++) issue_load(is, i);
     };
     auto issue_next = [&](int g) {
         const Issue is = issue_prep(g);
@@ -450,8 +455,9 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
     // not loaded before step 1, after that fold (the barrier of step 0 publishes the zeros)
     for (int i = tid; i < SSLOT / 16; i += NWAVE * 64)
         ((uint4 *)(sscale + (kPSlots - 1) * SSLOT))[i] = make_uint4(0, 0, 0, 0);
-    if (G > 0) issue_next(0);
-    if (G > 1) issue_next(1);
+#pragma unroll
+    for (int a = 0; a < AHEAD; a++)
+        if (G > a) issue_next(a);
 
     // ws of this lane's four columns, read from a slot's ws half
     float wsr[4];
@@ -501,11 +507,11 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
     // loads of step g + 2 issued 2 per K sub-step (past the end of the list they fetch rows beyond
     // the operands' range into stages no longer read, which is harmless)
     auto step = [&](int g, v16i (&cur)[4], const v16i (&prev)[4]) {
-        if (g + 1 < G) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
+        if (g + 1 < G) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         const bool tile_start = ckb == 0 && g > 0;  // prev is the previous tile's last step
-        const Issue is_next = issue_prep(g + 2);
+        const Issue is_next = issue_prep(g + AHEAD);
         const unsigned char *sb = smem + (g % kPStages) * TILE;
         const unsigned char *spb = sscale + ((g + kPSlots - 1) % kPSlots) * SSLOT;
         const float *sp = (const float *)spb;
@@ -557,9 +563,9 @@ __global__ __launch_bounds__(NWM * NWN * 64, 1) void k_gemm_p(GemmArgs p, int ti
     // RN(as[m] * ws[n]), 0), at the tile's last step, followed by its epilogue.
     auto step_tok = [&](int g) {
         if (g + 1 >= G) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
+        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
         __syncthreads();
-        const Issue is_next = issue_prep(g + 2);
+        const Issue is_next = issue_prep(g + AHEAD);
         const unsigned char *sb = smem + (g % kPStages) * TILE;
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
@@ -651,7 +657,7 @@ template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, bool T
 static int launch_p1(hipStream_t s, const GemmArgs &p) {
     constexpr size_t lds = p_lds_bytes<BM, BN, NWM * NWN>();
     static_assert(lds <= 160 * 1024, "LDS budget");
-    static_assert(EPI == EPI_F32 || (8 * 8 * ((EPI == EPI_GEGLU ? 64 : 128) + 4) + 8 * 32) * 4 <= (BM + BN) * 128,
+    static_assert(EPI == EPI_F32 || NWM * NWN * (8 * ((EPI == EPI_GEGLU ? 64 : 128) + 4) + 32) * 4 <= (BM + BN) * 128,
                   "epilogue scratch fits a stage");
     auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST, TOK>;
     static bool attr = false;
@@ -667,7 +673,7 @@ static int launch_p1(hipStream_t s, const GemmArgs &p) {
         set_error("gemm: too many tiles");
         return -1;
     }
-    const int grid = (int)min(tiles, (long)num_cus());
+    const int grid = (int)min(tiles, (long)num_cus() * (8 / (NWM * NWN)));
     hipLaunchKernelGGL(kern, dim3(grid), dim3(NWM * NWN * 64), lds, s, p, tiles_n, (int)tiles);
     return check_hip(hipGetLastError(), "gemm launch");
 }
