@@ -10,10 +10,12 @@
 //   EPI_GEGLU W rows interleaved per 64 as [32 gate | 32 up]; g = gelu_tanh(gate) * up is
 //             quantized per 128 (text.c:424-468 fused into the producing GEMM), g optionally kept
 //
-// The production kernel is k_gemm_p (a persistent, software-pipelined kernel; its design is
-// described above it); k_gemm_dump is a plain kernel that also writes every K block's int32
-// accumulators, the parity hook for the integer part. K is walked in 128-deep steps, one
-// quantization block per step, so the int32 accumulators are folded into f32 once per step.
+// The production kernels are persistent and software-pipelined: k_gemm_p for per-(row, 128)
+// activation scales (K is walked in 128-deep steps, one quantization block per step, so the int32
+// accumulators are folded into f32 once per step) and k_gemm_t for per-row (per-token) scales,
+// whose accumulators run over the whole K of a tile; their designs are described above them.
+// k_gemm_dump is a plain kernel that also writes every K block's int32 accumulators, the parity
+// hook for the integer part.
 // A and W tiles live in LDS as 128-byte K slices of consecutive rows whose fragment reads are
 // conflict-free on the 64-bank LDS (see swz).
 #include <stdlib.h>
@@ -263,7 +265,7 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArg
     };
     const int cr = lane >> 3, cc = (lane & 7) * CPL;  // transposed chunk: row, first column
     // output column of this lane's transposed values and the row stride
-    const int oc = (GG ? n0 / 2 + wn * 64 : n0) + cc;
+    const int oc = (GG ? n0 / 2 + wn * 64 : n0 + wn * 128) + cc;
     const int ldo = GG ? p.N / 2 : p.N;
     float v[4][CPL];  // per chunk, the lane's CPL output values of row 8c + cr
     float amax[4];
@@ -361,8 +363,7 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmA
 
 // 8 waves of 32 x 128 (one 32-row MFMA tile by four 32-column ones): NWM x NWN waves, BM = 32 NWM,
 // BN = 128 NWN
-// TOK: per-token activation scales (one per row) instead of one per (row, 128-element block)
-template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, bool TOK>
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
 __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(GemmArgs p, int tiles_n, int tiles) {
     constexpr int NWAVE = NWM * NWN;
     static_assert(BM == 32 * NWM && BN == 128 * NWN && (NWAVE == 8 || NWAVE == 4), "8 or 4 waves of 32x128");
@@ -372,7 +373,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
     constexpr int TILE = (BM + BN) * 128;                    // A | W of one step
     constexpr int SHALF = 64 * NWAVE * 4;                    // as of one step (one per lane)
     constexpr int SSLOT = 2 * SHALF;                         // as | ws
-    constexpr bool XACT = TOK || !FAST;
+    constexpr bool XACT = !FAST;
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned char *const sscale = smem + kPStages * TILE;
 
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / NWN, wn = wave % NWN;
     const int nb = p.K / kQBlock;   // K steps per tile
-    const int nsb = TOK ? 1 : nb;   // activation scales per row
+    const int nsb = nb;             // activation scales per row
 
     // this workgroup's tiles: chunk [c0, c1) of the tile list, every per-th tile from c0 + li
     const int nx = (gridDim.x % 8 == 0) ? 8 : 1;
@@ -421,7 +422,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
         is.st = lds0 + (uint32_t)((g % kPStages) * TILE);
         is.sl = lds0 + (uint32_t)(kPStages * TILE + (g % kPSlots) * SSLOT + wave * 256);
         is.ko = (uint32_t)(ikb * kQBlock);
-        is.ks = TOK ? 0u : (uint32_t)(ikb * 4);
+        is.ks = (uint32_t)(ikb * 4);
         if (++ikb == nb) {
             ikb = 0;
             ++ij;
@@ -558,60 +559,6 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
             ++cj;
         }
     };
-    // per-token scales (the reference built with a per-row block, E2_I8_BLOCK = K): the int32
-    // accumulators run over the whole K of a tile and are folded once, f = fma((float)acc,
-    // RN(as[m] * ws[n]), 0), at the tile's last step, followed by its epilogue.
-    auto step_tok = [&](int g) {
-        if (g + 1 >= G) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
-        __syncthreads();
-        const Issue is_next = issue_prep(g + AHEAD);
-        const unsigned char *sb = smem + (g % kPStages) * TILE;
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            issue_part(is_next, kk);
-            const v4i af = *(const v4i *)(sb + offa[kk]);
-            v4i bf[4];
-#pragma unroll
-            for (int t = 0; t < 4; t++) bf[t] = *(const v4i *)(sb + offb[kk] + t * 4096);
-#pragma unroll
-            for (int tn = 0; tn < 4; tn++) acc0[tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[tn], acc0[tn], 0, 0, 0);
-        }
-        if (++ckb == nb) {
-            const unsigned char *slot = sscale + (g % kPSlots) * SSLOT;
-            read_ws(slot);
-            const float *sp = (const float *)slot;
-            const int pm0 = tile_m0(cj), pn0 = tile_n0(cj);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 a4 = *(const float4 *)((const unsigned char *)sp + offs + q * 32);
-                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-#pragma unroll
-                for (int tn = 0; tn < 4; tn++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        f[tn][q * 4 + j] = __builtin_fmaf((float)acc0[tn][q * 4 + j], __fmul_rn(av[j], wsr[tn]), 0.f);
-            }
-#pragma unroll
-            for (int tn = 0; tn < 4; tn++) acc0[tn] = zero;
-            if constexpr (EPI == EPI_F32) {
-                p_epilogue_f32<POST, false>(p, f, wsr, pm0, pn0, wm, wn, lane);
-            } else {
-                __syncthreads();
-                p_epilogue_q<BM, BN, NWM, NWN, EPI, false, POST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
-                                                                 (float *)(smem + (g % kPStages) * TILE));
-            }
-            ckb = 0;
-            ++cj;
-        }
-    };
-    if constexpr (TOK) {
-#pragma unroll
-        for (int tn = 0; tn < 4; tn++) acc0[tn] = zero;
-        for (int g = 0; g < G; g++) step_tok(g);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        return;
-    }
     int g = 0;
     for (; g + 1 < G; g += 2) {
         step(g, acc0, acc1);
@@ -643,6 +590,171 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// Per-token GEMM with 64 x 128 wave tiles: 8 waves (4 x 2) of a 256 x 256 output tile, two A|W
+// stages of 64 KB, loads one step ahead. Per 32-deep K sub-step a wave reads 6 fragments (2 of A,
+// 4 of W) for 8 MFMAs, half the LDS bytes per MFMA of the 32 x 128 wave tile, and the next
+// sub-step's fragments are read while the current ones feed the MFMAs. With one scale per row the
+// int32 accumulators run over the whole K of a tile (no per-step fold); the tile's last step folds
+// them, f = fma((float)acc, RN(as[m] * ws[n]), 0), and runs the epilogue, one 32-row half at a time.
+template <int EPI, int POST>
+__global__ __launch_bounds__(512, 1) void k_gemm_t(GemmArgs p, int tiles_n, int tiles) {
+    constexpr int BM = 256, BN = 256, NWM = 4, NWN = 2, NWAVE = 8, STAGES = 2;
+    constexpr int AI = BM / 8 / NWAVE, BI = BN / 8 / NWAVE;  // 1-KB loads per wave per step
+    constexpr int L = AI + BI + 2;                           // loads per wave per step
+    constexpr int TILE = (BM + BN) * 128;                    // A | W of one step
+    constexpr int SHALF = 64 * NWAVE * 4;                    // as of one step (one per lane)
+    constexpr int SSLOT = 2 * SHALF;                         // as | ws
+    extern __shared__ __align__(16) unsigned char smem[];
+    unsigned char *const sscale = smem + STAGES * TILE;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / NWN, wn = wave % NWN;
+    const int nb = p.K / kQBlock;
+
+    const int nx = (gridDim.x % 8 == 0) ? 8 : 1;
+    const int grp = blockIdx.x % nx, li = blockIdx.x / nx, per = gridDim.x / nx;
+    const int c0 = (int)((long)tiles * grp / nx), c1 = (int)((long)tiles * (grp + 1) / nx);
+    const int ntile = (c1 - c0 > li) ? (c1 - c0 - li + per - 1) / per : 0;
+    const int G = ntile * nb;
+    auto tile_m0 = [&](int j) { return ((c0 + li + j * per) / tiles_n) * BM; };
+    auto tile_n0 = [&](int j) { return ((c0 + li + j * per) % tiles_n) * BN; };
+
+    const v4u rA = rsrc_words(p.A, (uint32_t)((size_t)p.M * p.lda));
+    const v4u rW = rsrc_words(p.W, (uint32_t)((size_t)p.N * p.ldw));
+    const v4u rS = rsrc_words(p.as, (uint32_t)((size_t)p.M * 4));
+    const v4u rV = rsrc_words(p.ws, (uint32_t)((size_t)p.N * 4));
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)smem);
+
+    // load i of a wave fills rows (i * NWAVE + wave) * 8 + lane / 8 of the tile (as in k_gemm_p);
+    // the slot gets the tile's activation scales (rows min(64 wave, BM - 64) + lane) and weight
+    // scales, loaded with every step of the tile and read at its last
+    const int swl = ((lane & 7) ^ ((wave & 1) * 4 + ((lane >> 4) & 3))) << 4;
+    const uint32_t vla = (uint32_t)(lane >> 3) * (uint32_t)p.lda + swl;
+    const uint32_t vlb = (uint32_t)(lane >> 3) * (uint32_t)p.ldw + swl;
+    int ij = 0, ikb = 0;
+    struct Issue {
+        uint32_t st, sl, ko;
+        int m0, n0;
+    };
+    auto issue_prep = [&](int g) {
+        Issue is;
+        is.m0 = tile_m0(ij);
+        is.n0 = tile_n0(ij);
+        is.st = lds0 + (uint32_t)((g % STAGES) * TILE);
+        is.sl = lds0 + (uint32_t)(STAGES * TILE + (g % kPSlots) * SSLOT + wave * 256);
+        is.ko = (uint32_t)(ikb * kQBlock);
+        if (++ikb == nb) {
+            ikb = 0;
+            ++ij;
+        }
+        return is;
+    };
+    auto issue_load = [&](const Issue &is, int i) {
+        if (i < AI)
+            dma16(rA, is.st + (i * NWAVE + wave) * 1024,
+                  vla + (uint32_t)(is.m0 + (i * NWAVE + wave) * 8) * (uint32_t)p.lda, is.ko);
+        else if (i < AI + BI)
+            dma16(rW, is.st + BM * 128 + ((i - AI) * NWAVE + wave) * 1024,
+                  vlb + (uint32_t)(is.n0 + ((i - AI) * NWAVE + wave) * 8) * (uint32_t)p.ldw, is.ko);
+        else if (i == AI + BI)
+            dma4(rS, is.sl, (uint32_t)(is.m0 + min(wave * 64, BM - 64) + lane) * 4, 0);
+        else
+            dma4(rV, is.sl + SHALF, (uint32_t)(is.n0 + min(wave * 64, BN - 64) + lane) * 4, 0);
+    };
+    auto issue_part = [&](const Issue &is, int part) {
+#pragma unroll
+        for (int i = part * L / 4; i < (part + 1) * L / 4; i++) issue_load(is, i);
+    };
+    if (G > 0) {
+        const Issue is = issue_prep(0);
+#pragma unroll
+        for (int q = 0; q < 4; q++) issue_part(is, q);
+    }
+
+    // fragment offsets inside a stage (row lane % 32 of a 32-row tile, 16-byte chunk 2 kk + lane / 32);
+    // A half h adds h * 4096, W tile t adds t * 4096
+    int offa[4], offb[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+        const int o = swz(lane & 31, kk * 2 + (lane >> 5));
+        offa[kk] = wm * 64 * 128 + o;
+        offb[kk] = BM * 128 + wn * 128 * 128 + o;
+    }
+    v16i acc[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[h][t] = (v16i){};
+
+    int cj = 0, ckb = 0;
+    for (int g = 0; g < G; g++) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        // the next step's loads go to the other stage, consumed by the previous step (past the end
+        // of the list they fetch rows beyond the operands' range into a stage no longer read)
+        const Issue is_next = issue_prep(g + 1);
+        const unsigned char *sb = smem + (g % STAGES) * TILE;
+        v4i af[2][2], bf[2][4];
+        auto frags = [&](int kk, v4i (&a)[2], v4i (&b)[4]) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) a[h] = *(const v4i *)(sb + offa[kk] + h * 4096);
+#pragma unroll
+            for (int t = 0; t < 4; t++) b[t] = *(const v4i *)(sb + offb[kk] + t * 4096);
+        };
+        frags(0, af[0], bf[0]);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const int c = kk & 1;
+            if (kk < 3) frags(kk + 1, af[c ^ 1], bf[c ^ 1]);
+            issue_part(is_next, kk);
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    acc[h][t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[c][h], bf[c][t], acc[h][t], 0, 0, 0);
+        }
+        if (++ckb == nb) {
+            const unsigned char *slot = sscale + (g % kPSlots) * SSLOT;
+            float wsr[4];
+#pragma unroll
+            for (int tn = 0; tn < 4; tn++)
+                wsr[tn] = *(const float *)(slot + SHALF + (wn * 128 + tn * 32 + (lane & 31)) * 4);
+            const int pm0 = tile_m0(cj), pn0 = tile_n0(cj);
+            // a requantizing epilogue stages through this step's stage once every wave is done
+            // with it; the stage is refilled only by the loads issued after the next barrier
+            if constexpr (EPI != EPI_F32) __syncthreads();
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int wmh = wm * 2 + h;  // the 32-row wave row of the epilogue
+                float f[4][16];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 a4 = *(const float4 *)(slot + (wmh * 32 + (lane >> 5) * 4 + q * 8) * 4);
+                    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+                    for (int tn = 0; tn < 4; tn++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            f[tn][q * 4 + j] = __builtin_fmaf((float)acc[h][tn][q * 4 + j], __fmul_rn(av[j], wsr[tn]), 0.f);
+                }
+#pragma unroll
+                for (int t = 0; t < 4; t++) acc[h][t] = (v16i){};
+                if constexpr (EPI == EPI_F32)
+                    p_epilogue_f32<POST, false>(p, f, wsr, pm0, pn0, wmh, wn, lane);
+                else
+                    p_epilogue_q<BM, BN, NWM, NWN, EPI, false, POST>(p, f, wsr, pm0, pn0, wave, wmh, wn, lane,
+                                                                     (float *)(smem + (g % STAGES) * TILE));
+            }
+            ckb = 0;
+            ++cj;
+        }
+    }
+    // the last step issued loads past the end of the list: they must land before the workgroup's
+    // LDS is released
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 static int num_cus() {
     static int cus = 0;
     if (!cus) {
@@ -653,13 +765,13 @@ static int num_cus() {
     return cus;
 }
 
-template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, bool TOK>
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
 static int launch_p1(hipStream_t s, const GemmArgs &p) {
     constexpr size_t lds = p_lds_bytes<BM, BN, NWM * NWN>();
     static_assert(lds <= 160 * 1024, "LDS budget");
     static_assert(EPI == EPI_F32 || NWM * NWN * (8 * ((EPI == EPI_GEGLU ? 64 : 128) + 4) + 32) * 4 <= (BM + BN) * 128,
                   "epilogue scratch fits a stage");
-    auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST, TOK>;
+    auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST>;
     static bool attr = false;
     if (!attr) {
         if (check_hip(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
@@ -678,21 +790,43 @@ static int launch_p1(hipStream_t s, const GemmArgs &p) {
     return check_hip(hipGetLastError(), "gemm launch");
 }
 
+template <int EPI, int POST>
+static int launch_t1(hipStream_t s, const GemmArgs &p) {
+    constexpr size_t lds = 2 * (256 + 256) * 128 + kPSlots * 2 * 64 * 8 * 4;
+    static_assert(lds <= 160 * 1024, "LDS budget");
+    auto kern = k_gemm_t<EPI, POST>;
+    static bool attr = false;
+    if (!attr) {
+        if (check_hip(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                      "gemm lds attribute"))
+            return -1;
+        attr = true;
+    }
+    const int tiles_n = (p.N + 255) / 256;
+    const long tiles = (long)((p.M + 255) / 256) * tiles_n;
+    if (tiles > (1L << 30)) {
+        set_error("gemm: too many tiles");
+        return -1;
+    }
+    const int grid = (int)min(tiles, (long)num_cus());
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), lds, s, p, tiles_n, (int)tiles);
+    return check_hip(hipGetLastError(), "gemm launch");
+}
+
+template <int EPI>
+static int launch_t(hipStream_t s, const GemmArgs &p) {
+    const bool post = p.bias != nullptr || p.lo > -1e30f || p.hi < 1e30f;
+    return post ? launch_t1<EPI, 3>(s, p) : launch_t1<EPI, 0>(s, p);
+}
+
 // POST: bit 0 adds a bias, bit 1 clamps to [lo, hi]; only "none" and "both" are instantiated (the
 // bias pointer may be null and an absent clamp is +-1e31)
 template <int BM, int BN, int NWM, int NWN, int EPI>
-static int launch_p(hipStream_t s, const GemmArgs &p, bool tok = false) {
+static int launch_p(hipStream_t s, const GemmArgs &p) {
     const bool post = p.bias != nullptr || p.lo > -1e30f || p.hi < 1e30f;
-    if constexpr (EPI != EPI_GEGLU) {
-        if (tok)  // one fold per output: the fast fold has nothing to save
-            return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3, true>(s, p)
-                        : launch_p1<BM, BN, NWM, NWN, EPI, false, 0, true>(s, p);
-    }
     if (fold_fast())
-        return post ? launch_p1<BM, BN, NWM, NWN, EPI, true, 3, false>(s, p)
-                    : launch_p1<BM, BN, NWM, NWN, EPI, true, 0, false>(s, p);
-    return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3, false>(s, p)
-                : launch_p1<BM, BN, NWM, NWN, EPI, false, 0, false>(s, p);
+        return post ? launch_p1<BM, BN, NWM, NWN, EPI, true, 3>(s, p) : launch_p1<BM, BN, NWM, NWN, EPI, true, 0>(s, p);
+    return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3>(s, p) : launch_p1<BM, BN, NWM, NWN, EPI, false, 0>(s, p);
 }
 
 static int launch_dump(hipStream_t s, const GemmArgs &p) {
@@ -742,7 +876,8 @@ int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump, bool tok = false) {
         }
         return launch_dump(s, p);
     }
-    return launch_p<256, 128, 8, 1, EPI_F32>(s, p, tok);
+    if (tok) return launch_t<EPI_F32>(s, p);
+    return launch_p<256, 128, 8, 1, EPI_F32>(s, p);
 }
 
 int launch_gemm_i8q(hipStream_t s, GemmArgs p, bool tok = false) {
@@ -752,7 +887,8 @@ int launch_gemm_i8q(hipStream_t s, GemmArgs p, bool tok = false) {
         set_error("i8_gemm_q: N must be a multiple of 128 with a 16-byte aligned int8 output");
         return -1;
     }
-    return launch_p<256, 128, 8, 1, EPI_I8Q>(s, p, tok);
+    if (tok) return launch_t<EPI_I8Q>(s, p);
+    return launch_p<256, 128, 8, 1, EPI_I8Q>(s, p);
 }
 
 int launch_gemm_geglu(hipStream_t s, GemmArgs p) {
