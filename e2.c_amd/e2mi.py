@@ -61,6 +61,8 @@ SIGNATURES = {
     "e2mi_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
     "e2mi_qkv_norm_rope_packed": (_I, [_P, _P, _I, _P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P]),
     "e2mi_attention_packed": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _I]),
+    "e2mi_attention_i8_workspace_bytes": (C.c_size_t, [_I, _I, _I, _I, _I]),
+    "e2mi_attention_i8_packed": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I]),
     "e2mi_pool_l2_packed": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "e2mi_gather_ids": (_I, [_P, _P, _P, _I, _P]),
     # backend-selection surface (include/e2_dispatch.h)
@@ -439,6 +441,30 @@ def attention_packed(q16, k16, vt16, start, lens, max_len, H, KV, scale=1.0, wan
                                        ptr(start), ptr(lens), start.shape[0], max_len, H, KV, D,
                                        scale, ptr(cq), ptr(cs), ptr(c32), ptr(work),
                                        0 if work is None else work.shape[0]), "attention_packed")
+    return cq, cs, c32
+
+
+def attention_i8_packed(q32, k32, v32, start, lens, max_len, H, KV, want_f32=True, cq=None, cs=None,
+                        c32=None, work=None, workspace=None, stream=None):
+    """The int8 attention variant (text.c:638-700) of each packed sequence; returns (cq, cs, c32)."""
+    import torch
+    M = q32.shape[0]
+    D = 256
+    dev = q32.device
+    B = start.shape[0]
+    lib = load()
+    if workspace is None:
+        nbytes = lib.e2mi_attention_i8_workspace_bytes(M, B, max_len, H, KV)
+        workspace = torch.empty(nbytes + 256, dtype=torch.uint8, device=dev)
+    cq = torch.zeros((M, H * D), dtype=torch.int8, device=dev) if cq is None else cq
+    cs = torch.zeros((M, H * D // 128), dtype=torch.float32, device=dev) if cs is None else cs
+    if want_f32 and c32 is None:
+        c32 = torch.zeros((M, H * D), dtype=torch.float32, device=dev)
+    wp = C.c_void_p((workspace.data_ptr() + 255) & ~255)
+    check(lib.e2mi_attention_i8_packed(stream_ptr(stream), ptr(q32), ptr(k32), ptr(v32), M, ptr(start),
+                                       ptr(lens), B, max_len, H, KV, D, wp, ptr(cq), ptr(cs), ptr(c32),
+                                       ptr(work), 0 if work is None else work.shape[0]),
+          "attention_i8_packed")
     return cq, cs, c32
 
 

@@ -178,6 +178,21 @@ int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, const uint16_
                           const int32_t *seq_len, int B, int max_len, int H, int KV, int D,
                           float scale, int8_t *ctx_q, float *ctx_s, float *ctx32,
                           const int32_t *work, int n_work);
+/* The reference's int8 attention (text.c:638-700 attb_i8; dispatch.c:51 selects it for long
+ * sequences on AVX-512) for packed batches: q32 [M][H*D], k32/v32 [M][KV*D] f32 after q/k norm and
+ * RoPE (e2mi_qkv_norm_rope_packed's optional f32 outputs), sequences as for
+ * e2mi_attention_packed (every seq_start a multiple of 8, M a multiple of 16). Q is quantized per
+ * (row, head, 128 dims), K per key row and V^T per (sequence, kv head, dim) with the reference's
+ * quantizers, scores and context are int8 GEMMs folded per 128-block in the reference's order,
+ * the probabilities are quantized per 128-key block. Outputs as e2mi_attention_packed (context
+ * quantized per 128 dims for the O projection, optional f32 copy). workspace: device memory of
+ * e2mi_attention_i8_workspace_bytes(M, B, max_len, H, KV) bytes, 256-byte aligned. */
+size_t e2mi_attention_i8_workspace_bytes(int M, int B, int max_len, int H, int KV);
+int e2mi_attention_i8_packed(e2mi_stream stream, const float *q32, const float *k32,
+                             const float *v32, int M, const int32_t *seq_start,
+                             const int32_t *seq_len, int B, int max_len, int H, int KV, int D,
+                             void *workspace, int8_t *ctx_q, float *ctx_s, float *ctx32,
+                             const int32_t *work, int n_work);
 /* mean pool + L2 of each packed sequence's rows (workspace: e2mi_pool_workspace_bytes(B, max_len, D)) */
 int e2mi_pool_l2_packed(e2mi_stream stream, const float *x, const int32_t *seq_start,
                         const int32_t *seq_len, int B, int max_len, int D, float *workspace,

@@ -71,6 +71,7 @@ class Oracle:
             "or_rope_rows": (None, [_P, _I, _I, _I, _P, _P]),
             "or_softmax": (None, [_P, _I]),
             "or_attention": (None, [_P, _I, _P, _I, _P, _I, _P, _I, _I, _I, _I, _F, _P, _I, _I]),
+            "or_attention_i8": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I]),
             "or_meanpool": (None, [_P, _I, _I, _P, _P]),
             "or_l2norm": (None, [_P, _I]),
             "or_embed": (None, [_P, _P, _I, _I, _F, _P]),
@@ -220,6 +221,16 @@ class Oracle:
         self.lib.or_attention(_ptr(_need(q, np.float32)), H * D, _ptr(_need(k, np.float32)), KV * D,
                               _ptr(_need(v, np.float32)), KV * D, _ptr(_need(valid, np.uint8)), S,
                               H, KV, D, scale, _ptr(ctx), H * D, nthreads)
+        return ctx
+
+    def attention_i8(self, q, k, v, H, KV, D):
+        """The reference's int8 attention (text.c:638-700) of one all-valid sequence:
+        q [S][H*D], k/v [S][KV*D] -> ctx [S][H*D]."""
+        S = q.shape[0]
+        ctx = np.zeros((S, H * D), np.float32)
+        if self.lib.or_attention_i8(_ptr(_need(q, np.float32)), H * D, _ptr(_need(k, np.float32)), KV * D,
+                                    _ptr(_need(v, np.float32)), KV * D, S, H, KV, D, _ptr(ctx), H * D):
+            raise MemoryError
         return ctx
 
     def meanpool_l2(self, x, valid):

@@ -23,6 +23,11 @@
  *                                   the formula test
  *   or_softmax / or_attention    — softmax within 3e-7 of double (test_softmax.c:33); attention vs
  *                                   a float64 brute force (test_oracle_math.py)
+ *   or_attention_i8              — composition of the pinned pieces above in text.c's order; vs a
+ *                                   float64 brute force within the reference's own int8 bar 2e-2
+ *                                   on its test inputs (test_text_attention.c:69-71), closed form for
+ *                                   K = 0 (uniform probabilities), int32 and per-step values vs a
+ *                                   numpy restatement (test_oracle_math.py)
  *   or_meanpool / or_l2norm      — within 1e-6 of _ref e2_meanpool_f32 / e2_l2norm_f32
  *   or_embed                     — closed form
  *   text recipe (e2_oracle_model.c) — layer order restated from text.c:817-984, pinned by special
@@ -448,6 +453,65 @@ void or_attention(const float *q, int ldq, const float *k, int ldk, const float 
                   int ldc, int nthreads) {
     attn_task t = { q, k, v, ldq, ldk, ldv, ldc, valid, S, H, KV, D, scale, ctx };
     or_parallel(attn_item, &t, H * S, nthreads);
+}
+
+/* ------------------------------------------------------------------ int8 attention
+ * text.c:638-700 (attb_i8) for one sequence of S valid rows, bidirectional (no window): per query
+ * head h (kv head h / (H / KV)),
+ *   Q rows quantized per 128 of D (e2_i8_quantize, text.c:660-663),
+ *   K packed as a weight, one scale per key row (e2_q8w_from_f32_ld, text.c:775),
+ *   scores = the int8 GEMM of Q with K (fold over D's blocks, text.c:664),
+ *   softmax over the row (text.c:677), P quantized per 128 keys with the row padded to Sp (a
+ *   multiple of 128) by zero bytes and zero block scales (text.c:683-688),
+ *   V^T [D][Sp] (zero-padded, kt_worker text.c:599-616) packed as a weight, one scale per dim
+ *   (e2_q8w_from_f32, text.c:776),
+ *   ctx = the int8 GEMM of P with V^T (fold over Sp's key blocks, text.c:689-692).
+ * Composed from or_quantize, or_q8w_from_f32 (+ unpack), or_i8_gemm and or_softmax, each pinned
+ * against the reference (header). Returns -1 on allocation failure. */
+int or_attention_i8(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                    int S, int H, int KV, int D, float *ctx, int ldc) {
+    if (S <= 0) return 0;
+    const int Sp = (S + 127) & ~127, nbD = (D + 127) / 128, nbS = (S + 127) / 128, nbsp = Sp / 128;
+    const int groups = H / KV, Spad = (S + 7) & ~7, Dpad = (D + 7) & ~7;
+    int8_t *q8 = malloc((size_t)S * D), *k8 = malloc((size_t)S * D), *kw = malloc((size_t)Spad * D + 4096);
+    float *qs = malloc(sizeof(float) * (size_t)S * nbD), *ks = malloc(sizeof(float) * (size_t)Spad);
+    int32_t *bsq = malloc(sizeof(int32_t) * (size_t)(Sp / 128 + nbD + 1) * (Spad > Dpad ? Spad : Dpad));
+    float *kt = malloc(sizeof(float) * (size_t)S * D), *sc = malloc(sizeof(float) * (size_t)S * S);
+    int8_t *p8 = calloc((size_t)S * Sp, 1), *pt = malloc((size_t)S * S);
+    float *ps = calloc((size_t)S * nbsp, sizeof(float)), *pst = malloc(sizeof(float) * (size_t)S * nbS);
+    float *vt = calloc((size_t)D * Sp, sizeof(float)), *vs = malloc(sizeof(float) * (size_t)Dpad);
+    int8_t *vw = malloc((size_t)Dpad * Sp + 4096), *v8 = malloc((size_t)D * Sp);
+    float *c = malloc(sizeof(float) * (size_t)S * D);
+    int rc = 0;
+    if (!q8 || !k8 || !kw || !qs || !ks || !bsq || !kt || !sc || !p8 || !pt || !ps || !pst || !vt ||
+        !vs || !vw || !v8 || !c) {
+        rc = -1;
+        goto out;
+    }
+    for (int h = 0; h < H; h++) {
+        const int kv = h / groups;
+        for (int j = 0; j < S; j++) memcpy(kt + (size_t)j * D, k + (size_t)j * ldk + (size_t)kv * D, sizeof(float) * D);
+        or_q8w_from_f32(kt, S, D, kw, ks, bsq);
+        or_q8w_unpack(kw, S, D, k8);
+        or_quantize(q + (size_t)h * D, S, D, ldq, 128, q8, qs);
+        or_i8_gemm(q8, qs, k8, ks, NULL, S, S, D, 128, -1e31f, 1e31f, sc);
+        for (int i = 0; i < S; i++) or_softmax(sc + (size_t)i * S, S);
+        or_quantize(sc, S, S, S, 128, pt, pst);
+        for (int i = 0; i < S; i++) {
+            memcpy(p8 + (size_t)i * Sp, pt + (size_t)i * S, (size_t)S);
+            memcpy(ps + (size_t)i * nbsp, pst + (size_t)i * nbS, sizeof(float) * nbS);
+        }
+        for (int d = 0; d < D; d++)
+            for (int j = 0; j < S; j++) vt[(size_t)d * Sp + j] = v[(size_t)j * ldv + (size_t)kv * D + d];
+        or_q8w_from_f32(vt, D, Sp, vw, vs, bsq);
+        or_q8w_unpack(vw, D, Sp, v8);
+        or_i8_gemm(p8, ps, v8, vs, NULL, S, D, Sp, 128, -1e31f, 1e31f, c);
+        for (int i = 0; i < S; i++) memcpy(ctx + (size_t)i * ldc + (size_t)h * D, c + (size_t)i * D, sizeof(float) * D);
+    }
+out:
+    free(q8); free(k8); free(kw); free(qs); free(ks); free(bsq); free(kt); free(sc); free(p8);
+    free(pt); free(ps); free(pst); free(vt); free(vs); free(vw); free(v8); free(c);
+    return rc;
 }
 
 /* ------------------------------------------------------------------ pooling / embedding */

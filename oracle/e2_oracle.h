@@ -63,6 +63,8 @@ void or_softmax(float *x, int n);
 void or_attention(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
                   const uint8_t *valid, int S, int H, int KV, int D, float scale, float *ctx,
                   int ldc, int nthreads);
+int or_attention_i8(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                    int S, int H, int KV, int D, float *ctx, int ldc);
 
 /* ---- a15/a16: pooling + L2 (kernels.c:22-39), embedding (text.c:917-921) */
 void or_meanpool(const float *x, int M, int D, const uint8_t *valid, float *out);

@@ -44,7 +44,7 @@ def _check_guard(buf, M, c0, c1, sent):
 
 
 @pytest.mark.parametrize("M", [300, 257, 33, 1000])
-@pytest.mark.parametrize("n0,n1", [(0, 384), (128, 320)])
+@pytest.mark.parametrize("n0,n1", [(0, 384), (128, 320), (3, 250)])
 def test_f32_gemm_bounds(gpu, oracle, rng, M, n0, n1):
     import torch
     import e2mi

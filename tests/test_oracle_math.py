@@ -80,3 +80,95 @@ def test_norms_closed_form(oracle, rng):
     assert np.allclose(oracle.norm_add(x, res, g, 1e-6), want + res, rtol=2e-6, atol=2e-6)
     xs, r = oracle.norm_split(x, g, 1e-6)
     assert np.array_equal(r, x) and np.allclose(xs, want, rtol=2e-6, atol=1e-6)
+
+
+def _ref_test_inputs(S, H, KV, D):
+    """The inputs of the reference's attention test (test_text_attention.c:47-53)."""
+    GD, KD = H * D, KV * D
+    i = np.arange(S * GD, dtype=np.float32)
+    q = (np.sin(i * np.float32(0.031)) * np.float32(0.12)).astype(np.float32).reshape(S, GD)
+    i = np.arange(S * KD, dtype=np.float32)
+    k = (np.cos(i * np.float32(0.017)) * np.float32(0.12)).astype(np.float32).reshape(S, KD)
+    v = np.sin(i * np.float32(0.007)).astype(np.float32).reshape(S, KD)
+    return q, k, v
+
+
+def _attention_f64(q, k, v, H, KV, D):
+    S = q.shape[0]
+    out = np.zeros((S, H * D))
+    for h in range(H):
+        kv = h // (H // KV)
+        s = q[:, h * D:(h + 1) * D].astype(np.float64) @ k[:, kv * D:(kv + 1) * D].astype(np.float64).T
+        p = np.exp(s - s.max(1, keepdims=True))
+        out[:, h * D:(h + 1) * D] = (p / p.sum(1, keepdims=True)) @ v[:, kv * D:(kv + 1) * D]
+    return out
+
+
+def test_attention_i8_oracle_within_reference_bar(oracle, rng):
+    """The int8 attention restatement (text.c:638-700) against a float64 brute force within the
+    reference's own bar for its int8 path, 2e-2 (test_text_attention.c:69-71), on the reference
+    test's inputs and on random ones, at lengths with partial 128-key blocks. A mistake in the
+    quantization points (a dropped scale, a transposed operand, the wrong softmax axis) is far
+    outside it."""
+    H, KV, D = 3, 1, 256
+    for S in (128, 197, 300):
+        q, k, v = _ref_test_inputs(S, H, KV, D)
+        got = oracle.attention_i8(q, k, v, H, KV, D)
+        assert np.abs(got - _attention_f64(q, k, v, H, KV, D)).max() < 2e-2
+    H, KV = 4, 2
+    q = (rng.standard_normal((150, H * D)) * 0.1).astype(np.float32)
+    k = (rng.standard_normal((150, KV * D)) * 0.1).astype(np.float32)
+    v = rng.standard_normal((150, KV * D)).astype(np.float32)
+    assert np.abs(oracle.attention_i8(q, k, v, H, KV, D) - _attention_f64(q, k, v, H, KV, D)).max() < 2e-2
+    # peaked attention (logit std ~2): per-(row, head) cosine with float64 >= 0.999, while
+    # normalizing over the query axis instead of the key axis drops it below 0.9
+    q = (rng.standard_normal((150, H * D)) * 0.35).astype(np.float32)
+    k = (rng.standard_normal((150, KV * D)) * 0.35).astype(np.float32)
+    want = _attention_f64(q, k, v, H, KV, D)
+    got = oracle.attention_i8(q, k, v, H, KV, D)
+    bad = np.zeros_like(want)
+    for h in range(H):
+        kv = h // (H // KV)
+        sc = q[:, h * D:(h + 1) * D].astype(np.float64) @ k[:, kv * D:(kv + 1) * D].astype(np.float64).T
+        pb = np.exp(sc - sc.max(0, keepdims=True))
+        bad[:, h * D:(h + 1) * D] = (pb / pb.sum(0, keepdims=True)) @ v[:, kv * D:(kv + 1) * D]
+
+    def cos(a, b):
+        a, b = a.reshape(-1, D), b.reshape(-1, D)
+        return (a * b).sum(1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))
+    assert cos(got, want).min() >= 0.999 and cos(bad, want).min() < 0.9
+
+
+def _q_f32(x):
+    """The reference quantizer's arithmetic for one block/row (int8.c:41-42, kernels_i8_avx512_vnni.c:
+    321-363 as compiled): scale amax * RN(1/127), bytes rne(x * RN(127 / amax))."""
+    amax = np.float32(np.abs(x).max())
+    inv127 = np.frombuffer(np.uint32(0x3C010204).tobytes(), np.float32)[0]
+    sc = np.float32(amax * inv127) if amax > 0 else np.float32(1)
+    inv = np.float32(np.float32(127) / amax) if amax > 0 else np.float32(1)
+    return np.rint((x * inv).astype(np.float32)).astype(np.int32), sc
+
+
+def test_attention_i8_oracle_uniform_closed_form(oracle, rng):
+    """K = 0: every score is 0, the softmax is uniform (p = RN(1/S) on every key), each 128-key block
+    of P quantizes to 127 with scale RN(p RN(1/127)), and ctx[d] = sum over key blocks (in order) of
+    fma(127 * sum_j v8[j][d], RN(ps * vs[d]), .), with V^T quantized per dim over the sequence."""
+    H, KV, D = 3, 1, 256
+    for S in (128, 200):
+        q = rng.standard_normal((S, H * D)).astype(np.float32)
+        k = np.zeros((S, KV * D), np.float32)
+        v = rng.standard_normal((S, KV * D)).astype(np.float32)
+        got = oracle.attention_i8(q, k, v, H, KV, D).astype(np.float64)
+        p = np.float32(np.float32(1) / np.float32(S))
+        qp, ps = _q_f32(np.full(128, p, np.float32))
+        assert np.all(qp == 127)
+        want = np.zeros(D)
+        for d in range(D):
+            v8, vs = _q_f32(v[:, d])
+            f = 0.0
+            for b0 in range(0, S, 128):
+                acc = 127 * int(v8[b0:b0 + 128].sum())
+                f = float(np.float32(acc * float(np.float32(ps * vs)) + f))
+            want[d] = f
+        for h in range(H):
+            assert np.allclose(got[:, h * D:(h + 1) * D], want[None, :], rtol=1e-6, atol=1e-7)
