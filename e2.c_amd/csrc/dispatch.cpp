@@ -11,8 +11,8 @@ namespace {
 
 constexpr unsigned kCpuI8 = E2_CAP_GEMM_I8 | E2_CAP_QUANT_I8 | E2_CAP_SOFTMAX_Q_I8;
 
-// caps per backend (dispatch.c:15-31); the gfx950 row has the int8 MFMA GEMM, the quantizer and
-// the f16-MFMA fused attention, no int8 attention kernel
+// caps per backend (dispatch.c:15-31); the gfx950 row has the int8 MFMA GEMM, the quantizer, the
+// f16-MFMA fused attention and the int8 attention kernel (attn_i8.hip, text only)
 unsigned caps_of(e2_backend bk) {
     switch (bk) {
     case E2_BK_CPU_SCALAR: return E2_CAP_GEMM_I8 | E2_CAP_QUANT_I8;
@@ -22,7 +22,7 @@ unsigned caps_of(e2_backend bk) {
     case E2_BK_CPU_NEON: return kCpuI8 | E2_CAP_ATTN_I8_FUSED;
     case E2_BK_INTEL_GPU: return kCpuI8 | E2_CAP_ATTN_I8_FUSED | E2_CAP_ATTN_F16;
     case E2_BK_HIP: return kCpuI8 | E2_CAP_ATTN_I8_FUSED;
-    case E2_BK_HIP_GFX950: return E2_CAP_GEMM_I8 | E2_CAP_QUANT_I8 | E2_CAP_ATTN_F16;
+    case E2_BK_HIP_GFX950: return E2_CAP_GEMM_I8 | E2_CAP_QUANT_I8 | E2_CAP_ATTN_I8_FUSED | E2_CAP_ATTN_F16;
     default: return 0;
     }
 }
@@ -44,7 +44,9 @@ Rule rule_of(e2_backend bk, e2_tower t) {
         case E2_BK_CPU_NEON: return {E2_ATTN_I8, E2_ATTN_F32, 128};
         case E2_BK_INTEL_GPU: return {E2_ATTN_I8, E2_ATTN_F16, 512};
         case E2_BK_HIP: return {E2_ATTN_I8, E2_ATTN_F32, 64};
-        // f16 MFMA attention at every length: no packing cost to amortise
+        // f16 MFMA attention at every length: measured faster than the int8 kernel at every
+        // length of the config-4 batch (the int8 one quantizes K and V^T per sequence first and
+        // walks the keys twice); E2_ATTN_TEXT=i8 selects the int8 kernel
         case E2_BK_HIP_GFX950: return {E2_ATTN_F16, E2_ATTN_F16, 0};
         default: return f32;
         }
@@ -55,8 +57,9 @@ Rule rule_of(e2_backend bk, e2_tower t) {
     case E2_BK_CPU_AVX512:
     case E2_BK_CPU_NEON:
     case E2_BK_INTEL_GPU:
-    case E2_BK_HIP:
-    case E2_BK_HIP_GFX950: return {E2_ATTN_I8, E2_ATTN_F32, 0};
+    case E2_BK_HIP: return {E2_ATTN_I8, E2_ATTN_F32, 0};
+    // no vision tower on this backend: the table keeps the f16 kernel's row
+    case E2_BK_HIP_GFX950: return {E2_ATTN_F16, E2_ATTN_F16, 0};
     default: return f32;
     }
 }
@@ -92,8 +95,7 @@ bool executable(e2_backend bk, e2_tower t, e2_attn_kind k) {
     if (k == E2_ATTN_F16) return (c & E2_CAP_ATTN_F16) != 0;
     if (t == E2_TOWER_TEXT) {
         // text int8 attention is the weight GEMM on quantized Q and P on the reference's
-        // backends; the gfx950 row would need its own fused int8 attention kernel, which this
-        // build does not have (so a forced i8 degrades to the f16 MFMA kernel)
+        // backends; the gfx950 row runs its own int8 attention kernel
         if (bk == E2_BK_HIP_GFX950) return (c & E2_CAP_ATTN_I8_FUSED) != 0;
         return (c & (E2_CAP_GEMM_I8 | E2_CAP_QUANT_I8)) == (E2_CAP_GEMM_I8 | E2_CAP_QUANT_I8);
     }

@@ -82,6 +82,12 @@ struct e2mi_engine {
     int32_t *h_rowmap = nullptr, *h_pos = nullptr, *h_start = nullptr, *h_len = nullptr;
     // attention work list (longest sequences first), a fixed number of slots per (sequences, rows)
     int32_t *work = nullptr, *h_work = nullptr;
+    // the int8 attention (text.c:638-700) when the selection surface picks it: sequences of at
+    // least kI8MinKeys keys go to its own work list, f32 q/k/v feed it (packed batches only)
+    bool attn_i8 = false;
+    float *q32 = nullptr, *k32 = nullptr, *v32 = nullptr;
+    unsigned char *i8ws = nullptr;
+    int32_t *work8 = nullptr, *h_work8 = nullptr;
     uint8_t *h_mask = nullptr;  // device-entry mask copy
     size_t mask_cap = 0;
     hipStream_t last_stream = nullptr;
@@ -192,6 +198,9 @@ static void rope_tables(const e2_config &c, std::vector<float> &cs, std::vector<
         }
 }
 
+// the shortest sequence the int8 attention takes (text.c:873-875: its blocked kernels need 32 rows)
+constexpr int kI8MinKeys = 32;
+
 // attention workgroups of a packed chunk of n sequences in M rows: at most H (M / 128 + n)
 static int work_slots(const e2mi_engine *g, int n, int M) { return g->cfg.n_heads * (M / 128 + n); }
 
@@ -217,11 +226,15 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
         RUN(e2mi_i8_gemm(s, g->qkv, qd + 2 * KV * D, g->qa, g->as, &L.qkv, M, 0, L.qkv.N));
         if (pk) {
             RUN(e2mi_qkv_norm_rope_packed(s, g->qkv, M, g->pos, H, KV, D, L.q_norm, L.k_norm, eps,
-                                          g->cos_tab, g->sin_tab, g->q16, g->k16, g->vt16, nullptr,
-                                          nullptr, nullptr));
+                                          g->cos_tab, g->sin_tab, g->q16, g->k16, g->vt16, g->q32,
+                                          g->k32, g->v32));
             RUN(e2mi_attention_packed(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len, B, S, H,
                                       KV, D, c.attn_scale, g->cq, g->cs, nullptr, g->work,
                                       work_slots(g, B, M)));
+            if (g->attn_i8)
+                RUN(e2mi_attention_i8_packed(s, g->q32, g->k32, g->v32, M, g->seq_start, g->seq_len, B, S,
+                                             H, KV, D, g->i8ws, g->cq, g->cs, nullptr, g->work8,
+                                             work_slots(g, B, M)));
         } else {
             RUN(e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, g->cos_tab,
                                    g->sin_tab, g->q16, g->k16, g->vt16, nullptr, nullptr, nullptr));
@@ -337,11 +350,22 @@ static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
     for (int b = 0; b < n; b++) order[b] = b;
     std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return g->h_len[x] > g->h_len[y]; });
     const int H = g->cfg.n_heads, slots = work_slots(g, n, Mp);
-    int k = 0;
-    for (int b : order)
+    int k = 0, k8 = 0;
+    for (int b : order) {
+        // text.c:873-875: shorter sequences, and sequences with padding inside (all rows of the
+        // trimmed sequence must be valid), take the f32 path there, the f16 kernel here
+        const int L = g->h_len[b], r0 = g->h_start[b];
+        const bool i8 = g->attn_i8 && L >= kI8MinKeys && g->h_pos[r0] == 0 && g->h_pos[r0 + L - 1] == L - 1;
         for (int h = 0; h < H; h++)
-            for (int q = 0; q < (g->h_len[b] + 127) / 128; q++) g->h_work[k++] = b | (h << 16) | (q << 24);
+            for (int q = 0; q < (g->h_len[b] + 127) / 128; q++) {
+                const int32_t item = b | (h << 16) | (q << 24);
+                if (i8) g->h_work8[k8++] = item;
+                else g->h_work[k++] = item;
+            }
+    }
     while (k < slots) g->h_work[k++] = -1;
+    if (g->attn_i8)
+        while (k8 < slots) g->h_work8[k8++] = -1;
     return Mp;
 }
 
@@ -375,8 +399,35 @@ static int upload_pack(e2mi_engine *g, int n, int Mp, const int32_t *host_ids, h
         check_hip(hipMemcpyAsync(g->seq_start, g->h_start, (size_t)n * 4, hipMemcpyHostToDevice, s), "start H2D") ||
         check_hip(hipMemcpyAsync(g->seq_len, g->h_len, (size_t)n * 4, hipMemcpyHostToDevice, s), "len H2D") ||
         check_hip(hipMemcpyAsync(g->work, g->h_work, (size_t)work_slots(g, n, Mp) * 4, hipMemcpyHostToDevice, s),
-                  "work H2D"))
+                  "work H2D") ||
+        (g->attn_i8 && check_hip(hipMemcpyAsync(g->work8, g->h_work8, (size_t)work_slots(g, n, Mp) * 4,
+                                                hipMemcpyHostToDevice, s), "int8 work H2D")))
         return -1;
+    return 0;
+}
+
+// switch the int8 attention on or off; its buffers (f32 q/k/v, the quantized operands, a second
+// work list) are allocated the first time it is switched on
+static int set_attention_i8(e2mi_engine *g, bool on) {
+    const e2_config &c = g->cfg;
+    if (on && c.attn_scale != 1.0f) {
+        set_error("int8 attention implements the reference's attention scale 1.0 (text.c:8-9), the model has %g",
+                  (double)c.attn_scale);
+        return -1;
+    }
+    if (on && !g->q32) {
+        const size_t R = (size_t)g->R;
+        const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+        const size_t wsb = e2mi_attention_i8_workspace_bytes(g->R, g->bmax, c.max_seq, c.n_heads, c.n_kv_heads);
+        if (dalloc(g, &g->q32, R * qd) || dalloc(g, &g->k32, R * kvd) || dalloc(g, &g->v32, R * kvd) ||
+            dalloc(g, &g->i8ws, wsb) || dalloc(g, &g->work8, (size_t)c.n_heads * (R / 128 + g->bmax)) ||
+            check_hip(hipHostMalloc((void **)&g->h_work8, (size_t)c.n_heads * (R / 128 + g->bmax) * 4),
+                      "pinned int8 work"))
+            return -1;
+    }
+    g->attn_i8 = on;
+    for (auto &kv : g->graphs) (void)hipGraphExecDestroy(kv.second);
+    g->graphs.clear();
     return 0;
 }
 
@@ -391,7 +442,7 @@ extern "C" void e2mi_destroy(e2mi_engine *g) {
     if (g->h_ids) (void)hipHostFree(g->h_ids);
     if (g->h_valid) (void)hipHostFree(g->h_valid);
     if (g->h_out) (void)hipHostFree(g->h_out);
-    for (int32_t *p : {g->h_rowmap, g->h_pos, g->h_start, g->h_len, g->h_work})
+    for (int32_t *p : {g->h_rowmap, g->h_pos, g->h_start, g->h_len, g->h_work, g->h_work8})
         if (p) (void)hipHostFree(p);
     if (g->h_mask) (void)hipHostFree(g->h_mask);
     if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
@@ -437,9 +488,8 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
     // the attention precision comes from the selection surface (dispatch.c:180-197)
     e2_attn_env_reload();
     const e2_attn_kind ak = e2_attn_pick(E2_BK_HIP_GFX950, E2_TOWER_TEXT, E2_ATTN_ANY_KEYS);
-    if (ak != E2_ATTN_F16) {
-        set_error("create: attention kind %s requested; this backend implements f16 only",
-                  e2_attn_kind_name(ak));
+    if (ak == E2_ATTN_F32) {
+        set_error("create: attention kind f32 requested; this backend implements f16 and i8");
         return fail();
     }
     if (check_hip(hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking), "stream")) return fail();
@@ -487,6 +537,7 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         return fail();
     const char *np = getenv("E2MI_NOPACK");
     g->packed = !(np && np[0] && np[0] != '0');
+    if (ak == E2_ATTN_I8 && set_attention_i8(g, true)) return fail();
     if (check_hip(hipStreamSynchronize(g->stream), "create sync")) return fail();
     return g;
 }
@@ -603,6 +654,17 @@ extern "C" int e2mi_set_packing(e2mi_engine *g, int on) {
     if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
     g->packed = on != 0;
     return 0;
+}
+
+extern "C" int e2mi_set_attention(e2mi_engine *g, int kind) {
+    if (!g || (kind != E2_ATTN_F16 && kind != E2_ATTN_I8)) {
+        set_error("set_attention: null engine or kind %d (f16 = %d, i8 = %d)", kind, (int)E2_ATTN_F16,
+                  (int)E2_ATTN_I8);
+        return -1;
+    }
+    if (g->stream) (void)hipStreamSynchronize(g->stream);
+    if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
+    return set_attention_i8(g, kind == E2_ATTN_I8);
 }
 
 extern "C" int e2mi_stats(e2mi_engine *g, long *calls, long *kernels_last, double *last_ms) {

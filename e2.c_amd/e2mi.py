@@ -95,6 +95,7 @@ SIGNATURES = {
     "e2mi_stats": (_I, [_P, C.POINTER(C.c_long), C.POINTER(C.c_long), C.POINTER(C.c_double)]),
     "e2mi_set_layer_limit": (_I, [_P, _I]),
     "e2mi_set_packing": (_I, [_P, _I]),
+    "e2mi_set_attention": (_I, [_P, _I]),
 }
 
 _lib = None
@@ -585,6 +586,11 @@ class Engine:
     def set_packing(self, on: bool):
         """Packed batches (valid tokens only) on or off; off computes every padded row."""
         check(load().e2mi_set_packing(self.h, 1 if on else 0), "set_packing")
+
+    def set_attention(self, kind: str):
+        """Text attention kind: "f16" (default) or "i8" (the reference's int8 attention for
+        sequences of at least 32 tokens)."""
+        check(load().e2mi_set_attention(self.h, {"f16": 1, "i8": 2}[kind]), "set_attention")
 
     def __del__(self):
         if _lib is not None and getattr(self, "h", None):

@@ -252,6 +252,13 @@ int e2mi_set_layer_limit(e2mi_engine *g, int n_layers);
 /* Packed batches on (1, the default; E2MI_NOPACK=1 turns it off at creation) or off (0: every
  * row of the padded batch is computed, as the reference does). No counterpart in the reference. */
 int e2mi_set_packing(e2mi_engine *g, int on);
+/* Text attention kind (the reference's E2_ATTN_TEXT / e2_attn_override, dispatch.h:34-41, read at
+ * e2mi_create): E2_ATTN_F16 (1, the gfx950 rule's choice) or E2_ATTN_I8 (2: sequences of at least 32
+ * valid tokens take the int8 attention of text.c:638-700, shorter ones the f16 kernel, as the
+ * reference's blocked path needs 32 rows, text.c:873-875). I8 needs packed batches (the padded
+ * forward keeps f16) and the reference's attention scale 1.0; its buffers are allocated on first
+ * use. */
+int e2mi_set_attention(e2mi_engine *g, int kind);
 
 #ifdef __cplusplus
 }

@@ -42,7 +42,7 @@ class OrModel(C.Structure):
     _fields_ = [("n_layers", _I), ("hidden", _I), ("ffn", _I), ("n_heads", _I), ("n_kv", _I),
                 ("head_dim", _I), ("vocab", _I), ("eps", _F), ("rope_theta", _F),
                 ("embed_scale", _F), ("attn_scale", _F), ("embed", _P), ("final_norm", _P),
-                ("layers", C.POINTER(OrLayer))]
+                ("layers", C.POINTER(OrLayer)), ("attn_i8", _I)]
 
 
 class Oracle:
@@ -245,7 +245,7 @@ class Oracle:
 class OracleModel:
     """Holds numpy weight arrays alive and exposes them as an or_model for the recipe functions."""
 
-    def __init__(self, oracle, cfg, layers, embed, final_norm, attn_scale=1.0):
+    def __init__(self, oracle, cfg, layers, embed, final_norm, attn_scale=1.0, attn_i8=False):
         self.o = oracle
         self._keep = [layers, embed, final_norm]
         arr = (OrLayer * len(layers))()
@@ -259,7 +259,7 @@ class OracleModel:
         self.m = OrModel(len(layers), cfg["hidden"], cfg["ffn"], cfg["n_heads"], cfg["n_kv_heads"],
                          cfg["head_dim"], cfg["vocab"], cfg["rms_eps"], cfg["rope_theta"],
                          cfg["embed_scale"], attn_scale, embed.ctypes.data, final_norm.ctypes.data,
-                         C.cast(arr, C.POINTER(OrLayer)))
+                         C.cast(arr, C.POINTER(OrLayer)), 1 if attn_i8 else 0)
 
     def encode(self, ids, valid, nthreads=8):
         B, S = ids.shape

@@ -98,6 +98,9 @@ typedef struct {
     const float *embed;      /* [vocab][hidden] */
     const float *final_norm; /* [hidden] */
     const or_layer *layers;
+    /* 1: the int8 attention (text.c:638-700) for sequences of >= 32 rows with no padding inside
+     * (the reference's blocked path, text.c:873-875, selected as dispatch.c picks i8); 0: f32 */
+    int attn_i8;
 } or_model;
 
 /* One layer's attention + FFN sublayers over B x S rows, x updated in place (text.c:939-961). */

@@ -59,9 +59,17 @@ int or_attention_sublayer(const or_model *m, int l, const float *x, int B, int S
         if (!Sb) continue;
         or_rope_rows(q + (size_t)b * S * GD, Sb * H, H, D, cs, sn);
         or_rope_rows(k + (size_t)b * S * KV * D, Sb * KV, KV, D, cs, sn);
-        or_attention(q + (size_t)b * S * GD, GD, k + (size_t)b * S * KV * D, KV * D,
-                     v + (size_t)b * S * KV * D, KV * D, vb, Sb, H, KV, D, m->attn_scale,
-                     ctx + (size_t)b * S * GD, GD, nthreads);
+        int all = 1;
+        for (int i = 0; i < Sb; i++) all &= vb[i] != 0;
+        if (m->attn_i8 && all && Sb >= 32 && m->attn_scale == 1.0f) {
+            if (or_attention_i8(q + (size_t)b * S * GD, GD, k + (size_t)b * S * KV * D, KV * D,
+                                v + (size_t)b * S * KV * D, KV * D, Sb, H, KV, D, ctx + (size_t)b * S * GD, GD))
+                goto fail;
+        } else {
+            or_attention(q + (size_t)b * S * GD, GD, k + (size_t)b * S * KV * D, KV * D,
+                         v + (size_t)b * S * KV * D, KV * D, vb, Sb, H, KV, D, m->attn_scale,
+                         ctx + (size_t)b * S * GD, GD, nthreads);
+        }
     }
     or_quantize_mt(ctx, M, GD, qa, as, nthreads);
     or_i8_gemm_mt(qa, as, L->wo, L->so, NULL, M, Dm, GD, out, nthreads);

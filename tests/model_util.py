@@ -16,7 +16,7 @@ def lname(l, s):
     return f"language_model.layers.{l}.{s}"
 
 
-def oracle_model(oracle, model, n_layers=None):
+def oracle_model(oracle, model, n_layers=None, attn_i8=False):
     """Build the oracle's or_model from the product model's host tensors (packed weights unpacked
     with the oracle's own layout code)."""
     from oracle.binding import OracleModel
@@ -45,7 +45,7 @@ def oracle_model(oracle, model, n_layers=None):
          "rope_theta": cfg.rope_theta, "embed_scale": cfg.embed_scale}
     embed = np.ascontiguousarray(model.tensor("language_model.embed_tokens.weight"), np.float32)
     fnorm = np.ascontiguousarray(model.tensor("language_model.norm.weight"), np.float32)
-    return OracleModel(oracle, c, layers, embed, fnorm, attn_scale=cfg.attn_scale)
+    return OracleModel(oracle, c, layers, embed, fnorm, attn_scale=cfg.attn_scale, attn_i8=attn_i8)
 
 
 def random_batch(rng, B, S, vocab, min_len=1, holes=False):

@@ -59,7 +59,7 @@ def test_image_and_audio_rules(d):
         assert pick(d, bk, IMAGE, 0) == want and pick(d, bk, IMAGE, 2520) == want
     assert pick(d, "CPU_SCALAR", IMAGE, 2520) == F32
     assert pick(d, "INTEL_GPU", IMAGE, 2520) == I8 and pick(d, "HIP", IMAGE, 2520) == I8
-    assert pick(d, "HIP_GFX950", IMAGE, 2520) == F16   # rule says I8, caps degrade to F16
+    assert pick(d, "HIP_GFX950", IMAGE, 2520) == F16   # no vision tower: the f16 row
     for bk in range(BK["COUNT"]):
         for keys in (0, 750, 2048):
             assert d.e2_attn_pick(bk, AUDIO, keys) == F32
@@ -81,7 +81,7 @@ def test_thresholds_and_caps(d):
     assert caps("INTEL_GPU") & CAP_ATTN_I8_FUSED and caps("INTEL_GPU") & CAP_ATTN_F16
     assert caps("HIP") & CAP_ATTN_I8_FUSED and not caps("HIP") & CAP_ATTN_F16
     g = caps("HIP_GFX950")
-    assert g & CAP_GEMM_I8 and g & CAP_QUANT_I8 and g & CAP_ATTN_F16 and not g & CAP_ATTN_I8_FUSED
+    assert g & CAP_GEMM_I8 and g & CAP_QUANT_I8 and g & CAP_ATTN_F16 and g & CAP_ATTN_I8_FUSED
     assert d.e2_backend_caps(99) == 0 and ANY >= 2048
 
 
@@ -106,7 +106,7 @@ def test_overrides(d, monkeypatch):
     assert pick(d, "CPU_VNNI", TEXT, 2048) == I8
     env(E2_ATTN_TEXT="i8")
     assert pick(d, "CPU_VNNI", TEXT, 0) == I8 and pick(d, "CPU_SCALAR", TEXT, 0) == I8
-    assert pick(d, "HIP_GFX950", TEXT, 0) == F16       # forced i8 degrades to the f16 MFMA kernel
+    assert pick(d, "HIP_GFX950", TEXT, 0) == I8        # forced i8: the int8 attention kernel
     env(E2_ATTN_TEXT="f32")
     assert pick(d, "CPU_VNNI", TEXT, 2048) == F32 and pick(d, "HIP_GFX950", TEXT, 512) == F32
     env(E2_ATTN_TEXT="auto")

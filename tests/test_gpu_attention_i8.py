@@ -175,3 +175,35 @@ def test_attention_i8_rejects_bad_geometry(gpu):
     assert lib.e2mi_attention_i8_packed(None, None, None, None, 17, None, None, 1, 8, 3, 1, 256, None,
                                         None, None, None, None, 0) == -1
     assert b"M % 16" in lib.e2mi_last_error() or b"head_dim" in lib.e2mi_last_error()
+
+
+def test_engine_int8_attention_vs_oracle(gpu, rng):
+    """The engine with the int8 attention selected (E2_ATTN_TEXT=i8's setter) against the oracle's
+    text recipe with the same selection: one layer at the reference's scale 1.0, right-padded
+    sequences of 1 to 300 tokens (those under 32 tokens take the f16 / f32 path in both); embeddings
+    within the north star's cosine bar. The f16 engine on the same batch is farther from it."""
+    import e2mi
+    from model_util import oracle_model, random_batch, small_config
+    from oracle.binding import Oracle
+    o = Oracle()
+    m = e2mi.Model.synthetic(small_config(e2mi, n_layers=1), 4242)
+    eng = e2mi.Engine(m, max_rows=2048)
+    ids, valid = random_batch(rng, 6, 300, 1000, min_len=1)
+    valid[0, :] = 1                                    # a full-length sequence
+    valid[1, 20:] = 0                                  # a short one (f16 / f32 path)
+    want = oracle_model(o, m, attn_i8=True).encode(ids, valid)
+    f16 = eng.embed_batch(ids, valid)
+    eng.set_attention("i8")
+    try:
+        got = eng.embed_batch(ids, valid)
+        again = eng.embed_batch(ids, valid)            # graph replay
+    finally:
+        eng.set_attention("f16")
+    assert np.array_equal(got, again)
+    cos = (got * want).sum(1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(want, axis=1))
+    cos16 = (f16 * want).sum(1) / (np.linalg.norm(f16, axis=1) * np.linalg.norm(want, axis=1))
+    print("engine int8 attention cos", cos, "f16 engine vs int8 oracle", cos16)
+    assert cos.min() >= 0.9999
+    assert np.array_equal(f16, eng.embed_batch(ids, valid))  # switched back
+    with pytest.raises(Exception):
+        e2mi.Engine(e2mi.Model.synthetic(small_config(e2mi, n_layers=1), 1), max_rows=512).set_attention("f32")
