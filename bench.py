@@ -240,6 +240,22 @@ def encoder_bench(torch, e2mi, steps, warmup, cpu_sample=4, padded=True):
             o_pad = out.cpu().numpy()
         finally:
             eng.set_packing(True)
+    # the reference's int8 attention path (E2_ATTN_TEXT=i8, text.c:638-700) on the same batch
+    eng.set_attention("i8")
+    try:
+        for _ in range(2):
+            eng.embed_batch_device(ids_d, valid_d, out, stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        n8 = max(3, steps // 2)
+        for _ in range(n8):
+            eng.embed_batch_device(ids_d, valid_d, out, stream)
+        torch.cuda.synchronize()
+        dt8 = (time.perf_counter() - t1) / n8
+        o8 = out.cpu().numpy()
+    finally:
+        eng.set_attention("f16")
+    cos8 = (o8 * o).sum(1) / (np.linalg.norm(o8, axis=1) * np.linalg.norm(o, axis=1))
     # the host-buffer entry point (PCIe-inclusive), for reference
     h_t = []
     for _ in range(3):
@@ -260,6 +276,12 @@ def encoder_bench(torch, e2mi, steps, warmup, cpu_sample=4, padded=True):
         "config": f"24 layers, B={ENC_B}, S={ENC_S}, lengths U[64,512] (mean {lens.mean():.0f}), vocab {cfg.vocab}",
         "model_build_s": round(t_model, 2),
         "kernels_per_forward": eng.stats()[1],
+        "int8_attention": {
+            "embeddings_per_s": round(ENC_B / dt8, 2), "ms_per_batch": round(dt8 * 1e3, 3),
+            "min_cosine_vs_f16_attention": round(float(cos8.min()), 6),
+            "note": "E2_ATTN_TEXT=i8 / Engine.set_attention('i8'): the reference's int8 attention "
+                    "(text.c:638-700) for every sequence (all have >= 64 tokens); the gfx950 rule "
+                    "keeps the f16 MFMA kernel, which is faster"},
     }
     res["_model"] = model
     res["_batch"] = (ids, valid)

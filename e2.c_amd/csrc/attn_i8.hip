@@ -33,7 +33,8 @@ namespace e2mi {
 constexpr int kI8D = 256;                           // head dim
 constexpr int kI8Tile = 8192;                       // K [32 keys][256] or V^T [256 d][32 keys]
 constexpr int kI8Buf = kI8Tile + 256;               // + the tile's key scales (64 loaded, 32 used)
-constexpr int kAttnI8Lds = 2 * kI8Buf + kI8D * 4;   // two buffers + the sequence's V scales
+constexpr int kI8Ring = 3;                          // tile buffers: loads two tiles ahead
+constexpr int kAttnI8Lds = kI8Ring * kI8Buf + kI8D * 4;  // + the sequence's V scales
 
 // ---------------------------------------------------------------- Q and K quantization
 struct I8PrepArgs {
@@ -42,7 +43,7 @@ struct I8PrepArgs {
     float *qs;                     // [M][H*2]
     int8_t *k8;                    // [M][KV*D]
     float *ks;                     // [M][KV]
-    int8_t *vt8;                   // [KV][D][M]
+    int8_t *vt8;                   // [KV][D][2 M]: sequence b's keys at columns 2 start[b] + j
     float *vpart;                  // [B][KV][nch][D] column maxima of 64-row chunks
     float *vs;                     // [B][KV][D]
     const int32_t *seq_start, *seq_len;
@@ -80,15 +81,22 @@ __global__ __launch_bounds__(256) void k_i8_vmax(I8PrepArgs a) {
     const int L = a.seq_len[b], r0 = 64 * c;
     if (r0 >= L) return;
     const int r1 = min(L, r0 + 64);
-    const float *src = a.v32 + ((size_t)a.seq_start[b] + r0) * a.KV * kI8D + kv * kI8D + d;
+    const size_t st = (size_t)a.KV * kI8D;
+    const float *src = a.v32 + ((size_t)a.seq_start[b] + r0) * st + kv * kI8D + d;
+    float m8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int r = r0;
+    for (; r + 8 <= r1; r += 8, src += 8 * st)
+#pragma unroll
+        for (int e = 0; e < 8; e++) m8[e] = fmaxf(m8[e], fabsf(src[e * st]));
+    for (; r < r1; r++, src += st) m8[0] = fmaxf(m8[0], fabsf(*src));
     float am = 0.f;
-    for (int r = r0; r < r1; r++, src += (size_t)a.KV * kI8D) am = fmaxf(am, fabsf(*src));
+#pragma unroll
+    for (int e = 0; e < 8; e++) am = fmaxf(am, m8[e]);
     a.vpart[((size_t)blockIdx.x * a.nch + c) * kI8D + d] = am;
 }
 
 // grid (B * KV, ceil(max_len / 32)): thread d reduces its column's chunk maxima, then quantizes rows
-// [32 c, 32 c + 32) of the sequence into 32 bytes of V^T row d (only the rows of the sequence are
-// written, in 8-byte units: sequences start on multiples of 8 rows)
+// [32 c, 32 c + 32) of the sequence into 32 bytes of V^T row d
 __global__ __launch_bounds__(256) void k_i8_vquant(I8PrepArgs a) {
     const int b = blockIdx.x / a.KV, kv = blockIdx.x % a.KV, c = blockIdx.y, d = threadIdx.x;
     const int L = a.seq_len[b], r0 = 32 * c;
@@ -113,10 +121,12 @@ __global__ __launch_bounds__(256) void k_i8_vquant(I8PrepArgs a) {
         }
         w[g] = pack4_magic(x[0], x[1], x[2], x[3], s.inv);
     }
-    int8_t *dst = a.vt8 + ((size_t)kv * kI8D + d) * a.M + row0;
+    // sequence b's keys start at column 2 start[b] (16-byte aligned; its columns end before the
+    // next sequence's, which starts at least L rows later): whole 16-byte chunks are its own
+    int8_t *dst = a.vt8 + ((size_t)kv * kI8D + d) * 2 * a.M + 2 * (size_t)a.seq_start[b] + r0;
 #pragma unroll
-    for (int g = 0; g < 4; g++)
-        if (8 * g < n) *(uint2 *)(dst + 8 * g) = make_uint2(w[2 * g], w[2 * g + 1]);
+    for (int g = 0; g < 2; g++)
+        if (16 * g < n) *(uint4 *)(dst + 16 * g) = make_uint4(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]);
 }
 
 // ---------------------------------------------------------------- attention
@@ -161,7 +171,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
         for (int kk = 0; kk < 8; kk++) qf[kk] = *(const v4i *)(qp + 32 * kk);
     }
     const float qs0 = a.qs[(row0 + qc) * a.H * 2 + h * 2], qs1 = a.qs[(row0 + qc) * a.H * 2 + h * 2 + 1];
-    float *vs_l = (float *)(smem + 2 * kI8Buf);
+    float *vs_l = (float *)(smem + kI8Ring * kI8Buf);
     vs_l[tid] = a.vs[((size_t)b * a.KV + kvh) * kI8D + tid];
     // the loads above complete here, under a wait the compiler sees: otherwise its wait would sit
     // inside the tile loop and also cover the tile loads in flight
@@ -171,7 +181,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
     const uint32_t rowB = (uint32_t)a.KV * kI8D;
     const v4u rK = rsrc_words(a.k8 + row0 * rowB + kvh * kI8D, (uint32_t)Sk * rowB);
     const v4u rKS = rsrc_words(a.ks + row0 * a.KV + kvh, (uint32_t)Sk * a.KV * 4);
-    const v4u rV = rsrc_words(a.vt8 + (size_t)kvh * kI8D * a.M, (uint32_t)((size_t)kI8D * a.M));
+    const v4u rV = rsrc_words(a.vt8 + (size_t)kvh * kI8D * 2 * a.M, (uint32_t)((size_t)kI8D * 2 * a.M));
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)smem);
     const int wu = __builtin_amdgcn_readfirstlane(w);
     // K tile: load i (wave w issues 2 w, 2 w + 1) fills physical rows rho = 4 i + lane / 16, 16-byte
@@ -183,14 +193,13 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
         const int i = 2 * wu + e;
         kvo[e] = (uint32_t)(lane >> 4) * rowB + (uint32_t)(((lane & 15) ^ ((4 * i + (lane >> 4)) & 15)) << 4);
     }
-    // V^T tile, in dwords (a sequence's V^T columns are only 8-byte aligned): load j (wave w issues
-    // 8 w .. 8 w + 7) fills rows d = 8 j + lane / 8, 16-byte position (lane % 8) / 4 holding chunk
-    // ((lane % 8) / 4) ^ ((d / 8) % 2) = ((lane % 8) / 4) ^ (j % 2), dword lane % 4 of it
-    uint32_t vvo[2];
-#pragma unroll
-    for (int e = 0; e < 2; e++)
-        vvo[e] = (uint32_t)(lane >> 3) * (uint32_t)a.M + (uint32_t)(lane & 3) * 4u +
-                 (uint32_t)((((lane & 7) >> 2) ^ e) << 4);
+    // V^T tile: load i (wave w issues 2 w, 2 w + 1) fills rows d = 32 i + lane / 2, position lane % 2
+    // holding chunk (lane % 2) ^ ((d / 8) % 2) = (lane % 2) ^ ((lane / 16) % 2)
+    const uint32_t vpitch = 2u * (uint32_t)a.M;
+    const uint32_t vvo = (uint32_t)(lane >> 1) * vpitch + (uint32_t)(((lane & 1) ^ ((lane >> 4) & 1)) << 4);
+    // every tile costs each wave 3 loads (K: 2 row loads + the key scales, which all waves load
+    // into the same place; V^T: 2 row loads + a spare scale load), so a wait for "all but the
+    // next tile's loads" is vmcnt(3)
     auto issue = [&](bool isk, int kt, int buf) {
         const int k0 = kt * 32;
         const uint32_t base = lds0 + (uint32_t)(buf * kI8Buf);
@@ -200,14 +209,49 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
                 const int i = 2 * wu + e;
                 dma16(rK, base + i * 1024, kvo[e], (uint32_t)(k0 + 16 * (i & 1) + 4 * (i >> 1)) * rowB);
             }
-            if (wu == 0) dma4(rKS, base + kI8Tile, (uint32_t)lane * a.KV * 4, (uint32_t)k0 * a.KV * 4);
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int j = 8 * wu + e;
-                dma4(rV, base + j * 256, vvo[e & 1], (uint32_t)(8 * j) * (uint32_t)a.M + (uint32_t)(row0 + k0));
+            for (int e = 0; e < 2; e++) {
+                const int i = 2 * wu + e;
+                dma16(rV, base + i * 1024, vvo, (uint32_t)(32 * i) * vpitch + (uint32_t)(2 * row0 + k0));
             }
         }
+        dma4(rKS, base + kI8Tile, (uint32_t)lane * a.KV * 4, (uint32_t)k0 * a.KV * 4);
+    };
+    // the tile stream: pass 1's K tiles, then per 128-key block its K tiles and its V^T tiles
+    const int NS = 3 * ntiles;
+    auto desc = [&](int n, bool &isk, int &kt) {
+        if (n < ntiles) {
+            isk = true;
+            kt = n;
+            return;
+        }
+        const int m = n - ntiles, full = 8 * (nblk - 1);
+        if (m < full) {
+            isk = (m & 7) < 4;
+            kt = 4 * (m >> 3) + (m & 3);
+            return;
+        }
+        const int ntl = ntiles - 4 * (nblk - 1), j = m - full;
+        isk = j < ntl;
+        kt = 4 * (nblk - 1) + (isk ? j : j - ntl);
+    };
+    int sn = 0;  // stream position of the step being computed
+    // wait for step sn's tile (every wave's), release the buffer of step sn - 1 and refill it with
+    // step sn + 2's tile; returns step sn's buffer
+    auto begin_step = [&]() -> const unsigned char * {
+        if (sn + 1 < NS) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (sn + 2 < NS) {
+            bool isk;
+            int kt;
+            desc(sn + 2, isk, kt);
+            issue(isk, kt, (sn + 2) % kI8Ring);
+        }
+        const unsigned char *sb = smem + (sn % kI8Ring) * kI8Buf;
+        ++sn;
+        return sb;
     };
     // fragment offsets: K row rho = lane % 32, chunk 2 kk + half at position (2 kk + half) ^ (rho % 16);
     // V^T row d = 32 dt + lane % 32, chunk half at position half ^ ((d / 8) % 2)
@@ -239,16 +283,17 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
         }
     };
 
-    int buf = 0;
-    // tile stream: pass 1 K tiles 0 .. ntiles-1, then per block the block's K tiles and V tiles
-    issue(true, 0, 0);
+    for (int n = 0; n < 2 && n < NS; n++) {
+        bool isk;
+        int kt;
+        desc(n, isk, kt);
+        issue(isk, kt, n);
+    }
     float mrun = -INFINITY, lrun = 0.f;
     for (int kt = 0; kt < ntiles; kt++) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        issue(true, kt + 1 < ntiles ? kt + 1 : 0, buf ^ 1);  // last: pass 2's first K tile
+        const unsigned char *sb = begin_step();
         float s[16];
-        scores(smem + buf * kI8Buf, kt * 32, s);
+        scores(sb, kt * 32, s);
         float mloc = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) mloc = fmaxf(mloc, s[r]);
@@ -261,7 +306,6 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
             lrun = (mrun == -INFINITY ? 0.f : lrun * __expf(mrun - mnew)) + ps;
             mrun = mnew;
         }
-        buf ^= 1;
     }
     const float ltot = lrun + __shfl_xor(lrun, 32);
     const float inv_l = ltot > 0.f ? __fdiv_rn(1.0f, ltot) : 0.f;
@@ -281,19 +325,15 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             if (t < nt) {
-                const int kt = 4 * blk + t;
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                __syncthreads();
-                issue(t + 1 < nt, t + 1 < nt ? kt + 1 : 4 * blk, buf ^ 1);
+                const unsigned char *sb = begin_step();
                 float s[16];
-                scores(smem + buf * kI8Buf, kt * 32, s);
+                scores(sb, (4 * blk + t) * 32, s);
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const float e = s[r] == -INFINITY ? 0.f : __expf(s[r] - mrun);
                     pv[t][r] = __fmul_rn(e, inv_l);
                     am = fmaxf(am, pv[t][r]);
                 }
-                buf ^= 1;
             } else {
 #pragma unroll
                 for (int r = 0; r < 16; r++) pv[t][r] = 0.f;
@@ -310,19 +350,12 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             if (t < nt) {
-                const int kt = 4 * blk + t;
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                __syncthreads();
-                // next: this block's next V tile, else the next block's first K tile
-                if (t + 1 < nt) issue(false, kt + 1, buf ^ 1);
-                else if (blk + 1 < nblk) issue(true, kt + 1, buf ^ 1);
-                const unsigned char *sb = smem + buf * kI8Buf;
+                const unsigned char *sb = begin_step();
 #pragma unroll
                 for (int dt = 0; dt < 8; dt++) {
                     const v4i vf = *(const v4i *)(sb + dt * 32 * 32 + vrd);
                     acco[dt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pq[t], acco[dt], 0, 0, 0);
                 }
-                buf ^= 1;
             }
         }
         // fold the block: d = 32 dt + 8 (r / 4) + 4 half + r % 4
@@ -380,7 +413,7 @@ static I8Ws i8_ws(int M, int B, int max_len, int H, int KV) {
     w.k8 = w.qs + al256((size_t)M * H * 2 * 4);
     w.ks = w.k8 + al256((size_t)M * KV * kI8D);
     w.vt8 = w.ks + al256((size_t)M * KV * 4);
-    w.vpart = w.vt8 + al256((size_t)KV * kI8D * M);
+    w.vpart = w.vt8 + al256((size_t)KV * kI8D * 2 * M);
     w.vs = w.vpart + al256((size_t)B * KV * nch * kI8D * 4);
     w.total = w.vs + al256((size_t)B * KV * kI8D * 4);
     return w;
@@ -411,7 +444,7 @@ extern "C" int e2mi_attention_i8_packed(e2mi_stream stream, const float *q32, co
         set_error("attention_i8_packed: null or misaligned pointer");
         return -1;
     }
-    if ((size_t)KV * kI8D * M >= 0x7fffffffu || (size_t)M * KV * kI8D >= 0x7fffffffu) {
+    if ((size_t)kI8D * 2 * M >= 0x7fffffffu || (size_t)M * KV * kI8D >= 0x7fffffffu) {
         set_error("attention_i8_packed: too many rows");
         return -1;
     }

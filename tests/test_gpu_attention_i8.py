@@ -36,7 +36,7 @@ def _packed(rng, e2mi, lens, S):
 
 
 def _ws_layout(M, B, max_len, H, KV):
-    """The workspace layout of attn_i8.hip (i8_ws): q8, qs, k8, ks, vt8, vpart, vs."""
+    """The workspace layout of attn_i8.hip (i8_ws): q8, qs, k8, ks, vt8 ([KV][D][2 M]), vpart, vs."""
     al = lambda x: (x + 255) & ~255
     nch = (max_len + 63) // 64
     q8 = 0
@@ -44,7 +44,7 @@ def _ws_layout(M, B, max_len, H, KV):
     k8 = qs + al(M * H * 2 * 4)
     ks = k8 + al(M * KV * D)
     vt8 = ks + al(M * KV * 4)
-    vpart = vt8 + al(KV * D * M)
+    vpart = vt8 + al(KV * D * 2 * M)
     vs = vpart + al(B * KV * nch * D * 4)
     return dict(q8=q8, qs=qs, k8=k8, ks=ks, vt8=vt8, vs=vs)
 
@@ -81,7 +81,7 @@ def test_i8_quantized_operands_bit_exact(gpu, oracle, rng, H, KV, lens):
     qs = raw[lay["qs"]:lay["qs"] + M * H * 8].view(np.float32).reshape(M, H, 2)
     k8 = raw[lay["k8"]:lay["k8"] + M * KV * D].view(np.int8).reshape(M, KV, D)
     ks = raw[lay["ks"]:lay["ks"] + M * KV * 4].view(np.float32).reshape(M, KV)
-    vt8 = raw[lay["vt8"]:lay["vt8"] + KV * D * M].view(np.int8).reshape(KV, D, M)
+    vt8 = raw[lay["vt8"]:lay["vt8"] + KV * D * 2 * M].view(np.int8).reshape(KV, D, 2 * M)
     vs = raw[lay["vs"]:lay["vs"] + B * KV * D * 4].view(np.float32).reshape(B, KV, D)
     live = rowmap >= 0
     # Q per (row, head, 128 dims): the activation quantizer
@@ -99,7 +99,8 @@ def test_i8_quantized_operands_bit_exact(gpu, oracle, rng, H, KV, lens):
                 continue
             r = slice(start[b], start[b] + L)
             wq, sc, _ = oracle.q8w_from_f32(np.ascontiguousarray(v[r][:, kv * D:(kv + 1) * D].T))
-            assert np.array_equal(vt8[kv][:, r], oracle.q8w_unpack(wq, D, L))
+            # sequence b's keys sit at V^T columns 2 start[b] + j (16-byte aligned tiles)
+            assert np.array_equal(vt8[kv][:, 2 * start[b]:2 * start[b] + L], oracle.q8w_unpack(wq, D, L))
             assert np.array_equal(vs[b, kv].view(np.uint32), sc[:D].view(np.uint32))
 
 
