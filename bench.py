@@ -71,6 +71,56 @@ def time_calls(torch, fn, iters):
     return s.elapsed_time(e) / iters * 1e-3
 
 
+# ------------------------------------------------------------------ vision projections
+def vision_bench(torch, e2mi, iters=20):
+    """The vision tower's int8 projections (vision.c:985-1110; model.h:20-27) at the largest image,
+    P = 2520 patches, per-128 activation blocks: per layer q|k|v 768->2304 (one quantization),
+    o 768->768, gate|up 768->2x3072 with the GeGLU epilogue, down 3072->768, 16 layers, plus the
+    patch projection 768->768 once. Random int8 weights and activations of those shapes."""
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(1006)
+    P, D, I = 2520, 768, 3072
+    x = torch.from_numpy(rng.standard_normal((P, D)).astype(np.float32)).to(dev)
+    q, s = e2mi.quantize(x)
+
+    def weight(N, K):
+        w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        return e2mi.DeviceWeight.from_rowmajor(w, rng.uniform(0.001, 0.02, N).astype(np.float32))
+    Wqkv, Wo, Wd = weight(3 * D, D), weight(D, D), weight(D, I)
+    wg = rng.integers(-127, 128, (I, D), dtype=np.int8)
+    wu = rng.integers(-127, 128, (I, D), dtype=np.int8)
+    wi, si = e2mi.interleave_gate_up(wg, rng.uniform(0.001, 0.02, I).astype(np.float32), wu,
+                                     rng.uniform(0.001, 0.02, I).astype(np.float32))
+    Wgu = e2mi.DeviceWeight.from_rowmajor(wi, si)
+    lib = e2mi.load()
+    y3 = torch.empty((P, 3 * D), device=dev)
+    y1 = torch.empty((P, D), device=dev)
+    gq = torch.empty((P, I), dtype=torch.int8, device=dev)
+    gs = torch.empty((P, I // 128), device=dev)
+    legs = {
+        "qkv_768x2304": (lambda: e2mi.i8_gemm(q, s, Wqkv, y=y3), 2 * P * 3 * D * D),
+        "o_768x768": (lambda: e2mi.i8_gemm(q, s, Wo, y=y1), 2 * P * D * D),
+        "gate_up_geglu_768x6144": (lambda: e2mi.check(lib.e2mi_i8_gemm_geglu(
+            e2mi.stream_ptr(None), e2mi.ptr(gq), e2mi.ptr(gs), None, e2mi.ptr(q), e2mi.ptr(s), Wgu.ref, P),
+            "geglu"), 2 * P * 2 * I * D),
+        "down_3072x768": (lambda: e2mi.i8_gemm(gq, gs, Wd, y=y1), 2 * P * D * I),
+    }
+    res, t_layer, ops_layer = {}, 0.0, 0
+    for name, (fn, ops) in legs.items():
+        fn()
+        torch.cuda.synchronize()
+        t = time_calls(torch, fn, iters)
+        res[name] = {"us": round(t * 1e6, 2), "tops": round(ops / t / 1e12, 1)}
+        t_layer += t
+        ops_layer += ops
+    t_img = 16 * t_layer + res["o_768x768"]["us"] * 1e-6  # + the patch projection (768 -> 768)
+    res.update({"per_layer_us": round(t_layer * 1e6, 2), "per_layer_tops": round(ops_layer / t_layer / 1e12, 1),
+                "images_per_s_projections_only": round(1 / t_img, 1),
+                "note": "P=2520 patches (the largest image), 16 layers; projections only (the vision "
+                        "attention, norms and RoPE are not part of this build)"})
+    return res
+
+
 # ------------------------------------------------------------------ CPU baseline
 def cpu_flags():
     try:
@@ -553,6 +603,7 @@ def main():
         "quantize_65536x768": {"us": round(q_t * 1e6, 2), "GB/s": round(q_bytes / q_t / 1e9, 1)},
         "roofline": roofline,
     }
+    out["vision_projections"] = vision_bench(torch, e2mi)
     if not args.no_encoder:
         enc = encoder_bench(torch, e2mi, max(5, args.steps // 2), args.warmup)
         model, (eids, evalid) = enc.pop("_model"), enc.pop("_batch")

@@ -863,6 +863,12 @@ static int check_args(const GemmArgs &p, const char *who) {
     return 0;
 }
 
+// fewer 256 x 128 tiles than CUs (the vision tower's 2520-patch projections, small batches):
+// 128 x 128 tiles of 4 waves, two workgroups per CU, four times the tiles
+static bool small_grid(const GemmArgs &p) {
+    return (long)((p.M + 255) / 256) * ((p.N + 127) / 128) < num_cus();
+}
+
 int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump, bool tok = false) {
     if (check_args(p, "i8_gemm")) return -1;
     if (!p.Y || p.ldy < p.N) {
@@ -877,6 +883,7 @@ int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump, bool tok = false) {
         return launch_dump(s, p);
     }
     if (tok) return launch_t<EPI_F32>(s, p);
+    if (small_grid(p)) return launch_p<128, 128, 4, 1, EPI_F32>(s, p);
     return launch_p<256, 128, 8, 1, EPI_F32>(s, p);
 }
 
@@ -888,6 +895,7 @@ int launch_gemm_i8q(hipStream_t s, GemmArgs p, bool tok = false) {
         return -1;
     }
     if (tok) return launch_t<EPI_I8Q>(s, p);
+    if (small_grid(p)) return launch_p<128, 128, 4, 1, EPI_I8Q>(s, p);
     return launch_p<256, 128, 8, 1, EPI_I8Q>(s, p);
 }
 
