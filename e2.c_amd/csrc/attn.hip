@@ -43,6 +43,10 @@ struct AttnArgs {
     const int32_t *work;
     int B, S, H, KV;
     float scale;
+    // packed batches, optional: keys with |pos_i - pos_j| > window are skipped (0: no window);
+    // pos [M] is each row's position in its padded sequence (null: the packed index)
+    int window;
+    const int32_t *pos;
 };
 
 __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
@@ -221,24 +225,43 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     }
 }
 
-// ---- packed batches: the same attention with K/V tiles fetched straight into LDS one tile ahead.
-// Every key of a packed sequence is valid, so no mask is read; the per-sequence work is the
-// arithmetic of k_attn bit for bit (same MFMA order, same softmax; masked keys read as zero here
-// and contribute p = 0 in both).
+// ---- packed batches: the same attention with K/V tiles fetched straight into LDS one tile ahead,
+// for head_dim D = 256 or 512 (the reference checkpoint's full-attention layers), with an optional
+// sliding window. Every key of a packed sequence is valid, so no mask is read; the per-sequence
+// work at D = 256 without a window is the arithmetic of k_attn bit for bit (same MFMA order, same
+// softmax; masked keys read as zero here and contribute p = 0 in both).
 //
-// LDS per workgroup: 2 buffers of [K tile 32 keys x 512 B | V^T tile 256 d x 64 B] = 64 KB.
+// At D = 512 a workgroup computes the logits over all 512 dims but owns half of the context dims
+// (DO = 256): Q fragments and a whole context take more registers than a lane has (measured: 223
+// spilled), so the two halves go to two workgroups (grid y, or work-list grid y), each reading the
+// K tiles and its half of the V^T tiles.
+//
+// LDS per workgroup: 2 buffers of [K tile 32 keys x 2D B | V^T tile DO rows x 64 B] (64 KB at
+// D = 256, two workgroups per CU; 96 KB at D = 512, one).
 //   K tile row i holds key swap23(i) (bits 2 and 3 of the index exchanged). The S^T MFMA then
 //     leaves in a lane's registers 8 j + e (e = 0..7) the keys 16 j + 8 half + e: consecutive keys,
 //     so the PV MFMA's A operand is one 16-byte chunk of a V^T row in natural key order.
-//   K rows are 512 B; 16-byte chunk x of row i sits at position x ^ (i & 7), so the eight lanes of
-//     a read group (rows i..i+7, one chunk) hit eight bank groups.
+//   K rows are 2D bytes; 16-byte chunk x of row i sits at position x ^ (i & 7), so the eight lanes
+//     of a read group (rows i..i+7, one chunk) hit eight bank groups.
 //   V^T rows (one d, 32 keys) are 64 B; chunk c of row d sits at position c ^ ((d >> 2) & 3)
 //     (conflict-free for rows d..d+7).
-// The tile loads are 16-byte direct-to-LDS buffer loads, 4 per wave for K (two rows each) and 4
-// for V^T (16 rows each), whose lanes fetch the permuted, swizzled source chunks. Keys past the
-// sequence read as zero (K: past the descriptor's range; V^T: 8-key chunks past the sequence get an
-// offset past it, and the sequence's rows end on an 8-row boundary of the slab).
-constexpr int kPKTile = kKT * 512, kPVTile = kD * 64, kPBuf = kPKTile + kPVTile;
+// The tile loads are 16-byte direct-to-LDS buffer loads: D/64 per wave for K (512/D rows each) and
+// DO/64 for V^T (16 rows each), whose lanes fetch the permuted, swizzled source chunks. Keys past
+// the sequence read as zero (K: past the descriptor's range; V^T: 8-key chunks past the sequence
+// get an offset past it, and the sequence's rows end on an 8-row boundary of the slab).
+//
+// Sliding window (text.c:542-546): query i reads key j when |pos_i - pos_j| <= window, pos being
+// the token's position in its padded sequence (a.pos; the packed index when a.pos is null). The
+// packed index never moves two tokens further apart than their positions, so the key tiles a query
+// block reads are those within window of its rows by index; a tile whose every key is within window
+// of every query of the block (checked on the positions of its first and last key and of the
+// block's first and last query) needs no per-key test.
+template <int D>
+struct PackedTile {
+    static constexpr int kDO = D < 256 ? D : 256, kSplit = D / kDO;  // context dims per workgroup
+    static constexpr int kK = kKT * 2 * D, kV = kDO * 64, kBuf = kK + kV;
+    static constexpr size_t kLds = 2 * (size_t)kBuf;
+};
 
 // dma16 without a compiler memory clobber: the loads of tile kt + 1 fill the LDS buffer that no
 // read of tile kt touches, so LDS reads and MFMAs may be scheduled across them; the loop-top wait
@@ -247,11 +270,19 @@ __device__ inline void dma16_nc(v4u r, uint32_t lds, uint32_t voff, uint32_t sof
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  ::"s"(lds), "v"(voff), "s"(r), "s"(soff));
 }
-constexpr size_t kAttnPackedLds = 2 * (size_t)kPBuf;
 
-__global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
+__device__ inline int swap23(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+template <int D>
+__global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs a) {
+    using T = PackedTile<D>;
+    constexpr int DO = T::kDO;
+    // Q fragments, O tiles, K and V^T loads per wave and tile
+    constexpr int NQ = D / 16, NO = DO / 32, NLK = D / 64, NLV = DO / 64;
+    constexpr int RPI = 512 / D, LPR = D / 8;  // K rows per load, lanes per K row
     extern __shared__ __align__(16) unsigned char pk_smem[];
-    int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    int qb = blockIdx.x, h = blockIdx.y / T::kSplit, b = blockIdx.z;
+    const int dh = blockIdx.y % T::kSplit;  // which DO context dims: a.work grids put it in y too
     if (a.work) {
         const int item = a.work[blockIdx.x];
         if (item < 0) return;
@@ -260,7 +291,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
         qb = item >> 24;
     }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5;
-    const int S = a.S, HD = a.H * kD, kvh = h / (a.H / a.KV);
+    const int S = a.S, HD = a.H * D, kvh = h / (a.H / a.KV);
     const size_t row0 = (size_t)a.seq_start[b];
     const int Sk = a.seq_len[b];
     if (qb * 128 >= Sk) return;  // no rows of this sequence in the block
@@ -268,52 +299,64 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
     const int qi = qb * 128 + w * 32 + (lane & 31);  // this lane's query
     const bool qvalid = qi < Sk;
     const int qc = min(qi, Sk - 1);
-    h8 qf[16];
+    h8 qf[NQ];
     {
-        const uint16_t *qp = a.q + (row0 + qc) * HD + h * kD + 8 * half;
+        const uint16_t *qp = a.q + (row0 + qc) * HD + h * D + 8 * half;
 #pragma unroll
-        for (int s = 0; s < 16; s++) qf[s] = *(const h8 *)(qp + 16 * s);
+        for (int s = 0; s < NQ; s++) qf[s] = *(const h8 *)(qp + 16 * s);
+    }
+    // key tiles of this block: all, or those within window of its rows (by packed index)
+    const int W = a.window;
+    int kt0 = 0, kt1 = (Sk + kKT - 1) / kKT;
+    int pq0 = 0, pq1 = 0, pqi = qc;
+    if (W > 0) {
+        const int q0 = qb * 128, q1 = min(q0 + 127, Sk - 1);
+        kt0 = max(q0 - W, 0) / kKT;
+        kt1 = min((min(q1 + W, Sk - 1)) / kKT + 1, kt1);
+        pq0 = a.pos ? a.pos[row0 + q0] : q0;
+        pq1 = a.pos ? a.pos[row0 + q1] : q1;
+        pqi = a.pos ? a.pos[row0 + qc] : qc;
     }
     // wait for the Q loads here, with a wait the compiler's wait-count pass sees: otherwise it
     // waits for them inside the tile loop, where the count would also cover the tile loads in
     // flight (s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15))
     __builtin_amdgcn_s_waitcnt(0x0F70);
-    f16v o[8];
+    f16v o[NO];
 #pragma unroll
-    for (int t = 0; t < 8; t++) o[t] = (f16v){};
+    for (int t = 0; t < NO; t++) o[t] = (f16v){};
     float mrun = -INFINITY, lrun = 0.f;
-    const int ntiles = (Sk + kKT - 1) / kKT;
 
     // sources: K rows of this kv head (row pitch KV*D halves), V^T slab [D][S] of this kv head
-    const uint32_t rowB = (uint32_t)a.KV * kD * 2;
-    const v4u rK = rsrc_words(a.k + row0 * a.KV * kD + kvh * kD, (uint32_t)Sk * rowB);
-    const uint16_t *vslab = a.vt + (size_t)kvh * kD * S + row0;
-    const v4u rV = rsrc_words(vslab, (uint32_t)((size_t)kD * S * 2));
+    const uint32_t rowB = (uint32_t)a.KV * D * 2;
+    const v4u rK = rsrc_words(a.k + row0 * a.KV * D + kvh * D, (uint32_t)Sk * rowB);
+    const uint16_t *vslab = a.vt + ((size_t)kvh * D + dh * DO) * S + row0;
+    const v4u rV = rsrc_words(vslab, (uint32_t)((size_t)DO * S * 2));
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)pk_smem);
     const int wu = __builtin_amdgcn_readfirstlane(w);
-    const int lh = lane >> 5, lc = lane & 31;
-    // K: instruction i of wave w fills LDS rows 8 w + 2 i + lane / 32, i.e. keys swap23 of that
-    // (the scalar part goes to the scalar offset); lane's chunk position lane % 32 holds source
-    // chunk (lane % 32) ^ (row & 7), row & 7 = (2 i + lane / 32) & 7.
-    // V^T: instruction i of wave w fills rows d = 64 w + 16 i + lane / 4, chunk position lane % 4,
+    const int lr = lane / LPR, lc = lane % LPR;
+    // K: load i of wave w fills LDS rows 8 w + RPI i + lane / LPR, i.e. keys swap23 of those
+    // (swap23 keeps bit 0, so the second row of a D = 256 load is the next key); lane's chunk
+    // position lane % LPR holds source chunk (lane % LPR) ^ (row & 7).
+    // V^T: load i of wave w fills rows d = (DO/4) w + 16 i + lane / 4, chunk position lane % 4,
     // which holds source chunk (lane % 4) ^ ((d >> 2) & 3) = (lane % 4) ^ ((lane >> 4) & 3).
     const uint32_t vlane = (uint32_t)(lane >> 2) * (uint32_t)S * 2;
     const int vchunk = (lane & 3) ^ ((lane >> 4) & 3);
-    // load j (0-3: K, 4-7: V^T) of tile kt; issued one per two S^T MFMAs of the previous tile
+    // load j (0 .. NLK-1: K, NLK .. NLK+NLV-1: V^T) of tile kt; issued one per two S^T MFMAs of
+    // the previous tile
     auto issue_load = [&](int kt, int j) {
         const int k0 = kt * kKT;
-        const uint32_t base = lds0 + (uint32_t)((kt & 1) * kPBuf);
-        if (j < 4) {
-            const int i = j;
-            const int ks = 16 * (wu >> 1) + 8 * ((i >> 1) & 1) + 4 * (wu & 1) + 2 * (i & 1);  // swap23(row) - lane / 32
-            const uint32_t voff = (uint32_t)lh * rowB + (uint32_t)((lc ^ ((2 * i + lh) & 7)) << 4);
-            dma16_nc(rK, __builtin_amdgcn_readfirstlane(base + (4 * wu + i) * 1024), voff,
-                     __builtin_amdgcn_readfirstlane((uint32_t)(ks + k0) * rowB));
+        const uint32_t base = lds0 + (uint32_t)((kt & 1) * T::kBuf);
+        if (j < NLK) {
+            // the key row goes into the per-lane offset, which the descriptor's range check covers:
+            // keys past the sequence read as zero without touching memory past it
+            const int i = j, r = 8 * wu + RPI * i;
+            const uint32_t voff = (uint32_t)(swap23(r) + k0 + lr) * rowB + (uint32_t)((lc ^ ((r + lr) & 7)) << 4);
+            dma16_nc(rK, __builtin_amdgcn_readfirstlane(base + (uint32_t)r * (2 * D)), voff, 0u);
         } else {
-            const int i = j - 4;
+            const int i = j - NLK, d0 = (DO / 4) * wu + 16 * i;
             const uint32_t vo = (k0 + 8 * vchunk < Sk) ? vlane + (uint32_t)vchunk * 16 : 0x80000000u;
-            dma16_nc(rV, __builtin_amdgcn_readfirstlane(base + kPKTile + (64 * wu + 16 * i) * 64), vo,
-                     __builtin_amdgcn_readfirstlane((uint32_t)((64 * wu + 16 * i) * S + k0) * 2));
+            dma16_nc(rV, __builtin_amdgcn_readfirstlane(base + T::kK + d0 * 64), vo,
+                     __builtin_amdgcn_readfirstlane((uint32_t)(d0 * S + k0) * 2));
         }
     };
 
@@ -322,31 +365,38 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
     const int kkey = lane & 31;
     uint32_t krd[4];
 #pragma unroll
-    for (int u = 0; u < 4; u++) krd[u] = (uint32_t)(kkey * 512 + (((2 * u + half) ^ (kkey & 7)) << 4));
+    for (int u = 0; u < 4; u++) krd[u] = (uint32_t)(kkey * 2 * D + (((2 * u + half) ^ (kkey & 7)) << 4));
     // V^T (PV A operand): row d = 32 t + lane % 32, chunk 2 j + half at position ^ ((d >> 2) & 3)
     uint32_t vrd[2];
 #pragma unroll
     for (int j = 0; j < 2; j++)
-        vrd[j] = (uint32_t)(kPKTile + (lane & 31) * 64 + (((2 * j + half) ^ (((lane & 31) >> 2) & 3)) << 4));
+        vrd[j] = (uint32_t)(T::kK + (lane & 31) * 64 + (((2 * j + half) ^ (((lane & 31) >> 2) & 3)) << 4));
 
-    if (ntiles > 0)
+    if (kt0 < kt1)
 #pragma unroll
-        for (int j = 0; j < 8; j++) issue_load(0, j);
-    for (int kt = 0; kt < ntiles; kt++) {
+        for (int j = 0; j < NLK + NLV; j++) issue_load(kt0, j);
+    for (int kt = kt0; kt < kt1; kt++) {
         const int k0 = kt * kKT;
         // this wave's loads of tile kt have landed; the barrier makes every wave's visible and
         // ends every wave's reads of tile kt - 1, whose buffer the next loads refill
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        const bool next = kt + 1 < ntiles;
-        const unsigned char *sb = pk_smem + (kt & 1) * kPBuf;
+        const bool next = kt + 1 < kt1;
+        const unsigned char *sb = pk_smem + (kt & 1) * T::kBuf;
 
         f16v st = (f16v){};
 #pragma unroll
-        for (int s = 0; s < 16; s++) {
+        for (int s = 0; s < NQ; s++) {
             const h8 kf = *(const h8 *)(sb + krd[s & 3] + (s >> 2) * 128);
             st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
-            if ((s & 1) && next) issue_load(kt + 1, s >> 1);
+            if ((s & 1) && (s >> 1) < NLK + NLV && next) issue_load(kt + 1, s >> 1);
+        }
+        // window: a tile inside the window of every query of the block needs no per-key test
+        bool edge = false;
+        if (W > 0) {
+            const int ka = k0, kb = min(k0 + kKT, Sk) - 1;
+            const int pka = a.pos ? a.pos[row0 + ka] : ka, pkb = a.pos ? a.pos[row0 + kb] : kb;
+            edge = pkb - pq0 > W || pq1 - pka > W;
         }
         float tv[16];
         float mloc = -INFINITY;
@@ -354,7 +404,12 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
         for (int r = 0; r < 16; r++) {
             // S^T row 8 (r / 4) + 4 half + r % 4 of this register holds key swap23(row)
             const int key = 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
-            tv[r] = (k0 + key < Sk) ? st[r] * a.scale : -INFINITY;
+            bool keep = k0 + key < Sk;
+            if (edge && keep) {
+                const int pk = a.pos ? a.pos[row0 + k0 + key] : k0 + key;
+                keep = pk - pqi <= W && pqi - pk <= W;
+            }
+            tv[r] = keep ? st[r] * a.scale : -INFINITY;
             mloc = fmaxf(mloc, tv[r]);
         }
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
@@ -379,7 +434,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
         // the running max rarely moves after the first tiles: skip the rescale when no lane's did
         if (__any(alpha != 1.f)) {
 #pragma unroll
-            for (int t = 0; t < 8; t++) o[t] *= alpha;
+            for (int t = 0; t < NO; t++) o[t] *= alpha;
         }
         h8 pb[2];
 #pragma unroll
@@ -387,7 +442,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; e++) pb[j][e] = ph[8 * j + e];
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
+        for (int t = 0; t < NO; t++) {
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 const h8 vf = *(const h8 *)(sb + vrd[j] + t * 32 * 64);
@@ -400,11 +455,12 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
     const float ltot = lrun + __shfl_xor(lrun, 32);
     const float inv = (qvalid && ltot > 0.f) ? __fdiv_rn(1.0f, ltot) : 0.f;
 #pragma unroll
-    for (int t = 0; t < 8; t++) o[t] *= inv;
+    for (int t = 0; t < NO; t++) o[t] *= inv;
     if (qi >= Sk) return;  // rows past the sequence belong to the next one
     const size_t orow = (row0 + qi);
+    const int dof = dh * DO;  // this workgroup's first context dim
 #pragma unroll
-    for (int blk = 0; blk < 2; blk++) {
+    for (int blk = 0; blk < DO / 128; blk++) {
         float am = 0.f;
 #pragma unroll
         for (int t = 4 * blk; t < 4 * blk + 4; t++)
@@ -416,23 +472,24 @@ __global__ __launch_bounds__(256, 2) void k_attn_packed(AttnArgs a) {
         for (int t = 4 * blk; t < 4 * blk + 4; t++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                const int d = 32 * t + 8 * g + 4 * half;
-                *(uint32_t *)(a.cq + orow * HD + h * kD + d) =
+                const int d = dof + 32 * t + 8 * g + 4 * half;
+                *(uint32_t *)(a.cq + orow * HD + h * D + d) =
                     pack4(qbyte(o[t][4 * g], qs.inv), qbyte(o[t][4 * g + 1], qs.inv),
                           qbyte(o[t][4 * g + 2], qs.inv), qbyte(o[t][4 * g + 3], qs.inv));
                 if (a.c32)
-                    *(float4 *)(a.c32 + orow * HD + h * kD + d) =
+                    *(float4 *)(a.c32 + orow * HD + h * D + d) =
                         make_float4(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]);
             }
-        if (half == 0) a.cs[orow * (HD / kQBlock) + h * 2 + blk] = qs.sc;
+        if (half == 0) a.cs[orow * (HD / kQBlock) + h * (D / 128) + dof / 128 + blk] = qs.sc;
     }
 }
 
+template <int D>
 static int attn_packed_attr() {
     static bool done = false;
     if (!done) {
-        if (check_hip(hipFuncSetAttribute((const void *)k_attn_packed, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          (int)kAttnPackedLds), "attention lds attribute"))
+        if (check_hip(hipFuncSetAttribute((const void *)k_attn_packed<D>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)PackedTile<D>::kLds), "attention lds attribute"))
             return -1;
         done = true;
     }
@@ -462,38 +519,70 @@ extern "C" int e2mi_attention(e2mi_stream stream, const uint16_t *q16, const uin
     return check_hip(hipGetLastError(), "attention launch");
 }
 
-extern "C" int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
-                                     const uint16_t *vt16, int M, const int32_t *seq_start,
-                                     const int32_t *seq_len, int B, int max_len, int H, int KV, int D,
-                                     float scale, int8_t *ctx_q, float *ctx_s, float *ctx32,
-                                     const int32_t *work, int n_work) {
-    if (D != kD || B <= 0 || M <= 0 || max_len <= 0 || H <= 0 || KV <= 0 || H % KV) {
-        set_error("attention_packed: needs head_dim 256 and H %% KV == 0 (B=%d M=%d H=%d KV=%d D=%d)", B,
-                  M, H, KV, D);
+static int attention_packed(const char *who, e2mi_stream stream, const uint16_t *q16,
+                            const uint16_t *k16, const uint16_t *vt16, int M, const int32_t *seq_start,
+                            const int32_t *seq_len, const int32_t *pos, int B, int max_len, int H,
+                            int KV, int D, float scale, int window, int8_t *ctx_q, float *ctx_s,
+                            float *ctx32, const int32_t *work, int n_work) {
+    if ((D != 256 && D != 512) || B <= 0 || M <= 0 || max_len <= 0 || H <= 0 || KV <= 0 || H % KV ||
+        window < 0) {
+        set_error("%s: needs head_dim 256 or 512, H %% KV == 0 and window >= 0 (B=%d M=%d H=%d KV=%d D=%d)",
+                  who, B, M, H, KV, D);
         return -1;
     }
     if (!q16 || !k16 || !vt16 || !seq_start || !seq_len || !ctx_q || !ctx_s || !aligned16(q16) ||
         !aligned16(k16) || ((uintptr_t)vt16 & 7) || ((uintptr_t)ctx_q & 3) ||
         (ctx32 && !aligned16(ctx32))) {
-        set_error("attention_packed: null or misaligned pointer");
+        set_error("%s: null or misaligned pointer", who);
         return -1;
     }
     if (work && (n_work <= 0 || B > 0xffff || H > 0xff || (max_len + 127) / 128 > 127)) {
-        set_error("attention_packed: work list needs n_work > 0, B < 65536, H < 256, max_len < 16257");
+        set_error("%s: work list needs n_work > 0, B < 65536, H < 256, max_len < 16257", who);
         return -1;
     }
-    AttnArgs a = {q16, k16, vt16, nullptr, ctx_q, ctx_s, ctx32, seq_start, seq_len, work, B, M, H, KV, scale};
+    AttnArgs a = {q16, k16, vt16, nullptr, ctx_q, ctx_s, ctx32, seq_start, seq_len, work, B, M, H, KV, scale,
+                  window, pos};
     // the direct-to-LDS kernel needs 4-byte-aligned V^T rows and 32-bit offsets into the V^T slab
     // and the K rows; every sequence must start on an even row (the engine starts them on
     // multiples of 8)
-    if (M % 2 == 0 && (size_t)KV * kD * M * 2 < 0x7fffffffu && (size_t)M * KV * kD * 2 < 0x7fffffffu &&
-        ((uintptr_t)vt16 & 3) == 0) {
-        if (attn_packed_attr()) return -1;
-        const dim3 grid = work ? dim3(n_work) : dim3((max_len + 127) / 128, H, B);
-        hipLaunchKernelGGL(k_attn_packed, grid, dim3(256), kAttnPackedLds, (hipStream_t)stream, a);
-    } else {
+    const bool direct = M % 2 == 0 && (size_t)KV * D * M * 2 < 0x7fffffffu &&
+                        (size_t)M * KV * D * 2 < 0x7fffffffu && ((uintptr_t)vt16 & 3) == 0;
+    const int split = D == 512 ? PackedTile<512>::kSplit : 1;
+    const dim3 grid = work ? dim3(n_work, split) : dim3((max_len + 127) / 128, H * split, B);
+    if (direct && D == 256) {
+        if (attn_packed_attr<256>()) return -1;
+        hipLaunchKernelGGL(k_attn_packed<256>, grid, dim3(256), PackedTile<256>::kLds, (hipStream_t)stream, a);
+    } else if (direct) {
+        if (attn_packed_attr<512>()) return -1;
+        hipLaunchKernelGGL(k_attn_packed<512>, grid, dim3(256), PackedTile<512>::kLds, (hipStream_t)stream, a);
+    } else if (D == 256 && window == 0) {
         a.work = nullptr;
         hipLaunchKernelGGL(k_attn, dim3((max_len + 127) / 128, H, B), dim3(256), 0, (hipStream_t)stream, a);
+    } else {
+        set_error("%s: head_dim 512 or a window needs an even M, 4-byte-aligned V^T and slabs under 2 GiB", who);
+        return -1;
     }
     return check_hip(hipGetLastError(), "attention launch");
+}
+
+extern "C" int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
+                                     const uint16_t *vt16, int M, const int32_t *seq_start,
+                                     const int32_t *seq_len, int B, int max_len, int H, int KV, int D,
+                                     float scale, int8_t *ctx_q, float *ctx_s, float *ctx32,
+                                     const int32_t *work, int n_work) {
+    if (D != 256) {
+        set_error("attention_packed: needs head_dim 256 (D=%d; e2mi_attention_packed_window takes 512)", D);
+        return -1;
+    }
+    return attention_packed("attention_packed", stream, q16, k16, vt16, M, seq_start, seq_len, nullptr, B,
+                            max_len, H, KV, D, scale, 0, ctx_q, ctx_s, ctx32, work, n_work);
+}
+
+extern "C" int e2mi_attention_packed_window(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
+                                            const uint16_t *vt16, int M, const int32_t *seq_start,
+                                            const int32_t *seq_len, const int32_t *pos, int B, int max_len,
+                                            int H, int KV, int D, float scale, int window, int8_t *ctx_q,
+                                            float *ctx_s, float *ctx32, const int32_t *work, int n_work) {
+    return attention_packed("attention_packed_window", stream, q16, k16, vt16, M, seq_start, seq_len, pos, B,
+                            max_len, H, KV, D, scale, window, ctx_q, ctx_s, ctx32, work, n_work);
 }

@@ -1,7 +1,7 @@
 // forward.cpp — the encoder on the device: weight upload, workspace, the per-layer kernel sequence,
 // hipGraph capture per (batch, seq_len) shape, and the e2hip-style entry points.
 //
-// Layer recipe (text.c:939-961 without PLE / layer_scalar), as fused launches:
+// Layer recipe (text.c:939-961), as fused launches:
 //   [embed | add_norm] + norm + quant -> int8 x     (e2mi_embed_norm_quant / e2mi_add_norm_quant)
 //   q|k|v int8 GEMM -> f32                          (one GEMM over the concatenated N = (H+2KV)*D)
 //   q/k/v RMSNorm + RoPE -> f16 q, k, V^T           (e2mi_qkv_norm_rope)
@@ -11,8 +11,16 @@
 //   gate|up int8 GEMM + GeGLU + quant -> int8       (e2mi_i8_gemm_geglu)
 //   down int8 GEMM -> f32
 // and after the last layer norm_add(post_ffn) + final RMSNorm, masked mean pool, L2
-// (text.c:963-981). The recorded graph is replayed for every later call of the same shape, like
-// the reference's HIP backend (forward.c:553-579).
+// (text.c:963-981). The reference checkpoint's geometry (e2_config_reference) adds:
+//   before the layers: quant(x0), the PLE model GEMM -> f32 [rows][L*P], scale + norm per slice
+//     (text.c:929-932: e2mi_quantize, e2mi_i8_gemm, e2mi_scale_norm);
+//   per layer its own head_dim / kv heads / RoPE table / window (text.c:467-478), and after the FFN
+//     norm_add(post_ffn) + quant of x itself, the PLE gate GEMM, gelu(gate) * ple slice + quant,
+//     the PLE projection GEMM, norm_add(ple_norm) * layer_scalar + the next norm + quant
+//     (text.c:906-915, 955-961: e2mi_add_norm_scale_quant, e2mi_gelu_mul_quant);
+//   after the final norm: quant + the embed_proj GEMM to out_dim, pooled (text.c:964-965).
+// The recorded graph is replayed for every later call of the same shape, like the reference's HIP
+// backend (forward.c:553-579).
 //
 // Packed batches (the default): only valid tokens are computed. Each sequence's valid tokens are
 // laid out in order from a row that is a multiple of 8, the total rounded up to a multiple of 256
@@ -41,9 +49,11 @@
 namespace e2mi {
 
 struct LayerDev {
-    e2mi_q8w qkv{}, o{}, gu{}, down{};
+    LayerGeom geo{};
+    e2mi_q8w qkv{}, o{}, gu{}, down{}, ple_gate{}, ple_proj{};
     float *ln_in = nullptr, *ln_attn = nullptr, *ln_pre = nullptr, *ln_ffn = nullptr;
-    float *q_norm = nullptr, *k_norm = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr, *ple_norm = nullptr;
+    float layer_scalar = 1.f;
 };
 
 static double now_ms() {
@@ -63,6 +73,11 @@ struct e2mi_engine {
     char devname[256] = "";
     std::vector<LayerDev> layers;
     float *embed = nullptr, *final_norm = nullptr, *cos_tab = nullptr, *sin_tab = nullptr;
+    // the reference checkpoint's extras: full-layer RoPE tables, PLE model projection and norm,
+    // embed_proj; ple32 holds the per-layer inputs [R][n_layers * ple_dim]
+    float *cos_full = nullptr, *sin_full = nullptr, *ple_proj_norm = nullptr, *ple32 = nullptr;
+    e2mi_q8w ple_model{}, embed_proj{};
+    int dout = 0;  // embedding width: out_dim, or hidden
     int R = 0;  // workspace capacity in rows (tokens)
     // activations
     float *x = nullptr, *tmp = nullptr, *qkv = nullptr, *xn = nullptr, *pool_ws = nullptr;
@@ -121,18 +136,39 @@ static int upload_f32(e2mi_engine *g, float **dst, const float *src, size_t n) {
     return check_hip(hipMemcpyAsync(*dst, src, n * 4, hipMemcpyHostToDevice, g->stream), "upload f32");
 }
 
+// one weight as it is (row-major device copy of its packed blob, per-row scales)
+static int upload_q8(e2mi_engine *g, e2mi_q8w &d, const HostQ8W *w) {
+    if (!w) {
+        set_error("create: missing int8 weight");
+        return -1;
+    }
+    memset(&d, 0, sizeof d);
+    d.N = w->N;
+    d.K = w->K;
+    d.ld = (w->K + 15) & ~15;
+    d.out_min = -1e31f;
+    d.out_max = 1e31f;
+    if (dalloc(g, &d.w, (size_t)w->N * d.ld) || dalloc(g, &d.scale, (size_t)w->N) ||
+        upload_packed_rows(d.w, d.ld, w->w, w->N, w->K, w->N, 0, 0, g->stream) ||
+        check_hip(hipMemcpyAsync(d.scale, w->scale, (size_t)w->N * 4, hipMemcpyHostToDevice, g->stream), "q8 scale"))
+        return -1;
+    return check_hip(hipStreamSynchronize(g->stream), "q8 upload sync");
+}
+
 // concatenate / interleave the reference's separate weights into the fused device operands
 static int upload_layer(e2mi_engine *g, const e2_model *m, int l, LayerDev &L) {
     const e2_config &c = g->cfg;
-    const HostQ8W *w[7];
-    for (int s = 0; s < 7; s++) {
+    const int nq8 = c.ple_dim > 0 ? 9 : 7;
+    const HostQ8W *w[9] = {};
+    for (int s = 0; s < nq8; s++) {
         w[s] = model_q8(m, layer_name(l, q8_suffix(s)));
         if (!w[s]) {
             set_error("create: layer %d: %s missing", l, q8_suffix(s));
             return -1;
         }
     }
-    const int K = c.hidden, qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    L.geo = layer_geom(c, l);
+    const int K = c.hidden, qd = c.n_heads * L.geo.D, kvd = L.geo.KV * L.geo.D;
     auto make = [&](e2mi_q8w &d, int N, int Kd) {
         memset(&d, 0, sizeof d);
         d.N = N;
@@ -176,26 +212,40 @@ static int upload_layer(e2mi_engine *g, const e2_model *m, int l, LayerDev &L) {
     }
     if (check_hip(hipMemcpyAsync(L.gu.scale, gus.data(), gus.size() * 4, hipMemcpyHostToDevice, g->stream), "gu scale"))
         return -1;
-    float **norms[6] = {&L.ln_in, &L.ln_attn, &L.ln_pre, &L.ln_ffn, &L.q_norm, &L.k_norm};
-    for (int s = 0; s < 6; s++) {
-        const size_t n = s < 4 ? (size_t)c.hidden : (size_t)c.head_dim;
+    float **norms[7] = {&L.ln_in, &L.ln_attn, &L.ln_pre, &L.ln_ffn, &L.q_norm, &L.k_norm, &L.ple_norm};
+    for (int s = 0; s < (c.ple_dim > 0 ? 7 : 6); s++) {
+        const size_t n = (s == 4 || s == 5) ? (size_t)L.geo.D : (size_t)c.hidden;
         if (upload_f32(g, norms[s], model_f32(m, layer_name(l, norm_suffix(s)), n), n)) return -1;
+    }
+    if (c.ple_dim > 0) {  // the PLE block's two GEMMs and the layer scale (text.c:906-915, 959)
+        if (upload_q8(g, L.ple_gate, w[7]) || upload_q8(g, L.ple_proj, w[8])) return -1;
+        const float *ls = model_f32(m, layer_name(l, layer_scalar_suffix()), 1);
+        if (!ls) {
+            set_error("create: layer %d: layer_scalar missing", l);
+            return -1;
+        }
+        L.layer_scalar = ls[0];
     }
     return check_hip(hipStreamSynchronize(g->stream), "layer upload sync");
 }
 
 // RoPE tables, text.c:483-506: inv = 1/theta^(2i/D), f = p * inv, duplicated over both halves
-static void rope_tables(const e2_config &c, std::vector<float> &cs, std::vector<float> &sn) {
-    const int D = c.head_dim, S = c.max_seq;
+static void rope_tables(int D, float theta, int S, std::vector<float> &cs, std::vector<float> &sn) {
     cs.resize((size_t)S * D);
     sn.resize((size_t)S * D);
     for (int p = 0; p < S; p++)
         for (int i = 0; i < D / 2; i++) {
-            const float inv = 1.0f / powf(c.rope_theta, (float)(2 * i) / (float)D);
+            const float inv = 1.0f / powf(theta, (float)(2 * i) / (float)D);
             const float f = (float)p * inv;
             cs[(size_t)p * D + i] = cs[(size_t)p * D + i + D / 2] = cosf(f);
             sn[(size_t)p * D + i] = sn[(size_t)p * D + i + D / 2] = sinf(f);
         }
+}
+
+// a geometry beyond the BASELINE one: only the packed forward implements it (window by position,
+// head_dim 512, PLE)
+static bool reference_geometry(const e2_config &c) {
+    return c.window > 0 || c.full_period > 0 || c.ple_dim > 0 || c.out_dim > 0;
 }
 
 // the shortest sequence the int8 attention takes (text.c:873-875: its blocked kernels need 32 rows)
@@ -209,8 +259,7 @@ static int work_slots(const e2mi_engine *g, int n, int M) { return g->cfg.n_head
 static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
     const e2_config &c = g->cfg;
     const bool pk = Mp > 0;
-    const int M = pk ? Mp : B * S, Dm = c.hidden, H = c.n_heads, KV = c.n_kv_heads, D = c.head_dim;
-    const int qd = H * D, F = c.ffn;
+    const int M = pk ? Mp : B * S, Dm = c.hidden, H = c.n_heads, P = c.ple_dim;
     const int nl = g->layer_limit > 0 && g->layer_limit < c.n_layers ? g->layer_limit : c.n_layers;
     const float eps = c.rms_eps;
     int k = 0;
@@ -221,23 +270,30 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
     } while (0)
     RUN(e2mi_embed_norm_quant(s, g->embed, c.vocab, g->ids, c.embed_scale, g->layers[0].ln_in, eps, M, Dm,
                               g->x, g->qa, g->as));
+    if (P > 0) {  // the per-layer inputs from the scaled embeddings (text.c:929-932)
+        const int NP = c.n_layers * P;
+        RUN(e2mi_quantize(s, g->qg, g->gs, g->x, M, Dm, Dm, 128));
+        RUN(e2mi_i8_gemm(s, g->ple32, NP, g->qg, g->gs, &g->ple_model, M, 0, NP));
+        RUN(e2mi_scale_norm(s, g->ple32, M * c.n_layers, P, c.ple_scale, g->ple_proj_norm, eps, g->ple32));
+    }
     for (int l = 0; l < nl; l++) {
         const LayerDev &L = g->layers[l];
+        const int D = L.geo.D, KV = L.geo.KV, qd = H * D;
+        const float *cs = L.geo.full ? g->cos_full : g->cos_tab, *sn = L.geo.full ? g->sin_full : g->sin_tab;
         RUN(e2mi_i8_gemm(s, g->qkv, qd + 2 * KV * D, g->qa, g->as, &L.qkv, M, 0, L.qkv.N));
         if (pk) {
-            RUN(e2mi_qkv_norm_rope_packed(s, g->qkv, M, g->pos, H, KV, D, L.q_norm, L.k_norm, eps,
-                                          g->cos_tab, g->sin_tab, g->q16, g->k16, g->vt16, g->q32,
-                                          g->k32, g->v32));
-            RUN(e2mi_attention_packed(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len, B, S, H,
-                                      KV, D, c.attn_scale, g->cq, g->cs, nullptr, g->work,
-                                      work_slots(g, B, M)));
+            RUN(e2mi_qkv_norm_rope_packed(s, g->qkv, M, g->pos, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn,
+                                          g->q16, g->k16, g->vt16, g->q32, g->k32, g->v32));
+            RUN(e2mi_attention_packed_window(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len, g->pos,
+                                             B, S, H, KV, D, c.attn_scale, L.geo.window, g->cq, g->cs,
+                                             nullptr, g->work, work_slots(g, B, M)));
             if (g->attn_i8)
                 RUN(e2mi_attention_i8_packed(s, g->q32, g->k32, g->v32, M, g->seq_start, g->seq_len, B, S,
                                              H, KV, D, g->i8ws, g->cq, g->cs, nullptr, g->work8,
                                              work_slots(g, B, M)));
         } else {
-            RUN(e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, g->cos_tab,
-                                   g->sin_tab, g->q16, g->k16, g->vt16, nullptr, nullptr, nullptr));
+            RUN(e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn, g->q16,
+                                   g->k16, g->vt16, nullptr, nullptr, nullptr));
             RUN(e2mi_attention(s, g->q16, g->k16, g->vt16, g->valid, B, S, H, KV, D, c.attn_scale,
                                g->cq, g->cs, nullptr));
         }
@@ -247,18 +303,32 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
         RUN(e2mi_i8_gemm_geglu(s, g->qg, g->gs, nullptr, g->qa, g->as, &L.gu, M));
         RUN(e2mi_i8_gemm(s, g->tmp, Dm, g->qg, g->gs, &L.down, M, 0, Dm));
         const bool last = l + 1 == nl;
-        if (!last)
-            RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, g->layers[l + 1].ln_in, eps, M, Dm,
-                                    g->x, nullptr, g->qa, g->as));
-        else
-            RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, g->final_norm, eps, M, Dm, g->x,
-                                    g->xn, nullptr, nullptr));
+        const float *gnext = last ? g->final_norm : g->layers[l + 1].ln_in;
+        if (P > 0) {
+            // post_ffn norm_add, x itself quantized for the PLE gate; the PLE block; layer scale
+            RUN(e2mi_add_norm_scale_quant(s, g->tmp, g->x, L.ln_ffn, 1.0f, nullptr, eps, M, Dm, g->x, nullptr,
+                                          g->qa, g->as));
+            RUN(e2mi_i8_gemm(s, g->qkv, P, g->qa, g->as, &L.ple_gate, M, 0, P));
+            RUN(e2mi_gelu_mul_quant(s, g->qkv, P, g->ple32 + (size_t)l * P, c.n_layers * P, M, P, g->qg, g->gs, 0));
+            RUN(e2mi_i8_gemm(s, g->tmp, Dm, g->qg, g->gs, &L.ple_proj, M, 0, Dm));
+            RUN(e2mi_add_norm_scale_quant(s, g->tmp, g->x, L.ple_norm, L.layer_scalar, gnext, eps, M, Dm, g->x,
+                                          last ? g->xn : nullptr, g->qa, g->as));
+        } else if (!last) {
+            RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, gnext, eps, M, Dm, g->x, nullptr, g->qa, g->as));
+        } else {
+            RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, gnext, eps, M, Dm, g->x, g->xn,
+                                    c.out_dim > 0 ? g->qa : nullptr, c.out_dim > 0 ? g->as : nullptr));
+        }
+    }
+    const float *rows = g->xn;
+    if (c.out_dim > 0) {  // embed_proj of the final-normed rows (text.c:964-965)
+        RUN(e2mi_i8_gemm(s, g->qkv, c.out_dim, g->qa, g->as, &g->embed_proj, M, 0, c.out_dim));
+        rows = g->qkv;
     }
     if (pk)
-        RUN(e2mi_pool_l2_packed(s, g->xn, g->seq_start, g->seq_len, B, S, Dm, g->pool_ws, g->out));
+        RUN(e2mi_pool_l2_packed(s, rows, g->seq_start, g->seq_len, B, S, g->dout, g->pool_ws, g->out));
     else
-        RUN(e2mi_pool_l2(s, g->xn, g->valid, B, S, Dm, g->pool_ws, g->out));
-    (void)F;
+        RUN(e2mi_pool_l2(s, rows, g->valid, B, S, g->dout, g->pool_ws, g->out));
 #undef RUN
     return k + 1;  // the pool is two launches
 }
@@ -410,6 +480,11 @@ static int upload_pack(e2mi_engine *g, int n, int Mp, const int32_t *host_ids, h
 // work list) are allocated the first time it is switched on
 static int set_attention_i8(e2mi_engine *g, bool on) {
     const e2_config &c = g->cfg;
+    if (on && (c.window > 0 || c.full_period > 0)) {
+        set_error("int8 attention: built for head_dim 256 without a sliding window; this model has "
+                  "windowed or head_dim-%d layers", c.full_head_dim);
+        return -1;
+    }
     if (on && c.attn_scale != 1.0f) {
         set_error("int8 attention implements the reference's attention scale 1.0 (text.c:8-9), the model has %g",
                   (double)c.attn_scale);
@@ -502,29 +577,47 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         upload_f32(g, &g->final_norm, model_f32(m, final_norm_name(), (size_t)c.hidden), (size_t)c.hidden))
         return fail();
     std::vector<float> cs, sn;
-    rope_tables(c, cs, sn);
+    rope_tables(c.head_dim, c.rope_theta, c.max_seq, cs, sn);
     if (upload_f32(g, &g->cos_tab, cs.data(), cs.size()) || upload_f32(g, &g->sin_tab, sn.data(), sn.size()))
         return fail();
-    // workspace for R rows
+    if (c.full_period > 0) {
+        rope_tables(c.full_head_dim, c.rope_theta_full, c.max_seq, cs, sn);
+        if (upload_f32(g, &g->cos_full, cs.data(), cs.size()) || upload_f32(g, &g->sin_full, sn.data(), sn.size()))
+            return fail();
+    }
+    if (c.ple_dim > 0 && (upload_q8(g, g->ple_model, model_q8(m, ple_model_name())) ||
+                          upload_f32(g, &g->ple_proj_norm, model_f32(m, ple_norm_name(), (size_t)c.ple_dim),
+                                     (size_t)c.ple_dim)))
+        return fail();
+    if (c.out_dim > 0 && upload_q8(g, g->embed_proj, model_q8(m, embed_proj_name()))) return fail();
+    g->dout = c.out_dim > 0 ? c.out_dim : c.hidden;
+    // workspace for R rows, sized for the widest layer
     const size_t R = (size_t)g->R;
-    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
-    const int kmax = c.hidden > c.ffn ? c.hidden : c.ffn;
+    int qd = 0, kvd = 0, nqkv = 0;
+    for (const LayerDev &L : g->layers) {
+        qd = std::max(qd, c.n_heads * L.geo.D);
+        kvd = std::max(kvd, L.geo.KV * L.geo.D);
+        nqkv = std::max(nqkv, (c.n_heads + 2 * L.geo.KV) * L.geo.D);
+    }
+    nqkv = std::max(nqkv, std::max(c.out_dim, c.ple_dim));  // also the PLE gate and embed_proj rows
+    const int kmax = std::max(c.hidden, c.ffn), gmax = std::max(kmax, c.ple_dim);
     g->bmax = g->R < 4096 ? g->R : 4096;
     if (dalloc(g, &g->x, R * c.hidden) || dalloc(g, &g->tmp, R * c.hidden) ||
-        dalloc(g, &g->xn, R * c.hidden) || dalloc(g, &g->qkv, R * (qd + 2 * kvd)) ||
+        dalloc(g, &g->xn, R * c.hidden) || dalloc(g, &g->qkv, R * nqkv) ||
         dalloc(g, &g->qa, R * kmax) || dalloc(g, &g->as, R * (kmax / 128)) ||
-        dalloc(g, &g->qg, R * c.ffn) || dalloc(g, &g->gs, R * (c.ffn / 128)) ||
+        dalloc(g, &g->qg, R * gmax) || dalloc(g, &g->gs, R * (gmax / 128)) ||
         dalloc(g, &g->cq, R * qd) || dalloc(g, &g->cs, R * (qd / 128)) ||
         dalloc(g, &g->q16, R * qd) || dalloc(g, &g->k16, R * kvd) || dalloc(g, &g->vt16, R * kvd) ||
-        dalloc(g, &g->ids, R) || dalloc(g, &g->valid, R) || dalloc(g, &g->out, R * c.hidden) ||
-        dalloc(g, &g->pool_ws, (R / 64 + R + 64) * (size_t)(c.hidden + 1)) ||
+        dalloc(g, &g->ids, R) || dalloc(g, &g->valid, R) || dalloc(g, &g->out, R * g->dout) ||
+        dalloc(g, &g->pool_ws, (R / 64 + R + 64) * (size_t)(g->dout + 1)) ||
+        (c.ple_dim > 0 && dalloc(g, &g->ple32, R * c.n_layers * c.ple_dim)) ||
         dalloc(g, &g->rowmap, R) || dalloc(g, &g->pos, R) || dalloc(g, &g->seq_start, (size_t)g->bmax) ||
         dalloc(g, &g->seq_len, (size_t)g->bmax) ||
         dalloc(g, &g->work, (size_t)c.n_heads * (R / 128 + g->bmax)))
         return fail();
     if (check_hip(hipHostMalloc((void **)&g->h_ids, R * 4), "pinned ids") ||
         check_hip(hipHostMalloc((void **)&g->h_valid, R), "pinned valid") ||
-        check_hip(hipHostMalloc((void **)&g->h_out, (size_t)g->bmax * c.hidden * 4), "pinned out") ||
+        check_hip(hipHostMalloc((void **)&g->h_out, (size_t)g->bmax * g->dout * 4), "pinned out") ||
         check_hip(hipHostMalloc((void **)&g->h_rowmap, R * 4), "pinned rowmap") ||
         check_hip(hipHostMalloc((void **)&g->h_pos, R * 4), "pinned pos") ||
         check_hip(hipHostMalloc((void **)&g->h_start, (size_t)g->bmax * 4), "pinned start") ||
@@ -537,6 +630,11 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         return fail();
     const char *np = getenv("E2MI_NOPACK");
     g->packed = !(np && np[0] && np[0] != '0');
+    if (!g->packed && reference_geometry(c)) {
+        set_error("create: the padded-rows forward takes the BASELINE geometry; this model (window, "
+                  "head_dim %d layers or PLE) runs packed batches only (unset E2MI_NOPACK)", c.full_head_dim);
+        return fail();
+    }
     if (ak == E2_ATTN_I8 && set_attention_i8(g, true)) return fail();
     if (check_hip(hipStreamSynchronize(g->stream), "create sync")) return fail();
     return g;
@@ -554,7 +652,7 @@ extern "C" int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const u
     }
     if (validate_batch(g, ids, batch, seq_len, true)) return -1;
     const double t0 = now_ms();
-    const int D = g->cfg.hidden;
+    const int D = g->dout;
     for (int b0 = 0; b0 < batch;) {
         const size_t off = (size_t)b0 * seq_len;
         const uint8_t *vchunk = valid ? valid + off : nullptr;
@@ -606,7 +704,7 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
         if (check_hip(hipMemcpyAsync(g->ids, ids, rows * 4, hipMemcpyDeviceToDevice, s), "ids D2D") ||
             check_hip(hipMemcpyAsync(g->valid, valid, rows, hipMemcpyDeviceToDevice, s), "valid D2D") ||
             run_shape(g, batch, seq_len, 0, s) ||
-            check_hip(hipMemcpyAsync(out, g->out, (size_t)batch * g->cfg.hidden * 4, hipMemcpyDeviceToDevice, s),
+            check_hip(hipMemcpyAsync(out, g->out, (size_t)batch * g->dout * 4, hipMemcpyDeviceToDevice, s),
                       "out D2D"))
             return -1;
     } else {
@@ -631,7 +729,7 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
             if (upload_pack(g, n, Mp, nullptr, s) ||
                 e2mi_gather_ids(s, ids + off, g->rowmap, Mp, g->ids) ||
                 run_shape(g, n, seq_len, Mp, s) ||
-                check_hip(hipMemcpyAsync(out + (size_t)b0 * g->cfg.hidden, g->out, (size_t)n * g->cfg.hidden * 4,
+                check_hip(hipMemcpyAsync(out + (size_t)b0 * g->dout, g->out, (size_t)n * g->dout * 4,
                                          hipMemcpyDeviceToDevice, s), "out D2D"))
                 return -1;
             b0 += n;
@@ -648,6 +746,10 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
 extern "C" int e2mi_set_packing(e2mi_engine *g, int on) {
     if (!g) {
         set_error("set_packing: null engine");
+        return -1;
+    }
+    if (!on && reference_geometry(g->cfg)) {
+        set_error("set_packing: this model (window, per-layer head_dim or PLE) runs packed batches only");
         return -1;
     }
     if (g->stream) (void)hipStreamSynchronize(g->stream);

@@ -36,24 +36,38 @@ std::string layer_name(int l, const char *suffix) {
 }
 static const char *kEmbed = "language_model.embed_tokens.weight";
 static const char *kFinalNorm = "language_model.norm.weight";
-static const char *kQ8Suffix[7] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight",
+// the reference checkpoint's extra tensors (e2.c:316-381)
+static const char *kPleModel = "language_model.ple.per_layer_model_projection.weight";
+static const char *kPleNorm = "language_model.ple.per_layer_projection_norm.weight";
+static const char *kEmbedProj = "language_model.embedding_projection.weight";
+static const char *kLayerScalar = "layer_scalar";
+static const char *kQ8Suffix[9] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight",
                                    "self_attn.v_proj.weight", "self_attn.o_proj.weight",
                                    "mlp.gate_proj.weight", "mlp.up_proj.weight",
-                                   "mlp.down_proj.weight"};
-static const char *kNormSuffix[6] = {"input_layernorm.weight", "post_attention_layernorm.weight",
+                                   "mlp.down_proj.weight", "ple_block.per_layer_input_gate.weight",
+                                   "ple_block.per_layer_projection.weight"};
+static const char *kNormSuffix[7] = {"input_layernorm.weight", "post_attention_layernorm.weight",
                                      "pre_feedforward_layernorm.weight",
                                      "post_feedforward_layernorm.weight", "self_attn.q_norm.weight",
-                                     "self_attn.k_norm.weight"};
+                                     "self_attn.k_norm.weight",
+                                     "ple_block.post_per_layer_input_norm.weight"};
 
-// (N, K) of weight s of a layer; norm s length
-static void q8_shape(const e2_config &c, int s, int *N, int *K) {
-    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
-    const int Ns[7] = {qd, kvd, kvd, c.hidden, c.ffn, c.ffn, c.hidden};
-    const int Ks[7] = {c.hidden, c.hidden, c.hidden, qd, c.hidden, c.hidden, c.ffn};
+// int8 weights and norms of layer l: 7 without PLE, 9 with; 6 norms without, 7 with
+static int n_q8(const e2_config &c) { return c.ple_dim > 0 ? 9 : 7; }
+static int n_norm(const e2_config &c) { return c.ple_dim > 0 ? 7 : 6; }
+
+// (N, K) of weight s of layer l; norm s length
+static void q8_shape(const e2_config &c, int l, int s, int *N, int *K) {
+    const LayerGeom g = layer_geom(c, l);
+    const int qd = c.n_heads * g.D, kvd = g.KV * g.D;
+    const int Ns[9] = {qd, kvd, kvd, c.hidden, c.ffn, c.ffn, c.hidden, c.ple_dim, c.hidden};
+    const int Ks[9] = {c.hidden, c.hidden, c.hidden, qd, c.hidden, c.hidden, c.ffn, c.hidden, c.ple_dim};
     *N = Ns[s];
     *K = Ks[s];
 }
-static int norm_len(const e2_config &c, int s) { return s < 4 ? c.hidden : c.head_dim; }
+static int norm_len(const e2_config &c, int l, int s) {
+    return (s == 4 || s == 5) ? layer_geom(c, l).D : c.hidden;
+}
 
 // ------------------------------------------------------------------ packing (int8.h:14-22)
 static void pack_rows(const int8_t *rm, int N, int K, HostQ8W &q) {
@@ -139,6 +153,16 @@ static bool config_ok(const e2_config &c) {
         (c.n_heads * c.head_dim) % 128) {
         set_error("config: unsupported geometry (hidden/ffn multiples of 128, hidden <= 1280, "
                   "head_dim 256, H %% KV == 0, 1 <= max_seq <= 2048)");
+        return false;
+    }
+    if (c.ple_dim < 0 || c.ple_dim % 128 || c.ple_dim > 1280 || c.out_dim < 0 || c.out_dim % 128 ||
+        c.out_dim > 1280 || c.window < 0 || c.full_period < 0 || (long)c.n_layers * c.ple_dim > (1 << 20) ||
+        (c.full_period > 0 && (c.full_kv_heads <= 0 || c.n_heads % c.full_kv_heads ||
+                               (c.full_head_dim != 256 && c.full_head_dim != 512) ||
+                               !(c.rope_theta_full > 0.f))) ||
+        (c.ple_dim > 0 && !(c.ple_scale > 0.f))) {
+        set_error("config: unsupported extras (ple_dim/out_dim multiples of 128 up to 1280, "
+                  "window >= 0, full layers with head_dim 256 or 512 and H %% kv == 0)");
         return false;
     }
     return true;
@@ -227,6 +251,7 @@ extern "C" const char *e2_last_error(void) { return e2mi_last_error(); }
 
 extern "C" void e2_config_baseline(e2_config *c) {
     if (!c) return;
+    memset(c, 0, sizeof *c);
     c->n_layers = 24;
     c->hidden = 768;
     c->ffn = 1152;
@@ -239,6 +264,31 @@ extern "C" void e2_config_baseline(e2_config *c) {
     c->rope_theta = 10000.0f;
     c->embed_scale = sqrtf(768.0f);
     c->attn_scale = 1.0f;
+}
+
+extern "C" void e2_config_reference(e2_config *c) {
+    if (!c) return;
+    memset(c, 0, sizeof *c);
+    c->n_layers = 24;
+    c->hidden = 512;
+    c->ffn = 2048;
+    c->n_heads = 4;
+    c->n_kv_heads = 2;
+    c->head_dim = 256;
+    c->vocab = 262144;
+    c->max_seq = 2048;
+    c->rms_eps = 1e-6f;
+    c->rope_theta = 10000.0f;
+    c->embed_scale = sqrtf(512.0f);
+    c->attn_scale = 1.0f;
+    c->ple_dim = 512;
+    c->out_dim = 768;
+    c->window = 512;
+    c->full_period = 6;
+    c->full_head_dim = 512;
+    c->full_kv_heads = 1;
+    c->rope_theta_full = 1000000.0f;
+    c->ple_scale = 1.0f / sqrtf(512.0f);
 }
 
 extern "C" e2_model *e2_model_synthetic(const e2_config *c, uint64_t seed) {
@@ -259,12 +309,29 @@ extern "C" e2_model *e2_model_synthetic(const e2_config *c, uint64_t seed) {
         for (int l = 0; l < c->n_layers; l++) {
             for (int s = 0; s < 7; s++) {
                 int N, K;
-                q8_shape(*c, s, &N, &K);
+                q8_shape(*c, l, s, &N, &K);
                 synth_q8(m->q8[layer_name(l, kQ8Suffix[s])], N, K, seed, t++);
             }
             for (int s = 0; s < 6; s++)
-                synth_f32(m->f32[layer_name(l, kNormSuffix[s])], 1, norm_len(*c, s), 1.0, 0.05, seed, t++);
+                synth_f32(m->f32[layer_name(l, kNormSuffix[s])], 1, norm_len(*c, l, s), 1.0, 0.05, seed, t++);
         }
+        // the reference geometry's extras draw from their own streams, so the BASELINE tensors
+        // are the same whichever geometry fields are set
+        int te = 1 << 20;
+        if (c->ple_dim > 0) {
+            synth_q8(m->q8[kPleModel], c->n_layers * c->ple_dim, c->hidden, seed, te++);
+            synth_f32(m->f32[kPleNorm], 1, c->ple_dim, 1.0, 0.05, seed, te++);
+            for (int l = 0; l < c->n_layers; l++) {
+                for (int s = 7; s < 9; s++) {
+                    int N, K;
+                    q8_shape(*c, l, s, &N, &K);
+                    synth_q8(m->q8[layer_name(l, kQ8Suffix[s])], N, K, seed, te++);
+                }
+                synth_f32(m->f32[layer_name(l, kNormSuffix[6])], 1, c->hidden, 1.0, 0.05, seed, te++);
+                synth_f32(m->f32[layer_name(l, kLayerScalar)], 1, 1, 1.0, 0.05, seed, te++);
+            }
+        }
+        if (c->out_dim > 0) synth_q8(m->q8[kEmbedProj], c->out_dim, c->hidden, seed, te++);
     } catch (...) {
         delete m;
         set_error("oom: synthetic weights");
@@ -489,20 +556,29 @@ extern "C" e2_model *e2_load_e8cq(const char *path, const e2_config *c) {
         }
         return true;
     };
+    auto need_q8 = [&](const std::string &name, int N, int K) {
+        auto it = m->q8.find(name);
+        if (it == m->q8.end() || it->second.N != N || it->second.K != K) {
+            set_error("%s: %s missing or mis-shaped", path, name.c_str());
+            return false;
+        }
+        return true;
+    };
     if (!need_f32(kEmbed, (size_t)cf.vocab * cf.hidden) || !need_f32(kFinalNorm, (size_t)cf.hidden))
         return fail();
+    if (cf.ple_dim > 0 && (!need_q8(kPleModel, cf.n_layers * cf.ple_dim, cf.hidden) ||
+                           !need_f32(kPleNorm, (size_t)cf.ple_dim)))
+        return fail();
+    if (cf.out_dim > 0 && !need_q8(kEmbedProj, cf.out_dim, cf.hidden)) return fail();
     for (int l = 0; l < cf.n_layers; l++) {
-        for (int s = 0; s < 7; s++) {
+        for (int s = 0; s < n_q8(cf); s++) {
             int N, K;
-            q8_shape(cf, s, &N, &K);
-            auto it = m->q8.find(layer_name(l, kQ8Suffix[s]));
-            if (it == m->q8.end() || it->second.N != N || it->second.K != K) {
-                set_error("%s: %s missing or mis-shaped", path, layer_name(l, kQ8Suffix[s]).c_str());
-                return fail();
-            }
+            q8_shape(cf, l, s, &N, &K);
+            if (!need_q8(layer_name(l, kQ8Suffix[s]), N, K)) return fail();
         }
-        for (int s = 0; s < 6; s++)
-            if (!need_f32(layer_name(l, kNormSuffix[s]), (size_t)norm_len(cf, s))) return fail();
+        for (int s = 0; s < n_norm(cf); s++)
+            if (!need_f32(layer_name(l, kNormSuffix[s]), (size_t)norm_len(cf, l, s))) return fail();
+        if (cf.ple_dim > 0 && !need_f32(layer_name(l, kLayerScalar), 1)) return fail();
     }
     return m;
 }
@@ -521,4 +597,8 @@ const char *q8_suffix(int s) { return kQ8Suffix[s]; }
 const char *norm_suffix(int s) { return kNormSuffix[s]; }
 const char *embed_name() { return kEmbed; }
 const char *final_norm_name() { return kFinalNorm; }
+const char *ple_model_name() { return kPleModel; }
+const char *ple_norm_name() { return kPleNorm; }
+const char *embed_proj_name() { return kEmbedProj; }
+const char *layer_scalar_suffix() { return kLayerScalar; }
 }  // namespace e2mi

@@ -34,13 +34,36 @@ struct F32T {
     }
 };
 
+// geometry of layer l (text.c:467-478): head_dim, kv heads, RoPE theta, window (0 = none), and
+// whether it is a full-attention layer (layers l % full_period == full_period - 1)
+struct LayerGeom {
+    int D, KV, window;
+    float theta;
+    bool full;
+};
+inline LayerGeom layer_geom(const e2_config &c, int l) {
+    const bool full = c.full_period > 0 && l % c.full_period == c.full_period - 1;
+    LayerGeom g;
+    g.full = full;
+    g.D = full ? c.full_head_dim : c.head_dim;
+    g.KV = full ? c.full_kv_heads : c.n_kv_heads;
+    g.theta = full ? c.rope_theta_full : c.rope_theta;
+    g.window = full ? 0 : c.window;
+    return g;
+}
+
 std::string layer_name(int l, const char *suffix);
 const HostQ8W *model_q8(const e2_model *m, const std::string &name);
 const float *model_f32(const e2_model *m, const std::string &name, size_t count);
-const char *q8_suffix(int s);    // 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down
-const char *norm_suffix(int s);  // 0 input, 1 post_attn, 2 pre_ffn, 3 post_ffn, 4 q_norm, 5 k_norm
+const char *q8_suffix(int s);    // 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down, 7 ple gate, 8 ple proj
+const char *norm_suffix(int s);  // 0 input, 1 post_attn, 2 pre_ffn, 3 post_ffn, 4 q_norm, 5 k_norm,
+                                 // 6 ple norm
 const char *embed_name();
 const char *final_norm_name();
+const char *ple_model_name();
+const char *ple_norm_name();
+const char *embed_proj_name();
+const char *layer_scalar_suffix();
 
 // weights.hip: unpack a packed [Npad/8][K/4][8][4] blob into dst rows (n / grp) * gstride + goff +
 // n % grp of a row-major [*][ld] device matrix

@@ -32,9 +32,11 @@ struct RowArgs {
     float eps;
     float *x_out;          // new residual stream x (may alias res), or NULL
     float *xn_out;         // normed rows (f32), or NULL
-    int8_t *q;             // quantized normed rows [M][D], or NULL
+    int8_t *q;             // quantized rows [M][D] (normed; the rows themselves if gamma_n is NULL), or NULL
     float *qs;             // their per-128 scales [M][D/128]
     int M, D;
+    float pre_scale = 1.f;   // PLAIN: rows scaled before the norm (the PLE inputs, text.c:930-931)
+    float post_scale = 1.f;  // ADDNORM: x scaled after the add (layer_scalar, text.c:959)
 };
 
 __device__ inline float4 ld4(const float *p) { return *(const float4 *)p; }
@@ -67,13 +69,14 @@ __global__ __launch_bounds__(256) void k_rows(RowArgs a) {
         escale = a.embed_scale;
     } else {
         row = a.src + (size_t)m * D;
+        if (MODE == ROW_PLAIN) escale = a.pre_scale;
     }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NC; i++) {
         const int c = l + 64 * i;
         v[i] = c < nch ? ld4(row + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (MODE == ROW_EMBED)
+        if (MODE == ROW_EMBED || (MODE == ROW_PLAIN && escale != 1.f))
             v[i] = make_float4(__fmul_rn(v[i].x, escale), __fmul_rn(v[i].y, escale),
                                __fmul_rn(v[i].z, escale), __fmul_rn(v[i].w, escale));
         ss += sumsq4(v[i]);
@@ -89,6 +92,9 @@ __global__ __launch_bounds__(256) void k_rows(RowArgs a) {
                 const float4 g = ld4(a.gamma_a + 4 * c), r = ld4(a.res + (size_t)m * D + 4 * c);
                 const float4 t = scale4(v[i], inv, g);
                 v[i] = make_float4(t.x + r.x, t.y + r.y, t.z + r.z, t.w + r.w);
+                if (a.post_scale != 1.f)
+                    v[i] = make_float4(__fmul_rn(v[i].x, a.post_scale), __fmul_rn(v[i].y, a.post_scale),
+                                       __fmul_rn(v[i].z, a.post_scale), __fmul_rn(v[i].w, a.post_scale));
             }
             ss += sumsq4(v[i]);
         }
@@ -98,13 +104,14 @@ __global__ __launch_bounds__(256) void k_rows(RowArgs a) {
         for (int i = 0; i < NC; i++)
             if (l + 64 * i < nch) st4(a.x_out + (size_t)m * D + 4 * (l + 64 * i), v[i]);
     }
-    if (!a.gamma_n) return;
-    const float inv = rms_inv(group_sum<64>(ss), D, a.eps);
+    if (a.gamma_n) {
+        const float inv = rms_inv(group_sum<64>(ss), D, a.eps);
 #pragma unroll
-    for (int i = 0; i < NC; i++) {
-        const int c = l + 64 * i;
-        if (c < nch) v[i] = scale4(v[i], inv, ld4(a.gamma_n + 4 * c));
-        if (a.xn_out && c < nch) st4(a.xn_out + (size_t)m * D + 4 * c, v[i]);
+        for (int i = 0; i < NC; i++) {
+            const int c = l + 64 * i;
+            if (c < nch) v[i] = scale4(v[i], inv, ld4(a.gamma_n + 4 * c));
+            if (a.xn_out && c < nch) st4(a.xn_out + (size_t)m * D + 4 * c, v[i]);
+        }
     }
     if (!a.q) return;
     const int nb = D / kQBlock;
@@ -146,12 +153,26 @@ __device__ inline uint16_t f2h(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
+// a' = a c - y s and y' = y c + a s, each product rounded, then the sum (kernels.c:112-126)
+__device__ inline float4 rot_lo(float4 a, float4 y, float4 c, float4 s) {
+    return make_float4(__fmul_rn(a.x, c.x) - __fmul_rn(y.x, s.x), __fmul_rn(a.y, c.y) - __fmul_rn(y.y, s.y),
+                       __fmul_rn(a.z, c.z) - __fmul_rn(y.z, s.z), __fmul_rn(a.w, c.w) - __fmul_rn(y.w, s.w));
+}
+__device__ inline float4 rot_hi(float4 y, float4 a, float4 c, float4 s) {
+    return make_float4(__fmul_rn(y.x, c.x) + __fmul_rn(a.x, s.x), __fmul_rn(y.y, c.y) + __fmul_rn(a.y, s.y),
+                       __fmul_rn(y.z, c.z) + __fmul_rn(a.z, s.z), __fmul_rn(y.w, c.w) + __fmul_rn(a.w, s.w));
+}
+
 // The first nv blocks take the v heads, 32 rows each (one block per kv head and row block), and
 // write V^T through LDS so that each d row of V^T gets 64 contiguous bytes instead of one 2-byte
 // store per (row, d); they come first so that their longer chains overlap the q/k blocks. The other
-// blocks take the q and k heads, one wave per (row, head).
+// blocks take the q and k heads, one wave per (row, head). D = 256 or 512 (the reference
+// checkpoint's full-attention layers): a lane holds D/256 float4 of a row, chunk c covering
+// elements 4 (l + 64 c) .. +3; the rotate-half partner of element e is e + D/2, in lane l ^ 32 at
+// D = 256 and in the lane's other chunk at D = 512.
+template <int D>
 __global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a, int nv) {
-    constexpr int D = 256, VR = 32;
+    constexpr int VR = 32, NCH = D / 256;
     const int heads = a.H + 2 * a.KV;
     const int l = threadIdx.x & 63;
     if ((int)blockIdx.x < nv) {
@@ -162,40 +183,56 @@ __global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a, int nv) {
         // wave w: rows 8 w .. 8 w + 7, four at a time (independent loads in flight)
 #pragma unroll
         for (int r0 = 8 * w; r0 < 8 * w + 8; r0 += 4) {
-            float4 v[4];
+            float4 v[4][NCH];
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                v[j] = m0 + r0 + j < a.M ? ld4(a.qkv + (size_t)(m0 + r0 + j) * heads * D + h * D + 4 * l)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int c = 0; c < NCH; c++)
+                    v[j][c] = m0 + r0 + j < a.M
+                                  ? ld4(a.qkv + (size_t)(m0 + r0 + j) * heads * D + h * D + 4 * (l + 64 * c))
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float inv = rms_inv(group_sum<64>(sumsq4(v[j])), D, a.eps);
-                const float4 x = make_float4(__fmul_rn(v[j].x, inv), __fmul_rn(v[j].y, inv),
-                                             __fmul_rn(v[j].z, inv), __fmul_rn(v[j].w, inv));
-                const uint32_t lo = (uint32_t)f2h(x.x) | ((uint32_t)f2h(x.y) << 16);
-                const uint32_t hi = (uint32_t)f2h(x.z) | ((uint32_t)f2h(x.w) << 16);
-                *(uint2 *)(vbuf + (r0 + j) * D + 4 * l) = make_uint2(lo, hi);
-                if (a.v32 && m0 + r0 + j < a.M) st4(a.v32 + (size_t)(m0 + r0 + j) * a.KV * D + vh * D + 4 * l, x);
+                float ss = 0.f;
+#pragma unroll
+                for (int c = 0; c < NCH; c++) ss += sumsq4(v[j][c]);
+                const float inv = rms_inv(group_sum<64>(ss), D, a.eps);
+#pragma unroll
+                for (int c = 0; c < NCH; c++) {
+                    const int e = 4 * (l + 64 * c);
+                    const float4 x = make_float4(__fmul_rn(v[j][c].x, inv), __fmul_rn(v[j][c].y, inv),
+                                                 __fmul_rn(v[j][c].z, inv), __fmul_rn(v[j][c].w, inv));
+                    const uint32_t lo = (uint32_t)f2h(x.x) | ((uint32_t)f2h(x.y) << 16);
+                    const uint32_t hi = (uint32_t)f2h(x.z) | ((uint32_t)f2h(x.w) << 16);
+                    *(uint2 *)(vbuf + (r0 + j) * D + e) = make_uint2(lo, hi);
+                    if (a.v32 && m0 + r0 + j < a.M) st4(a.v32 + (size_t)(m0 + r0 + j) * a.KV * D + vh * D + e, x);
+                }
             }
         }
         __syncthreads();
-        // thread d writes V^T row d for the block's rows: [B][KV][D][S], row m at (m / S, m % S)
-        const int d = threadIdx.x, nr = min(VR, a.M - m0);
+        // thread t writes V^T rows d = t + 256 c for the block's rows: [B][KV][D][S], row m at
+        // (m / S, m % S)
+        const int nr = min(VR, a.M - m0);
         const int b0 = m0 / a.S, p0 = m0 % a.S;
-        uint16_t *dst = a.vt16 + ((size_t)(b0 * a.KV + vh) * D + d) * a.S + p0;
-        if (nr == VR && p0 + VR <= a.S && ((uintptr_t)dst & 15) == 0) {
 #pragma unroll
-            for (int c = 0; c < VR / 8; c++) {
-                uint32_t wv[4];
+        for (int c = 0; c < NCH; c++) {
+            const int d = threadIdx.x + 256 * c;
+            uint16_t *dst = a.vt16 + ((size_t)(b0 * a.KV + vh) * D + d) * a.S + p0;
+            if (nr == VR && p0 + VR <= a.S && ((uintptr_t)dst & 15) == 0) {
 #pragma unroll
-                for (int k = 0; k < 4; k++)
-                    wv[k] = (uint32_t)vbuf[(8 * c + 2 * k) * D + d] | ((uint32_t)vbuf[(8 * c + 2 * k + 1) * D + d] << 16);
-                *(uint4 *)(dst + 8 * c) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-            }
-        } else {
-            for (int r = 0; r < nr; r++) {
-                const int m = m0 + r, b = m / a.S, p = m % a.S;
-                a.vt16[((size_t)(b * a.KV + vh) * D + d) * a.S + p] = vbuf[r * D + d];
+                for (int k8 = 0; k8 < VR / 8; k8++) {
+                    uint32_t wv[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        wv[k] = (uint32_t)vbuf[(8 * k8 + 2 * k) * D + d] |
+                                ((uint32_t)vbuf[(8 * k8 + 2 * k + 1) * D + d] << 16);
+                    *(uint4 *)(dst + 8 * k8) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+                }
+            } else {
+                for (int r = 0; r < nr; r++) {
+                    const int m = m0 + r, b = m / a.S, p = m % a.S;
+                    a.vt16[((size_t)(b * a.KV + vh) * D + d) * a.S + p] = vbuf[r * D + d];
+                }
             }
         }
         return;
@@ -205,32 +242,46 @@ __global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a, int nv) {
     if (item >= (long)a.M * qkh) return;
     const int m = (int)(item / qkh), h = (int)(item % qkh);
     const int kind = h < a.H ? 0 : 1;  // q, k
-    float4 v = ld4(a.qkv + (size_t)m * heads * D + h * D + 4 * l);
-    const float inv = rms_inv(group_sum<64>(sumsq4(v)), D, a.eps);
-    {
-        v = scale4(v, inv, ld4((kind == 0 ? a.q_gamma : a.k_gamma) + 4 * l));
-        // rotate-half: lane l < 32 holds a = x[i], lane l + 32 holds y = x[i + 128]
-        const int pos = a.pos ? a.pos[m] : m % a.S;
-        const float4 c = ld4(a.cs + (size_t)pos * D + 4 * l), s = ld4(a.sn + (size_t)pos * D + 4 * l);
-        const float4 o = make_float4(__shfl_xor(v.x, 32), __shfl_xor(v.y, 32), __shfl_xor(v.z, 32),
-                                     __shfl_xor(v.w, 32));
-        if (l < 32) {  // a' = a c - y s
-            v = make_float4(__fmul_rn(v.x, c.x) - __fmul_rn(o.x, s.x), __fmul_rn(v.y, c.y) - __fmul_rn(o.y, s.y),
-                            __fmul_rn(v.z, c.z) - __fmul_rn(o.z, s.z), __fmul_rn(v.w, c.w) - __fmul_rn(o.w, s.w));
-        } else {       // y' = y c + a s
-            v = make_float4(__fmul_rn(v.x, c.x) + __fmul_rn(o.x, s.x), __fmul_rn(v.y, c.y) + __fmul_rn(o.y, s.y),
-                            __fmul_rn(v.z, c.z) + __fmul_rn(o.z, s.z), __fmul_rn(v.w, c.w) + __fmul_rn(o.w, s.w));
-        }
+    const float *src = a.qkv + (size_t)m * heads * D + h * D;
+    float4 v[NCH];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        v[c] = ld4(src + 4 * (l + 64 * c));
+        ss += sumsq4(v[c]);
     }
-    const uint32_t lo = (uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16);
-    const uint32_t hi = (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16);
-    if (kind == 0) {
-        *(uint2 *)(a.q16 + (size_t)m * a.H * D + h * D + 4 * l) = make_uint2(lo, hi);
-        if (a.q32) st4(a.q32 + (size_t)m * a.H * D + h * D + 4 * l, v);
+    const float inv = rms_inv(group_sum<64>(ss), D, a.eps);
+    const float *gam = kind == 0 ? a.q_gamma : a.k_gamma;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) v[c] = scale4(v[c], inv, ld4(gam + 4 * (l + 64 * c)));
+    // rotate-half (kernels.c:112-126): a' = a c - y s for the first half, y' = y c + a s for the
+    // second, with a = x[i], y = x[i + D/2] and c, s the angle of i (duplicated at i + D/2)
+    const int pos = a.pos ? a.pos[m] : m % a.S;
+    const float *cp = a.cs + (size_t)pos * D, *sp = a.sn + (size_t)pos * D;
+    if (NCH == 1) {
+        const float4 c = ld4(cp + 4 * l), s = ld4(sp + 4 * l);
+        const float4 o = make_float4(__shfl_xor(v[0].x, 32), __shfl_xor(v[0].y, 32), __shfl_xor(v[0].z, 32),
+                                     __shfl_xor(v[0].w, 32));
+        v[0] = l < 32 ? rot_lo(v[0], o, c, s) : rot_hi(v[0], o, c, s);
     } else {
-        const int kh = h - a.H;
-        *(uint2 *)(a.k16 + (size_t)m * a.KV * D + kh * D + 4 * l) = make_uint2(lo, hi);
-        if (a.k32) st4(a.k32 + (size_t)m * a.KV * D + kh * D + 4 * l, v);
+        const float4 c = ld4(cp + 4 * l), s = ld4(sp + 4 * l);
+        const float4 x0 = v[0], x1 = v[NCH - 1];
+        v[0] = rot_lo(x0, x1, c, s);
+        v[NCH - 1] = rot_hi(x1, x0, c, s);
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int e = 4 * (l + 64 * c);
+        const uint32_t lo = (uint32_t)f2h(v[c].x) | ((uint32_t)f2h(v[c].y) << 16);
+        const uint32_t hi = (uint32_t)f2h(v[c].z) | ((uint32_t)f2h(v[c].w) << 16);
+        if (kind == 0) {
+            *(uint2 *)(a.q16 + (size_t)m * a.H * D + h * D + e) = make_uint2(lo, hi);
+            if (a.q32) st4(a.q32 + (size_t)m * a.H * D + h * D + e, v[c]);
+        } else {
+            const int kh = h - a.H;
+            *(uint2 *)(a.k16 + (size_t)m * a.KV * D + kh * D + e) = make_uint2(lo, hi);
+            if (a.k32) st4(a.k32 + (size_t)m * a.KV * D + kh * D + e, v[c]);
+        }
     }
 }
 
@@ -371,14 +422,17 @@ static int row_launch(hipStream_t s, int mode, const RowArgs &a) {
 
 int launch_rows(hipStream_t s, int mode, const RowArgs &a) { return row_launch(s, mode, a); }
 
-int launch_qkv_norm_rope(hipStream_t s, const QkvArgs &a) {
+int launch_qkv_norm_rope(hipStream_t s, const QkvArgs &a, int D) {
     const long nqk = ((long)a.M * (a.H + a.KV) + 3) / 4;
     const long nv = (long)a.KV * ((a.M + 31) / 32);
     if (nqk + nv > 0x7fffffffL) {
         set_error("qkv_norm_rope: too many rows");
         return -1;
     }
-    hipLaunchKernelGGL(k_qkv_norm_rope, dim3((unsigned)(nqk + nv)), dim3(256), 0, s, a, (int)nv);
+    if (D == 512)
+        hipLaunchKernelGGL(k_qkv_norm_rope<512>, dim3((unsigned)(nqk + nv)), dim3(256), 0, s, a, (int)nv);
+    else
+        hipLaunchKernelGGL(k_qkv_norm_rope<256>, dim3((unsigned)(nqk + nv)), dim3(256), 0, s, a, (int)nv);
     return check_hip(hipGetLastError(), "qkv_norm_rope launch");
 }
 
@@ -432,6 +486,32 @@ extern "C" int e2mi_add_norm_quant(e2mi_stream stream, const float *src, const f
     return launch_rows((hipStream_t)stream, ROW_ADDNORM, a);
 }
 
+extern "C" int e2mi_add_norm_scale_quant(e2mi_stream stream, const float *src, const float *res,
+                                         const float *gamma_add, float post_scale, const float *gamma_next,
+                                         float eps, int M, int D, float *x_out, float *xn_out, int8_t *q,
+                                         float *qs) {
+    if (!src || !res || !gamma_add || !al16(src) || !al16(res) || !al16(x_out) || !al16(xn_out) ||
+        (xn_out && !gamma_next) || (!q) != (!qs)) {
+        set_error("add_norm_scale_quant: null/misaligned pointer, or normed output without gamma_next");
+        return -1;
+    }
+    RowArgs a = {};
+    a.src = src; a.res = res; a.gamma_a = gamma_add; a.gamma_n = gamma_next; a.eps = eps;
+    a.x_out = x_out; a.xn_out = xn_out; a.q = q; a.qs = qs; a.M = M; a.D = D; a.post_scale = post_scale;
+    return launch_rows((hipStream_t)stream, ROW_ADDNORM, a);
+}
+
+extern "C" int e2mi_scale_norm(e2mi_stream stream, const float *x, int rows, int D, float pre_scale,
+                               const float *gamma, float eps, float *out) {
+    if (!x || !gamma || !out || !al16(x) || !al16(out) || !al16(gamma) || rows <= 0) {
+        set_error("scale_norm: null/misaligned pointer or rows <= 0");
+        return -1;
+    }
+    RowArgs a = {};
+    a.src = x; a.gamma_n = gamma; a.eps = eps; a.xn_out = out; a.M = rows; a.D = D; a.pre_scale = pre_scale;
+    return launch_rows((hipStream_t)stream, ROW_PLAIN, a);
+}
+
 extern "C" int e2mi_embed_norm_quant(e2mi_stream stream, const float *table, int vocab,
                                      const int32_t *ids, float embed_scale, const float *gamma, float eps, int M, int D,
                                      float *x_out, int8_t *q, float *qs) {
@@ -462,7 +542,7 @@ extern "C" int e2mi_qkv_norm_rope(e2mi_stream stream, const float *qkv, int M, i
         return -1;
     }
     QkvArgs a = {qkv, q_gamma, k_gamma, cos_tab, sin_tab, eps, q16, k16, vt16, q32, k32, v32, nullptr, M, S, H, KV};
-    return launch_qkv_norm_rope((hipStream_t)stream, a);
+    return launch_qkv_norm_rope((hipStream_t)stream, a, D);
 }
 
 extern "C" int e2mi_qkv_norm_rope_packed(e2mi_stream stream, const float *qkv, int M, const int32_t *pos,
@@ -470,9 +550,9 @@ extern "C" int e2mi_qkv_norm_rope_packed(e2mi_stream stream, const float *qkv, i
                                          float eps, const float *cos_tab, const float *sin_tab,
                                          uint16_t *q16, uint16_t *k16, uint16_t *vt16, float *q32,
                                          float *k32, float *v32) {
-    if (D != 256 || H <= 0 || KV <= 0 || H % KV || M <= 0) {
-        set_error("qkv_norm_rope_packed: needs head_dim 256 and H %% KV == 0 (M=%d H=%d KV=%d D=%d)", M, H,
-                  KV, D);
+    if ((D != 256 && D != 512) || H <= 0 || KV <= 0 || H % KV || M <= 0) {
+        set_error("qkv_norm_rope_packed: needs head_dim 256 or 512 and H %% KV == 0 (M=%d H=%d KV=%d D=%d)", M,
+                  H, KV, D);
         return -1;
     }
     if (!qkv || !pos || !q_gamma || !k_gamma || !cos_tab || !sin_tab || !q16 || !k16 || !vt16 ||
@@ -482,7 +562,7 @@ extern "C" int e2mi_qkv_norm_rope_packed(e2mi_stream stream, const float *qkv, i
         return -1;
     }
     QkvArgs a = {qkv, q_gamma, k_gamma, cos_tab, sin_tab, eps, q16, k16, vt16, q32, k32, v32, pos, M, M, H, KV};
-    return launch_qkv_norm_rope((hipStream_t)stream, a);
+    return launch_qkv_norm_rope((hipStream_t)stream, a, D);
 }
 
 extern "C" int e2mi_gelu_mul_quant(e2mi_stream stream, float *gate, int ldg, const float *up,

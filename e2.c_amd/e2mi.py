@@ -26,7 +26,16 @@ class E2Config(C.Structure):
     """e2_config (include/e2.h)."""
     _fields_ = [("n_layers", _I), ("hidden", _I), ("ffn", _I), ("n_heads", _I),
                 ("n_kv_heads", _I), ("head_dim", _I), ("vocab", _I), ("max_seq", _I),
-                ("rms_eps", _F), ("rope_theta", _F), ("embed_scale", _F), ("attn_scale", _F)]
+                ("rms_eps", _F), ("rope_theta", _F), ("embed_scale", _F), ("attn_scale", _F),
+                ("ple_dim", _I), ("out_dim", _I), ("window", _I), ("full_period", _I),
+                ("full_head_dim", _I), ("full_kv_heads", _I), ("rope_theta_full", _F), ("ple_scale", _F)]
+
+    def layer_geom(self, l):
+        """(head_dim, kv heads, RoPE theta, window) of layer l (text.c:467-478)."""
+        full = self.full_period > 0 and l % self.full_period == self.full_period - 1
+        if full:
+            return self.full_head_dim, self.full_kv_heads, self.rope_theta_full, 0
+        return self.head_dim, self.n_kv_heads, self.rope_theta, self.window
 
 
 class TensorView(C.Structure):
@@ -61,6 +70,10 @@ SIGNATURES = {
     "e2mi_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
     "e2mi_qkv_norm_rope_packed": (_I, [_P, _P, _I, _P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P]),
     "e2mi_attention_packed": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _I]),
+    "e2mi_attention_packed_window": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P,
+                                          _P, _I]),
+    "e2mi_add_norm_scale_quant": (_I, [_P, _P, _P, _P, _F, _P, _F, _I, _I, _P, _P, _P, _P]),
+    "e2mi_scale_norm": (_I, [_P, _P, _I, _I, _F, _P, _F, _P]),
     "e2mi_attention_i8_workspace_bytes": (C.c_size_t, [_I, _I, _I, _I, _I]),
     "e2mi_attention_i8_packed": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I]),
     "e2mi_pool_l2_packed": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
@@ -77,6 +90,7 @@ SIGNATURES = {
     "e2_attn_pick": (_I, [_I, _I, _I]),
     # model container (include/e2.h)
     "e2_config_baseline": (None, [C.POINTER(E2Config)]),
+    "e2_config_reference": (None, [C.POINTER(E2Config)]),
     "e2_model_synthetic": (_P, [C.POINTER(E2Config), C.c_uint64]),
     "e2_load_e8cq": (_P, [C.c_char_p, C.POINTER(E2Config)]),
     "e2_save_e8cq": (_I, [_P, C.c_char_p]),
@@ -402,10 +416,9 @@ def pack_plan(valid):
 
 
 def qkv_norm_rope_packed(qkv, pos, H, KV, q_gamma, k_gamma, cos_tab, sin_tab, eps=1e-6,
-                         want_f32=True, stream=None):
+                         want_f32=True, stream=None, D=256):
     import torch
     M = qkv.shape[0]
-    D = 256
     dev = qkv.device
     q16 = torch.empty((M, H * D), dtype=torch.float16, device=dev)
     k16 = torch.empty((M, KV * D), dtype=torch.float16, device=dev)
@@ -443,6 +456,51 @@ def attention_packed(q16, k16, vt16, start, lens, max_len, H, KV, scale=1.0, wan
                                        scale, ptr(cq), ptr(cs), ptr(c32), ptr(work),
                                        0 if work is None else work.shape[0]), "attention_packed")
     return cq, cs, c32
+
+
+def attention_packed_window(q16, k16, vt16, start, lens, max_len, H, KV, D, window=0, pos=None,
+                            scale=1.0, want_f32=True, cq=None, cs=None, c32=None, work=None, stream=None):
+    """Packed attention at head_dim 256 or 512 with the sliding window of text.c:542-546 (keys with
+    |pos_i - pos_j| <= window; pos None: the packed index); returns (cq, cs, c32)."""
+    import torch
+    M = q16.shape[0]
+    dev = q16.device
+    cq = torch.zeros((M, H * D), dtype=torch.int8, device=dev) if cq is None else cq
+    cs = torch.zeros((M, H * D // 128), dtype=torch.float32, device=dev) if cs is None else cs
+    if want_f32 and c32 is None:
+        c32 = torch.zeros((M, H * D), dtype=torch.float32, device=dev)
+    check(load().e2mi_attention_packed_window(stream_ptr(stream), ptr(q16), ptr(k16), ptr(vt16), M,
+                                              ptr(start), ptr(lens), ptr(pos), start.shape[0], max_len,
+                                              H, KV, D, scale, window, ptr(cq), ptr(cs), ptr(c32), ptr(work),
+                                              0 if work is None else work.shape[0]), "attention_packed_window")
+    return cq, cs, c32
+
+
+def add_norm_scale_quant(src, res, gamma_add, post_scale, gamma_next=None, eps=1e-6, x_out=None,
+                         want_xn=True, quant=True, stream=None):
+    """x = (rms(src)*gamma_add + res) * post_scale; with gamma_next its norm (+ quant), without it
+    x itself quantized (text.c:957-961, 911). Returns (x, xn, q, qs)."""
+    import torch
+    M, D = src.shape
+    x_out = torch.empty_like(src) if x_out is None else x_out
+    has_next = gamma_next is not None
+    xn = torch.empty_like(src) if (want_xn and has_next) else None
+    q = torch.empty((M, D), dtype=torch.int8, device=src.device) if quant else None
+    qs = torch.empty((M, D // 128), dtype=torch.float32, device=src.device) if quant else None
+    check(load().e2mi_add_norm_scale_quant(stream_ptr(stream), ptr(src), ptr(res), ptr(gamma_add), post_scale,
+                                           ptr(gamma_next), eps, M, D, ptr(x_out), ptr(xn), ptr(q), ptr(qs)),
+          "add_norm_scale_quant")
+    return x_out, xn, q, qs
+
+
+def scale_norm(x, pre_scale, gamma, eps=1e-6, out=None, stream=None):
+    """rms(x * pre_scale) * gamma per row of x [rows][D] (text.c:930-931)."""
+    import torch
+    rows, D = x.shape
+    out = torch.empty_like(x) if out is None else out
+    check(load().e2mi_scale_norm(stream_ptr(stream), ptr(x), rows, D, pre_scale, ptr(gamma), eps, ptr(out)),
+          "scale_norm")
+    return out
 
 
 def attention_i8_packed(q32, k32, v32, start, lens, max_len, H, KV, want_f32=True, cq=None, cs=None,
@@ -494,6 +552,15 @@ def gather_ids(ids, rowmap, stream=None):
 def baseline_config(**over):
     c = E2Config()
     load().e2_config_baseline(C.byref(c))
+    for k, v in over.items():
+        setattr(c, k, v)
+    return c
+
+
+def reference_config(**over):
+    """The reference checkpoint's text geometry (include/e2.h e2_config_reference)."""
+    c = E2Config()
+    load().e2_config_reference(C.byref(c))
     for k, v in over.items():
         setattr(c, k, v)
     return c
@@ -553,7 +620,9 @@ class Engine:
         if not h:
             raise E2MIError(f"create: {last_error()}")
         self.h = C.c_void_p(h)
-        self.hidden = model.config.hidden
+        cfg = model.config
+        self.hidden = cfg.hidden
+        self.dim = cfg.out_dim if cfg.out_dim > 0 else cfg.hidden  # embedding width
 
     @property
     def device(self) -> str:
@@ -564,7 +633,7 @@ class Engine:
         ids = np.ascontiguousarray(ids, np.int32)
         B, S = ids.shape
         v = None if valid is None else np.ascontiguousarray(valid, np.uint8)
-        out = np.empty((B, self.hidden), np.float32)
+        out = np.empty((B, self.dim), np.float32)
         check(load().e2mi_text_embed_batch(self.h, ptr(ids), ptr(v), B, S, ptr(out)),
               "text_embed_batch")
         return out

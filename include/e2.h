@@ -1,9 +1,10 @@
 /* e2.h — the model container of the int8 encoder (host side).
  *
  * Mirrors the reference's include/e2.h handle (e2_model, e2_free, e2_last_error; e2.h:21-22,159)
- * for the tier's geometry. The reference's e2_load reads its own checkpoint (hidden 512, PLE, ...,
- * e2.c:254-434), which this tier does not run; a model here comes from
- *   - e2_model_synthetic: seeded random-init int8 weights at a given geometry (BASELINE config 4),
+ * for two geometries: the BASELINE one (hidden 768, every layer alike) and the reference
+ * checkpoint's own (hidden 512, PLE, sliding window, per-layer head_dim, embed_proj; e2.c:254-434,
+ * e2_config_reference below). A model here comes from
+ *   - e2_model_synthetic: seeded random-init int8 weights at a given geometry,
  *   - e2_load_e8cq: an E8CQ packed int8 cache, the reference's q8cache.c v1 format (q8cache.c:1-13):
  *     header "E8CQ" v1, 16-byte aligned blobs, 152-byte index entries; int8 weights as kind 3
  *     (quad-interleaved w | per-row scale | per-block sums bsq), f32 tensors as kind 2.
@@ -38,10 +39,35 @@ typedef struct {
     float rope_theta;  /* 10000 */
     float embed_scale; /* sqrt(hidden) (e2.c:298) */
     float attn_scale;  /* 1.0: the reference does not scale the logits (text.c:8-9) */
+    /* The reference checkpoint's extras (e2.c:294-301, text.c:467-478). Zeros give the BASELINE
+     * geometry: every layer alike (head_dim, n_kv_heads, rope_theta), no window, no PLE, the
+     * embeddings are the final-normed hidden rows. */
+    int ple_dim;           /* per-layer embedding width: 512 (0 = no PLE) */
+    int out_dim;           /* embed_proj output width: 768 (0 = no embed_proj) */
+    int window;            /* sliding layers keep keys with |i-j| <= window: 512 (0 = no window) */
+    int full_period;       /* layer l is a full-attention layer when l % full_period ==
+                            * full_period - 1: 6, i.e. layers 5, 11, 17, 23 (text.c:267); 0 = none */
+    int full_head_dim;     /* head_dim of the full-attention layers: 512 */
+    int full_kv_heads;     /* kv heads of the full-attention layers: 1 */
+    float rope_theta_full; /* RoPE theta of the full-attention layers: 1e6 */
+    float ple_scale;       /* 1/sqrt(hidden) */
 } e2_config;
 
-/* The BASELINE config-4 geometry (values in the comments above). */
+/* The BASELINE config-4 geometry (values in the comments above, extras zero). */
 void e2_config_baseline(e2_config *c);
+/* The reference checkpoint's text-tower geometry (e2.c:294-301, model.h:12-16, text.c:467-478):
+ * 24 layers, hidden 512, ffn 2048, 4 query heads; sliding layers head_dim 256 with 2 kv heads,
+ * RoPE theta 1e4 and window 512; full layers (5, 11, 17, 23) head_dim 512 with 1 kv head, theta
+ * 1e6; PLE 24 x 512 with ple_scale 1/sqrt(512); embed_scale sqrt(512); embed_proj 512 -> 768;
+ * vocab 262144, max_seq 2048. Tensors beyond the BASELINE set (reference names, e2.c:316-381):
+ *   language_model.ple.per_layer_model_projection.weight    int8 [n_layers*ple_dim][hidden]
+ *   language_model.ple.per_layer_projection_norm.weight     f32 [ple_dim]
+ *   language_model.embedding_projection.weight              int8 [out_dim][hidden]
+ *   language_model.layers.L.ple_block.per_layer_input_gate.weight       int8 [ple_dim][hidden]
+ *   language_model.layers.L.ple_block.per_layer_projection.weight       int8 [hidden][ple_dim]
+ *   language_model.layers.L.ple_block.post_per_layer_input_norm.weight  f32 [hidden]
+ *   language_model.layers.L.layer_scalar                                 f32 [1] */
+void e2_config_reference(e2_config *c);
 
 /* Random-init model: int8 weights uniform in [-127,127] with per-row scales U(0.001, 0.02), norm
  * gammas ~N(1, 0.05), embedding table ~N(0, 0.02). Deterministic in `seed` (the reference tests'

@@ -144,6 +144,20 @@ int e2mi_qkv_norm_rope(e2mi_stream stream, const float *qkv, int M, int S, int H
                        const float *sin_tab, uint16_t *q16, uint16_t *k16, uint16_t *vt16,
                        float *q32, float *k32, float *v32);
 
+/* The reference checkpoint's norm_add + layer_scalar (text.c:957-961: ple_block's map_norm_add,
+ * then map_scale by layer_scalar) and the next operand, one pass per row:
+ * x = (rmsnorm(src)*gamma_add + res) * post_scale -> x_out (may alias res); then, when gamma_next
+ * != NULL, xn = rmsnorm(x)*gamma_next -> xn_out (optional) and q/qs (optional); when gamma_next is
+ * NULL, q/qs (optional) quantize x itself per 128 (the PLE gate GEMM's operand, text.c:911). */
+int e2mi_add_norm_scale_quant(e2mi_stream stream, const float *src, const float *res,
+                              const float *gamma_add, float post_scale, const float *gamma_next,
+                              float eps, int M, int D, float *x_out, float *xn_out, int8_t *q,
+                              float *qs);
+/* The per-layer embedding norm (text.c:930-931: map_scale by ple_scale, then map_norm per slice):
+ * out = rmsnorm(x * pre_scale) * gamma over rows of D (out may alias x). */
+int e2mi_scale_norm(e2mi_stream stream, const float *x, int rows, int D, float pre_scale,
+                    const float *gamma, float eps, float *out);
+
 /* Standalone GeGLU product + quantize (text.c:424-468 gate_quant): g = gelu_tanh(gate)*up per
  * element, quantized per 128 into q [M][D] / qs [M][D/128]; g written back into gate when
  * write_back != 0 (the reference overwrites gate). */
@@ -167,6 +181,8 @@ int e2mi_qkv_norm_rope_packed(e2mi_stream stream, const float *qkv, int M, const
                               int H, int KV, int D, const float *q_gamma, const float *k_gamma,
                               float eps, const float *cos_tab, const float *sin_tab, uint16_t *q16,
                               uint16_t *k16, uint16_t *vt16, float *q32, float *k32, float *v32);
+/* (qkv_norm_rope_packed takes head_dim 256 or 512: the reference checkpoint's full-attention
+ * layers have 512, text.c:476.) */
 /* attention of each packed sequence over its own rows (all valid); vt16 [KV][D][M] from
  * e2mi_qkv_norm_rope_packed, seq_len[b] <= max_len, every seq_start a multiple of 8 (the
  * e2mi.pack_plan layout); rows outside every sequence are not written. work (optional, device):
@@ -178,6 +194,16 @@ int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, const uint16_
                           const int32_t *seq_len, int B, int max_len, int H, int KV, int D,
                           float scale, int8_t *ctx_q, float *ctx_s, float *ctx32,
                           const int32_t *work, int n_work);
+/* The same for the reference checkpoint's layers (text.c:467-478, 534-572): head_dim D = 256 or 512
+ * and, when window > 0, the sliding window: query i reads key j only when |pos_i - pos_j| <= window
+ * (text.c:542-546), pos [M] being each row's position in its padded sequence (the pos table of
+ * e2mi_qkv_norm_rope_packed; NULL: the packed index). At D = 512 each work entry runs as two
+ * workgroups (256 context dims each). Needs M even and vt16 4-byte aligned. */
+int e2mi_attention_packed_window(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
+                                 const uint16_t *vt16, int M, const int32_t *seq_start,
+                                 const int32_t *seq_len, const int32_t *pos, int B, int max_len,
+                                 int H, int KV, int D, float scale, int window, int8_t *ctx_q,
+                                 float *ctx_s, float *ctx32, const int32_t *work, int n_work);
 /* The reference's int8 attention (text.c:638-700 attb_i8; dispatch.c:51 selects it for long
  * sequences on AVX-512) for packed batches: q32 [M][H*D], k32/v32 [M][KV*D] f32 after q/k norm and
  * RoPE (e2mi_qkv_norm_rope_packed's optional f32 outputs), sequences as for

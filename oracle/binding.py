@@ -32,17 +32,24 @@ def _need(a, dtype, shape=None):
     return a
 
 
+_LAYER_PTRS = ("wqkv", "sqkv", "wo", "so", "wgate", "sgate", "wup", "sup", "wdown", "sdown",
+               "input_ln", "post_attn_ln", "pre_ffn_ln", "post_ffn_ln", "q_norm", "k_norm")
+_LAYER_PLE = ("wple_gate", "sple_gate", "wple_proj", "sple_proj", "ple_norm")
+
+
 class OrLayer(C.Structure):
-    _fields_ = [(n, _P) for n in (
-        "wqkv", "sqkv", "wo", "so", "wgate", "sgate", "wup", "sup", "wdown", "sdown",
-        "input_ln", "post_attn_ln", "pre_ffn_ln", "post_ffn_ln", "q_norm", "k_norm")]
+    _fields_ = [(n, _P) for n in _LAYER_PTRS + _LAYER_PLE] + [("layer_scalar", _F)]
 
 
 class OrModel(C.Structure):
     _fields_ = [("n_layers", _I), ("hidden", _I), ("ffn", _I), ("n_heads", _I), ("n_kv", _I),
                 ("head_dim", _I), ("vocab", _I), ("eps", _F), ("rope_theta", _F),
                 ("embed_scale", _F), ("attn_scale", _F), ("embed", _P), ("final_norm", _P),
-                ("layers", C.POINTER(OrLayer)), ("attn_i8", _I)]
+                ("layers", C.POINTER(OrLayer)), ("attn_i8", _I),
+                ("ple_dim", _I), ("out_dim", _I), ("window", _I), ("full_period", _I),
+                ("full_head_dim", _I), ("full_kv", _I), ("rope_theta_full", _F), ("ple_scale", _F),
+                ("wple_model", _P), ("sple_model", _P), ("ple_proj_norm", _P),
+                ("wembed_proj", _P), ("sembed_proj", _P)]
 
 
 class Oracle:
@@ -71,6 +78,7 @@ class Oracle:
             "or_rope_rows": (None, [_P, _I, _I, _I, _P, _P]),
             "or_softmax": (None, [_P, _I]),
             "or_attention": (None, [_P, _I, _P, _I, _P, _I, _P, _I, _I, _I, _I, _F, _P, _I, _I]),
+            "or_attention_win": (None, [_P, _I, _P, _I, _P, _I, _P, _I, _I, _I, _I, _F, _I, _P, _I, _I]),
             "or_attention_i8": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I]),
             "or_meanpool": (None, [_P, _I, _I, _P, _P]),
             "or_l2norm": (None, [_P, _I]),
@@ -79,6 +87,8 @@ class Oracle:
             "or_attention_sublayer": (_I, [C.POINTER(OrModel), _I, _P, _I, _I, _P, _P, _I]),
             "or_ffn_sublayer": (_I, [C.POINTER(OrModel), _I, _P, _I, _I]),
             "or_encode": (_I, [C.POINTER(OrModel), _P, _P, _I, _I, _P, _I]),
+            "or_layer_forward_ple": (_I, [C.POINTER(OrModel), _I, _P, _P, _I, _I, _P, _I]),
+            "or_ple_inputs": (_I, [C.POINTER(OrModel), _P, _I, _P, _I]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -214,13 +224,14 @@ class Oracle:
         self.lib.or_softmax(_ptr(x), x.size)
         return x
 
-    def attention(self, q, k, v, valid, H, KV, D, scale=1.0, nthreads=8):
-        """q [S][H*D], k/v [S][KV*D] (contiguous), valid [S] u8 -> ctx [S][H*D]."""
+    def attention(self, q, k, v, valid, H, KV, D, scale=1.0, nthreads=8, window=0):
+        """q [S][H*D], k/v [S][KV*D] (contiguous), valid [S] u8 -> ctx [S][H*D]; window > 0 keeps
+        the keys with |i-j| <= window (text.c:542-546)."""
         S = q.shape[0]
         ctx = np.zeros((S, H * D), np.float32)
-        self.lib.or_attention(_ptr(_need(q, np.float32)), H * D, _ptr(_need(k, np.float32)), KV * D,
-                              _ptr(_need(v, np.float32)), KV * D, _ptr(_need(valid, np.uint8)), S,
-                              H, KV, D, scale, _ptr(ctx), H * D, nthreads)
+        self.lib.or_attention_win(_ptr(_need(q, np.float32)), H * D, _ptr(_need(k, np.float32)), KV * D,
+                                  _ptr(_need(v, np.float32)), KV * D, _ptr(_need(valid, np.uint8)), S,
+                                  H, KV, D, scale, window, _ptr(ctx), H * D, nthreads)
         return ctx
 
     def attention_i8(self, q, k, v, H, KV, D):
@@ -243,32 +254,64 @@ class Oracle:
 
 
 class OracleModel:
-    """Holds numpy weight arrays alive and exposes them as an or_model for the recipe functions."""
+    """Holds numpy weight arrays alive and exposes them as an or_model for the recipe functions.
 
-    def __init__(self, oracle, cfg, layers, embed, final_norm, attn_scale=1.0, attn_i8=False):
+    cfg keys: hidden, ffn, n_heads, n_kv_heads, head_dim, vocab, rms_eps, rope_theta, embed_scale;
+    for the reference checkpoint's geometry also ple_dim, out_dim, window, full_period,
+    full_head_dim, full_kv_heads, rope_theta_full, ple_scale, with `extra` holding ple_model (w, s),
+    ple_proj_norm and embed_proj (w, s), and each layer dict wple_gate/sple_gate, wple_proj/sple_proj,
+    ple_norm and layer_scalar."""
+
+    def __init__(self, oracle, cfg, layers, embed, final_norm, attn_scale=1.0, attn_i8=False, extra=None):
         self.o = oracle
-        self._keep = [layers, embed, final_norm]
+        extra = extra or {}
+        self._keep = [layers, embed, final_norm, extra]
+        ple = cfg.get("ple_dim", 0) > 0
         arr = (OrLayer * len(layers))()
         for i, Lw in enumerate(layers):
-            for name, _ in OrLayer._fields_:
+            for name in _LAYER_PTRS + (_LAYER_PLE if ple else ()):
                 a = Lw[name]
                 if not a.flags.c_contiguous:
                     raise ValueError(name)
                 setattr(arr[i], name, a.ctypes.data)
+            arr[i].layer_scalar = float(Lw.get("layer_scalar", 1.0))
         self._arr = arr
+
+        def p(name):
+            return extra[name].ctypes.data if name in extra else None
         self.m = OrModel(len(layers), cfg["hidden"], cfg["ffn"], cfg["n_heads"], cfg["n_kv_heads"],
                          cfg["head_dim"], cfg["vocab"], cfg["rms_eps"], cfg["rope_theta"],
                          cfg["embed_scale"], attn_scale, embed.ctypes.data, final_norm.ctypes.data,
-                         C.cast(arr, C.POINTER(OrLayer)), 1 if attn_i8 else 0)
+                         C.cast(arr, C.POINTER(OrLayer)), 1 if attn_i8 else 0,
+                         cfg.get("ple_dim", 0), cfg.get("out_dim", 0), cfg.get("window", 0),
+                         cfg.get("full_period", 0), cfg.get("full_head_dim", 0), cfg.get("full_kv_heads", 0),
+                         cfg.get("rope_theta_full", 0.0), cfg.get("ple_scale", 0.0),
+                         p("wple_model"), p("sple_model"), p("ple_proj_norm"), p("wembed_proj"),
+                         p("sembed_proj"))
+        self.out_dim = cfg.get("out_dim", 0) or cfg["hidden"]
 
     def encode(self, ids, valid, nthreads=8):
         B, S = ids.shape
-        out = np.empty((B, self.m.hidden), np.float32)
+        out = np.empty((B, self.out_dim), np.float32)
         rc = self.o.lib.or_encode(C.byref(self.m), _ptr(_need(ids, np.int32)),
                                   _ptr(_need(valid, np.uint8)), B, S, _ptr(out), nthreads)
         if rc:
             raise RuntimeError("or_encode failed")
         return out
+
+    def ple_inputs(self, x, nthreads=8):
+        """x [rows][hidden] (the scaled embeddings) -> ple [rows][n_layers*ple_dim]."""
+        x = _need(np.ascontiguousarray(x, np.float32), np.float32)
+        ple = np.empty((x.shape[0], self.m.n_layers * self.m.ple_dim), np.float32)
+        if self.o.lib.or_ple_inputs(C.byref(self.m), _ptr(x), x.shape[0], _ptr(ple), nthreads):
+            raise RuntimeError("or_ple_inputs failed")
+        return ple
+
+    def layer_ple(self, l, x, ple, valid, B, S, nthreads=8):
+        x = np.array(x, np.float32, copy=True, order="C")
+        if self.o.lib.or_layer_forward_ple(C.byref(self.m), l, _ptr(x), _ptr(ple), B, S, _ptr(valid), nthreads):
+            raise RuntimeError("or_layer_forward_ple failed")
+        return x
 
     def layer(self, l, x, valid, B, S, nthreads=8):
         x = np.array(x, np.float32, copy=True, order="C")

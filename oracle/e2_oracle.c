@@ -413,10 +413,12 @@ typedef struct {
     int S, H, KV, D;
     float scale;
     float *ctx;
+    int window;
 } attn_task;
 
 /* One (head, query row): text.c:534-572. Keys outside `valid` are skipped, an invalid query row
- * gets a zero context, the logits are scaled by `scale` (1.0 in the reference, text.c:8-9). */
+ * gets a zero context, the logits are scaled by `scale` (1.0 in the reference, text.c:8-9); with a
+ * window the key loop runs over [max(i - window, 0), min(i + window + 1, S)) (text.c:542-546). */
 static void attn_item(void *arg, int item) {
     const attn_task *t = arg;
     const int h = item / t->S, i = item % t->S;
@@ -427,8 +429,13 @@ static void attn_item(void *arg, int item) {
     const float *qh = t->q + (size_t)i * t->ldq + (size_t)h * t->D;
     float *sc = malloc(sizeof(float) * (size_t)t->S);
     if (!sc) return;
+    int lo = 0, hi = t->S;
+    if (t->window > 0) {
+        lo = i - t->window > 0 ? i - t->window : 0;
+        hi = i + t->window + 1 < t->S ? i + t->window + 1 : t->S;
+    }
     int n = 0;
-    for (int j = 0; j < t->S; j++) {
+    for (int j = lo; j < hi; j++) {
         if (!t->valid[j]) continue;
         const float *kj = t->k + (size_t)j * t->ldk + (size_t)kvh * t->D;
         float s = 0.f;
@@ -438,7 +445,7 @@ static void attn_item(void *arg, int item) {
     if (n) {
         or_softmax(sc, n);
         n = 0;
-        for (int j = 0; j < t->S; j++) {
+        for (int j = lo; j < hi; j++) {
             if (!t->valid[j]) continue;
             const float *vj = t->v + (size_t)j * t->ldv + (size_t)kvh * t->D;
             const float p = sc[n++];
@@ -451,7 +458,13 @@ static void attn_item(void *arg, int item) {
 void or_attention(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
                   const uint8_t *valid, int S, int H, int KV, int D, float scale, float *ctx,
                   int ldc, int nthreads) {
-    attn_task t = { q, k, v, ldq, ldk, ldv, ldc, valid, S, H, KV, D, scale, ctx };
+    or_attention_win(q, ldq, k, ldk, v, ldv, valid, S, H, KV, D, scale, 0, ctx, ldc, nthreads);
+}
+
+void or_attention_win(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                      const uint8_t *valid, int S, int H, int KV, int D, float scale, int window,
+                      float *ctx, int ldc, int nthreads) {
+    attn_task t = { q, k, v, ldq, ldk, ldv, ldc, valid, S, H, KV, D, scale, ctx, window };
     or_parallel(attn_item, &t, H * S, nthreads);
 }
 

@@ -63,6 +63,11 @@ void or_softmax(float *x, int n);
 void or_attention(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
                   const uint8_t *valid, int S, int H, int KV, int D, float scale, float *ctx,
                   int ldc, int nthreads);
+/* the same with the sliding window of text.c:542-546: query i reads keys j with |i-j| <= window
+ * (window <= 0: all keys) */
+void or_attention_win(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                      const uint8_t *valid, int S, int H, int KV, int D, float scale, int window,
+                      float *ctx, int ldc, int nthreads);
 int or_attention_i8(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
                     int S, int H, int KV, int D, float *ctx, int ldc);
 
@@ -76,7 +81,8 @@ void or_i8_gemm_mt(const int8_t *qa, const float *as, const int8_t *w, const flo
                    const float *bias, int M, int N, int K, float *y, int nthreads);
 void or_quantize_mt(const float *x, int M, int K, int8_t *q, float *scales, int nthreads);
 
-/* ---- a9/a12 + text_forward (text.c:817-984) at the BASELINE geometry, no PLE/embed_proj */
+/* ---- a9/a12 + text_forward (text.c:817-984): the BASELINE geometry, or the reference
+ *      checkpoint's (PLE, sliding window, per-layer head_dim, embed_proj) */
 typedef struct {
     const int8_t *wqkv;  /* [(H+2KV)*D][hidden] row-major: q rows, then k, then v */
     const float *sqkv;
@@ -90,6 +96,14 @@ typedef struct {
     const float *sdown;
     const float *input_ln, *post_attn_ln, *pre_ffn_ln, *post_ffn_ln; /* [hidden] */
     const float *q_norm, *k_norm;                                    /* [head_dim] */
+    /* the reference checkpoint's PLE block (text.c:906-915) and layer scale (text.c:959-961);
+     * unused when the model has no PLE (ple_dim 0) */
+    const int8_t *wple_gate; /* [ple_dim][hidden] */
+    const float *sple_gate;
+    const int8_t *wple_proj; /* [hidden][ple_dim] */
+    const float *sple_proj;
+    const float *ple_norm;   /* [hidden] */
+    float layer_scalar;      /* 1.0 where the model has none */
 } or_layer;
 
 typedef struct {
@@ -101,17 +115,42 @@ typedef struct {
     /* 1: the int8 attention (text.c:638-700) for sequences of >= 32 rows with no padding inside
      * (the reference's blocked path, text.c:873-875, selected as dispatch.c picks i8); 0: f32 */
     int attn_i8;
+    /* the reference checkpoint's geometry (e2.c:294-301, text.c:467-478); zeros give the BASELINE
+     * geometry (every layer alike, no window, no PLE, embeddings are hidden rows) */
+    int ple_dim;           /* per-layer embedding width (512); 0 = no PLE */
+    int out_dim;           /* embed_proj output width (768); 0 = no embed_proj */
+    int window;            /* sliding layers keep keys with |i-j| <= window (512); 0 = no window */
+    int full_period;       /* layer l is a full-attention layer when l % full_period == full_period-1
+                            * (6: layers 5, 11, 17, 23, text.c:267); 0 = none */
+    int full_head_dim, full_kv; /* head_dim and kv heads of the full layers (512, 1) */
+    float rope_theta_full; /* RoPE theta of the full layers (1e6); the others use rope_theta */
+    float ple_scale;       /* 1/sqrt(hidden) */
+    const int8_t *wple_model;   /* [n_layers*ple_dim][hidden] */
+    const float *sple_model;
+    const float *ple_proj_norm; /* [ple_dim] */
+    const int8_t *wembed_proj;  /* [out_dim][hidden] */
+    const float *sembed_proj;
 } or_model;
 
-/* One layer's attention + FFN sublayers over B x S rows, x updated in place (text.c:939-961). */
+/* Geometry of layer l: head_dim, kv heads, RoPE theta and window (0 = none) (text.c:467-478). */
+void or_layer_geom(const or_model *m, int l, int *head_dim, int *kv, float *theta, int *window);
+
+/* One layer over B x S rows, x updated in place (text.c:939-961): attention and FFN sublayers,
+ * then, with PLE, the PLE block on this layer's slice of `ple` ([B*S][n_layers*ple_dim], from
+ * or_ple_inputs; NULL without PLE) and the layer scale. */
 int or_layer_forward(const or_model *m, int l, float *x, int B, int S, const uint8_t *valid,
                      int nthreads);
+int or_layer_forward_ple(const or_model *m, int l, float *x, const float *ple, int B, int S,
+                         const uint8_t *valid, int nthreads);
+/* The per-layer inputs (text.c:929-932): ple = rms(int8 GEMM(quant(x), ple_model) * ple_scale)
+ * * ple_proj_norm per ple_dim slice; x = the scaled embeddings [rows][hidden]. */
+int or_ple_inputs(const or_model *m, const float *x, int rows, float *ple, int nthreads);
 /* Attention sublayer only: x [B*S][hidden] -> out = O-proj of the context. */
 int or_attention_sublayer(const or_model *m, int l, const float *x, int B, int S,
                           const uint8_t *valid, float *out, int nthreads);
 /* FFN sublayer: x -> norm_split -> gate|up -> GeGLU -> down -> norm_add. */
 int or_ffn_sublayer(const or_model *m, int l, float *x, int rows, int nthreads);
-/* The whole encoder: ids [B][S] -> out [B][hidden] (text.c:924-984 without PLE/embed_proj). */
+/* The whole encoder: ids [B][S] -> out [B][out_dim or hidden] (text.c:924-984). */
 int or_encode(const or_model *m, const int32_t *ids, const uint8_t *valid, int B, int S,
               float *out, int nthreads);
 

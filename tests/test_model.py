@@ -167,3 +167,54 @@ def test_bad_configs_refused(e2mi_mod):
     for over in (dict(head_dim=128), dict(hidden=700), dict(n_heads=3, n_kv_heads=2), dict(max_seq=4096)):
         with pytest.raises(e2mi_mod.E2MIError):
             e2mi_mod.Model.synthetic(e2mi_mod.baseline_config(n_layers=1, vocab=10, **over), 1)
+
+
+def test_reference_config(e2mi_mod):
+    """The reference checkpoint's text geometry (e2.c:294-301, model.h:12-16, text.c:467-478)."""
+    c = e2mi_mod.reference_config()
+    assert (c.n_layers, c.hidden, c.ffn, c.n_heads, c.n_kv_heads, c.head_dim, c.vocab, c.max_seq) == \
+        (24, 512, 2048, 4, 2, 256, 262144, 2048)
+    assert (c.ple_dim, c.out_dim, c.window, c.full_period, c.full_head_dim, c.full_kv_heads) == \
+        (512, 768, 512, 6, 512, 1)
+    assert c.rope_theta == 1e4 and c.rope_theta_full == 1e6
+    assert c.embed_scale == np.float32(np.sqrt(512)) and c.ple_scale == np.float32(1 / np.sqrt(512))
+    # full-attention layers 5, 11, 17, 23 (text.c:267)
+    assert [l for l in range(24) if c.layer_geom(l)[0] == 512] == [5, 11, 17, 23]
+    b = e2mi_mod.baseline_config()
+    assert (b.ple_dim, b.out_dim, b.window, b.full_period) == (0, 0, 0, 0)
+
+
+def test_reference_geometry_tensors_and_e8cq(e2mi_mod, tmp_path):
+    """The reference geometry's extra tensors (names of e2.c:316-381, shapes per layer type), the
+    BASELINE tensors unchanged by the extras' seeds, and an E8CQ round trip that checks them."""
+    cfg = e2mi_mod.reference_config(n_layers=6, vocab=100)
+    m = e2mi_mod.Model.synthetic(cfg, 9)
+    shapes = {"language_model.ple.per_layer_model_projection.weight": (6 * 512, 512),
+              "language_model.embedding_projection.weight": (768, 512)}
+    for name, nk in shapes.items():
+        assert m.tensor(name)[3:5] == nk
+    assert m.tensor("language_model.ple.per_layer_projection_norm.weight").shape == (512,)
+    for l, (qd, kvd) in ((0, (1024, 512)), (5, (2048, 512))):
+        assert m.tensor(lname(l, Q8[0]))[3:5] == (qd, 512)
+        assert m.tensor(lname(l, Q8[1]))[3:5] == (kvd, 512)
+        assert m.tensor(lname(l, Q8[3]))[3:5] == (512, qd)
+        assert m.tensor(lname(l, "self_attn.q_norm.weight")).shape == (qd // 4,)
+        assert m.tensor(lname(l, "ple_block.per_layer_input_gate.weight"))[3:5] == (512, 512)
+        assert m.tensor(lname(l, "ple_block.per_layer_projection.weight"))[3:5] == (512, 512)
+        assert m.tensor(lname(l, "layer_scalar")).shape == (1,)
+    p = str(tmp_path / "ref.e8cq")
+    m.save_e8cq(p)
+    m2 = e2mi_mod.Model.load_e8cq(p, cfg)
+    for name in list(shapes) + [lname(5, "ple_block.per_layer_projection.weight")]:
+        assert all(np.array_equal(x, y) for x, y in zip(m.tensor(name)[:3], m2.tensor(name)[:3]))
+    assert np.array_equal(m.tensor(lname(3, "layer_scalar")), m2.tensor(lname(3, "layer_scalar")))
+    # a cache without the PLE tensors is refused for this geometry, accepted for the BASELINE one
+    b = e2mi_mod.Model.synthetic(e2mi_mod.baseline_config(n_layers=1, vocab=100), 9)
+    pb = str(tmp_path / "b.e8cq")
+    b.save_e8cq(pb)
+    with pytest.raises(e2mi_mod.E2MIError, match="missing or mis-shaped"):
+        e2mi_mod.Model.load_e8cq(pb, e2mi_mod.reference_config(n_layers=1, vocab=100, hidden=768, ffn=1152,
+                                                                 n_heads=3, n_kv_heads=1, full_period=0))
+    # the extras draw from their own streams: the shared tensors match a BASELINE-extras-free model
+    plain = e2mi_mod.Model.synthetic(e2mi_mod.reference_config(n_layers=6, vocab=100, ple_dim=0, out_dim=0), 9)
+    assert np.array_equal(plain.tensor(lname(2, Q8[4]))[0], m.tensor(lname(2, Q8[4]))[0])
