@@ -338,6 +338,64 @@ def encoder_bench(torch, e2mi, steps, warmup, cpu_sample=4, padded=True):
     return res
 
 
+def reference_geometry_bench(torch, e2mi, steps, warmup, cpu_sample=0):
+    """The reference checkpoint's own text geometry (e2_config_reference: 24 layers, hidden 512,
+    FFN 2048, 4 query heads; sliding layers head_dim 256 / 2 kv heads / window 512, full layers
+    5, 11, 17, 23 head_dim 512 / 1 kv head; PLE 24 x 512; embed_proj 512 -> 768) with random-init
+    int8 weights, on two batches: the config-4 shape (64 x 512, lengths U[64, 512], where the
+    window never cuts) and 16 x 2048 with lengths U[1024, 2048] (the window cuts on every sliding
+    layer). Ids, mask and output in HBM, packed batches, graph replay, as the encoder leg."""
+    cfg = e2mi.reference_config()
+    t0 = time.perf_counter()
+    model = e2mi.Model.synthetic(cfg, 1004)
+    t_model = time.perf_counter() - t0
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    eng = e2mi.Engine(model, max_rows=ENC_B * ENC_S)
+    res = {"config": "reference checkpoint geometry, 24 layers, random-init int8 weights, vocab 262144",
+           "model_build_s": round(t_model, 2)}
+    rng = np.random.default_rng(1004)
+    for name, B, S, lo in (("config4_64x512", ENC_B, ENC_S, 64), ("long_16x2048", 16, 2048, 1024)):
+        ids = rng.integers(0, cfg.vocab, (B, S)).astype(np.int32)
+        lens = rng.integers(lo, S + 1, B)
+        valid = (np.arange(S)[None, :] < lens[:, None]).astype(np.uint8)
+        ids_d, valid_d = torch.from_numpy(ids).to(dev), torch.from_numpy(valid).to(dev)
+        out = torch.empty((B, cfg.out_dim), device=dev)
+        for _ in range(max(2, warmup)):
+            eng.embed_batch_device(ids_d, valid_d, out, stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            eng.embed_batch_device(ids_d, valid_d, out, stream)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t1) / steps
+        o = out.cpu().numpy()
+        leg = {"embeddings_per_s": round(B / dt, 2), "ms_per_batch": round(dt * 1e3, 3),
+               "tokens_per_s_valid": round(float(valid.sum()) / dt, 1),
+               "lengths": f"U[{lo}, {S}] (mean {lens.mean():.0f})",
+               "unit_norm_ok": bool(np.allclose(np.linalg.norm(o, axis=1), 1, atol=1e-4)),
+               "kernels_per_forward": eng.stats()[1]}
+        if cpu_sample and name.startswith("config4"):
+            sys.path.insert(0, ROOT)
+            sys.path.insert(0, os.path.join(ROOT, "tests"))
+            from oracle.binding import Oracle
+            from model_util import oracle_model
+            threads = physical_cores()
+            om = oracle_model(Oracle(), model)
+            t2 = time.perf_counter()
+            om.encode(np.ascontiguousarray(ids[:cpu_sample]), np.ascontiguousarray(valid[:cpu_sample]),
+                      nthreads=threads)
+            dc = time.perf_counter() - t2
+            leg["cpu_baseline"] = {
+                "value": round(cpu_sample / dc, 4), "unit": "embeddings/s", "cores": threads, "kind": "port",
+                "sample": f"{cpu_sample} of the {B} sequences (lengths {valid[:cpu_sample].sum(1).tolist()}), "
+                          f"24 layers, {dc:.1f} s"}
+            del om
+        res[name] = leg
+    del eng, model
+    return res
+
+
 def encoder_cpu_baseline(model, ids, valid, nseq=24):
     """The oracle's text recipe (oracle/e2_oracle_model.c, a C port: VNNI int8 GEMMs, fp32 row-wise
     attention) on the host cores, over the first nseq sequences of the benchmark batch."""
@@ -410,6 +468,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-encoder", action="store_true", help="skip the config-4 encoder leg")
+    ap.add_argument("--reference-only", action="store_true",
+                    help="only the reference checkpoint geometry's encoder leg")
     ap.add_argument("--encoder-only", action="store_true",
                     help="only the config-4 encoder leg (for profiling; prints its own line)")
     ap.add_argument("--no-padded", action="store_true",
@@ -436,6 +496,9 @@ def main():
         enc = encoder_bench(torch, e2mi, args.steps, args.warmup, padded=not args.no_padded)
         enc.pop("_model"), enc.pop("_batch")
         print(json.dumps({"encoder": enc}))
+        return
+    if args.reference_only:
+        print(json.dumps({"reference_geometry": reference_geometry_bench(torch, e2mi, args.steps, args.warmup)}))
         return
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
@@ -612,6 +675,8 @@ def main():
         if not args.no_cpu_baseline:
             out["encoder_cpu_baseline"] = encoder_cpu_baseline(model, eids, evalid)
         del model
+        out["reference_geometry"] = reference_geometry_bench(
+            torch, e2mi, max(5, args.steps // 2), args.warmup, cpu_sample=0 if args.no_cpu_baseline else 8)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
