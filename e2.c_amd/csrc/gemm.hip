@@ -240,6 +240,14 @@ constexpr int p_lds_bytes() {
 // a wave-private LDS area (8 rows at a time) with no workgroup barrier; GEGLU exchanges only the
 // per-row partial maxima between the two waves of a block (one barrier). scr: 8 waves x 8 rows x
 // (RW + 4) floats, then GEGLU's exchange area of 8 waves x 32 floats.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// cache policy of the f32 output stores: sc0 | nt (non-temporal, streamed past the caches). The
+// outputs are written once and read by the next kernel; measured on the per-token f32 sweep at
+// M = 65536: 1124 -> 1350 TOPS (768x1280: 121.5 -> 96.6 us) against the default policy
+constexpr int kStoreNT = 3;
+
 template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
 __device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArgs &p, float (&f)[4][16],
                                                                    const float (&wsr)[4], int m0, int n0,
@@ -321,14 +329,17 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArg
 #pragma unroll
             for (int i = 0; i < CPL / 4; i++)
                 w4[i] = pack4_magic(v[c][4 * i], v[c][4 * i + 1], v[c][4 * i + 2], v[c][4 * i + 3], s.inv);
+            // non-temporal stores: the outputs are read by the next kernel, not by this one
             int8_t *dst = p.Yq + (size_t)m * p.ldyq + oc;
-            if constexpr (CPL == 16) *(uint4 *)dst = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-            else *(uint2 *)dst = make_uint2(w4[0], w4[1]);
-            if ((lane & 7) == 0 && (!GG || (wn & 1) == 0)) p.ys[(size_t)m * p.ldys + (oc >> 7)] = s.sc;
+            if constexpr (CPL == 16) __builtin_nontemporal_store((u32x4){w4[0], w4[1], w4[2], w4[3]}, (u32x4 *)dst);
+            else __builtin_nontemporal_store((u32x2){w4[0], w4[1]}, (u32x2 *)dst);
+            if ((lane & 7) == 0 && (!GG || (wn & 1) == 0))
+                __builtin_nontemporal_store(s.sc, p.ys + (size_t)m * p.ldys + (oc >> 7));
             if (GG && p.Y) {
 #pragma unroll
                 for (int i = 0; i < CPL; i += 4)
-                    *(float4 *)(p.Y + (size_t)m * p.ldy + oc + i) = make_float4(v[c][i], v[c][i + 1], v[c][i + 2], v[c][i + 3]);
+                    __builtin_nontemporal_store((f32x4){v[c][i], v[c][i + 1], v[c][i + 2], v[c][i + 3]},
+                                                (f32x4 *)(p.Y + (size_t)m * p.ldy + oc + i));
             }
         }
     }
@@ -356,7 +367,7 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmA
             if constexpr (POST & 1) v = v + b;
             if constexpr (POST & 2) v = fminf(fmaxf(v, p.lo), p.hi);
             const int srow = __builtin_amdgcn_readfirstlane(((r >> 2) * 8 + (r & 3)) * p.ldy * 4);
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry, voff + tn * 128, srow, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry, voff + tn * 128, srow, kStoreNT);
         }
     }
 }
