@@ -15,9 +15,9 @@
 //   before the layers: quant(x0), the PLE model GEMM -> f32 [rows][L*P], scale + norm per slice
 //     (text.c:929-932: e2mi_quantize, e2mi_i8_gemm, e2mi_scale_norm);
 //   per layer its own head_dim / kv heads / RoPE table / window (text.c:467-478), and after the FFN
-//     norm_add(post_ffn) + quant of x itself, the PLE gate GEMM, gelu(gate) * ple slice + quant,
-//     the PLE projection GEMM, norm_add(ple_norm) * layer_scalar + the next norm + quant
-//     (text.c:906-915, 955-961: e2mi_add_norm_scale_quant, e2mi_gelu_mul_quant);
+//     norm_add(post_ffn) + quant of x itself, the PLE gate GEMM with gelu(gate) * ple slice + quant
+//     in its epilogue, the PLE projection GEMM, norm_add(ple_norm) * layer_scalar + the next norm +
+//     quant (text.c:906-915, 955-961: e2mi_add_norm_scale_quant, e2mi_i8_gemm_gelu_mul);
 //   after the final norm: quant + the embed_proj GEMM to out_dim, pooled (text.c:964-965).
 // The recorded graph is replayed for every later call of the same shape, like the reference's HIP
 // backend (forward.c:553-579).
@@ -308,8 +308,8 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
             // post_ffn norm_add, x itself quantized for the PLE gate; the PLE block; layer scale
             RUN(e2mi_add_norm_scale_quant(s, g->tmp, g->x, L.ln_ffn, 1.0f, nullptr, eps, M, Dm, g->x, nullptr,
                                           g->qa, g->as));
-            RUN(e2mi_i8_gemm(s, g->qkv, P, g->qa, g->as, &L.ple_gate, M, 0, P));
-            RUN(e2mi_gelu_mul_quant(s, g->qkv, P, g->ple32 + (size_t)l * P, c.n_layers * P, M, P, g->qg, g->gs, 0));
+            RUN(e2mi_i8_gemm_gelu_mul(s, g->qg, g->gs, nullptr, g->qa, g->as, &L.ple_gate, M,
+                                      g->ple32 + (size_t)l * P, c.n_layers * P));
             RUN(e2mi_i8_gemm(s, g->tmp, Dm, g->qg, g->gs, &L.ple_proj, M, 0, Dm));
             RUN(e2mi_add_norm_scale_quant(s, g->tmp, g->x, L.ple_norm, L.layer_scalar, gnext, eps, M, Dm, g->x,
                                           last ? g->xn : nullptr, g->qa, g->as));

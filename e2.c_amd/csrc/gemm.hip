@@ -7,6 +7,8 @@
 // then one of the fused epilogues:
 //   EPI_F32   y (+bias), clamped to [lo,hi], stored f32 (the reference contract)
 //   EPI_I8Q   y (+bias) requantized per (row, 128 output columns) for the next GEMM: int8 + scale
+//   EPI_GELUMUL g = gelu_tanh(y) * mul[m][n] (mul from memory: the PLE gate, text.c:906-913),
+//             quantized per (row, 128 columns) like EPI_I8Q; g optionally stored f32
 //   EPI_GEGLU W rows interleaved per 64 as [32 gate | 32 up]; g = gelu_tanh(gate) * up is
 //             quantized per 128 (text.c:424-468 fused into the producing GEMM), g optionally kept
 //
@@ -26,7 +28,7 @@
 
 namespace e2mi {
 
-enum { EPI_F32 = 0, EPI_I8Q = 1, EPI_GEGLU = 2 };
+enum { EPI_F32 = 0, EPI_I8Q = 1, EPI_GEGLU = 2, EPI_GELUMUL = 3 };
 
 struct GemmArgs {
     const int8_t *A;
@@ -38,6 +40,8 @@ struct GemmArgs {
     int8_t *Yq;      // EPI_I8Q / EPI_GEGLU quantized output
     float *ys;       // ... and its per-128 scales [M][ldys]
     int32_t *accd;   // optional int32 accumulator dump [nb][M][N] (parity tests)
+    const float *mul;  // EPI_GELUMUL: the multiplier of gelu(y) [M][ldmul]
+    int ldmul;
     int lda, ldw, ldy, ldyq, ldys;
     int M, N, K;
     float lo, hi;
@@ -253,7 +257,7 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArg
                                                                    const float (&wsr)[4], int m0, int n0,
                                                                    int wave, int wm, int wn, int lane,
                                                                    float *scr) {
-    constexpr bool GG = EPI == EPI_GEGLU;
+    constexpr bool GG = EPI == EPI_GEGLU, GM = EPI == EPI_GELUMUL;
     constexpr int RW = GG ? 64 : 128;  // output columns per wave row
     constexpr int FP = RW + 4;          // f32 pitch of the wave-private rows
     constexpr int CPL = RW / 8;         // output columns per lane in the transposed chunk (16 | 8)
@@ -303,6 +307,20 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArg
             v[c][i + 2] = x.z;
             v[c][i + 3] = x.w;
         }
+        if constexpr (GM) {
+            // g = gelu_tanh(y) * mul for the lane's CPL consecutive columns of row 8c + cr (rows
+            // past M read row M - 1; their outputs are not stored)
+            const int m = min(m0 + wm * 32 + 8 * c + cr, p.M - 1);
+            const float *mp = p.mul + (size_t)m * p.ldmul + oc;
+#pragma unroll
+            for (int i = 0; i < CPL; i += 4) {
+                const float4 u = oc < ldo ? *(const float4 *)(mp + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                v[c][i] = gelu_tanh(v[c][i]) * u.x;
+                v[c][i + 1] = gelu_tanh(v[c][i + 1]) * u.y;
+                v[c][i + 2] = gelu_tanh(v[c][i + 2]) * u.z;
+                v[c][i + 3] = gelu_tanh(v[c][i + 3]) * u.w;
+            }
+        }
         float a = 0.f;
 #pragma unroll
         for (int i = 0; i < CPL; i++) a = fmaxf(a, fabsf(v[c][i]));
@@ -335,7 +353,7 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArg
             else __builtin_nontemporal_store((u32x2){w4[0], w4[1]}, (u32x2 *)dst);
             if ((lane & 7) == 0 && (!GG || (wn & 1) == 0))
                 __builtin_nontemporal_store(s.sc, p.ys + (size_t)m * p.ldys + (oc >> 7));
-            if (GG && p.Y) {
+            if ((GG || GM) && p.Y) {
 #pragma unroll
                 for (int i = 0; i < CPL; i += 4)
                     __builtin_nontemporal_store((f32x4){v[c][i], v[c][i + 1], v[c][i + 2], v[c][i + 3]},
@@ -910,6 +928,18 @@ int launch_gemm_i8q(hipStream_t s, GemmArgs p, bool tok = false) {
     return launch_p<256, 128, 8, 1, EPI_I8Q>(s, p);
 }
 
+int launch_gemm_gelumul(hipStream_t s, GemmArgs p) {
+    if (check_args(p, "i8_gemm_gelu_mul")) return -1;
+    if (p.N % 128 || !p.Yq || !p.ys || p.ldyq < p.N || p.ldyq % 16 || !aligned16(p.Yq) ||
+        p.ldys < p.N / 128 || !p.mul || p.ldmul < p.N || p.ldmul % 4 || !aligned16(p.mul) ||
+        (p.Y && (p.ldy < p.N || p.ldy % 4 || !aligned16(p.Y)))) {
+        set_error("i8_gemm_gelu_mul: N must be a multiple of 128; outputs and multiplier 16-byte aligned");
+        return -1;
+    }
+    if (small_grid(p)) return launch_p<128, 128, 4, 1, EPI_GELUMUL>(s, p);
+    return launch_p<256, 128, 8, 1, EPI_GELUMUL>(s, p);
+}
+
 int launch_gemm_geglu(hipStream_t s, GemmArgs p) {
     if (check_args(p, "i8_gemm_geglu")) return -1;
     if (p.N % 256 || !p.Yq || !p.ys || p.ldyq < p.N / 2 || p.ldyq % 16 || !aligned16(p.Yq) ||
@@ -1026,6 +1056,22 @@ extern "C" int e2mi_i8_gemm_tok_q(e2mi_stream stream, int8_t *yq, float *ys, con
     p.ys = ys;
     p.ldys = w->N / 128;
     return launch_gemm_i8q((hipStream_t)stream, p, true);
+}
+
+extern "C" int e2mi_i8_gemm_gelu_mul(e2mi_stream stream, int8_t *yq, float *ys, float *g, const int8_t *qa,
+                                     const float *a_scales, const e2mi_q8w *w, int M, const float *mul,
+                                     int ldmul) {
+    if (!weight_ok(w, "i8_gemm_gelu_mul")) return -1;
+    GemmArgs p = make_args(qa, a_scales, w, M, 0, w->N);
+    p.Yq = yq;
+    p.ldyq = w->N;
+    p.ys = ys;
+    p.ldys = w->N / 128;
+    p.Y = g;
+    p.ldy = w->N;
+    p.mul = mul;
+    p.ldmul = ldmul;
+    return launch_gemm_gelumul((hipStream_t)stream, p);
 }
 
 extern "C" int e2mi_i8_gemm_geglu(e2mi_stream stream, int8_t *q, float *qs, float *g,

@@ -74,6 +74,7 @@ SIGNATURES = {
                                           _P, _I]),
     "e2mi_add_norm_scale_quant": (_I, [_P, _P, _P, _P, _F, _P, _F, _I, _I, _P, _P, _P, _P]),
     "e2mi_scale_norm": (_I, [_P, _P, _I, _I, _F, _P, _F, _P]),
+    "e2mi_i8_gemm_gelu_mul": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(Q8W), _I, _P, _I]),
     "e2mi_attention_i8_workspace_bytes": (C.c_size_t, [_I, _I, _I, _I, _I]),
     "e2mi_attention_i8_packed": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I]),
     "e2mi_pool_l2_packed": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
@@ -281,6 +282,20 @@ def i8_gemm_tok_q(qa, as_, w: DeviceWeight, stream=None):
     check(load().e2mi_i8_gemm_tok_q(stream_ptr(stream), ptr(yq), ptr(ys), ptr(qa), ptr(as_), w.ref, M),
           "i8_gemm_tok_q")
     return yq, ys
+
+
+def i8_gemm_gelu_mul(qa, as_, w: DeviceWeight, mul, want_g=True, stream=None):
+    """q, qs = quantize(gelu_tanh(qa . W) * mul) per 128 (the PLE gate, text.c:906-913); mul may be a
+    column slice of a wider row-major f32 tensor. Returns (q, qs, g)."""
+    import torch
+    M = qa.shape[0]
+    N = w.q.N
+    q = torch.empty((M, N), dtype=torch.int8, device=qa.device)
+    qs = torch.empty((M, N // 128), dtype=torch.float32, device=qa.device)
+    g = torch.empty((M, N), dtype=torch.float32, device=qa.device) if want_g else None
+    check(load().e2mi_i8_gemm_gelu_mul(stream_ptr(stream), ptr(q), ptr(qs), ptr(g), ptr(qa), ptr(as_),
+                                       w.ref, M, ptr(mul), mul.stride(0)), "i8_gemm_gelu_mul")
+    return q, qs, g
 
 
 def i8_gemm_geglu(qa, as_, w: DeviceWeight, want_g=True, stream=None):

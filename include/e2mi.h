@@ -74,6 +74,15 @@ int e2mi_i8_gemm(e2mi_stream stream, float *y, int ldy, const int8_t *qa, const 
 int e2mi_i8_gemm_acc(e2mi_stream stream, float *y, int ldy, int32_t *acc, const int8_t *qa,
                      const float *a_scales, const e2mi_q8w *w, int M, int n0, int n1);
 
+/* The reference checkpoint's PLE gate (text.c:906-913: gemm into gate, gate_quant with the layer's
+ * per-layer-input slice as `up`): g = gelu_tanh(qa . W) * mul[m][n], quantized per (row, 128
+ * columns) into yq [M][N] / ys [M][N/128] for the PLE projection GEMM; g [M][N] f32 also written
+ * when non-NULL. mul [M][ldmul] (the slice of [rows][n_layers * ple_dim] at column l * ple_dim),
+ * N % 128 == 0, 16-byte aligned rows. GELU within the reference's bar (test_gpu_ffn.c:104). */
+int e2mi_i8_gemm_gelu_mul(e2mi_stream stream, int8_t *yq, float *ys, float *g, const int8_t *qa,
+                          const float *a_scales, const e2mi_q8w *w, int M, const float *mul,
+                          int ldmul);
+
 /* GEMM whose epilogue requantizes the output per (row, 128 columns) for the next GEMM instead of
  * writing f32: the quantization the reference runs on y (text.c:321-339), fused. N % 128 == 0.
  * yq [M][N] int8, ys [M][N/128]. */

@@ -156,6 +156,31 @@ def test_add_norm_scale_quant_and_scale_norm(gpu, oracle, rng):
     assert_f32_close(_np(t), want, rtol=1e-5, atol=1e-6, what="scale_norm")
 
 
+@pytest.mark.parametrize("M", [4096, 1000])
+def test_ple_gate_gemm_gelu_mul(gpu, oracle, rng, M):
+    """The PLE gate GEMM with gelu(gate) * ple slice quantized in its epilogue (text.c:906-913),
+    the slice a column range of the [rows][layers * 512] per-layer inputs."""
+    import e2mi
+    K = N = 512
+    qa = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    as_ = rng.uniform(0.001, 0.01, (M, K // 128)).astype(np.float32)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    ple = rng.standard_normal((M, 3 * N)).astype(np.float32)
+    W = e2mi.DeviceWeight.from_rowmajor(w, ws)
+    pt = _t(ple, gpu)
+    q, qs, g = e2mi.i8_gemm_gelu_mul(_t(qa, gpu), _t(as_, gpu), W, pt[:, N:2 * N])
+    gate = oracle.i8_gemm(qa, as_, w, ws)
+    go, _, _ = oracle.gelu_mul_quant(gate, np.ascontiguousarray(ple[:, N:2 * N]))
+    gk = _np(g)
+    assert_f32_close(gk, go, rtol=1e-4, atol=1e-4, what="gelu(gate) * ple")
+    qo, so = oracle.quantize(gk)
+    assert np.array_equal(_np(q), qo) and np.array_equal(_np(qs).view(np.uint32), so.view(np.uint32))
+    # the slice of another layer gives other bytes: the multiplier is read at its own columns
+    q2, _, _ = e2mi.i8_gemm_gelu_mul(_t(qa, gpu), _t(as_, gpu), W, pt[:, 2 * N:], want_g=False)
+    assert not np.array_equal(_np(q2), _np(q))
+
+
 @pytest.fixture(scope="module")
 def ref_setup(gpu):
     import e2mi
