@@ -226,18 +226,12 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
 }
 
 // ---- packed batches: the same attention with K/V tiles fetched straight into LDS one tile ahead,
-// for head_dim D = 256 or 512 (the reference checkpoint's full-attention layers), with an optional
-// sliding window. Every key of a packed sequence is valid, so no mask is read; the per-sequence
+// with an optional sliding window (head_dim 256; k_attn_packed_d512 below takes 512). Every key of a packed sequence is valid, so no mask is read; the per-sequence
 // work at D = 256 without a window is the arithmetic of k_attn bit for bit (same MFMA order, same
 // softmax; masked keys read as zero here and contribute p = 0 in both).
 //
-// At D = 512 a workgroup computes the logits over all 512 dims but owns half of the context dims
-// (DO = 256): Q fragments and a whole context take more registers than a lane has (measured: 223
-// spilled), so the two halves go to two workgroups (grid y, or work-list grid y), each reading the
-// K tiles and its half of the V^T tiles.
-//
-// LDS per workgroup: 2 buffers of [K tile 32 keys x 2D B | V^T tile DO rows x 64 B] (64 KB at
-// D = 256, two workgroups per CU; 96 KB at D = 512, one).
+// LDS per workgroup: 2 buffers of [K tile 32 keys x 2D B | V^T tile D rows x 64 B] (64 KB at
+// D = 256, two workgroups per CU).
 //   K tile row i holds key swap23(i) (bits 2 and 3 of the index exchanged). The S^T MFMA then
 //     leaves in a lane's registers 8 j + e (e = 0..7) the keys 16 j + 8 half + e: consecutive keys,
 //     so the PV MFMA's A operand is one 16-byte chunk of a V^T row in natural key order.
@@ -246,7 +240,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
 //   V^T rows (one d, 32 keys) are 64 B; chunk c of row d sits at position c ^ ((d >> 2) & 3)
 //     (conflict-free for rows d..d+7).
 // The tile loads are 16-byte direct-to-LDS buffer loads: D/64 per wave for K (512/D rows each) and
-// DO/64 for V^T (16 rows each), whose lanes fetch the permuted, swizzled source chunks. Keys past
+// D/64 for V^T (16 rows each), whose lanes fetch the permuted, swizzled source chunks. Keys past
 // the sequence read as zero (K: past the descriptor's range; V^T: 8-key chunks past the sequence
 // get an offset past it, and the sequence's rows end on an 8-row boundary of the slab).
 //
@@ -258,8 +252,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
 // block's first and last query) needs no per-key test.
 template <int D>
 struct PackedTile {
-    static constexpr int kDO = D < 256 ? D : 256, kSplit = D / kDO;  // context dims per workgroup
-    static constexpr int kK = kKT * 2 * D, kV = kDO * 64, kBuf = kK + kV;
+    static constexpr int kK = kKT * 2 * D, kV = D * 64, kBuf = kK + kV;
     static constexpr size_t kLds = 2 * (size_t)kBuf;
 };
 
@@ -276,13 +269,11 @@ __device__ inline int swap23(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 
 template <int D>
 __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs a) {
     using T = PackedTile<D>;
-    constexpr int DO = T::kDO;
     // Q fragments, O tiles, K and V^T loads per wave and tile
-    constexpr int NQ = D / 16, NO = DO / 32, NLK = D / 64, NLV = DO / 64;
+    constexpr int NQ = D / 16, NO = D / 32, NLK = D / 64, NLV = D / 64;
     constexpr int RPI = 512 / D, LPR = D / 8;  // K rows per load, lanes per K row
     extern __shared__ __align__(16) unsigned char pk_smem[];
-    int qb = blockIdx.x, h = blockIdx.y / T::kSplit, b = blockIdx.z;
-    const int dh = blockIdx.y % T::kSplit;  // which DO context dims: a.work grids put it in y too
+    int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     if (a.work) {
         const int item = a.work[blockIdx.x];
         if (item < 0) return;
@@ -329,15 +320,15 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
     // sources: K rows of this kv head (row pitch KV*D halves), V^T slab [D][S] of this kv head
     const uint32_t rowB = (uint32_t)a.KV * D * 2;
     const v4u rK = rsrc_words(a.k + row0 * a.KV * D + kvh * D, (uint32_t)Sk * rowB);
-    const uint16_t *vslab = a.vt + ((size_t)kvh * D + dh * DO) * S + row0;
-    const v4u rV = rsrc_words(vslab, (uint32_t)((size_t)DO * S * 2));
+    const uint16_t *vslab = a.vt + (size_t)kvh * D * S + row0;
+    const v4u rV = rsrc_words(vslab, (uint32_t)((size_t)D * S * 2));
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)pk_smem);
     const int wu = __builtin_amdgcn_readfirstlane(w);
     const int lr = lane / LPR, lc = lane % LPR;
     // K: load i of wave w fills LDS rows 8 w + RPI i + lane / LPR, i.e. keys swap23 of those
     // (swap23 keeps bit 0, so the second row of a D = 256 load is the next key); lane's chunk
     // position lane % LPR holds source chunk (lane % LPR) ^ (row & 7).
-    // V^T: load i of wave w fills rows d = (DO/4) w + 16 i + lane / 4, chunk position lane % 4,
+    // V^T: load i of wave w fills rows d = (D/4) w + 16 i + lane / 4, chunk position lane % 4,
     // which holds source chunk (lane % 4) ^ ((d >> 2) & 3) = (lane % 4) ^ ((lane >> 4) & 3).
     const uint32_t vlane = (uint32_t)(lane >> 2) * (uint32_t)S * 2;
     const int vchunk = (lane & 3) ^ ((lane >> 4) & 3);
@@ -353,7 +344,7 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
             const uint32_t voff = (uint32_t)(swap23(r) + k0 + lr) * rowB + (uint32_t)((lc ^ ((r + lr) & 7)) << 4);
             dma16_nc(rK, __builtin_amdgcn_readfirstlane(base + (uint32_t)r * (2 * D)), voff, 0u);
         } else {
-            const int i = j - NLK, d0 = (DO / 4) * wu + 16 * i;
+            const int i = j - NLK, d0 = (D / 4) * wu + 16 * i;
             const uint32_t vo = (k0 + 8 * vchunk < Sk) ? vlane + (uint32_t)vchunk * 16 : 0x80000000u;
             dma16_nc(rV, __builtin_amdgcn_readfirstlane(base + T::kK + d0 * 64), vo,
                      __builtin_amdgcn_readfirstlane((uint32_t)(d0 * S + k0) * 2));
@@ -458,9 +449,225 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
     for (int t = 0; t < NO; t++) o[t] *= inv;
     if (qi >= Sk) return;  // rows past the sequence belong to the next one
     const size_t orow = (row0 + qi);
-    const int dof = dh * DO;  // this workgroup's first context dim
 #pragma unroll
-    for (int blk = 0; blk < DO / 128; blk++) {
+    for (int blk = 0; blk < D / 128; blk++) {
+        float am = 0.f;
+#pragma unroll
+        for (int t = 4 * blk; t < 4 * blk + 4; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) am = fmaxf(am, fabsf(o[t][r]));
+        am = fmaxf(am, __shfl_xor(am, 32));
+        const QScale qs = qscale(am);
+#pragma unroll
+        for (int t = 4 * blk; t < 4 * blk + 4; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int d = 32 * t + 8 * g + 4 * half;
+                *(uint32_t *)(a.cq + orow * HD + h * D + d) =
+                    pack4(qbyte(o[t][4 * g], qs.inv), qbyte(o[t][4 * g + 1], qs.inv),
+                          qbyte(o[t][4 * g + 2], qs.inv), qbyte(o[t][4 * g + 3], qs.inv));
+                if (a.c32)
+                    *(float4 *)(a.c32 + orow * HD + h * D + d) =
+                        make_float4(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]);
+            }
+        if (half == 0) a.cs[orow * (HD / kQBlock) + h * (D / 128) + blk] = qs.sc;
+    }
+}
+
+// ---- head_dim 512 (the reference checkpoint's full-attention layers): one 8-wave workgroup per
+// (sequence, head, 128 queries). Waves w and w + 4 own the same 32 queries; wave w computes the
+// logits over dims 0..255 and wave w + 4 over 256..511 (each holds only its half of the Q
+// fragments), they add each other's partial logits through LDS, run the same softmax on the same
+// sums, and each accumulates the context for its own 256 dims. The MFMA work is that of one pass
+// (4 L^2 512 flops per head) and two waves share each SIMD.
+//
+// LDS: 2 buffers of [K tile 32 keys x 1024 B | V^T tile 512 rows x 64 B] (64 KB each), then the
+// partial-logit exchange, 8 waves x 64 lanes x 16 floats (32 KB): 160 KB, one workgroup per CU.
+// Tile layouts and swizzles are those of k_attn_packed (K row i holds key swap23(i), chunk x at
+// x ^ (i & 7); V^T chunk c of row d at c ^ ((d >> 2) & 3)). Per tile: wait for its loads and a
+// barrier; the partial S^T (16 MFMAs, the next tile's 8 loads per wave between them); write the
+// partial logits; a barrier; read the partner's, softmax, PV (16 MFMAs). The exchange area is
+// written after the first barrier of a tile and read before the first barrier of the next.
+constexpr int kK512 = kKT * 1024, kV512 = 512 * 64, kBuf512 = kK512 + kV512;
+constexpr int kXch512 = 8 * 64 * 16 * 4;
+constexpr size_t kLds512 = 2 * (size_t)kBuf512 + kXch512;
+
+__global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
+    constexpr int D = 512, DH = 256;
+    extern __shared__ __align__(16) unsigned char pk_smem[];
+    int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    if (a.work) {
+        const int item = a.work[blockIdx.x];
+        if (item < 0) return;
+        b = item & 0xffff;
+        h = (item >> 16) & 0xff;
+        qb = item >> 24;
+    }
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5;
+    const int qw = w & 3, dh = w >> 2;  // query sub-block, dim half
+    const int S = a.S, HD = a.H * D, kvh = h / (a.H / a.KV);
+    const size_t row0 = (size_t)a.seq_start[b];
+    const int Sk = a.seq_len[b];
+    if (qb * 128 >= Sk) return;
+
+    const int qi = qb * 128 + qw * 32 + (lane & 31);
+    const bool qvalid = qi < Sk;
+    const int qc = min(qi, Sk - 1);
+    h8 qf[16];  // this wave's 256 dims of the query
+    {
+        const uint16_t *qp = a.q + (row0 + qc) * HD + h * D + dh * DH + 8 * half;
+#pragma unroll
+        for (int s = 0; s < 16; s++) qf[s] = *(const h8 *)(qp + 16 * s);
+    }
+    const int W = a.window;
+    int kt0 = 0, kt1 = (Sk + kKT - 1) / kKT;
+    int pq0 = 0, pq1 = 0, pqi = qc;
+    if (W > 0) {
+        const int q0 = qb * 128, q1 = min(q0 + 127, Sk - 1);
+        kt0 = max(q0 - W, 0) / kKT;
+        kt1 = min((min(q1 + W, Sk - 1)) / kKT + 1, kt1);
+        pq0 = a.pos ? a.pos[row0 + q0] : q0;
+        pq1 = a.pos ? a.pos[row0 + q1] : q1;
+        pqi = a.pos ? a.pos[row0 + qc] : qc;
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // the Q loads, before the tile loop (see k_attn_packed)
+    f16v o[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) o[t] = (f16v){};
+    float mrun = -INFINITY, lrun = 0.f;
+
+    const uint32_t rowB = (uint32_t)a.KV * D * 2;
+    const v4u rK = rsrc_words(a.k + row0 * a.KV * D + kvh * D, (uint32_t)Sk * rowB);
+    const uint16_t *vslab = a.vt + (size_t)kvh * D * S + row0;
+    const v4u rV = rsrc_words(vslab, (uint32_t)((size_t)D * S * 2));
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)pk_smem);
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    // K: load i of wave w fills row r = 4 w + i (key swap23(r)), lane = chunk position holding
+    // source chunk lane ^ (r & 7); V^T: load i of wave w fills rows d = 64 w + 16 i + lane / 4
+    const uint32_t vlane = (uint32_t)(lane >> 2) * (uint32_t)S * 2;
+    const int vchunk = (lane & 3) ^ ((lane >> 4) & 3);
+    auto issue_load = [&](int kt, int j) {
+        const int k0 = kt * kKT;
+        const uint32_t base = lds0 + (uint32_t)((kt & 1) * kBuf512);
+        if (j < 4) {
+            const int r = 4 * wu + j;
+            const uint32_t voff = (uint32_t)(swap23(r) + k0) * rowB + (uint32_t)((lane ^ (r & 7)) << 4);
+            dma16_nc(rK, __builtin_amdgcn_readfirstlane(base + (uint32_t)r * 1024), voff, 0u);
+        } else {
+            const int d0 = 64 * wu + 16 * (j - 4);
+            const uint32_t vo = (k0 + 8 * vchunk < Sk) ? vlane + (uint32_t)vchunk * 16 : 0x80000000u;
+            dma16_nc(rV, __builtin_amdgcn_readfirstlane(base + kK512 + d0 * 64), vo,
+                     __builtin_amdgcn_readfirstlane((uint32_t)(d0 * S + k0) * 2));
+        }
+    };
+    const int kkey = lane & 31;
+    uint32_t krd[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        krd[u] = (uint32_t)(kkey * 1024 + dh * 512 + (((2 * u + half) ^ (kkey & 7)) << 4));
+    uint32_t vrd[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+        vrd[j] = (uint32_t)(kK512 + (dh * DH + (lane & 31)) * 64 + (((2 * j + half) ^ (((lane & 31) >> 2) & 3)) << 4));
+    float *xw = (float *)(pk_smem + 2 * kBuf512) + (w * 64 + lane) * 16;          // this wave's slot
+    const float *xp = (const float *)(pk_smem + 2 * kBuf512) + ((w ^ 4) * 64 + lane) * 16;  // partner's
+
+    if (kt0 < kt1)
+#pragma unroll
+        for (int j = 0; j < 8; j++) issue_load(kt0, j);
+    for (int kt = kt0; kt < kt1; kt++) {
+        const int k0 = kt * kKT;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const bool next = kt + 1 < kt1;
+        const unsigned char *sb = pk_smem + (kt & 1) * kBuf512;
+        f16v st = (f16v){};
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const h8 kf = *(const h8 *)(sb + krd[s & 3] + (s >> 2) * 128);
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
+            if ((s & 1) && next) issue_load(kt + 1, s >> 1);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r += 4) *(float4 *)(xw + r) = make_float4(st[r], st[r + 1], st[r + 2], st[r + 3]);
+        __syncthreads();
+        float sfull[16];
+#pragma unroll
+        for (int r = 0; r < 16; r += 4) {
+            const float4 x = *(const float4 *)(xp + r);
+            // one rounded addition, commutative: both waves of the pair get the same sums
+            sfull[r] = st[r] + x.x;
+            sfull[r + 1] = st[r + 1] + x.y;
+            sfull[r + 2] = st[r + 2] + x.z;
+            sfull[r + 3] = st[r + 3] + x.w;
+        }
+        bool edge = false;
+        if (W > 0) {
+            const int ka = k0, kb = min(k0 + kKT, Sk) - 1;
+            const int pka = a.pos ? a.pos[row0 + ka] : ka, pkb = a.pos ? a.pos[row0 + kb] : kb;
+            edge = pkb - pq0 > W || pq1 - pka > W;
+        }
+        float tv[16];
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int key = 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
+            bool keep = k0 + key < Sk;
+            if (edge && keep) {
+                const int pk = a.pos ? a.pos[row0 + k0 + key] : k0 + key;
+                keep = pk - pqi <= W && pqi - pk <= W;
+            }
+            tv[r] = keep ? sfull[r] * a.scale : -INFINITY;
+            mloc = fmaxf(mloc, tv[r]);
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        const float mnew = fmaxf(mrun, mloc);
+        float alpha = 1.f;
+        float psum = 0.f;
+        _Float16 ph[16];
+        if (mnew == -INFINITY) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) ph[r] = (_Float16)0.f;
+        } else {
+            alpha = __expf(mrun - mnew);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float pr = tv[r] == -INFINITY ? 0.f : __expf(tv[r] - mnew);
+                psum += pr;
+                ph[r] = (_Float16)pr;
+            }
+        }
+        lrun = lrun * alpha + psum;
+        mrun = mnew;
+        if (__any(alpha != 1.f)) {
+#pragma unroll
+            for (int t = 0; t < 8; t++) o[t] *= alpha;
+        }
+        h8 pb[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) pb[j][e] = ph[8 * j + e];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const h8 vf = *(const h8 *)(sb + vrd[j] + t * 32 * 64);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[j], o[t], 0, 0, 0);
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    const float ltot = lrun + __shfl_xor(lrun, 32);
+    const float inv = (qvalid && ltot > 0.f) ? __fdiv_rn(1.0f, ltot) : 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; t++) o[t] *= inv;
+    if (qi >= Sk) return;
+    const size_t orow = (row0 + qi);
+    const int dof = dh * DH;
+#pragma unroll
+    for (int blk = 0; blk < 2; blk++) {
         float am = 0.f;
 #pragma unroll
         for (int t = 4 * blk; t < 4 * blk + 4; t++)
@@ -480,7 +687,7 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
                     *(float4 *)(a.c32 + orow * HD + h * D + d) =
                         make_float4(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]);
             }
-        if (half == 0) a.cs[orow * (HD / kQBlock) + h * (D / 128) + dof / 128 + blk] = qs.sc;
+        if (half == 0) a.cs[orow * (HD / kQBlock) + h * 4 + dh * 2 + blk] = qs.sc;
     }
 }
 
@@ -547,14 +754,20 @@ static int attention_packed(const char *who, e2mi_stream stream, const uint16_t 
     // multiples of 8)
     const bool direct = M % 2 == 0 && (size_t)KV * D * M * 2 < 0x7fffffffu &&
                         (size_t)M * KV * D * 2 < 0x7fffffffu && ((uintptr_t)vt16 & 3) == 0;
-    const int split = D == 512 ? PackedTile<512>::kSplit : 1;
-    const dim3 grid = work ? dim3(n_work, split) : dim3((max_len + 127) / 128, H * split, B);
+    const dim3 grid = work ? dim3(n_work) : dim3((max_len + 127) / 128, H, B);
     if (direct && D == 256) {
         if (attn_packed_attr<256>()) return -1;
         hipLaunchKernelGGL(k_attn_packed<256>, grid, dim3(256), PackedTile<256>::kLds, (hipStream_t)stream, a);
     } else if (direct) {
-        if (attn_packed_attr<512>()) return -1;
-        hipLaunchKernelGGL(k_attn_packed<512>, grid, dim3(256), PackedTile<512>::kLds, (hipStream_t)stream, a);
+        static bool attr512 = false;
+        if (!attr512) {
+            if (check_hip(hipFuncSetAttribute((const void *)k_attn_packed_d512,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds512),
+                          "attention lds attribute"))
+                return -1;
+            attr512 = true;
+        }
+        hipLaunchKernelGGL(k_attn_packed_d512, grid, dim3(512), kLds512, (hipStream_t)stream, a);
     } else if (D == 256 && window == 0) {
         a.work = nullptr;
         hipLaunchKernelGGL(k_attn, dim3((max_len + 127) / 128, H, B), dim3(256), 0, (hipStream_t)stream, a);
