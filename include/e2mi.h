@@ -206,8 +206,8 @@ int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, const uint16_
 /* The same for the reference checkpoint's layers (text.c:467-478, 534-572): head_dim D = 256 or 512
  * and, when window > 0, the sliding window: query i reads key j only when |pos_i - pos_j| <= window
  * (text.c:542-546), pos [M] being each row's position in its padded sequence (the pos table of
- * e2mi_qkv_norm_rope_packed; NULL: the packed index). At D = 512 each work entry runs as two
- * workgroups (256 context dims each). Needs M even and vt16 4-byte aligned. */
+ * e2mi_qkv_norm_rope_packed; NULL: the packed index). At D = 512 each work entry runs as one
+ * 512-thread workgroup. Needs M even and vt16 4-byte aligned. */
 int e2mi_attention_packed_window(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
                                  const uint16_t *vt16, int M, const int32_t *seq_start,
                                  const int32_t *seq_len, const int32_t *pos, int B, int max_len,
