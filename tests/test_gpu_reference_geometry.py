@@ -235,3 +235,15 @@ def test_engine_reference_geometry_refusals(ref_setup):
         eng.set_packing(False)
     with pytest.raises(e2mi.E2MIError, match="int8 attention"):
         eng.set_attention("i8")
+
+
+def test_engine_reference_geometry_from_e8cq(ref_setup, rng, tmp_path):
+    """The production weight path at this geometry (an E8CQ cache with the PLE / embed_proj tensors,
+    q8cache.c:242-385, re-laid out on the device) gives the in-memory model's embeddings, bit for bit."""
+    e2mi, o, m, eng = ref_setup
+    p = str(tmp_path / "ref.e8cq")
+    m.save_e8cq(p)
+    m2 = e2mi.Model.load_e8cq(p, m.config)
+    eng2 = e2mi.Engine(m2, max_rows=4096)
+    ids, valid = random_batch(rng, 3, 700, 1000, min_len=100)
+    assert np.array_equal(eng2.embed_batch(ids, valid), eng.embed_batch(ids, valid))
