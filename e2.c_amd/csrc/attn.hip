@@ -266,7 +266,7 @@ __device__ inline void dma16_nc(v4u r, uint32_t lds, uint32_t voff, uint32_t sof
 
 __device__ inline int swap23(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
-template <int D>
+template <int D, bool WIN>
 __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs a) {
     using T = PackedTile<D>;
     // Q fragments, O tiles, K and V^T loads per wave and tile
@@ -297,10 +297,10 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
         for (int s = 0; s < NQ; s++) qf[s] = *(const h8 *)(qp + 16 * s);
     }
     // key tiles of this block: all, or those within window of its rows (by packed index)
-    const int W = a.window;
+    const int W = WIN ? a.window : 0;
     int kt0 = 0, kt1 = (Sk + kKT - 1) / kKT;
     int pq0 = 0, pq1 = 0, pqi = qc;
-    if (W > 0) {
+    if constexpr (WIN) {
         const int q0 = qb * 128, q1 = min(q0 + 127, Sk - 1);
         kt0 = max(q0 - W, 0) / kKT;
         kt1 = min((min(q1 + W, Sk - 1)) / kKT + 1, kt1);
@@ -338,11 +338,12 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
         const int k0 = kt * kKT;
         const uint32_t base = lds0 + (uint32_t)((kt & 1) * T::kBuf);
         if (j < NLK) {
-            // the key row goes into the per-lane offset, which the descriptor's range check covers:
-            // keys past the sequence read as zero without touching memory past it
+            // the first row's key goes to the scalar offset (range-checked with the lane offset:
+            // keys past the sequence read as zero)
             const int i = j, r = 8 * wu + RPI * i;
-            const uint32_t voff = (uint32_t)(swap23(r) + k0 + lr) * rowB + (uint32_t)((lc ^ ((r + lr) & 7)) << 4);
-            dma16_nc(rK, __builtin_amdgcn_readfirstlane(base + (uint32_t)r * (2 * D)), voff, 0u);
+            const uint32_t voff = (uint32_t)lr * rowB + (uint32_t)((lc ^ ((r + lr) & 7)) << 4);
+            dma16_nc(rK, __builtin_amdgcn_readfirstlane(base + (uint32_t)r * (2 * D)), voff,
+                     __builtin_amdgcn_readfirstlane((uint32_t)(swap23(r) + k0) * rowB));
         } else {
             const int i = j - NLK, d0 = (D / 4) * wu + 16 * i;
             const uint32_t vo = (k0 + 8 * vchunk < Sk) ? vlane + (uint32_t)vchunk * 16 : 0x80000000u;
@@ -384,7 +385,7 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
         }
         // window: a tile inside the window of every query of the block needs no per-key test
         bool edge = false;
-        if (W > 0) {
+        if constexpr (WIN) {
             const int ka = k0, kb = min(k0 + kKT, Sk) - 1;
             const int pka = a.pos ? a.pos[row0 + ka] : ka, pkb = a.pos ? a.pos[row0 + kb] : kb;
             edge = pkb - pq0 > W || pq1 - pka > W;
@@ -691,11 +692,11 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
     }
 }
 
-template <int D>
+template <int D, bool WIN>
 static int attn_packed_attr() {
     static bool done = false;
     if (!done) {
-        if (check_hip(hipFuncSetAttribute((const void *)k_attn_packed<D>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (check_hip(hipFuncSetAttribute((const void *)k_attn_packed<D, WIN>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                           (int)PackedTile<D>::kLds), "attention lds attribute"))
             return -1;
         done = true;
@@ -755,9 +756,12 @@ static int attention_packed(const char *who, e2mi_stream stream, const uint16_t 
     const bool direct = M % 2 == 0 && (size_t)KV * D * M * 2 < 0x7fffffffu &&
                         (size_t)M * KV * D * 2 < 0x7fffffffu && ((uintptr_t)vt16 & 3) == 0;
     const dim3 grid = work ? dim3(n_work) : dim3((max_len + 127) / 128, H, B);
-    if (direct && D == 256) {
-        if (attn_packed_attr<256>()) return -1;
-        hipLaunchKernelGGL(k_attn_packed<256>, grid, dim3(256), PackedTile<256>::kLds, (hipStream_t)stream, a);
+    if (direct && D == 256 && window > 0) {
+        if (attn_packed_attr<256, true>()) return -1;
+        hipLaunchKernelGGL((k_attn_packed<256, true>), grid, dim3(256), PackedTile<256>::kLds, (hipStream_t)stream, a);
+    } else if (direct && D == 256) {
+        if (attn_packed_attr<256, false>()) return -1;
+        hipLaunchKernelGGL((k_attn_packed<256, false>), grid, dim3(256), PackedTile<256>::kLds, (hipStream_t)stream, a);
     } else if (direct) {
         static bool attr512 = false;
         if (!attr512) {

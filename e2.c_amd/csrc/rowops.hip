@@ -18,7 +18,8 @@
 
 namespace e2mi {
 
-enum { ROW_PLAIN = 0, ROW_EMBED = 1, ROW_ADDNORM = 2 };
+// ROW_ADDSCALE: ROW_ADDNORM with x scaled after the add and, without gamma_n, x itself quantized
+enum { ROW_PLAIN = 0, ROW_EMBED = 1, ROW_ADDNORM = 2, ROW_ADDSCALE = 3 };
 
 struct RowArgs {
     const float *src;      // PLAIN/ADDNORM input rows [M][D] (ld = D)
@@ -81,8 +82,8 @@ __global__ __launch_bounds__(256) void k_rows(RowArgs a) {
                                __fmul_rn(v[i].z, escale), __fmul_rn(v[i].w, escale));
         ss += sumsq4(v[i]);
     }
-    if (MODE == ROW_ADDNORM) {
-        // x = rmsnorm(src) * gamma_a + res
+    if (MODE == ROW_ADDNORM || MODE == ROW_ADDSCALE) {
+        // x = rmsnorm(src) * gamma_a + res (ROW_ADDSCALE: then * post_scale)
         const float inv = rms_inv(group_sum<64>(ss), D, a.eps);
         ss = 0.f;
 #pragma unroll
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(256) void k_rows(RowArgs a) {
                 const float4 g = ld4(a.gamma_a + 4 * c), r = ld4(a.res + (size_t)m * D + 4 * c);
                 const float4 t = scale4(v[i], inv, g);
                 v[i] = make_float4(t.x + r.x, t.y + r.y, t.z + r.z, t.w + r.w);
-                if (a.post_scale != 1.f)
+                if (MODE == ROW_ADDSCALE)
                     v[i] = make_float4(__fmul_rn(v[i].x, a.post_scale), __fmul_rn(v[i].y, a.post_scale),
                                        __fmul_rn(v[i].z, a.post_scale), __fmul_rn(v[i].w, a.post_scale));
             }
@@ -104,6 +105,7 @@ __global__ __launch_bounds__(256) void k_rows(RowArgs a) {
         for (int i = 0; i < NC; i++)
             if (l + 64 * i < nch) st4(a.x_out + (size_t)m * D + 4 * (l + 64 * i), v[i]);
     }
+    if (MODE != ROW_ADDSCALE && !a.gamma_n) return;
     if (a.gamma_n) {
         const float inv = rms_inv(group_sum<64>(ss), D, a.eps);
 #pragma unroll
@@ -262,7 +264,8 @@ __global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a, int nv) {
         const float4 c = ld4(cp + 4 * l), s = ld4(sp + 4 * l);
         const float4 o = make_float4(__shfl_xor(v[0].x, 32), __shfl_xor(v[0].y, 32), __shfl_xor(v[0].z, 32),
                                      __shfl_xor(v[0].w, 32));
-        v[0] = l < 32 ? rot_lo(v[0], o, c, s) : rot_hi(v[0], o, c, s);
+        if (l < 32) v[0] = rot_lo(v[0], o, c, s);
+        else v[0] = rot_hi(v[0], o, c, s);
     } else {
         const float4 c = ld4(cp + 4 * l), s = ld4(sp + 4 * l);
         const float4 x0 = v[0], x1 = v[NCH - 1];
@@ -415,6 +418,7 @@ static int row_launch(hipStream_t s, int mode, const RowArgs &a) {
     }
     if (mode == ROW_EMBED) { ROWK(ROW_EMBED) }
     else if (mode == ROW_ADDNORM) { ROWK(ROW_ADDNORM) }
+    else if (mode == ROW_ADDSCALE) { ROWK(ROW_ADDSCALE) }
     else { ROWK(ROW_PLAIN) }
 #undef ROWK
     return check_hip(hipGetLastError(), "row kernel launch");
@@ -498,7 +502,7 @@ extern "C" int e2mi_add_norm_scale_quant(e2mi_stream stream, const float *src, c
     RowArgs a = {};
     a.src = src; a.res = res; a.gamma_a = gamma_add; a.gamma_n = gamma_next; a.eps = eps;
     a.x_out = x_out; a.xn_out = xn_out; a.q = q; a.qs = qs; a.M = M; a.D = D; a.post_scale = post_scale;
-    return launch_rows((hipStream_t)stream, ROW_ADDNORM, a);
+    return launch_rows((hipStream_t)stream, ROW_ADDSCALE, a);
 }
 
 extern "C" int e2mi_scale_norm(e2mi_stream stream, const float *x, int rows, int D, float pre_scale,
