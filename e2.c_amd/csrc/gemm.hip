@@ -247,12 +247,15 @@ constexpr int p_lds_bytes() {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-// cache policy of the f32 output stores: sc0 | nt (non-temporal, streamed past the caches). The
-// outputs are written once and read by the next kernel; measured on the per-token f32 sweep at
-// M = 65536: 1124 -> 1350 TOPS (768x1280: 121.5 -> 96.6 us) against the default policy
+// cache policy of the per-token kernel's output stores (epilogues with NT = true): sc0 | nt
+// (non-temporal, streamed past the caches). Measured on the per-token f32 sweep at M = 65536, whose
+// outputs nothing re-reads: 1124 -> 1350 TOPS (768x1280: 121.5 -> 96.6 us) against the default
+// policy. The per-128 kernel keeps the default: in the encoder's forward the next kernel reads its
+// outputs at once, and streaming them cost 2 % end to end. A runtime choice between the two (a
+// uniform branch per store) cost the epilogues 2-5 %, so it is per kernel, at compile time.
 constexpr int kStoreNT = 3;
 
-template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, bool NT = false>
 __device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArgs &p, float (&f)[4][16],
                                                                    const float (&wsr)[4], int m0, int n0,
                                                                    int wave, int wm, int wn, int lane,
@@ -347,17 +350,22 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArg
 #pragma unroll
             for (int i = 0; i < CPL / 4; i++)
                 w4[i] = pack4_magic(v[c][4 * i], v[c][4 * i + 1], v[c][4 * i + 2], v[c][4 * i + 3], s.inv);
-            // non-temporal stores: the outputs are read by the next kernel, not by this one
             int8_t *dst = p.Yq + (size_t)m * p.ldyq + oc;
-            if constexpr (CPL == 16) __builtin_nontemporal_store((u32x4){w4[0], w4[1], w4[2], w4[3]}, (u32x4 *)dst);
-            else __builtin_nontemporal_store((u32x2){w4[0], w4[1]}, (u32x2 *)dst);
-            if ((lane & 7) == 0 && (!GG || (wn & 1) == 0))
-                __builtin_nontemporal_store(s.sc, p.ys + (size_t)m * p.ldys + (oc >> 7));
+            float *sdst = p.ys + (size_t)m * p.ldys + (oc >> 7);
+            const bool sw = (lane & 7) == 0 && (!GG || (wn & 1) == 0);
+            if constexpr (NT) {
+                if constexpr (CPL == 16) __builtin_nontemporal_store((u32x4){w4[0], w4[1], w4[2], w4[3]}, (u32x4 *)dst);
+                else __builtin_nontemporal_store((u32x2){w4[0], w4[1]}, (u32x2 *)dst);
+                if (sw) __builtin_nontemporal_store(s.sc, sdst);
+            } else {
+                if constexpr (CPL == 16) *(u32x4 *)dst = (u32x4){w4[0], w4[1], w4[2], w4[3]};
+                else *(u32x2 *)dst = (u32x2){w4[0], w4[1]};
+                if (sw) *sdst = s.sc;
+            }
             if ((GG || GM) && p.Y) {
 #pragma unroll
                 for (int i = 0; i < CPL; i += 4)
-                    __builtin_nontemporal_store((f32x4){v[c][i], v[c][i + 1], v[c][i + 2], v[c][i + 3]},
-                                                (f32x4 *)(p.Y + (size_t)m * p.ldy + oc + i));
+                    *(f32x4 *)(p.Y + (size_t)m * p.ldy + oc + i) = (f32x4){v[c][i], v[c][i + 1], v[c][i + 2], v[c][i + 3]};
             }
         }
     }
@@ -365,7 +373,7 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_q(const GemmArg
 
 // f32 epilogue straight from the accumulator registers: buffer stores whose row step is a scalar
 // offset; rows past M fall outside the descriptor's range and are dropped, columns past N masked
-template <int POST, bool FAST>
+template <int POST, bool FAST, bool NT = false>
 __device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmArgs &p, float (&f)[4][16],
                                                                      const float (&wsr)[4], int m0, int n0,
                                                                      int wm, int wn, int lane) {
@@ -385,7 +393,8 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmA
             if constexpr (POST & 1) v = v + b;
             if constexpr (POST & 2) v = fminf(fmaxf(v, p.lo), p.hi);
             const int srow = __builtin_amdgcn_readfirstlane(((r >> 2) * 8 + (r & 3)) * p.ldy * 4);
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry, voff + tn * 128, srow, kStoreNT);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry, voff + tn * 128, srow,
+                                                  NT ? kStoreNT : 0);
         }
     }
 }
@@ -770,9 +779,9 @@ __global__ __launch_bounds__(512, 1) void k_gemm_t(GemmArgs p, int tiles_n, int 
 #pragma unroll
                 for (int t = 0; t < 4; t++) acc[h][t] = (v16i){};
                 if constexpr (EPI == EPI_F32)
-                    p_epilogue_f32<POST, false>(p, f, wsr, pm0, pn0, wmh, wn, lane);
+                    p_epilogue_f32<POST, false, true>(p, f, wsr, pm0, pn0, wmh, wn, lane);
                 else
-                    p_epilogue_q<BM, BN, NWM, NWN, EPI, false, POST>(p, f, wsr, pm0, pn0, wave, wmh, wn, lane,
+                    p_epilogue_q<BM, BN, NWM, NWN, EPI, false, POST, true>(p, f, wsr, pm0, pn0, wave, wmh, wn, lane,
                                                                      (float *)(smem + (g % STAGES) * TILE));
             }
             ckb = 0;
