@@ -217,11 +217,12 @@ def test_gemm_per_token_column_range_clamp_and_requant(gpu, oracle, rng):
 
 @pytest.mark.parametrize("M,N,K,n0,n1", [(300, 1152, 768, 0, 1152), (77, 200, 512, 0, 200),
                                          (515, 384, 1152, 4, 380), (130, 77, 768, 0, 77),
-                                         (64, 256, 768, 3, 250), (257, 1280, 640, 128, 1280)])
+                                         (64, 256, 768, 3, 250), (257, 1280, 640, 128, 1280),
+                                         (1, 128, 1152, 0, 128), (700, 512, 768, 128, 512)])
 def test_gemm_per_token_no_post_bit_exact(gpu, oracle, rng, M, N, K, n0, n1):
-    """Per-token GEMM without bias or clamp: the 16-byte-store epilogue (rows of 4 columns formed by
-    a transpose across lane quads) where N, the column offset and the pitch allow it, the 4-byte
-    one otherwise; columns outside [n0, n1) untouched."""
+    """Per-token GEMM without bias or clamp, at shapes that take each per-token f32 kernel: the
+    overlapped-epilogue one (N a multiple of 128, K = 768 or 1152) and the general one (any other
+    N, column offset or K); columns outside [n0, n1) untouched."""
     import e2mi
     import torch
     qa = rng.integers(-127, 128, (M, K), dtype=np.int8)

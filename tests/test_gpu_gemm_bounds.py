@@ -45,10 +45,13 @@ def _check_guard(buf, M, c0, c1, sent):
 
 @pytest.mark.parametrize("M", [300, 257, 33, 1000])
 @pytest.mark.parametrize("n0,n1", [(0, 384), (128, 320), (3, 250)])
-def test_f32_gemm_bounds(gpu, oracle, rng, M, n0, n1):
+@pytest.mark.parametrize("K", [256, 768])
+def test_f32_gemm_bounds(gpu, oracle, rng, M, n0, n1, K):
+    """(K = 768 with whole 128-column blocks also takes the per-token kernel with the overlapped
+    epilogue.)"""
     import torch
     import e2mi
-    N, K = 384, 256
+    N = 384
     qa, as_, w, ws = _case(rng, M, N, K)
     W = e2mi.DeviceWeight.from_rowmajor(w, ws)
     ld = N + 96

@@ -147,3 +147,28 @@ def test_gemm_per_token_large_bit_exact(gpu, oracle, rng, K, N):
     qo, so = oracle.quantize(yo)
     assert np.array_equal(yq.cpu().numpy()[rows], qo)
     assert np.array_equal(ys.cpu().numpy()[rows].view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,K,n0,n1", [(30000, 1152, 768, 0, 1152), (40003, 768, 1152, 0, 768),
+                                         (20000, 1280, 768, 128, 1280), (9000, 2304, 1152, 256, 1792)])
+def test_gemm_per_token_overlapped_epilogue(gpu, oracle, rng, M, N, K, n0, n1):
+    """The per-token f32 kernel that stores a tile while computing the next (N a multiple of 128,
+    K = 768 or 1152, no bias or clamp): tile counts that do not divide over the CUs, so workgroups
+    walk different numbers of tiles (odd and even, with the last tile's epilogue after the loop),
+    a partial last row block, and column ranges starting inside the weight; columns outside
+    [n0, n1) untouched, sampled rows bit-exact."""
+    import e2mi
+    import torch
+    qa = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    as_ = rng.uniform(0.001, 0.05, (M, 1)).astype(np.float32)
+    as_[rng.integers(0, M, 16)] *= 40.0
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    W = e2mi.DeviceWeight.from_rowmajor(w, ws)
+    y = torch.full((M, N), 7.0, device=gpu)
+    e2mi.i8_gemm_tok(_t(qa, gpu), _t(as_, gpu), W, n0=n0, n1=n1, y=y)
+    rows = _rows(rng, M)
+    yo = oracle.i8_gemm(qa[rows], as_[rows], w, ws, block=K)
+    got = y.cpu().numpy()[rows]
+    assert np.all(got[:, :n0] == 7.0) and np.all(got[:, n1:] == 7.0)
+    assert np.array_equal(got[:, n0:n1].view(np.uint32), yo[:, n0:n1].view(np.uint32))
