@@ -105,9 +105,15 @@ struct e2mi_engine {
     int32_t *work8 = nullptr, *h_work8 = nullptr;
     uint8_t *h_mask = nullptr;  // device-entry mask copy
     size_t mask_cap = 0;
+    // the stream of the previous call: a call on another stream first waits for it (the calls share
+    // the workspace and the pinned staging arrays)
     hipStream_t last_stream = nullptr;
+    // device-side id check of the device entry: the embedding kernel raises d_bad for an id outside
+    // the vocabulary; h_bad is its pinned copy, read once the call's stream has drained
+    int *d_bad = nullptr, *h_bad = nullptr;
+    bool bad_pending = false;  // a previous asynchronous call's flag still to be read
     bool packed = true;
-    std::map<std::tuple<int, int, int>, hipGraphExec_t> graphs;  // (sequences, seq_len, rows)
+    std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;  // (sequences, seq_len, rows, packed)
     bool use_graph = true;
     int layer_limit = 0;
     long calls = 0, kernels_last = 0;
@@ -116,6 +122,14 @@ struct e2mi_engine {
 };
 
 namespace e2mi {
+
+// rowops.hip
+int launch_embed_checked(hipStream_t s, const float *table, int vocab, const int32_t *ids, float embed_scale,
+                         const float *gamma, float eps, int M, int D, float *x_out, int8_t *q, float *qs,
+                         int *bad_id);
+int launch_zero_f32(hipStream_t s, float *p, long n);
+int launch_zero_flag(hipStream_t s, int *p);
+int launch_check_ids(hipStream_t s, const int32_t *ids, long n, int vocab, int *flag);
 
 template <class T>
 static int dalloc(e2mi_engine *g, T **p, size_t count) {
@@ -256,10 +270,13 @@ static int work_slots(const e2mi_engine *g, int n, int M) { return g->cfg.n_head
 
 // every kernel of one forward over B sequences of S tokens (M rows: B * S padded, or the packed
 // row count), on stream s; returns the launch count or -1
-static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
+static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s) {
     const e2_config &c = g->cfg;
-    const bool pk = Mp > 0;
     const int M = pk ? Mp : B * S, Dm = c.hidden, H = c.n_heads, P = c.ple_dim;
+    if (M <= 0 || M > g->R) {
+        set_error("forward: %d rows for a %d-row workspace", M, g->R);
+        return -1;
+    }
     const int nl = g->layer_limit > 0 && g->layer_limit < c.n_layers ? g->layer_limit : c.n_layers;
     const float eps = c.rms_eps;
     int k = 0;
@@ -268,8 +285,8 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
         if ((call) != 0) return -1;                                                                \
         k++;                                                                                       \
     } while (0)
-    RUN(e2mi_embed_norm_quant(s, g->embed, c.vocab, g->ids, c.embed_scale, g->layers[0].ln_in, eps, M, Dm,
-                              g->x, g->qa, g->as));
+    RUN(launch_embed_checked(s, g->embed, c.vocab, g->ids, c.embed_scale, g->layers[0].ln_in, eps, M, Dm,
+                             g->x, g->qa, g->as, g->d_bad));
     if (P > 0) {  // the per-layer inputs from the scaled embeddings (text.c:929-932)
         const int NP = c.n_layers * P;
         RUN(e2mi_quantize(s, g->qg, g->gs, g->x, M, Dm, Dm, 128));
@@ -333,25 +350,25 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
     return k + 1;  // the pool is two launches
 }
 
-static int run_shape(e2mi_engine *g, int B, int S, int Mp, hipStream_t s) {
+static int run_shape(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s) {
     if (!g->use_graph) {
-        const int k = enqueue(g, B, S, Mp, s);
+        const int k = enqueue(g, B, S, Mp, pk, s);
         if (k < 0) return -1;
         g->kernels_last = k;
         return 0;
     }
-    auto key = std::make_tuple(B, S, Mp);
+    auto key = std::make_tuple(B, S, Mp, pk ? 1 : 0);
     auto it = g->graphs.find(key);
     if (it == g->graphs.end()) {
         // the first call of a shape runs eagerly (kernel attributes get set outside any capture),
         // then the sequence is recorded for every later call
-        const int k = enqueue(g, B, S, Mp, s);
+        const int k = enqueue(g, B, S, Mp, pk, s);
         if (k < 0) return -1;
         g->kernels_last = k;
         hipGraph_t graph = nullptr;
         if (check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"))
             return -1;
-        const int k2 = enqueue(g, B, S, Mp, s);
+        const int k2 = enqueue(g, B, S, Mp, pk, s);
         const hipError_t e = hipStreamEndCapture(s, &graph);
         if (k2 < 0 || check_hip(e, "end capture")) {
             if (graph) (void)hipGraphDestroy(graph);
@@ -520,6 +537,7 @@ extern "C" void e2mi_destroy(e2mi_engine *g) {
     for (int32_t *p : {g->h_rowmap, g->h_pos, g->h_start, g->h_len, g->h_work, g->h_work8})
         if (p) (void)hipHostFree(p);
     if (g->h_mask) (void)hipHostFree(g->h_mask);
+    if (g->h_bad) (void)hipHostFree(g->h_bad);
     if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
     if (g->stream) (void)hipStreamDestroy(g->stream);
     delete g;
@@ -613,7 +631,7 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         (c.ple_dim > 0 && dalloc(g, &g->ple32, R * c.n_layers * c.ple_dim)) ||
         dalloc(g, &g->rowmap, R) || dalloc(g, &g->pos, R) || dalloc(g, &g->seq_start, (size_t)g->bmax) ||
         dalloc(g, &g->seq_len, (size_t)g->bmax) ||
-        dalloc(g, &g->work, (size_t)c.n_heads * (R / 128 + g->bmax)))
+        dalloc(g, &g->work, (size_t)c.n_heads * (R / 128 + g->bmax)) || dalloc(g, &g->d_bad, 1))
         return fail();
     if (check_hip(hipHostMalloc((void **)&g->h_ids, R * 4), "pinned ids") ||
         check_hip(hipHostMalloc((void **)&g->h_valid, R), "pinned valid") ||
@@ -622,8 +640,11 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         check_hip(hipHostMalloc((void **)&g->h_pos, R * 4), "pinned pos") ||
         check_hip(hipHostMalloc((void **)&g->h_start, (size_t)g->bmax * 4), "pinned start") ||
         check_hip(hipHostMalloc((void **)&g->h_len, (size_t)g->bmax * 4), "pinned len") ||
-        check_hip(hipHostMalloc((void **)&g->h_work, (size_t)c.n_heads * (R / 128 + g->bmax) * 4), "pinned work"))
+        check_hip(hipHostMalloc((void **)&g->h_work, (size_t)c.n_heads * (R / 128 + g->bmax) * 4), "pinned work") ||
+        check_hip(hipHostMalloc((void **)&g->h_bad, 4), "pinned flag"))
         return fail();
+    *g->h_bad = 0;
+    if (launch_zero_flag(g->stream, g->d_bad)) return fail();
     // filler rows of packed batches read contexts that no attention writes: start them at zero
     if (check_hip(hipMemsetAsync(g->cq, 0, R * qd, g->stream), "clear ctx") ||
         check_hip(hipMemsetAsync(g->cs, 0, R * (qd / 128) * 4, g->stream), "clear ctx scales"))
@@ -644,13 +665,36 @@ extern "C" e2mi_engine *e2mi_create(const e2_model *m) { return e2mi_create_rows
 
 extern "C" const char *e2mi_device(e2mi_engine *g) { return g ? g->devname : ""; }
 
+namespace e2mi {
+// a call on stream s first drains the previous call's stream when it is another one (the calls
+// share the workspace and the pinned staging arrays), and reads the id flag an asynchronous device
+// call left behind
+static int begin_call(e2mi_engine *g, hipStream_t s) {
+    if (g->last_stream && g->last_stream != s && check_hip(hipStreamSynchronize(g->last_stream), "previous call sync"))
+        return -1;
+    if (g->bad_pending) {
+        if (check_hip(hipStreamSynchronize(g->last_stream ? g->last_stream : s), "previous call sync")) return -1;
+        g->bad_pending = false;
+        if (*g->h_bad) {
+            *g->h_bad = 0;
+            g->last_stream = s;
+            set_error("text_embed_batch_device: the previous asynchronous call had a token id outside [0,%d); "
+                      "its embeddings are not valid", g->cfg.vocab);
+            return -1;
+        }
+    }
+    g->last_stream = s;
+    return 0;
+}
+}  // namespace e2mi
+
 extern "C" int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const uint8_t *valid, int batch,
                                      int seq_len, float *out) {
     if (!g || !out) {
         set_error("text_embed_batch: null engine or output");
         return -1;
     }
-    if (validate_batch(g, ids, batch, seq_len, true)) return -1;
+    if (validate_batch(g, ids, batch, seq_len, true) || begin_call(g, g->stream)) return -1;
     const double t0 = now_ms();
     const int D = g->dout;
     for (int b0 = 0; b0 < batch;) {
@@ -661,6 +705,13 @@ extern "C" int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const u
         int Mp = 0;
         if (g->packed) {
             Mp = plan_pack(g, vchunk, n, seq_len);
+            if (Mp == 0) {
+                // no valid token in the chunk: every sequence's embedding is the zero vector
+                // (text.c:968-980), nothing to run
+                memset(out + (size_t)b0 * D, 0, (size_t)n * D * 4);
+                b0 += n;
+                continue;
+            }
             if (upload_pack(g, n, Mp, ids + off, g->stream)) return -1;
         } else {
             memcpy(g->h_ids, ids + off, rows * 4);
@@ -669,7 +720,7 @@ extern "C" int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const u
                 check_hip(hipMemcpyAsync(g->valid, g->h_valid, rows, hipMemcpyHostToDevice, g->stream), "valid H2D"))
                 return -1;
         }
-        if (run_shape(g, n, seq_len, Mp, g->stream) ||
+        if (run_shape(g, n, seq_len, Mp, g->packed, g->stream) ||
             check_hip(hipMemcpyAsync(g->h_out, g->out, (size_t)n * D * 4, hipMemcpyDeviceToHost, g->stream), "out D2H") ||
             check_hip(hipStreamSynchronize(g->stream), "forward sync"))
             return -1;
@@ -693,8 +744,13 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
     }
     if (validate_batch(g, ids, batch, seq_len, false)) return -1;
     hipStream_t s = stream ? (hipStream_t)stream : g->stream;
+    if (begin_call(g, s)) return -1;
     const size_t rows = (size_t)batch * seq_len;
     const double t0 = now_ms();
+    // ids are checked on the device, masked positions included (the embedding kernel also raises
+    // the flag); the flag is read once the stream drains: at the end of this call, or at the next
+    // call when the caller passes a stream
+    if (launch_zero_flag(s, g->d_bad) || launch_check_ids(s, ids, (long)rows, g->cfg.vocab, g->d_bad)) return -1;
     if (!g->packed) {
         if ((long)batch * seq_len > g->R) {
             set_error("text_embed_batch_device: %d x %d rows exceed the engine's %d-row workspace",
@@ -703,7 +759,7 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
         }
         if (check_hip(hipMemcpyAsync(g->ids, ids, rows * 4, hipMemcpyDeviceToDevice, s), "ids D2D") ||
             check_hip(hipMemcpyAsync(g->valid, valid, rows, hipMemcpyDeviceToDevice, s), "valid D2D") ||
-            run_shape(g, batch, seq_len, 0, s) ||
+            run_shape(g, batch, seq_len, 0, false, s) ||
             check_hip(hipMemcpyAsync(out, g->out, (size_t)batch * g->dout * 4, hipMemcpyDeviceToDevice, s),
                       "out D2D"))
             return -1;
@@ -717,30 +773,70 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
             g->h_mask = m;
             g->mask_cap = rows;
         }
-        if ((g->last_stream && g->last_stream != s && check_hip(hipStreamSynchronize(g->last_stream), "sync")) ||
-            check_hip(hipMemcpyAsync(g->h_mask, valid, rows, hipMemcpyDeviceToHost, s), "mask D2H") ||
+        if (check_hip(hipMemcpyAsync(g->h_mask, valid, rows, hipMemcpyDeviceToHost, s), "mask D2H") ||
             check_hip(hipStreamSynchronize(s), "mask sync"))
             return -1;
-        g->last_stream = s;
         for (int b0 = 0; b0 < batch;) {
             const size_t off = (size_t)b0 * seq_len;
             const int n = chunk_size(g, g->h_mask + off, b0, batch, seq_len);
             const int Mp = plan_pack(g, g->h_mask + off, n, seq_len);
-            if (upload_pack(g, n, Mp, nullptr, s) ||
-                e2mi_gather_ids(s, ids + off, g->rowmap, Mp, g->ids) ||
-                run_shape(g, n, seq_len, Mp, s) ||
-                check_hip(hipMemcpyAsync(out + (size_t)b0 * g->dout, g->out, (size_t)n * g->dout * 4,
-                                         hipMemcpyDeviceToDevice, s), "out D2D"))
+            if (Mp == 0) {
+                // no valid token in the chunk: zero embeddings (a fill kernel, capturable)
+                if (launch_zero_f32(s, out + (size_t)b0 * g->dout, (long)n * g->dout)) return -1;
+            } else if (upload_pack(g, n, Mp, nullptr, s) ||
+                       e2mi_gather_ids(s, ids + off, g->rowmap, Mp, g->ids) ||
+                       run_shape(g, n, seq_len, Mp, true, s) ||
+                       check_hip(hipMemcpyAsync(out + (size_t)b0 * g->dout, g->out, (size_t)n * g->dout * 4,
+                                                hipMemcpyDeviceToDevice, s), "out D2D")) {
                 return -1;
+            }
             b0 += n;
             // the staging arrays are reused by the next chunk
             if (b0 < batch && check_hip(hipStreamSynchronize(s), "chunk sync")) return -1;
         }
     }
-    if (!stream && check_hip(hipStreamSynchronize(s), "forward sync")) return -1;
+    if (check_hip(hipMemcpyAsync(g->h_bad, g->d_bad, 4, hipMemcpyDeviceToHost, s), "flag D2H")) return -1;
+    if (stream) {
+        g->bad_pending = true;
+    } else {
+        if (check_hip(hipStreamSynchronize(s), "forward sync")) return -1;
+        if (*g->h_bad) {
+            *g->h_bad = 0;
+            set_error("text_embed_batch_device: a token id is outside [0,%d); the embeddings are not valid",
+                      g->cfg.vocab);
+            return -1;
+        }
+    }
     g->calls++;
     g->last_ms = now_ms() - t0;
     return 0;
+}
+
+// ------------------------------------------------------------------ e2.h text entries
+// (include/e2.h:25,35-36): the model's engine, created at the first call and owned by the model
+static e2mi_engine *model_engine(e2_model *m) {
+    if (!m) {
+        set_error("text_embed: null model");
+        return nullptr;
+    }
+    void **slot = e2mi::model_engine_slot(m);
+    if (!*slot) {
+        e2mi_engine *g = e2mi_create(m);
+        if (!g) return nullptr;
+        *slot = g;
+        e2mi::model_set_engine_free(m, [](void *p) { e2mi_destroy((e2mi_engine *)p); });
+    }
+    return (e2mi_engine *)*slot;
+}
+
+extern "C" int e2_text_embed_batch(e2_model *m, const int32_t *ids, const uint8_t *valid, int batch,
+                                   int seq_len, float *out) {
+    e2mi_engine *g = model_engine(m);
+    return g ? e2mi_text_embed_batch(g, ids, valid, batch, seq_len, out) : -1;
+}
+
+extern "C" int e2_text_embed(e2_model *m, const int32_t *ids, int n_ids, float *out768) {
+    return e2_text_embed_batch(m, ids, nullptr, 1, n_ids, out768);
 }
 
 extern "C" int e2mi_set_packing(e2mi_engine *g, int on) {

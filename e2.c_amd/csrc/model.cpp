@@ -24,6 +24,8 @@ struct e2_model {
     std::map<std::string, e2mi::F32T> f32;
     void *map = nullptr;
     size_t map_size = 0;
+    void *engine = nullptr;                    // created by e2_text_embed*, destroyed by e2_free
+    void (*engine_free)(void *) = nullptr;
 };
 
 namespace e2mi {
@@ -340,8 +342,14 @@ extern "C" e2_model *e2_model_synthetic(const e2_config *c, uint64_t seed) {
     return m;
 }
 
+namespace e2mi {
+void **model_engine_slot(e2_model *m) { return &m->engine; }
+void model_set_engine_free(e2_model *m, void (*destroy)(void *)) { m->engine_free = destroy; }
+}  // namespace e2mi
+
 extern "C" void e2_free(e2_model *m) {
     if (!m) return;
+    if (m->engine && m->engine_free) m->engine_free(m->engine);
     if (m->map) munmap(m->map, m->map_size);
     delete m;
 }

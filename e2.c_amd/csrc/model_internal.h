@@ -65,6 +65,10 @@ const char *ple_norm_name();
 const char *embed_proj_name();
 const char *layer_scalar_suffix();
 
+// the engine e2_text_embed* created for a model, owned by it: e2_free calls the destructor
+void **model_engine_slot(e2_model *m);
+void model_set_engine_free(e2_model *m, void (*destroy)(void *));
+
 // weights.hip: unpack a packed [Npad/8][K/4][8][4] blob into dst rows (n / grp) * gstride + goff +
 // n % grp of a row-major [*][ld] device matrix
 int upload_packed_rows(int8_t *dst, int ld, const int8_t *wq, int N, int K, int grp, int gstride,

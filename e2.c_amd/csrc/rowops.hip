@@ -14,6 +14,8 @@
 // and a 128-element quantization block is exactly one half-wave's float4 slice, so the per-block
 // amax is a 32-lane reduction. The fused variants read each row once and write the next GEMM's int8
 // operand directly, instead of the reference's separate norm, copy and quantize passes.
+#include <algorithm>
+
 #include "common.h"
 
 namespace e2mi {
@@ -27,6 +29,7 @@ struct RowArgs {
     const float *table;    // EMBED table [vocab][D]
     const int32_t *ids;    // EMBED token ids [M], clamped into [0, vocab)
     int vocab;
+    int *bad_id;           // EMBED: set to 1 when an id was outside [0, vocab) (optional)
     float embed_scale;
     const float *gamma_a;  // ADDNORM: gamma of the norm applied to src
     const float *gamma_n;  // gamma of the norm producing the quantized operand (NULL: no norm)
@@ -65,7 +68,9 @@ __global__ __launch_bounds__(256) void k_rows(RowArgs a) {
     const float *row;
     float escale = 1.f;
     if (MODE == ROW_EMBED) {
-        const int id = min(max(a.ids[m], 0), a.vocab - 1);
+        const int id0 = a.ids[m];
+        if ((id0 < 0 || id0 >= a.vocab) && a.bad_id && l == 0) *a.bad_id = 1;
+        const int id = min(max(id0, 0), a.vocab - 1);
         row = a.table + (size_t)id * D;
         escale = a.embed_scale;
     } else {
@@ -360,6 +365,10 @@ __global__ __launch_bounds__(256) void k_pool_partial_packed(const float *__rest
     if (threadIdx.x == 0) cnt[b * chunks + ch] = max(0, r1 - r0);
 }
 
+// the finishing kernel keeps up to kPoolPerThread means per thread: D <= 256 * kPoolPerThread
+constexpr int kPoolPerThread = 5;
+constexpr int kPoolMaxD = 256 * kPoolPerThread;
+
 __global__ __launch_bounds__(256) void k_pool_finish(const float *__restrict__ part,
                                                      const int *__restrict__ cnt, int chunks,
                                                      int D, float *__restrict__ out) {
@@ -368,13 +377,13 @@ __global__ __launch_bounds__(256) void k_pool_finish(const float *__restrict__ p
     int n = 0;
     for (int ch = 0; ch < chunks; ch++) n += cnt[b * chunks + ch];
     float ss = 0.f;
-    float vals[4];
+    float vals[kPoolPerThread];
     int k = 0;
     for (int d = threadIdx.x; d < D; d += blockDim.x, k++) {
         float s = 0.f;
         for (int ch = 0; ch < chunks; ch++) s += part[((size_t)b * chunks + ch) * D + d];
         const float mean = n > 0 ? __fdiv_rn(s, (float)n) : 0.f;
-        if (k < 4) vals[k] = mean;
+        if (k < kPoolPerThread) vals[k] = mean;
         ss += mean * mean;
     }
     ss = group_sum<64>(ss);
@@ -385,8 +394,22 @@ __global__ __launch_bounds__(256) void k_pool_finish(const float *__restrict__ p
     // all-invalid sequences stay an exact zero vector (text.c:968-980)
     const float inv = n > 0 ? __fdiv_rn(1.0f, __fsqrt_rn(tot)) : 1.0f;
     k = 0;
-    for (int d = threadIdx.x; d < D && k < 4; d += blockDim.x, k++)
+    for (int d = threadIdx.x; d < D && k < kPoolPerThread; d += blockDim.x, k++)
         out[(size_t)b * D + d] = n > 0 ? __fmul_rn(vals[k], inv) : 0.f;
+}
+
+// zero n floats (an all-padding chunk's embeddings): a kernel rather than a memset node, so a
+// caller may capture it
+__global__ __launch_bounds__(256) void k_zero_f32(float *__restrict__ p, long n) {
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) p[i] = 0.f;
+}
+__global__ void k_zero_i32(int *p) { *p = 0; }
+// raise *flag when any of n ids lies outside [0, vocab) (masked positions included, e2.h:31-32)
+__global__ __launch_bounds__(256) void k_check_ids(const int32_t *__restrict__ ids, long n, int vocab, int *flag) {
+    bool bad = false;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+        bad |= ids[i] < 0 || ids[i] >= vocab;
+    if (bad) *flag = 1;
 }
 
 // ---- packed batches: token ids of the packed rows (filler rows, rowmap < 0, get token 0)
@@ -516,6 +539,35 @@ extern "C" int e2mi_scale_norm(e2mi_stream stream, const float *x, int rows, int
     return launch_rows((hipStream_t)stream, ROW_PLAIN, a);
 }
 
+namespace e2mi {
+// the engine's embedding launch: e2mi_embed_norm_quant that also raises *bad_id for an id outside
+// the vocabulary (the id itself is clamped, so the gather stays in the table)
+int launch_embed_checked(hipStream_t s, const float *table, int vocab, const int32_t *ids, float embed_scale,
+                         const float *gamma, float eps, int M, int D, float *x_out, int8_t *q, float *qs,
+                         int *bad_id) {
+    RowArgs a = {};
+    a.table = table; a.vocab = vocab; a.ids = ids; a.embed_scale = embed_scale; a.gamma_n = gamma; a.eps = eps;
+    a.x_out = x_out; a.q = q; a.qs = qs; a.M = M; a.D = D; a.bad_id = bad_id;
+    return launch_rows(s, ROW_EMBED, a);
+}
+int launch_zero_f32(hipStream_t s, float *p, long n) {
+    if (n <= 0) return 0;
+    const long blocks = std::min((n + 255) / 256, 4096L);
+    hipLaunchKernelGGL(k_zero_f32, dim3((unsigned)blocks), dim3(256), 0, s, p, n);
+    return check_hip(hipGetLastError(), "zero fill launch");
+}
+int launch_check_ids(hipStream_t s, const int32_t *ids, long n, int vocab, int *flag) {
+    if (n <= 0) return 0;
+    const long blocks = std::min((n + 255) / 256, 1024L);
+    hipLaunchKernelGGL(k_check_ids, dim3((unsigned)blocks), dim3(256), 0, s, ids, n, vocab, flag);
+    return check_hip(hipGetLastError(), "id check launch");
+}
+int launch_zero_flag(hipStream_t s, int *p) {
+    hipLaunchKernelGGL(k_zero_i32, dim3(1), dim3(1), 0, s, p);
+    return check_hip(hipGetLastError(), "flag clear launch");
+}
+}  // namespace e2mi
+
 extern "C" int e2mi_embed_norm_quant(e2mi_stream stream, const float *table, int vocab,
                                      const int32_t *ids, float embed_scale, const float *gamma, float eps, int M, int D,
                                      float *x_out, int8_t *q, float *qs) {
@@ -584,9 +636,9 @@ extern "C" int e2mi_gelu_mul_quant(e2mi_stream stream, float *gate, int ldg, con
 
 extern "C" int e2mi_pool_l2(e2mi_stream stream, const float *x, const uint8_t *valid, int B, int S,
                             int D, float *workspace, float *out) {
-    if (!x || !valid || !workspace || !out || B <= 0 || S <= 0 || D <= 0 || D % 4 || D > 1024 ||
+    if (!x || !valid || !workspace || !out || B <= 0 || S <= 0 || D <= 0 || D % 4 || D > kPoolMaxD ||
         !aligned16(x) || !aligned16(workspace)) {
-        set_error("pool_l2: bad geometry or pointers");
+        set_error("pool_l2: bad geometry or pointers (D a multiple of 4 up to %d)", kPoolMaxD);
         return -1;
     }
     const int chunks = (S + 63) / 64;
@@ -599,8 +651,8 @@ extern "C" int e2mi_pool_l2_packed(e2mi_stream stream, const float *x, const int
                                    const int32_t *seq_len, int B, int max_len, int D, float *workspace,
                                    float *out) {
     if (!x || !seq_start || !seq_len || !workspace || !out || B <= 0 || max_len <= 0 || D <= 0 ||
-        D % 4 || D > 1024 || !aligned16(x) || !aligned16(workspace)) {
-        set_error("pool_l2_packed: bad geometry or pointers");
+        D % 4 || D > kPoolMaxD || !aligned16(x) || !aligned16(workspace)) {
+        set_error("pool_l2_packed: bad geometry or pointers (D a multiple of 4 up to %d)", kPoolMaxD);
         return -1;
     }
     const int chunks = (max_len + 63) / 64;

@@ -96,6 +96,8 @@ SIGNATURES = {
     "e2_load_e8cq": (_P, [C.c_char_p, C.POINTER(E2Config)]),
     "e2_save_e8cq": (_I, [_P, C.c_char_p]),
     "e2_free": (None, [_P]),
+    "e2_text_embed": (_I, [_P, _P, _I, _P]),
+    "e2_text_embed_batch": (_I, [_P, _P, _P, _I, _I, _P]),
     "e2_last_error": (C.c_char_p, []),
     "e2_model_config": (_I, [_P, C.POINTER(E2Config)]),
     "e2_model_tensor": (_I, [_P, C.c_char_p, C.POINTER(TensorView)]),

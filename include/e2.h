@@ -81,7 +81,21 @@ e2_model *e2_load_e8cq(const char *path, const e2_config *c);
 /* Write the model as an E8CQ cache (atomic: temp file + rename, q8cache.c:183-222). */
 int e2_save_e8cq(const e2_model *m, const char *path);
 
+/* Releases the model and the GPU engine e2_text_embed* created for it. */
 void e2_free(e2_model *m);
+
+/* Text: token ids -> embedding unit vector (include/e2.h:25); e2_text_embed_batch with one
+ * all-valid sequence. */
+int e2_text_embed(e2_model *m, const int32_t *ids, int n_ids, float *out768);
+/* Batch (include/e2.h:35-36): ids/valid row-major [batch, seq_len], out [batch, 768]; valid may be
+ * NULL (all valid), any nonzero byte keeps the token; seq_len 1..max_seq, batch > 0; every id,
+ * masked or not, inside the vocabulary; all-invalid sequences give an exact zero vector. Returns 0,
+ * or -1 without writing out when the input is invalid (e2_last_error). The reference runs this on
+ * its CPU backends; here the first call creates the model's gfx950 engine (e2mi.h, e2mi_create),
+ * which the model owns until e2_free. Not reentrant, like the reference. */
+int e2_text_embed_batch(e2_model *m, const int32_t *ids, const uint8_t *valid, int batch, int seq_len,
+                        float *out);
+
 /* Last error of this process (e2.h:159). Never NULL. */
 const char *e2_last_error(void);
 

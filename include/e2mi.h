@@ -263,7 +263,8 @@ void e2mi_destroy(e2mi_engine *g);
 /* Device name, architecture and CU count, for logging (e2_hip_device). */
 const char *e2mi_device(e2mi_engine *g);
 
-/* One sequence of n_ids tokens -> one unit vector of `hidden` floats (e2_hip_text_embed). */
+/* One sequence of n_ids tokens -> one unit vector (e2_hip_text_embed); its width is the model's
+ * out_dim, or hidden when there is no embed_proj. */
 int e2mi_text_embed(e2mi_engine *g, const int32_t *ids, int n_ids, float *out);
 /* `batch` sequences of `seq_len` tokens, row-major; valid marks real tokens (NULL: all valid; any
  * nonzero byte keeps a row). Positions restart per sequence; all-invalid sequences give an exact
@@ -274,9 +275,16 @@ int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const uint8_t *val
                           int seq_len, float *out);
 /* The same forward with DEVICE buffers already resident in HBM: ids [batch*seq_len], valid
  * [batch*seq_len], out [batch][hidden]. Enqueued on `stream` (NULL: the engine's own stream, then
- * synchronised). Ids are clamped, not validated. With packed batches the mask is first copied to
- * the host (one synchronous copy of batch*seq_len bytes) to plan the packing, and batches larger
- * than the workspace run in chunks; unpacked, batch*seq_len must fit the workspace. */
+ * synchronised). With packed batches the mask is first copied to the host (one synchronous copy of
+ * batch*seq_len bytes) to plan the packing, and batches larger than the workspace run in chunks
+ * (a chunk with no valid token is filled with zero vectors by a kernel, nothing else runs);
+ * unpacked, batch*seq_len must fit the workspace.
+ * Ids are checked on the device, masked positions included (text.c:1008-1013 checks them on the
+ * host): an id outside [0, vocab) makes the call return -1 with e2mi_last_error set, and the
+ * embeddings it wrote are not valid. With a caller stream the call returns before the forward
+ * ends, so the check is reported by the engine's next call (which returns -1 and does no work).
+ * Calls on one engine are serialised: a call on a stream other than the previous call's first waits
+ * for that stream (the calls share the workspace and the pinned staging arrays). */
 int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, const uint8_t *valid,
                                  int batch, int seq_len, float *out, e2mi_stream stream);
 /* Calls served, kernels launched by the last forward, wall time of the last call (e2_hip_stats). */

@@ -117,9 +117,11 @@ def test_gelu_mul_quant(gpu, oracle, rng, M):
     _bytes_rule(_np(q), go, oracle)
 
 
-def test_pool_l2(gpu, oracle, rng):
+@pytest.mark.parametrize("D", [768, 1280])
+def test_pool_l2(gpu, oracle, rng, D):
+    """(D = 1280: the widest hidden/out_dim the model container accepts.)"""
     import e2mi
-    B, S, D = 5, 200, 768
+    B, S = 5, 200
     x = rng.standard_normal((B * S, D)).astype(np.float32)
     valid = (rng.random(B * S) > 0.3).astype(np.uint8)
     valid[2 * S:3 * S] = 0                             # an all-invalid sequence -> exact zeros
