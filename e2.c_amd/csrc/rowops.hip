@@ -15,6 +15,7 @@
 // amax is a 32-lane reduction. The fused variants read each row once and write the next GEMM's int8
 // operand directly, instead of the reference's separate norm, copy and quantize passes.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -675,4 +676,52 @@ extern "C" int e2mi_gather_ids(e2mi_stream stream, const int32_t *ids, const int
     hipLaunchKernelGGL(k_gather_ids, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        ids, rowmap, M, out);
     return check_hip(hipGetLastError(), "gather_ids launch");
+}
+
+// ------------------------------------------------------------------ allocation-free pooling
+// e2mi_pool_l2 with its partial sums in a file-scope device array instead of a caller workspace,
+// for callers that cannot allocate (graph capture, serving loops). The array's address on each
+// device is looked up once, with that device current, and kept; host code passes that address to
+// the kernels, never the array's name.
+namespace {
+constexpr size_t kPoolScratchFloats = (size_t)2 << 20;  // 8 MiB per device
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+static __device__ __align__(256) float scratch[kPoolScratchFloats];
+
+static float *pool_scratch(int dev) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        float *p = nullptr;
+        if (check_hip(hipGetSymbolAddress((void **)&p, HIP_SYMBOL(scratch)), "pool scratch address")) return nullptr;
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+extern "C" int e2mi_pool_l2_noalloc(e2mi_stream stream, const float *x, const uint8_t *valid, int B, int S,
+                                    int D, float *out) {
+    if (!x || !valid || !out || B <= 0 || S <= 0 || D <= 0 || D % 4 || D > kPoolMaxD || !aligned16(x)) {
+        set_error("pool_l2_noalloc: bad geometry or pointers (D a multiple of 4 up to %d)", kPoolMaxD);
+        return -1;
+    }
+    const size_t need = e2mi_pool_workspace_bytes(B, S, D) / sizeof(float);
+    if (need > kPoolScratchFloats) {
+        set_error("pool_l2_noalloc: %d sequences of %d rows x %d need %zu bytes of scratch, the limit is %zu",
+                  B, S, D, need * sizeof(float), kPoolScratchFloats * sizeof(float));
+        return -1;
+    }
+    int dev = 0;
+    if (check_hip(hipGetDevice(&dev), "get device")) return -1;
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_error("pool_l2_noalloc: device %d beyond the %d this library tracks", dev, kMaxDevices);
+        return -1;
+    }
+    float *ws = pool_scratch(dev);
+    if (!ws) return -1;
+    // every partial sum and count slot is written by the first kernel: nothing to clear
+    const int chunks = (S + 63) / 64;
+    return launch_pool((hipStream_t)stream, x, valid, B, S, D, ws, (int *)(ws + (size_t)B * chunks * D), out);
 }

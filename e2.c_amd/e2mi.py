@@ -66,6 +66,7 @@ SIGNATURES = {
     "e2mi_qkv_norm_rope": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P]),
     "e2mi_gelu_mul_quant": (_I, [_P, _P, _I, _P, _I, _I, _I, _P, _P, _I]),
     "e2mi_pool_l2": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
+    "e2mi_pool_l2_noalloc": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "e2mi_pool_workspace_bytes": (C.c_size_t, [_I, _I, _I]),
     "e2mi_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
     "e2mi_qkv_norm_rope_packed": (_I, [_P, _P, _I, _P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P]),

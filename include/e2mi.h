@@ -179,6 +179,14 @@ int e2mi_gelu_mul_quant(e2mi_stream stream, float *gate, int ldg, const float *u
 int e2mi_pool_l2(e2mi_stream stream, const float *x, const uint8_t *valid, int B, int S, int D,
                  float *workspace, float *out);
 size_t e2mi_pool_workspace_bytes(int B, int S, int D);
+/* e2mi_pool_l2 without a workspace argument and without allocating: the partial sums live in a
+ * static device array of 8 MiB per GPU (held until the process ends), so
+ * e2mi_pool_workspace_bytes(B, S, D) must be at most 8 MiB (e.g. 340 sequences of 512 at D = 768);
+ * larger requests fail with -1. No counterpart in the reference: for callers that cannot allocate
+ * (code under graph capture, serving loops, harnesses that forbid hipMalloc). All calls on one GPU
+ * share the array: calls that overlap on one GPU race (serialise them on one stream). */
+int e2mi_pool_l2_noalloc(e2mi_stream stream, const float *x, const uint8_t *valid, int B, int S, int D,
+                         float *out);
 
 /* Packed batches (no counterpart in the reference, which computes padding rows): the valid tokens
  * of B sequences laid out back to back, sequence b in rows [seq_start[b], seq_start[b] +
