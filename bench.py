@@ -132,6 +132,32 @@ def cpu_flags():
     return set()
 
 
+def cpu_model():
+    """The host CPU's model name (what `lscpu` prints as "Model name")."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def pinned_one_core(fn):
+    """Run fn() with this process pinned to one allowed CPU (kernel_bench.c:13-16 pins its runs the
+    same way), then restore the affinity mask."""
+    try:
+        allowed = os.sched_getaffinity(0)
+    except AttributeError:
+        return fn(), None
+    cpu = min(allowed)
+    os.sched_setaffinity(0, {cpu})
+    try:
+        return fn(), cpu
+    finally:
+        os.sched_setaffinity(0, allowed)
+
+
 def physical_cores():
     """One thread per physical core (the reference's default pool policy, threads.c:177-215),
     capped by the affinity mask and by this box's share (16 per GPU)."""
@@ -215,8 +241,9 @@ def cpu_baseline(budget_s=12.0):
         for t in ts:
             t.join()
 
-    for item in work:  # warm-up (3 runs, text_bench.c:52-80)
-        run_shape(item)
+    for _ in range(3):  # three warm-up passes (text_bench.c:52-80)
+        for item in work:
+            run_shape(item)
     ops_per_pass = sum(2.0 * Ms * N * K for K, N, *_ in work)
     times = []
     t_start = time.time()
@@ -226,6 +253,21 @@ def cpu_baseline(budget_s=12.0):
             run_shape(item)
         times.append(time.perf_counter() - t0)
     best = min(times)
+
+    def one_core():  # one thread, pinned: the same pass over the four shapes, best of 3
+        nonlocal threads
+        saved, threads = threads, 1
+        try:
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                for item in work:
+                    run_shape(item)
+                ts.append(time.perf_counter() - t0)
+            return min(ts)
+        finally:
+            threads = saved
+    t1, cpu = pinned_one_core(one_core)
     return {
         "value": round(ops_per_pass / best / 1e12, 4),
         "unit": "TOPS",
@@ -238,6 +280,9 @@ def cpu_baseline(budget_s=12.0):
                    f"{len(times)} passes; median {ops_per_pass / float(np.median(times)) / 1e12:.4f} TOPS"),
         "kernel": f"e2_i8_gemm_{which}" if which else "or_i8_gemm_mt",
         "cpu_avx512_vnni": "avx512_vnni" in flags,
+        "cpu_model": cpu_model(),
+        "single_core": {"value": round(ops_per_pass / t1 / 1e12, 4), "unit": "TOPS",
+                        "sample": f"the same pass on one thread pinned to cpu {cpu}, best of 3"},
     }
 
 
@@ -380,24 +425,70 @@ def reference_geometry_bench(torch, e2mi, steps, warmup, cpu_sample=0):
                "unit_norm_ok": bool(np.allclose(np.linalg.norm(o, axis=1), 1, atol=1e-4)),
                "kernels_per_forward": eng.stats()[1]}
         if cpu_sample and name.startswith("config4"):
-            sys.path.insert(0, ROOT)
-            sys.path.insert(0, os.path.join(ROOT, "tests"))
-            from oracle.binding import Oracle
-            from model_util import oracle_model
-            threads = physical_cores()
-            om = oracle_model(Oracle(), model)
-            t2 = time.perf_counter()
-            om.encode(np.ascontiguousarray(ids[:cpu_sample]), np.ascontiguousarray(valid[:cpu_sample]),
-                      nthreads=threads)
-            dc = time.perf_counter() - t2
-            leg["cpu_baseline"] = {
-                "value": round(cpu_sample / dc, 4), "unit": "embeddings/s", "cores": threads, "kind": "port",
-                "sample": f"{cpu_sample} of the {B} sequences (lengths {valid[:cpu_sample].sum(1).tolist()}), "
-                          f"24 layers, {dc:.1f} s"}
-            del om
+            leg["cpu_baseline"] = reference_text_cpu_baseline(model, ids, valid, nseq=cpu_sample)
         res[name] = leg
     del eng, model
     return res
+
+
+def reference_text_cpu_baseline(model, ids, valid, nseq=8, budget_s=25.0):
+    """The reference's own CPU path: e2_text_embed_batch (text.c:997-1027) with its AVX-512 VNNI
+    kernels, its int8 attention where dispatch.c's rule picks it (S >= 128 keys, no padding inside)
+    and its worker pool, built from the reference sources into oracle/_ref/libreftext.so and run on
+    this model's weights (written as an E8CQ cache, read by the reference's q8c reader; the token
+    table is held in bf16 as the reference holds it). Timing follows text_bench.c:52-80: three
+    warm-up calls, then timed calls over the same nseq sequences, best and median. Threads: one per
+    physical core (threads.c:177-215's policy) within this box's share. Also a single-core rate with
+    the process pinned to one CPU and a one-thread pool."""
+    sys.path.insert(0, ROOT)
+    from oracle.binding import RefText
+    if not RefText.available():
+        return None
+    import shutil
+    import tempfile
+    tmp = tempfile.mkdtemp(prefix="e2mi_reftext_")
+    try:
+        path = os.path.join(tmp, "model.e8cq")
+        model.save_e8cq(path)
+        cfg = model.config
+        threads = physical_cores()
+        ids_s = np.ascontiguousarray(ids[:nseq])
+        valid_s = np.ascontiguousarray(valid[:nseq])
+        rt = RefText(path, cfg.n_layers, cfg.vocab, nthreads=threads)
+        threads = rt.threads
+        for _ in range(3):
+            rt.embed_batch(ids_s, valid_s)
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+            t0 = time.perf_counter()
+            out = rt.embed_batch(ids_s, valid_s)
+            times.append(time.perf_counter() - t0)
+        rt.close()
+        unit_ok = bool(np.allclose(np.linalg.norm(out, axis=1), 1, atol=1e-4))
+
+        def one_core():
+            r1 = RefText(path, cfg.n_layers, cfg.vocab, nthreads=1)
+            one_i, one_v = np.ascontiguousarray(ids_s[:1]), np.ascontiguousarray(valid_s[:1])
+            r1.embed_batch(one_i, one_v)
+            t0 = time.perf_counter()
+            r1.embed_batch(one_i, one_v)
+            dt = time.perf_counter() - t0
+            r1.close()
+            return dt
+        dt1, cpu = pinned_one_core(one_core)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    best, med = min(times), float(np.median(times))
+    return {"value": round(nseq / best, 3), "unit": "embeddings/s", "cores": threads, "kind": "reference",
+            "sample": (f"the first {nseq} of the batch's sequences (lengths {valid_s.sum(1).tolist()}, padded "
+                       f"to {ids.shape[1]}) through e2_text_embed_batch, {cfg.n_layers} layers; 3 warm-ups, best "
+                       f"of {len(times)} calls, median {nseq / med:.3f} emb/s"),
+            "best_ms": round(best * 1e3, 1), "median_ms": round(med * 1e3, 1),
+            "single_core": {"value": round(1 / dt1, 4), "unit": "embeddings/s",
+                            "sample": f"sequence 0 (length {int(valid_s[0].sum())}), pinned to cpu {cpu}, "
+                                      "one-thread pool"},
+            "cpu_model": cpu_model(), "unit_norm_ok": unit_ok}
 
 
 def encoder_cpu_baseline(model, ids, valid, nseq=24):
@@ -414,7 +505,12 @@ def encoder_cpu_baseline(model, ids, valid, nseq=24):
     dt = time.perf_counter() - t0
     return {"value": round(nseq / dt, 4), "unit": "embeddings/s", "cores": threads, "kind": "port",
             "sample": f"{nseq} of the {ENC_B} benchmark sequences (lengths {valid[:nseq].sum(1).tolist()}), "
-                      f"24 layers, {dt:.1f} s"}
+                      f"24 layers, {dt:.1f} s",
+            "cpu_model": cpu_model(),
+            "note": "the reference's text.c is hard-wired to its checkpoint's geometry (four heads, "
+                    "PLE, embed_proj; text.c:467-478, 906-984), so config 4's geometry runs only in "
+                    "this port (scalar-order int8 GEMMs, f32 row-wise attention); the reference's "
+                    "own CPU path is timed at its geometry under reference_geometry"}
 
 
 # ------------------------------------------------------------------ HBM traffic from PMC runs

@@ -14,6 +14,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libe2ref.so")
+REFTEXT_SO = os.path.join(HERE, "_ref", "libreftext.so")
 
 _P = C.c_void_p
 _I = C.c_int
@@ -49,7 +50,7 @@ class OrModel(C.Structure):
                 ("ple_dim", _I), ("out_dim", _I), ("window", _I), ("full_period", _I),
                 ("full_head_dim", _I), ("full_kv", _I), ("rope_theta_full", _F), ("ple_scale", _F),
                 ("wple_model", _P), ("sple_model", _P), ("ple_proj_norm", _P),
-                ("wembed_proj", _P), ("sembed_proj", _P)]
+                ("wembed_proj", _P), ("sembed_proj", _P), ("i8_min_keys", _I)]
 
 
 class Oracle:
@@ -262,7 +263,8 @@ class OracleModel:
     ple_proj_norm and embed_proj (w, s), and each layer dict wple_gate/sple_gate, wple_proj/sple_proj,
     ple_norm and layer_scalar."""
 
-    def __init__(self, oracle, cfg, layers, embed, final_norm, attn_scale=1.0, attn_i8=False, extra=None):
+    def __init__(self, oracle, cfg, layers, embed, final_norm, attn_scale=1.0, attn_i8=False, extra=None,
+                 i8_min_keys=0):
         self.o = oracle
         extra = extra or {}
         self._keep = [layers, embed, final_norm, extra]
@@ -287,7 +289,7 @@ class OracleModel:
                          cfg.get("full_period", 0), cfg.get("full_head_dim", 0), cfg.get("full_kv_heads", 0),
                          cfg.get("rope_theta_full", 0.0), cfg.get("ple_scale", 0.0),
                          p("wple_model"), p("sple_model"), p("ple_proj_norm"), p("wembed_proj"),
-                         p("sembed_proj"))
+                         p("sembed_proj"), i8_min_keys)
         self.out_dim = cfg.get("out_dim", 0) or cfg["hidden"]
 
     def encode(self, ids, valid, nthreads=8):
@@ -438,6 +440,59 @@ class Ref:
         self.lib.e2_meanpool_f32(_ptr(out), _ptr(x), M, D, _ptr(valid))
         self.lib.e2_l2norm_f32(_ptr(out), D)
         return out
+
+
+class RefText:
+    """The reference's own text tower (text.c, with the rest of the reference library) driven by
+    oracle/ref_text.c on a model read from an E8CQ cache of the reference geometry. One model per
+    process: the reference keeps its worker pool and cache reader global."""
+
+    def __init__(self, cache, n_layers, vocab, nthreads=0, path=REFTEXT_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        L = self.lib = C.CDLL(path)
+        L.rt_open.argtypes = [C.c_char_p, _I, _I, _I]
+        L.rt_embed_batch.argtypes = [_P, _P, _I, _I, _P]
+        L.rt_identity_layer.argtypes = [_I]
+        L.rt_error.restype = C.c_char_p
+        L.rt_cpu.restype = C.c_char_p
+        L.rt_close.restype = None
+        if L.rt_open(os.fsencode(cache), n_layers, vocab, nthreads):
+            raise RuntimeError("rt_open: " + L.rt_error().decode())
+        self.vocab = vocab
+        self.dim = 768
+
+    @staticmethod
+    def available(path=REFTEXT_SO):
+        return os.path.exists(path)
+
+    @property
+    def threads(self):
+        return self.lib.rt_threads()
+
+    @property
+    def cpu(self):
+        return self.lib.rt_cpu().decode()
+
+    def attn_i8(self, S):
+        """Whether the reference takes int8 attention for S keys on this CPU."""
+        return bool(self.lib.rt_attn_i8(S))
+
+    def identity_layer(self, l):
+        if self.lib.rt_identity_layer(l):
+            raise ValueError(l)
+
+    def embed_batch(self, ids, valid=None):
+        ids = _need(np.ascontiguousarray(ids, np.int32), np.int32)
+        B, S = ids.shape
+        v = None if valid is None else _need(np.ascontiguousarray(valid, np.uint8), np.uint8)
+        out = np.zeros((B, self.dim), np.float32)
+        if self.lib.rt_embed_batch(_ptr(ids), _ptr(v), B, S, _ptr(out)):
+            raise RuntimeError("e2_text_embed_batch: " + self.lib.rt_error().decode())
+        return out
+
+    def close(self):
+        self.lib.rt_close()
 
 
 _FN = C.CFUNCTYPE

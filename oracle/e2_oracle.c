@@ -480,9 +480,20 @@ void or_attention_win(const float *q, int ldq, const float *k, int ldk, const fl
  *   (e2_q8w_from_f32, text.c:776),
  *   ctx = the int8 GEMM of P with V^T (fold over Sp's key blocks, text.c:689-692).
  * Composed from or_quantize, or_q8w_from_f32 (+ unpack), or_i8_gemm and or_softmax, each pinned
- * against the reference (header). Returns -1 on allocation failure. */
+ * against the reference (header). Returns -1 on allocation failure.
+ *
+ * or_attention_i8_win adds the sliding window of the same worker (text.c:667-686): query i's
+ * softmax runs over keys [max(0, i-window), min(S, i+window+1)) and the rest of its row is zero
+ * before P is quantized over all S keys, so blocks outside the window get zero bytes and a zero
+ * scale. The GEMM's column range there (lo rounded down to 8, text.c:670) only trims columns the
+ * mask zeroes. window <= 0: no window. */
 int or_attention_i8(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
                     int S, int H, int KV, int D, float *ctx, int ldc) {
+    return or_attention_i8_win(q, ldq, k, ldk, v, ldv, S, H, KV, D, 0, ctx, ldc);
+}
+
+int or_attention_i8_win(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                        int S, int H, int KV, int D, int window, float *ctx, int ldc) {
     if (S <= 0) return 0;
     const int Sp = (S + 127) & ~127, nbD = (D + 127) / 128, nbS = (S + 127) / 128, nbsp = Sp / 128;
     const int groups = H / KV, Spad = (S + 7) & ~7, Dpad = (D + 7) & ~7;
@@ -508,7 +519,17 @@ int or_attention_i8(const float *q, int ldq, const float *k, int ldk, const floa
         or_q8w_unpack(kw, S, D, k8);
         or_quantize(q + (size_t)h * D, S, D, ldq, 128, q8, qs);
         or_i8_gemm(q8, qs, k8, ks, NULL, S, S, D, 128, -1e31f, 1e31f, sc);
-        for (int i = 0; i < S; i++) or_softmax(sc + (size_t)i * S, S);
+        for (int i = 0; i < S; i++) {
+            float *row = sc + (size_t)i * S;
+            int first = 0, end = S;
+            if (window > 0) {
+                first = i - window > 0 ? i - window : 0;
+                end = i + window + 1 < S ? i + window + 1 : S;
+            }
+            or_softmax(row + first, end - first);
+            memset(row, 0, sizeof(float) * (size_t)first);
+            memset(row + end, 0, sizeof(float) * (size_t)(S - end));
+        }
         or_quantize(sc, S, S, S, 128, pt, pst);
         for (int i = 0; i < S; i++) {
             memcpy(p8 + (size_t)i * Sp, pt + (size_t)i * S, (size_t)S);

@@ -70,6 +70,8 @@ void or_attention_win(const float *q, int ldq, const float *k, int ldk, const fl
                       float *ctx, int ldc, int nthreads);
 int or_attention_i8(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
                     int S, int H, int KV, int D, float *ctx, int ldc);
+int or_attention_i8_win(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                        int S, int H, int KV, int D, int window, float *ctx, int ldc);
 
 /* ---- a15/a16: pooling + L2 (kernels.c:22-39), embedding (text.c:917-921) */
 void or_meanpool(const float *x, int M, int D, const uint8_t *valid, float *out);
@@ -112,8 +114,9 @@ typedef struct {
     const float *embed;      /* [vocab][hidden] */
     const float *final_norm; /* [hidden] */
     const or_layer *layers;
-    /* 1: the int8 attention (text.c:638-700) for sequences of >= 32 rows with no padding inside
-     * (the reference's blocked path, text.c:873-875, selected as dispatch.c picks i8); 0: f32 */
+    /* 1: the int8 attention (text.c:638-700, with the layer's window) for sequences of >= 32 rows
+     * with no padding inside (the reference's blocked path, text.c:873-875, selected as dispatch.c
+     * picks i8); 0: f32 */
     int attn_i8;
     /* the reference checkpoint's geometry (e2.c:294-301, text.c:467-478); zeros give the BASELINE
      * geometry (every layer alike, no window, no PLE, embeddings are hidden rows) */
@@ -130,6 +133,9 @@ typedef struct {
     const float *ple_proj_norm; /* [ple_dim] */
     const int8_t *wembed_proj;  /* [out_dim][hidden] */
     const float *sembed_proj;
+    /* with attn_i8: the fewest keys that take the int8 attention (dispatch.c:46-52 rule's gate:
+     * 128 on the reference's CPU backends); 0 = only the blocked path's own 32 (an override) */
+    int i8_min_keys;
 } or_model;
 
 /* Geometry of layer l: head_dim, kv heads, RoPE theta and window (0 = none) (text.c:467-478). */

@@ -78,10 +78,10 @@ int or_attention_sublayer(const or_model *m, int l, const float *x, int B, int S
         or_rope_rows(k + (size_t)b * S * KV * D, Sb * KV, KV, D, cs, sn);
         int all = 1;
         for (int i = 0; i < Sb; i++) all &= vb[i] != 0;
-        if (m->attn_i8 && window > 0 && Sb > window + 1) goto fail; /* no windowed int8 path */
-        if (m->attn_i8 && all && Sb >= 32 && m->attn_scale == 1.0f) {
-            if (or_attention_i8(q + (size_t)b * S * GD, GD, k + (size_t)b * S * KV * D, KV * D,
-                                v + (size_t)b * S * KV * D, KV * D, Sb, H, KV, D, ctx + (size_t)b * S * GD, GD))
+        if (m->attn_i8 && all && Sb >= 32 && Sb >= m->i8_min_keys && m->attn_scale == 1.0f) {
+            if (or_attention_i8_win(q + (size_t)b * S * GD, GD, k + (size_t)b * S * KV * D, KV * D,
+                                    v + (size_t)b * S * KV * D, KV * D, Sb, H, KV, D, window,
+                                    ctx + (size_t)b * S * GD, GD))
                 goto fail;
         } else {
             or_attention_win(q + (size_t)b * S * GD, GD, k + (size_t)b * S * KV * D, KV * D,

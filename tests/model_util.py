@@ -26,9 +26,18 @@ def lname(l, s):
     return f"language_model.layers.{l}.{s}"
 
 
-def oracle_model(oracle, model, n_layers=None, attn_i8=False):
+def bf16_round(a):
+    """Round f32 values to bf16 (nearest even), kept in f32: the precision the reference holds its
+    token table in (e2.c:316-317)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def oracle_model(oracle, model, n_layers=None, attn_i8=False, embed_bf16=False, i8_min_keys=0):
     """Build the oracle's or_model from the product model's host tensors (packed weights unpacked
-    with the oracle's own layout code)."""
+    with the oracle's own layout code). embed_bf16: the token table rounded to bf16, as the
+    reference's own text tower holds it."""
     from oracle.binding import OracleModel
     cfg = model.config
     L = cfg.n_layers if n_layers is None else n_layers
@@ -75,9 +84,11 @@ def oracle_model(oracle, model, n_layers=None, attn_i8=False):
     if cfg.out_dim > 0:
         extra["wembed_proj"], extra["sembed_proj"] = q8("language_model.embedding_projection.weight")
     embed = np.ascontiguousarray(model.tensor("language_model.embed_tokens.weight"), np.float32)
+    if embed_bf16:
+        embed = bf16_round(embed)
     fnorm = np.ascontiguousarray(model.tensor("language_model.norm.weight"), np.float32)
     return OracleModel(oracle, c, layers, embed, fnorm, attn_scale=cfg.attn_scale, attn_i8=attn_i8,
-                       extra=extra)
+                       extra=extra, i8_min_keys=i8_min_keys)
 
 
 def random_batch(rng, B, S, vocab, min_len=1, holes=False):
