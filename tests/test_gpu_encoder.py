@@ -147,9 +147,15 @@ def test_config3_attention_sublayer(setup, rng):
     got = e2mi.i8_gemm(cq, csc, Wo).cpu().numpy()
     v = valid.astype(bool)
     rc = _rowcos(got[v], want[v])
-    print("attn sublayer cos", cosine(got[v], want[v]), "row min", rc.min(), "median", np.median(rc))
+    q = np.quantile(1 - rc, [0.5, 0.9, 0.99, 0.999, 1.0])
+    print("attn sublayer cos", cosine(got[v], want[v]), "1-cos quantiles 50/90/99/99.9/100 %", q,
+          "rows below 0.9999:", int((rc < 0.9999).sum()), "of", int(v.sum()))
+    # The f16 attention of config 3 rounds q and k to f16 (relative 2^-11) before QK^T; at the
+    # reference's logit scale 1.0 (logit std ~16) that moves a logit by ~0.01, which is what
+    # separates the rows from the f32 oracle (measured on this seed: 1 - cos median 5e-6, max
+    # 7e-5). Every row holds the north star's 0.9999.
     assert cosine(got[v], want[v]) >= 0.9999
-    assert _rowcos(got[v], want[v]).min() >= 0.999
+    assert rc.min() >= 0.9999
 
 
 def test_config2_ffn_sublayer(setup, rng):
@@ -175,3 +181,40 @@ def test_config2_ffn_sublayer(setup, rng):
     # elementwise differences come from +-1 requantization steps at rounding boundaries (the
     # reference's own byte rule); the bar is the BASELINE one, cosine >= 0.9999 per row
     assert rc.min() >= 0.9999
+
+
+def test_config4_full_size_properties(gpu, rng):
+    """BASELINE config 4 at its stated size: 24 layers at the reference recipe's attention scale
+    1.0, vocabulary 262144, B = 64 x S = 512 with lengths U[64, 512]. No oracle comparison at this
+    depth (random-init stacks at scale 1.0 are chaotic, see above); size-independent properties
+    instead: every embedding finite and unit-norm, packed and padded-rows forwards bit-identical,
+    graph replays bit-identical to the eager first call, and a sample of sequences embedded alone
+    bit-identical to their batch rows."""
+    import torch
+    import e2mi
+    cfg = small_config(e2mi, n_layers=24, vocab=262144)
+    m = e2mi.Model.synthetic(cfg, 4044)
+    eng = e2mi.Engine(m, max_rows=64 * 512)
+    B, S = 64, 512
+    ids = rng.integers(0, cfg.vocab, (B, S)).astype(np.int32)
+    lens = rng.integers(64, S + 1, B)
+    valid = (np.arange(S)[None, :] < lens[:, None]).astype(np.uint8)
+    first = eng.embed_batch(ids, valid)                 # eager + graph record
+    assert np.all(np.isfinite(first))
+    assert np.abs(np.linalg.norm(first.astype(np.float64), axis=1) - 1).max() < 1e-5
+    dev = torch.device("cuda:0")
+    out = torch.empty((B, cfg.hidden), device=dev)
+    for _ in range(2):                                  # replays, device entry
+        eng.embed_batch_device(_t(ids, dev), _t(valid, dev), out)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), first)
+    eng.set_packing(False)
+    try:
+        padded = eng.embed_batch(ids, valid)
+    finally:
+        eng.set_packing(True)
+    assert np.array_equal(padded, first)
+    for b in rng.choice(B, 4, replace=False):
+        L = int(lens[b])
+        single = eng.embed_batch(ids[b:b + 1, :L], None)
+        assert np.array_equal(single[0], first[b]), b

@@ -172,3 +172,42 @@ def test_gemm_per_token_overlapped_epilogue(gpu, oracle, rng, M, N, K, n0, n1):
     got = y.cpu().numpy()[rows]
     assert np.all(got[:, :n0] == 7.0) and np.all(got[:, n1:] == 7.0)
     assert np.array_equal(got[:, n0:n1].view(np.uint32), yo[:, n0:n1].view(np.uint32))
+
+
+def _packed_blob(w):
+    """The reference's quad-interleaved weight blob (int8.h:80, [N/8][K/4][8][4]) of row-major w."""
+    N, K = w.shape
+    Npad = (N + 7) & ~7
+    wp = np.zeros((Npad, K), np.int8)
+    wp[:N] = w
+    return wp.reshape(Npad // 8, 8, K // 4, 4).transpose(0, 2, 1, 3).copy().reshape(-1)
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+def test_config5_end_to_end(gpu, oracle, rng, K, N):
+    """BASELINE config 5 end to end at M = 65536: heavy-tailed Student-t (nu = 3) activations with
+    0.1 % of the channels scaled x50, quantized per token on the device (e2mi_quantize with one
+    block per row), the weight handed over as the reference's packed blob and re-laid out on the
+    device, then the per-token GEMM with f32 output and with the requantizing epilogue. On sampled
+    rows the quantized bytes and scales, the f32 outputs and the requantized bytes are bit-exact
+    with the oracle run on the same f32 activations."""
+    import e2mi
+    M = 65536
+    x = rng.standard_t(3, (M, K)).astype(np.float32)
+    cols = rng.choice(K, max(1, int(np.ceil(0.001 * K))), replace=False)
+    x[:, cols] *= 50.0
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    W = e2mi.DeviceWeight.from_packed(_packed_blob(w), ws, N, K)
+    qt, st = e2mi.quantize(_t(x, gpu), block=K)
+    rows = _rows(rng, M)
+    qo, so = oracle.quantize(np.ascontiguousarray(x[rows]), block=K)
+    assert np.array_equal(qt.cpu().numpy()[rows], qo)
+    assert np.array_equal(st.cpu().numpy()[rows].view(np.uint32), so.view(np.uint32))
+    y = e2mi.i8_gemm_tok(qt, st, W).cpu().numpy()
+    yo = oracle.i8_gemm(qo, so, w, ws, block=K)
+    assert np.array_equal(y[rows].view(np.uint32), yo.view(np.uint32))
+    yq, ys = e2mi.i8_gemm_tok_q(qt, st, W)
+    q2, s2 = oracle.quantize(yo)
+    assert np.array_equal(yq.cpu().numpy()[rows], q2)
+    assert np.array_equal(ys.cpu().numpy()[rows].view(np.uint32), s2.view(np.uint32))
