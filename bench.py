@@ -560,6 +560,108 @@ def summarize_pmc(fetch_csv, write_csv):
     print(json.dumps(res, indent=1))
 
 
+N_SIMD = 1024  # 256 CUs x 4 SIMDs
+N_XCC = 8
+
+
+def _short(name):
+    n = name.split("(")[0]
+    for p in ("void ", "e2mi::"):
+        n = n.replace(p, "")
+    return n.strip()
+
+
+def summarize_counters(fetch_csv, write_csv, mfma_csv, trace_csv):
+    """Per kernel of a --probe-all run: HBM bytes per dispatch from FETCH_SIZE / WRITE_SIZE (KiB),
+    each scaled by what the counter reads for the calibration copy of COPY_BYTES; the dispatch's
+    duration from a kernel trace of the same command (dispatches matched by kernel name and
+    occurrence); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES (summed over the 1024 SIMDs) / (the
+    dispatch's active cycles, GRBM_GUI_ACTIVE / 8 XCCs, x 1024), i.e. the fraction of the MFMA
+    peak at the clock the kernel ran at; int8 ops = SQ_INSTS_VALU_MFMA_MOPS_I8 x 512, divided by
+    the traced duration against the 5.0 POP/s spec."""
+    import csv
+    from collections import defaultdict
+
+    def per_dispatch(path):
+        # one value per dispatch and counter, summed over the counter's instances (SEs, XCCs,
+        # channels): GRBM_GUI_ACTIVE is then the dispatch's active clock cycles times the 8 XCCs
+        d = defaultdict(dict)
+        names = {}
+        for r in csv.DictReader(open(path)):
+            i, n, v = int(r["Dispatch_Id"]), r["Counter_Name"], float(r["Counter_Value"])
+            d[i][n] = d[i].get(n, 0.0) + v
+            names[i] = r["Kernel_Name"]
+        return [(names[i], d[i]) for i in sorted(d)]
+
+    def occurrences(rows):
+        seen = defaultdict(int)
+        out = []
+        for name, v in rows:
+            out.append(((name, seen[name]), v))
+            seen[name] += 1
+        return dict(out)
+
+    fetch_rows = per_dispatch(fetch_csv)
+    fetch = occurrences(fetch_rows)
+    write = occurrences(per_dispatch(write_csv))
+    mfma = occurrences(per_dispatch(mfma_csv))
+    trace = []
+    for r in csv.DictReader(open(trace_csv)):
+        trace.append((int(r["Dispatch_Id"]), r["Kernel_Name"],
+                      (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9))
+    trace.sort()
+    dur = occurrences([(n, t) for _, n, t in trace])
+    # the calibration copy: the last copy / elementwise dispatch before the second sweep's first
+    # per-token GEMM (the warm copy)
+    seen = defaultdict(int)
+    keys = []
+    for name, _ in fetch_rows:
+        keys.append((name, seen[name]))
+        seen[name] += 1
+    gemm_at = [i for i, k in enumerate(keys) if "k_gemm_tv" in k[0]]
+    first_warm = gemm_at[len(gemm_at) // 2]
+    copy_key = next(keys[i] for i in range(first_warm - 1, -1, -1)
+                    if "copy" in keys[i][0].lower() or "elementwise" in keys[i][0].lower())
+    f_scale = COPY_BYTES / (fetch[copy_key]["FETCH_SIZE"] * 1024)
+    w_scale = COPY_BYTES / (write[copy_key]["WRITE_SIZE"] * 1024)
+    copy_rate = 2 * COPY_BYTES / dur[copy_key] / 1e9
+    agg = defaultdict(lambda: defaultdict(float))
+    for key in fetch:
+        name = key[0]
+        if "e2mi::" not in name or key not in write or key not in dur or key[1] < seen[name] // 2:
+            continue  # the second (warm) half of each kernel's dispatches
+        a = agg[_short(name)]
+        a["n"] += 1
+        a["rd"] += fetch[key]["FETCH_SIZE"] * 1024 * f_scale
+        a["wr"] += write[key]["WRITE_SIZE"] * 1024 * w_scale
+        a["t"] += dur[key]
+        m = mfma.get(key, {})
+        a["busy"] += m.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+        a["active"] += m.get("GRBM_GUI_ACTIVE", 0.0) / N_XCC * N_SIMD
+        a["ops"] += m.get("SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0) * 512
+    lines = [
+        "| kernel | dispatches | HBM read MB / dispatch | HBM write MB / dispatch | µs / dispatch | HBM GB/s | "
+        "% of 8 TB/s | % of copy | MFMA busy % | int8 POP/s (counter) | % of 5.0 POP/s |",
+        "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for name, a in sorted(agg.items(), key=lambda kv: -kv[1]["t"]):
+        n = a["n"]
+        gbs = (a["rd"] + a["wr"]) / a["t"] / 1e9
+        busy = 100 * a["busy"] / a["active"] if a["active"] else 0.0
+        pops = a["ops"] / a["t"] / 1e15
+        lines.append(f"| `{name}` | {int(n)} | {a['rd'] / n / 1e6:.1f} | {a['wr'] / n / 1e6:.1f} | "
+                     f"{a['t'] / n * 1e6:.1f} | {gbs:.0f} | {100 * gbs / PEAK_HBM_GBS:.1f} | "
+                     f"{100 * gbs / copy_rate:.1f} | {busy:.1f} | "
+                     f"{pops:.3f} | {100 * pops / (PEAK_INT8_TOPS / 1e3):.1f} |")
+    head = [f"Calibration: a {COPY_BYTES >> 20} MiB device copy (`{_short(copy_key[0])[:60]}`) reads "
+            f"{fetch[copy_key]['FETCH_SIZE'] / 1024:.1f} MiB by FETCH_SIZE and writes "
+            f"{write[copy_key]['WRITE_SIZE'] / 1024:.1f} MiB by WRITE_SIZE: scale factors "
+            f"{f_scale:.4f} (read) and {w_scale:.4f} (write). The copy itself ran at {copy_rate:.0f} GB/s "
+            f"(read + write, {dur[copy_key] * 1e6:.1f} µs): the measured copy roof.", ""]
+    text = "\n".join(head + lines) + "\n"
+    print(text)
+    return text
+
+
 # ------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -576,12 +678,21 @@ def main():
                     help="skip the encoder leg's padded-rows comparison run")
     ap.add_argument("--probe", action="store_true",
                     help="one calibration copy + one launch per GEMM (for rocprofv3 --pmc runs)")
+    ap.add_argument("--probe-all", action="store_true",
+                    help="--probe plus one launch of every GEMM contract and quantizer on the sweep's "
+                         "shapes and one eager config-4 forward (rocprofv3 --pmc runs of every kernel)")
+    ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "MFMA_CSV", "TRACE_CSV"),
+                    help="turn the counter CSVs and the kernel trace of --probe-all runs into "
+                         "profiles/counters_probe_all.md")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn FETCH_SIZE / WRITE_SIZE counter CSVs of a --probe run into "
                          "profiles/gemm_tok_traffic.json")
     args = ap.parse_args()
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
+        return
+    if args.summarize_counters:
+        summarize_counters(*args.summarize_counters)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the "
@@ -643,16 +754,42 @@ def main():
         for c in cases:
             gemm_tok(c)
 
-    if args.probe:
+    if args.probe or args.probe_all:
         # calibration: a plain copy of COPY_BYTES (read COPY_BYTES, write COPY_BYTES), then one
         # launch of each GEMM of the step, in SHAPES order
         src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).uniform_()
         dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        step()
-        torch.cuda.synchronize()
+        # --probe-all: everything twice, so that the second (warm) dispatch of each kernel can be
+        # read; every other GEMM contract and the quantizers on the same shapes, then eager
+        # config-4 forwards (E2MI_NOGRAPH=1, set before the engine exists)
+        for _ in range(2 if args.probe_all else 1):
+            torch.cuda.synchronize()
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            step()
+            torch.cuda.synchronize()
+            if args.probe_all:
+                for c in cases:
+                    gemm_tok_q(c)
+                    gemm_q(c)
+                    gemm_f32(c)
+                    e2mi.quantize(c["x"], block=c["K"], q=c["qt"], scales=c["st"], stream=stream)
+                    e2mi.quantize(c["x"], q=c["qa"], scales=c["as_"], stream=stream)
+                torch.cuda.synchronize()
+        if args.probe_all:
+            del cases[:]
+            os.environ["E2MI_NOGRAPH"] = "1"
+            model = e2mi.Model.synthetic(e2mi.baseline_config(), 1004)
+            eng = e2mi.Engine(model, max_rows=ENC_B * ENC_S)
+            r = np.random.default_rng(1004)
+            ids = r.integers(0, model.config.vocab, (ENC_B, ENC_S)).astype(np.int32)
+            lens = r.integers(64, ENC_S + 1, ENC_B)
+            valid = (np.arange(ENC_S)[None, :] < lens[:, None]).astype(np.uint8)
+            out = torch.empty((ENC_B, model.config.hidden), device=dev)
+            for _ in range(2):
+                eng.embed_batch_device(torch.from_numpy(ids).to(dev), torch.from_numpy(valid).to(dev), out,
+                                       stream)
+                torch.cuda.synchronize()
         print("probe done")
         return
 
@@ -729,7 +866,7 @@ def main():
     else:
         roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS,
                     "unit": "TFLOP/s", "frac": round(ach / PEAK_INT8_TOPS, 4)}
-    roofline.update({"traffic": traffic, "kernel": f"k_gemm_t per-token f32 {c['K']}x{c['N']}",
+    roofline.update({"traffic": traffic, "kernel": f"k_gemm_tv per-token f32 {c['K']}x{c['N']}",
                      "algorithmic_bytes": algo_bytes, "ops": ops[dom],
                      "t_mfma_us": round(t_mfma * 1e6, 2), "t_hbm_us": round(t_hbm * 1e6, 2),
                      "mfma_TOPS": round(ach, 2), "mfma_frac": round(ach / PEAK_INT8_TOPS, 4),
