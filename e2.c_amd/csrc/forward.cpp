@@ -54,6 +54,9 @@ struct LayerDev {
     float *ln_in = nullptr, *ln_attn = nullptr, *ln_pre = nullptr, *ln_ffn = nullptr;
     float *q_norm = nullptr, *k_norm = nullptr, *ple_norm = nullptr;
     float layer_scalar = 1.f;
+    // the q|k|v weight is stored in the fused GEMM's rotate-half pair order (head_dim 256 layers):
+    // e2mi_i8_gemm_qkv runs the q/k/v norms and RoPE in its epilogue
+    bool qkv_fused = false;
 };
 
 static double now_ms() {
@@ -115,6 +118,7 @@ struct e2mi_engine {
     bool packed = true;
     std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;  // (sequences, seq_len, rows, packed)
     bool use_graph = true;
+    bool fuse_qkv = true;  // E2MI_NOFUSE=1: the q|k|v GEMM and the norm/RoPE kernel run separately
     int layer_limit = 0;
     long calls = 0, kernels_last = 0;
     double last_ms = 0.0;
@@ -193,14 +197,19 @@ static int upload_layer(e2mi_engine *g, const e2_model *m, int l, LayerDev &L) {
         if (dalloc(g, &d.w, (size_t)N * d.ld) || dalloc(g, &d.scale, (size_t)N)) return -1;
         return 0;
     };
-    // q|k|v rows
+    // q|k|v rows (head_dim 256: in the fused GEMM's pair order, bits 6 and 7 of the row swapped)
     if (make(L.qkv, qd + 2 * kvd, K)) return -1;
+    L.qkv_fused = g->fuse_qkv && L.geo.D == 256;
     const int off[3] = {0, qd, qd + kvd}, nrows[3] = {qd, kvd, kvd};
     std::vector<float> sc(qd + 2 * kvd);
     for (int s = 0; s < 3; s++) {
-        if (upload_packed_rows(L.qkv.w, L.qkv.ld, w[s]->w, nrows[s], K, nrows[s], 0, off[s], g->stream))
+        if (upload_packed_rows(L.qkv.w, L.qkv.ld, w[s]->w, nrows[s], K, nrows[s], 0, off[s], g->stream,
+                               L.qkv_fused))
             return -1;
-        memcpy(sc.data() + off[s], w[s]->scale, sizeof(float) * nrows[s]);
+        for (int n = 0; n < nrows[s]; n++) {
+            const int r = off[s] + n;
+            sc[L.qkv_fused ? (r & ~0xC0) | ((r & 0x40) << 1) | ((r & 0x80) >> 1) : r] = w[s]->scale[n];
+        }
     }
     if (check_hip(hipMemcpyAsync(L.qkv.scale, sc.data(), sc.size() * 4, hipMemcpyHostToDevice, g->stream),
                   "upload qkv scale") ||
@@ -297,10 +306,16 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s)
         const LayerDev &L = g->layers[l];
         const int D = L.geo.D, KV = L.geo.KV, qd = H * D;
         const float *cs = L.geo.full ? g->cos_full : g->cos_tab, *sn = L.geo.full ? g->sin_full : g->sin_tab;
-        RUN(e2mi_i8_gemm(s, g->qkv, qd + 2 * KV * D, g->qa, g->as, &L.qkv, M, 0, L.qkv.N));
+        if (L.qkv_fused)
+            RUN(e2mi_i8_gemm_qkv(s, g->qa, g->as, &L.qkv, M, pk ? M : S, pk ? g->pos : nullptr, H, KV, L.q_norm,
+                                 L.k_norm, eps, cs, sn, g->q16, g->k16, g->vt16, g->attn_i8 ? g->q32 : nullptr,
+                                 g->attn_i8 ? g->k32 : nullptr, g->attn_i8 ? g->v32 : nullptr));
+        else
+            RUN(e2mi_i8_gemm(s, g->qkv, qd + 2 * KV * D, g->qa, g->as, &L.qkv, M, 0, L.qkv.N));
         if (pk) {
-            RUN(e2mi_qkv_norm_rope_packed(s, g->qkv, M, g->pos, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn,
-                                          g->q16, g->k16, g->vt16, g->q32, g->k32, g->v32));
+            if (!L.qkv_fused)
+                RUN(e2mi_qkv_norm_rope_packed(s, g->qkv, M, g->pos, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn,
+                                              g->q16, g->k16, g->vt16, g->q32, g->k32, g->v32));
             RUN(e2mi_attention_packed_window(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len, g->pos,
                                              B, S, H, KV, D, c.attn_scale, L.geo.window, g->cq, g->cs,
                                              nullptr, g->work, work_slots(g, B, M)));
@@ -309,8 +324,9 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s)
                                              H, KV, D, g->i8ws, g->cq, g->cs, nullptr, g->work8,
                                              work_slots(g, B, M)));
         } else {
-            RUN(e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn, g->q16,
-                                   g->k16, g->vt16, nullptr, nullptr, nullptr));
+            if (!L.qkv_fused)
+                RUN(e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn, g->q16,
+                                       g->k16, g->vt16, nullptr, nullptr, nullptr));
             RUN(e2mi_attention(s, g->q16, g->k16, g->vt16, g->valid, B, S, H, KV, D, c.attn_scale,
                                g->cq, g->cs, nullptr));
         }
@@ -565,6 +581,8 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
     g->R = (g->R + 255) & ~255;  // a packed chunk of one full sequence fits
     const char *ng = getenv("E2MI_NOGRAPH");
     g->use_graph = !(ng && ng[0] && ng[0] != '0');
+    const char *nf = getenv("E2MI_NOFUSE");
+    g->fuse_qkv = !(nf && nf[0] && nf[0] != '0');
     auto fail = [&]() -> e2mi_engine * {
         e2mi_destroy(g);
         return nullptr;

@@ -11,6 +11,10 @@
 //             quantized per (row, 128 columns) like EPI_I8Q; g optionally stored f32
 //   EPI_GEGLU W rows interleaved per 64 as [32 gate | 32 up]; g = gelu_tanh(gate) * up is
 //             quantized per 128 (text.c:424-468 fused into the producing GEMM), g optionally kept
+//   EPI_QKV   the q|k|v projection with the attention's row stage fused in (text.c:836-854): per
+//             256-wide head, RMSNorm (q/k with their gamma, v without), RoPE on q and k, f16
+//             outputs for the attention (q, k row-major, V transposed); W's rows of each head in
+//             rotate-half pair order (see p_epilogue_qkv)
 //
 // The production kernels are persistent and software-pipelined: k_gemm_p for per-(row, 128)
 // activation scales (K is walked in 128-deep steps, one quantization block per step, so the int32
@@ -30,7 +34,7 @@
 
 namespace e2mi {
 
-enum { EPI_F32 = 0, EPI_I8Q = 1, EPI_GEGLU = 2, EPI_GELUMUL = 3 };
+enum { EPI_F32 = 0, EPI_I8Q = 1, EPI_GEGLU = 2, EPI_GELUMUL = 3, EPI_QKV = 4 };
 
 struct GemmArgs {
     const int8_t *A;
@@ -47,6 +51,15 @@ struct GemmArgs {
     int lda, ldw, ldy, ldyq, ldys;
     int M, N, K;
     float lo, hi;
+    // EPI_QKV: q/k gammas [256], RoPE tables [positions][256], each row's position (packed
+    // batches) or none (row % qS), f16 outputs q [M][qH*256], k [M][qKV*256] and V^T
+    // [M/qS][qKV][256][qS], optional f32 copies q, k, v [M][heads*256]
+    const float *q_gamma, *k_gamma, *cs, *sn;
+    const int32_t *pos;
+    uint16_t *q16, *k16, *vt16;
+    float *q32, *k32, *v32;
+    int qH, qKV, qS;
+    float eps;
 };
 
 
@@ -401,6 +414,161 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmA
     }
 }
 
+// ds_swizzle in bit mode: lane l reads lane l ^ X of its 32-lane half
+template <int X>
+__device__ inline float swz_xor(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (X << 10)));
+}
+// one halving step of a transposing reduction over lanes: 2N partial sums -> N, the lanes with
+// bit X set keeping the upper half (each gives away the half it does not keep)
+template <int X, int N>
+__device__ inline void halve(const float (&v)[2 * N], float (&o)[N], bool up) {
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float keep = up ? v[i + N] : v[i], give = up ? v[i] : v[i + N];
+        o[i] = keep + swz_xor<X>(give);
+    }
+}
+// f16 of an f32 value that is already rounded (the register barrier keeps the compiler from
+// folding the multiply that produced x into the conversion)
+__device__ inline uint16_t f2h_rn(float x) {
+    asm volatile("" : "+v"(x));
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+__device__ inline float rms_inv256(float ss, float eps) {
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, 256.0f) + eps));
+}
+
+// The q|k|v epilogue (EPI_QKV) of a 128 x 256 tile, which is one head of 128 rows: 8 waves, wave
+// (wm, wn) holding rows wm * 32 .. + 31 and W rows wn * 128 .. + 127 of the head. W's rows of each
+// 256-row head are stored with bits 6 and 7 of the row index swapped, so that wave wn's column tile
+// t (lane column c) is head dimension (t >> 1) * 128 + wn * 64 + (t & 1) * 32 + c: the rotate-half
+// partners i and i + 128 of RoPE sit in tiles t and t + 2 of the same lane.
+//  1. the row's sum of squares: per lane over its 4 tiles, over the 32 lanes of each half by a
+//     transposing halving exchange (16 values -> 1 in four swizzle steps, then the pair), and over
+//     the two waves of the head through LDS (one barrier);
+//  2. inv = 1 / sqrt(ss / 256 + eps) (the row kernel's arithmetic), shared through LDS per wave;
+//  3. q/k: x = (y * inv) * gamma, then a' = a c - b s, b' = b c + a s (products rounded, then the
+//     sum; kernels.c:112-126), f16; v: y * inv, f16, stored transposed per sequence.
+// scr: 2 x 8 x 32 floats of the step's free A|W stage.
+template <bool FAST>
+__device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmArgs &p, float (&f)[4][16],
+                                                                     const float (&wsr)[4], int m0, int n0,
+                                                                     int wave, int wm, int wn, int lane,
+                                                                     float *scr) {
+    if constexpr (FAST) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) f[t][r] = __fmul_rn(f[t][r], wsr[t]);
+    }
+    const int hd = n0 >> 8, nqk = p.qH + p.qKV;
+    const int hh = lane >> 5, c = lane & 31;
+    // 1. register r = 4 g + j holds row 8 g + 4 hh + j of the wave's 32
+    float s16[16], s8[8], s4[4], s2[2], s1[1];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        float a = __fmul_rn(f[0][r], f[0][r]);
+#pragma unroll
+        for (int t = 1; t < 4; t++) a = a + __fmul_rn(f[t][r], f[t][r]);
+        s16[r] = a;
+    }
+    halve<16, 8>(s16, s8, lane & 16);
+    halve<8, 4>(s8, s4, lane & 8);
+    halve<4, 2>(s4, s2, lane & 4);
+    halve<2, 1>(s2, s1, lane & 2);
+    const float part = s1[0] + swz_xor<1>(s1[0]);
+    const int j = ((lane >> 4) & 1) * 8 + ((lane >> 3) & 1) * 4 + ((lane >> 2) & 1) * 2 + ((lane >> 1) & 1);
+    const int rw = 8 * (j >> 2) + 4 * hh + (j & 3);
+    float *xs = scr, *xi = scr + 8 * 32;
+    if ((lane & 1) == 0) xs[wave * 32 + rw] = part;
+    __syncthreads();
+    // 2. the two waves add the same two partial sums (addition commutes: both get the same inv)
+    const float inv = rms_inv256(part + xs[(wm * 2 + (wn ^ 1)) * 32 + rw], p.eps);
+    if ((lane & 1) == 0) xi[wave * 32 + rw] = inv;
+    // 3. four rows at a time (registers 4 g .. 4 g + 3, rows rb + 8 g + 0..3), their inv read back
+    // from LDS (LDS operations of one wave complete in order: the reads see this wave's writes);
+    // buffer stores whose range ends at row M drop the rows past it
+    const int rb = m0 + wm * 32 + 4 * hh;
+    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+    if (hd < nqk) {
+        const bool isq = hd < p.qH;
+        const int hq = isq ? hd : hd - p.qH, ld = (isq ? p.qH : p.qKV) * 256;
+        const float *gam = isq ? p.q_gamma : p.k_gamma;
+        const __amdgpu_buffer_rsrc_t r16 =
+            __builtin_amdgcn_make_buffer_rsrc(isq ? p.q16 : p.k16, 0, (int)min((long)p.M * ld * 2, 0x7fffffffL), 0x00020000);
+        float *o32 = isq ? p.q32 : p.k32;
+        const __amdgpu_buffer_rsrc_t r32 =
+            __builtin_amdgcn_make_buffer_rsrc(o32, 0, o32 ? (int)min((long)p.M * ld * 4, 0x7fffffffL) : 0, 0x00020000);
+        const int i0 = wn * 64 + c;  // tiles t = 0, 1: dimensions i0 + 32 t and i0 + 32 t + 128
+        const float g00 = gam[i0], g01 = gam[i0 + 128], g10 = gam[i0 + 32], g11 = gam[i0 + 160];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const float4 i4 = *(const float4 *)(xi + wave * 32 + 8 * g + 4 * hh);
+            const float ivg[4] = {i4.x, i4.y, i4.z, i4.w};
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const int r = 4 * g + jj, m = rb + 8 * g + jj, mc = min(m, p.M - 1);
+                const int ps = p.pos ? p.pos[mc] : mc % p.qS;
+                const float *cr = p.cs + (size_t)ps * 256 + i0, *sr = p.sn + (size_t)ps * 256 + i0;
+                const int o = (m * ld + hq * 256 + i0) * 2;
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const float cv = cr[32 * t], sv = sr[32 * t];
+                    const float a = __fmul_rn(__fmul_rn(f[t][r], ivg[jj]), t ? g10 : g00);
+                    const float b = __fmul_rn(__fmul_rn(f[t + 2][r], ivg[jj]), t ? g11 : g01);
+                    const float lo = __fmul_rn(a, cv) - __fmul_rn(b, sv);
+                    const float hi = __fmul_rn(b, cv) + __fmul_rn(a, sv);
+                    __builtin_amdgcn_raw_buffer_store_b16(f2h_rn(lo), r16, o + 64 * t, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b16(f2h_rn(hi), r16, o + 64 * t + 256, 0, 0);
+                    if (o32) {
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, lo), r32, 2 * o + 128 * t, 0, 0);
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, hi), r32, 2 * o + 128 * t + 512, 0, 0);
+                    }
+                }
+            }
+        }
+    } else {
+        const int vh = hd - nqk, S = p.qS, ld32 = p.qKV * 256;
+        const bool fast = S % 4 == 0;
+        float *o32 = p.v32;
+        const __amdgpu_buffer_rsrc_t r32 =
+            __builtin_amdgcn_make_buffer_rsrc(o32, 0, o32 ? (int)min((long)p.M * ld32 * 4, 0x7fffffffL) : 0, 0x00020000);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const float4 i4 = *(const float4 *)(xi + wave * 32 + 8 * g + 4 * hh);
+            const float ivg[4] = {i4.x, i4.y, i4.z, i4.w};
+            const int m = rb + 8 * g;  // rows m .. m + 3, m a multiple of 4
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int d = (t >> 1) * 128 + wn * 64 + (t & 1) * 32 + c;
+                float x[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) x[jj] = __fmul_rn(f[t][4 * g + jj], ivg[jj]);
+                if (fast && m + 3 < p.M) {
+                    // four consecutive positions of one sequence: one 8-byte store
+                    uint16_t *dst = p.vt16 + ((size_t)((m / S) * p.qKV + vh) * 256 + d) * S + m % S;
+                    *(u32x2v *)dst = (u32x2v){(uint32_t)f2h_rn(x[0]) | ((uint32_t)f2h_rn(x[1]) << 16),
+                                              (uint32_t)f2h_rn(x[2]) | ((uint32_t)f2h_rn(x[3]) << 16)};
+                } else {
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) {
+                        const int mm = m + jj;
+                        if (mm < p.M)
+                            p.vt16[((size_t)((mm / S) * p.qKV + vh) * 256 + d) * S + mm % S] = f2h_rn(x[jj]);
+                    }
+                }
+                if (o32) {
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++)
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x[jj]), r32,
+                                                              ((m + jj) * ld32 + vh * 256 + d) * 4, 0, 0);
+                }
+            }
+        }
+    }
+}
+
 // 8 waves of 32 x 128 (one 32-row MFMA tile by four 32-column ones): NWM x NWN waves, BM = 32 NWM,
 // BN = 128 NWN
 template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
@@ -584,6 +752,10 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
             const int pm0 = tile_m0(cj - 1), pn0 = tile_n0(cj - 1);
             if constexpr (EPI == EPI_F32) {
                 p_epilogue_f32<POST, FAST>(p, f, wsr, pm0, pn0, wm, wn, lane);
+            } else if constexpr (EPI == EPI_QKV) {
+                __syncthreads();
+                p_epilogue_qkv<FAST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
+                                     (float *)(smem + (g % kPStages) * TILE));
             } else {
                 __syncthreads();
                 p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
@@ -621,6 +793,9 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
         const int pm0 = tile_m0(ntile - 1), pn0 = tile_n0(ntile - 1);
         if constexpr (EPI == EPI_F32)
             p_epilogue_f32<POST, FAST>(p, f, wsr, pm0, pn0, wm, wn, lane);
+        else if constexpr (EPI == EPI_QKV)
+            p_epilogue_qkv<FAST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
+                                 (float *)(smem + ((G - 1) % kPStages) * TILE));
         else
             p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
                                                             (float *)(smem + ((G - 1) % kPStages) * TILE));
@@ -1078,7 +1253,8 @@ template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
 static int launch_p1(hipStream_t s, const GemmArgs &p) {
     constexpr size_t lds = p_lds_bytes<BM, BN, NWM * NWN>();
     static_assert(lds <= 160 * 1024, "LDS budget");
-    static_assert(EPI == EPI_F32 || NWM * NWN * (8 * ((EPI == EPI_GEGLU ? 64 : 128) + 4) + 32) * 4 <= (BM + BN) * 128,
+    static_assert(EPI == EPI_F32 || EPI == EPI_QKV ||
+                      NWM * NWN * (8 * ((EPI == EPI_GEGLU ? 64 : 128) + 4) + 32) * 4 <= (BM + BN) * 128,
                   "epilogue scratch fits a stage");
     auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST>;
     static bool attr = false;
@@ -1260,6 +1436,27 @@ int launch_gemm_geglu(hipStream_t s, GemmArgs p) {
     return launch_p<128, 256, 4, 2, EPI_GEGLU>(s, p);
 }
 
+int launch_gemm_qkv(hipStream_t s, GemmArgs p) {
+    if (check_args(p, "i8_gemm_qkv")) return -1;
+    const int heads = p.qH + 2 * p.qKV;
+    if (p.qH <= 0 || p.qKV <= 0 || p.qH % p.qKV || p.N != heads * 256 || p.qS <= 0 ||
+        (p.pos && p.qS != p.M) || (!p.pos && p.M % p.qS)) {
+        set_error("i8_gemm_qkv: needs N = (H + 2 KV) * 256, H %% KV == 0 and M = B * S (packed: S = M) "
+                  "(M=%d N=%d H=%d KV=%d S=%d)", p.M, p.N, p.qH, p.qKV, p.qS);
+        return -1;
+    }
+    if (p.bias || p.lo > -1e30f || p.hi < 1e30f) {
+        set_error("i8_gemm_qkv: the q|k|v weight takes no bias or clamp");
+        return -1;
+    }
+    if (!p.q_gamma || !p.k_gamma || !p.cs || !p.sn || !p.q16 || !p.k16 || !p.vt16 || ((uintptr_t)p.vt16 & 7)) {
+        set_error("i8_gemm_qkv: null gamma/table/output pointer or V^T not 8-byte aligned");
+        return -1;
+    }
+    // 128 x 256 tiles: a tile is one head of 128 rows
+    return launch_p<128, 256, 4, 2, EPI_QKV>(s, p);
+}
+
 }  // namespace e2mi
 
 // ------------------------------------------------------------------ C ABI
@@ -1381,6 +1578,31 @@ extern "C" int e2mi_i8_gemm_gelu_mul(e2mi_stream stream, int8_t *yq, float *ys, 
     p.mul = mul;
     p.ldmul = ldmul;
     return launch_gemm_gelumul((hipStream_t)stream, p);
+}
+
+extern "C" int e2mi_i8_gemm_qkv(e2mi_stream stream, const int8_t *qa, const float *a_scales,
+                                const e2mi_q8w *w_qkv, int M, int S, const int32_t *pos, int H, int KV,
+                                const float *q_gamma, const float *k_gamma, float eps, const float *cos_tab,
+                                const float *sin_tab, uint16_t *q16, uint16_t *k16, uint16_t *vt16,
+                                float *q32, float *k32, float *v32) {
+    if (!weight_ok(w_qkv, "i8_gemm_qkv")) return -1;
+    GemmArgs p = make_args(qa, a_scales, w_qkv, M, 0, w_qkv->N);
+    p.q_gamma = q_gamma;
+    p.k_gamma = k_gamma;
+    p.cs = cos_tab;
+    p.sn = sin_tab;
+    p.pos = pos;
+    p.q16 = q16;
+    p.k16 = k16;
+    p.vt16 = vt16;
+    p.q32 = q32;
+    p.k32 = k32;
+    p.v32 = v32;
+    p.qH = H;
+    p.qKV = KV;
+    p.qS = S;
+    p.eps = eps;
+    return launch_gemm_qkv((hipStream_t)stream, p);
 }
 
 extern "C" int e2mi_i8_gemm_geglu(e2mi_stream stream, int8_t *q, float *qs, float *g,

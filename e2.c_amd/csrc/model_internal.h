@@ -70,8 +70,9 @@ void **model_engine_slot(e2_model *m);
 void model_set_engine_free(e2_model *m, void (*destroy)(void *));
 
 // weights.hip: unpack a packed [Npad/8][K/4][8][4] blob into dst rows (n / grp) * gstride + goff +
-// n % grp of a row-major [*][ld] device matrix
+// n % grp of a row-major [*][ld] device matrix; pair_order swaps bits 6 and 7 of that row index
+// (the rotate-half pair order of the fused q|k|v GEMM, e2mi_i8_gemm_qkv)
 int upload_packed_rows(int8_t *dst, int ld, const int8_t *wq, int N, int K, int grp, int gstride,
-                       int goff, hipStream_t s);
+                       int goff, hipStream_t s, bool pair_order = false);
 
 }  // namespace e2mi

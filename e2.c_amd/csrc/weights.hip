@@ -17,18 +17,19 @@ namespace e2mi {
 // identity for a plain upload, an offset for q|k|v concatenation, and the per-32 gate|up
 // interleave the GeGLU epilogue reads
 __global__ void k_unpack_quads(int8_t *__restrict__ dst, int ld, const int8_t *__restrict__ src,
-                               int N, int K, int grp, int gstride, int goff) {
+                               int N, int K, int grp, int gstride, int goff, int pair_order) {
     const int kq_n = (K + 3) / 4;
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)N * kq_n) return;
     const int n = (int)(i / kq_n), kq = (int)(i % kq_n);
     const uint32_t v = *(const uint32_t *)(src + ((size_t)(n >> 3) * kq_n + kq) * 32 + (n & 7) * 4);
-    const size_t row = (size_t)(n / grp) * gstride + goff + n % grp;
+    size_t row = (size_t)(n / grp) * gstride + goff + n % grp;
+    if (pair_order) row = (row & ~(size_t)0xC0) | ((row & 0x40) << 1) | ((row & 0x80) >> 1);
     *(uint32_t *)(dst + row * ld + kq * 4) = v;
 }
 
 int upload_packed_rows(int8_t *dst, int ld, const int8_t *wq, int N, int K, int grp, int gstride,
-                       int goff, hipStream_t s) {
+                       int goff, hipStream_t s, bool pair_order) {
     const size_t bytes = (size_t)((N + 7) / 8) * ((K + 3) / 4) * 32;
     int8_t *staging = nullptr;
     if (check_hip(hipMalloc(&staging, bytes), "hipMalloc staging")) return -1;
@@ -36,7 +37,7 @@ int upload_packed_rows(int8_t *dst, int ld, const int8_t *wq, int N, int K, int 
     if (!rc) {
         const long n = (long)N * ((K + 3) / 4);
         hipLaunchKernelGGL(k_unpack_quads, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst,
-                           ld, staging, N, K, grp, gstride, goff);
+                           ld, staging, N, K, grp, gstride, goff, pair_order ? 1 : 0);
         rc = check_hip(hipGetLastError(), "unpack launch");
     }
     // the staging blob must outlive the kernel

@@ -58,6 +58,8 @@ SIGNATURES = {
     "e2mi_i8_gemm_tok": (_I, [_P, _P, _I, _P, _P, C.POINTER(Q8W), _I, _I, _I]),
     "e2mi_i8_gemm_tok_q": (_I, [_P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
     "e2mi_i8_gemm_geglu": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(Q8W), _I]),
+    "e2mi_i8_gemm_qkv": (_I, [_P, _P, _P, C.POINTER(Q8W), _I, _I, _P, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P,
+                              _P, _P]),
     "e2mi_gemm_set_fold": (_I, [_I]),
     "e2mi_interleave_gate_up": (_I, [_P, _P, _P, _P, _P, _P, _I, _I]),
     "e2mi_norm_quant": (_I, [_P, _P, _P, _F, _I, _I, _P, _P, _P]),
@@ -369,6 +371,34 @@ def qkv_norm_rope(qkv, S, H, KV, q_gamma, k_gamma, cos_tab, sin_tab, eps=1e-6, w
                                     ptr(k_gamma), eps, ptr(cos_tab), ptr(sin_tab), ptr(q16),
                                     ptr(k16), ptr(vt16), ptr(q32), ptr(k32), ptr(v32)),
           "qkv_norm_rope")
+    return q16, k16, vt16, q32, k32, v32
+
+
+def qkv_pair_order(n):
+    """Row order of the fused q|k|v weight (e2mi_i8_gemm_qkv): device row r holds logical row
+    pair_order(r), bits 6 and 7 of the index swapped (its own inverse)."""
+    import numpy as np
+    n = np.asarray(n)
+    return (n & ~0xC0) | ((n & 0x40) << 1) | ((n & 0x80) >> 1)
+
+
+def i8_gemm_qkv(qa, as_, w: DeviceWeight, H, KV, q_gamma, k_gamma, cos_tab, sin_tab, S=None, pos=None,
+                eps=1e-6, want_f32=False, stream=None):
+    """The fused q|k|v GEMM + norms + RoPE (w uploaded in qkv_pair_order). pos given: packed rows
+    (V^T [KV][256][M]); else positions m % S (V^T [M/S][KV][256][S])."""
+    import torch
+    M = qa.shape[0]
+    D = 256
+    dev = qa.device
+    S = M if pos is not None else S
+    q16 = torch.empty((M, H * D), dtype=torch.float16, device=dev)
+    k16 = torch.empty((M, KV * D), dtype=torch.float16, device=dev)
+    vt16 = torch.empty((M // S, KV, D, S), dtype=torch.float16, device=dev)
+    f = (lambda *s: torch.empty(s, dtype=torch.float32, device=dev)) if want_f32 else (lambda *s: None)
+    q32, k32, v32 = f(M, H * D), f(M, KV * D), f(M, KV * D)
+    check(load().e2mi_i8_gemm_qkv(stream_ptr(stream), ptr(qa), ptr(as_), w.ref, M, S, ptr(pos), H, KV,
+                                  ptr(q_gamma), ptr(k_gamma), eps, ptr(cos_tab), ptr(sin_tab), ptr(q16),
+                                  ptr(k16), ptr(vt16), ptr(q32), ptr(k32), ptr(v32)), "i8_gemm_qkv")
     return q16, k16, vt16, q32, k32, v32
 
 

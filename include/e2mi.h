@@ -106,6 +106,24 @@ int e2mi_i8_gemm_tok_q(e2mi_stream stream, int8_t *yq, float *ys, const int8_t *
 int e2mi_i8_gemm_geglu(e2mi_stream stream, int8_t *q, float *qs, float *g, const int8_t *qa,
                        const float *a_scales, const e2mi_q8w *w_gate_up, int M);
 
+/* The q|k|v projection with the attention's row stage in its epilogue: the reference runs
+ * e2_i8_gemm for q|k|v, then the q/k/v RMSNorm and RoPE over the f32 result (text.c:836-854); this
+ * computes the same per 128 x 256 tile (one head) without the f32 round trip: per head of 256,
+ * rmsnorm (q/k times their gamma, v without), rotate-half RoPE on q and k, f16 q16 [M][H*256],
+ * k16 [M][KV*256] and V^T vt16 [M/S][KV][256][S], optional f32 copies q32/k32 (same layouts) and
+ * v32 [M][KV*256]: the outputs of e2mi_i8_gemm followed by e2mi_qkv_norm_rope (pos == NULL:
+ * positions m % S, M a multiple of S) or e2mi_qkv_norm_rope_packed (pos != NULL: S must be M).
+ * The row sums of squares are added in another order than the row kernel's, so an output can
+ * differ from that pair's by one f16 (f32) rounding step. head_dim 256 only, no bias or clamp.
+ * w_qkv holds the q|k|v rows [(H+2KV)*256][K] with the rows of every 256-row head in rotate-half
+ * pair order: bits 6 and 7 of the row index swapped (the epilogue then finds RoPE partners i and
+ * i + 128 in one lane); its scales permuted alike. */
+int e2mi_i8_gemm_qkv(e2mi_stream stream, const int8_t *qa, const float *a_scales,
+                     const e2mi_q8w *w_qkv, int M, int S, const int32_t *pos, int H, int KV,
+                     const float *q_gamma, const float *k_gamma, float eps, const float *cos_tab,
+                     const float *sin_tab, uint16_t *q16, uint16_t *k16, uint16_t *vt16, float *q32,
+                     float *k32, float *v32);
+
 /* Fold order of every GEMM above (process-wide; no counterpart in the reference, which has one):
  *   0 (default) the reference's per-block f = fma((float)acc_b, RN(as[m,b]*ws[n]), f), bit-exact;
  *   1 f = fma((float)acc_b, as[m,b], f) per block and one multiply by ws[n] at the end: two VALU
