@@ -450,7 +450,7 @@ __device__ inline float rms_inv256(float ss, float eps) {
 //  2. inv = 1 / sqrt(ss / 256 + eps) (the row kernel's arithmetic), shared through LDS per wave;
 //  3. q/k: x = (y * inv) * gamma, then a' = a c - b s, b' = b c + a s (products rounded, then the
 //     sum; kernels.c:112-126), f16; v: y * inv, f16, stored transposed per sequence.
-// scr: 2 x 8 x 32 floats of the step's free A|W stage.
+// scr: 3 x 8 x 32 words of the step's free A|W stage (partial sums, inverse rms, positions).
 template <bool FAST>
 __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmArgs &p, float (&f)[4][16],
                                                                      const float (&wsr)[4], int m0, int n0,
@@ -502,23 +502,40 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmA
             __builtin_amdgcn_make_buffer_rsrc(o32, 0, o32 ? (int)min((long)p.M * ld * 4, 0x7fffffffL) : 0, 0x00020000);
         const int i0 = wn * 64 + c;  // tiles t = 0, 1: dimensions i0 + 32 t and i0 + 32 t + 128
         const float g00 = gam[i0], g01 = gam[i0 + 128], g10 = gam[i0 + 32], g11 = gam[i0 + 160];
+        // the 16 rows' positions, then per group of 4 rows its 16 table entries, each batch of
+        // loads issued before any is used (every wait here also waits for the K loop's loads in
+        // flight, so one wait per batch rather than per value)
+        // the wave's 32 row positions go through LDS (lane l < 32: row wm * 32 + l)
+        int *xp = (int *)(scr + 2 * 8 * 32) + wave * 32;
+        if (lane < 32) {
+            const int m = min(m0 + wm * 32 + lane, p.M - 1);
+            xp[lane] = p.pos ? p.pos[m] : m % p.qS;
+        }
 #pragma unroll
         for (int g = 0; g < 4; g++) {
+            const int4 p4 = *(const int4 *)(xp + 8 * g + 4 * hh);
+            const int pg[4] = {p4.x, p4.y, p4.z, p4.w};
+            float cv[4][2], sv[4][2];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const size_t e = (size_t)pg[jj] * 256 + i0 + 32 * t;
+                    cv[jj][t] = p.cs[e];
+                    sv[jj][t] = p.sn[e];
+                }
             const float4 i4 = *(const float4 *)(xi + wave * 32 + 8 * g + 4 * hh);
             const float ivg[4] = {i4.x, i4.y, i4.z, i4.w};
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) {
-                const int r = 4 * g + jj, m = rb + 8 * g + jj, mc = min(m, p.M - 1);
-                const int ps = p.pos ? p.pos[mc] : mc % p.qS;
-                const float *cr = p.cs + (size_t)ps * 256 + i0, *sr = p.sn + (size_t)ps * 256 + i0;
+                const int r = 4 * g + jj, m = rb + 8 * g + jj;
                 const int o = (m * ld + hq * 256 + i0) * 2;
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
-                    const float cv = cr[32 * t], sv = sr[32 * t];
                     const float a = __fmul_rn(__fmul_rn(f[t][r], ivg[jj]), t ? g10 : g00);
                     const float b = __fmul_rn(__fmul_rn(f[t + 2][r], ivg[jj]), t ? g11 : g01);
-                    const float lo = __fmul_rn(a, cv) - __fmul_rn(b, sv);
-                    const float hi = __fmul_rn(b, cv) + __fmul_rn(a, sv);
+                    const float lo = __fmul_rn(a, cv[jj][t]) - __fmul_rn(b, sv[jj][t]);
+                    const float hi = __fmul_rn(b, cv[jj][t]) + __fmul_rn(a, sv[jj][t]);
                     __builtin_amdgcn_raw_buffer_store_b16(f2h_rn(lo), r16, o + 64 * t, 0, 0);
                     __builtin_amdgcn_raw_buffer_store_b16(f2h_rn(hi), r16, o + 64 * t + 256, 0, 0);
                     if (o32) {
