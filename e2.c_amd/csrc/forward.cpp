@@ -69,6 +69,12 @@ static double now_ms() {
 
 using namespace e2mi;
 
+// one launch's event pair of the per-kernel profile
+struct ProfEv {
+    const char *name;
+    hipEvent_t a, b;
+};
+
 struct e2mi_engine {
     e2_config cfg{};
     int dev = 0;
@@ -123,6 +129,17 @@ struct e2mi_engine {
     long calls = 0, kernels_last = 0;
     double last_ms = 0.0;
     std::vector<void *> allocs;
+    // diagnostics (the reference's E2_HIP_PROFILE and E2_HIP_DUMP, hip.c:51-108,138-139,279,
+    // forward.c:715-759). E2MI_PROFILE: the first call runs without a graph with an event pair per
+    // launch, totalled per stage into prof_text (printed to stderr). E2MI_DUMP=dir: after call
+    // number E2MI_DUMP_CALL (default 1) the workspace of its last chunk is written to dir.
+    bool prof_on = false, prof_rec = false;
+    std::vector<ProfEv> pev;
+    std::string prof_text;
+    std::string dump_dir;
+    long dump_call = 1;
+    int last_M = 0, last_B = 0, last_S = 0, last_layer = 0;
+    bool last_pk = false;
 };
 
 namespace e2mi {
@@ -289,85 +306,106 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s)
     const int nl = g->layer_limit > 0 && g->layer_limit < c.n_layers ? g->layer_limit : c.n_layers;
     const float eps = c.rms_eps;
     int k = 0;
-#define RUN(call)                                                                                  \
+    g->last_M = M;
+    g->last_B = B;
+    g->last_S = S;
+    g->last_pk = pk;
+    g->last_layer = nl - 1;
+    // with the per-kernel profile on (E2MI_PROFILE, first call only), each launch is bracketed by
+    // an event pair on its stream; the times are read after the call has synchronized
+#define RUN(name, call)                                                                            \
     do {                                                                                           \
-        if ((call) != 0) return -1;                                                                \
+        hipEvent_t ea_ = nullptr, eb_ = nullptr;                                                   \
+        if (g->prof_rec && (hipEventCreate(&ea_) != hipSuccess || hipEventCreate(&eb_) != hipSuccess || \
+                            hipEventRecord(ea_, s) != hipSuccess)) {                               \
+            if (ea_) (void)hipEventDestroy(ea_);                                                   \
+            if (eb_) (void)hipEventDestroy(eb_);                                                   \
+            ea_ = eb_ = nullptr;                                                                   \
+        }                                                                                          \
+        if ((call) != 0) {                                                                         \
+            if (ea_) (void)hipEventDestroy(ea_), (void)hipEventDestroy(eb_);                       \
+            return -1;                                                                             \
+        }                                                                                          \
         k++;                                                                                       \
+        if (ea_) {                                                                                 \
+            if (hipEventRecord(eb_, s) == hipSuccess) g->pev.push_back({name, ea_, eb_});          \
+            else (void)hipEventDestroy(ea_), (void)hipEventDestroy(eb_);                           \
+        }                                                                                          \
     } while (0)
-    RUN(launch_embed_checked(s, g->embed, c.vocab, g->ids, c.embed_scale, g->layers[0].ln_in, eps, M, Dm,
+    RUN("embed", launch_embed_checked(s, g->embed, c.vocab, g->ids, c.embed_scale, g->layers[0].ln_in, eps, M, Dm,
                              g->x, g->qa, g->as, g->d_bad));
     if (P > 0) {  // the per-layer inputs from the scaled embeddings (text.c:929-932)
         const int NP = c.n_layers * P;
-        RUN(e2mi_quantize(s, g->qg, g->gs, g->x, M, Dm, Dm, 128));
-        RUN(e2mi_i8_gemm(s, g->ple32, NP, g->qg, g->gs, &g->ple_model, M, 0, NP));
-        RUN(e2mi_scale_norm(s, g->ple32, M * c.n_layers, P, c.ple_scale, g->ple_proj_norm, eps, g->ple32));
+        RUN("ple_quant", e2mi_quantize(s, g->qg, g->gs, g->x, M, Dm, Dm, 128));
+        RUN("ple_model", e2mi_i8_gemm(s, g->ple32, NP, g->qg, g->gs, &g->ple_model, M, 0, NP));
+        RUN("ple_norm", e2mi_scale_norm(s, g->ple32, M * c.n_layers, P, c.ple_scale, g->ple_proj_norm, eps, g->ple32));
     }
     for (int l = 0; l < nl; l++) {
         const LayerDev &L = g->layers[l];
         const int D = L.geo.D, KV = L.geo.KV, qd = H * D;
         const float *cs = L.geo.full ? g->cos_full : g->cos_tab, *sn = L.geo.full ? g->sin_full : g->sin_tab;
         if (L.qkv_fused)
-            RUN(e2mi_i8_gemm_qkv(s, g->qa, g->as, &L.qkv, M, pk ? M : S, pk ? g->pos : nullptr, H, KV, L.q_norm,
+            RUN("qkv_norm_rope_gemm", e2mi_i8_gemm_qkv(s, g->qa, g->as, &L.qkv, M, pk ? M : S, pk ? g->pos : nullptr, H, KV, L.q_norm,
                                  L.k_norm, eps, cs, sn, g->q16, g->k16, g->vt16, g->attn_i8 ? g->q32 : nullptr,
                                  g->attn_i8 ? g->k32 : nullptr, g->attn_i8 ? g->v32 : nullptr));
         else
-            RUN(e2mi_i8_gemm(s, g->qkv, qd + 2 * KV * D, g->qa, g->as, &L.qkv, M, 0, L.qkv.N));
+            RUN("qkv", e2mi_i8_gemm(s, g->qkv, qd + 2 * KV * D, g->qa, g->as, &L.qkv, M, 0, L.qkv.N));
         if (pk) {
             if (!L.qkv_fused)
-                RUN(e2mi_qkv_norm_rope_packed(s, g->qkv, M, g->pos, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn,
+                RUN("qkv_norm_rope", e2mi_qkv_norm_rope_packed(s, g->qkv, M, g->pos, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn,
                                               g->q16, g->k16, g->vt16, g->q32, g->k32, g->v32));
-            RUN(e2mi_attention_packed_window(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len, g->pos,
+            RUN("attention", e2mi_attention_packed_window(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len, g->pos,
                                              B, S, H, KV, D, c.attn_scale, L.geo.window, g->cq, g->cs,
                                              nullptr, g->work, work_slots(g, B, M)));
             if (g->attn_i8)
-                RUN(e2mi_attention_i8_packed(s, g->q32, g->k32, g->v32, M, g->seq_start, g->seq_len, B, S,
+                RUN("attention_i8", e2mi_attention_i8_packed(s, g->q32, g->k32, g->v32, M, g->seq_start, g->seq_len, B, S,
                                              H, KV, D, g->i8ws, g->cq, g->cs, nullptr, g->work8,
                                              work_slots(g, B, M)));
         } else {
             if (!L.qkv_fused)
-                RUN(e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn, g->q16,
+                RUN("qkv_norm_rope", e2mi_qkv_norm_rope(s, g->qkv, M, S, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn, g->q16,
                                        g->k16, g->vt16, nullptr, nullptr, nullptr));
-            RUN(e2mi_attention(s, g->q16, g->k16, g->vt16, g->valid, B, S, H, KV, D, c.attn_scale,
+            RUN("attention", e2mi_attention(s, g->q16, g->k16, g->vt16, g->valid, B, S, H, KV, D, c.attn_scale,
                                g->cq, g->cs, nullptr));
         }
-        RUN(e2mi_i8_gemm(s, g->tmp, Dm, g->cq, g->cs, &L.o, M, 0, Dm));
-        RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_attn, L.ln_pre, eps, M, Dm, g->x, nullptr,
+        RUN("o_proj", e2mi_i8_gemm(s, g->tmp, Dm, g->cq, g->cs, &L.o, M, 0, Dm));
+        RUN("add_norm", e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_attn, L.ln_pre, eps, M, Dm, g->x, nullptr,
                                 g->qa, g->as));
-        RUN(e2mi_i8_gemm_geglu(s, g->qg, g->gs, nullptr, g->qa, g->as, &L.gu, M));
-        RUN(e2mi_i8_gemm(s, g->tmp, Dm, g->qg, g->gs, &L.down, M, 0, Dm));
+        RUN("gate_up_geglu", e2mi_i8_gemm_geglu(s, g->qg, g->gs, nullptr, g->qa, g->as, &L.gu, M));
+        RUN("down", e2mi_i8_gemm(s, g->tmp, Dm, g->qg, g->gs, &L.down, M, 0, Dm));
         const bool last = l + 1 == nl;
         const float *gnext = last ? g->final_norm : g->layers[l + 1].ln_in;
         if (P > 0) {
             // post_ffn norm_add, x itself quantized for the PLE gate; the PLE block; layer scale
-            RUN(e2mi_add_norm_scale_quant(s, g->tmp, g->x, L.ln_ffn, 1.0f, nullptr, eps, M, Dm, g->x, nullptr,
+            RUN("add_norm", e2mi_add_norm_scale_quant(s, g->tmp, g->x, L.ln_ffn, 1.0f, nullptr, eps, M, Dm, g->x, nullptr,
                                           g->qa, g->as));
-            RUN(e2mi_i8_gemm_gelu_mul(s, g->qg, g->gs, nullptr, g->qa, g->as, &L.ple_gate, M,
+            RUN("ple_gate", e2mi_i8_gemm_gelu_mul(s, g->qg, g->gs, nullptr, g->qa, g->as, &L.ple_gate, M,
                                       g->ple32 + (size_t)l * P, c.n_layers * P));
-            RUN(e2mi_i8_gemm(s, g->tmp, Dm, g->qg, g->gs, &L.ple_proj, M, 0, Dm));
-            RUN(e2mi_add_norm_scale_quant(s, g->tmp, g->x, L.ple_norm, L.layer_scalar, gnext, eps, M, Dm, g->x,
+            RUN("ple_proj", e2mi_i8_gemm(s, g->tmp, Dm, g->qg, g->gs, &L.ple_proj, M, 0, Dm));
+            RUN("add_norm", e2mi_add_norm_scale_quant(s, g->tmp, g->x, L.ple_norm, L.layer_scalar, gnext, eps, M, Dm, g->x,
                                           last ? g->xn : nullptr, g->qa, g->as));
         } else if (!last) {
-            RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, gnext, eps, M, Dm, g->x, nullptr, g->qa, g->as));
+            RUN("add_norm", e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, gnext, eps, M, Dm, g->x, nullptr, g->qa, g->as));
         } else {
-            RUN(e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, gnext, eps, M, Dm, g->x, g->xn,
+            RUN("add_norm", e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_ffn, gnext, eps, M, Dm, g->x, g->xn,
                                     c.out_dim > 0 ? g->qa : nullptr, c.out_dim > 0 ? g->as : nullptr));
         }
     }
     const float *rows = g->xn;
     if (c.out_dim > 0) {  // embed_proj of the final-normed rows (text.c:964-965)
-        RUN(e2mi_i8_gemm(s, g->qkv, c.out_dim, g->qa, g->as, &g->embed_proj, M, 0, c.out_dim));
+        RUN("embed_proj", e2mi_i8_gemm(s, g->qkv, c.out_dim, g->qa, g->as, &g->embed_proj, M, 0, c.out_dim));
         rows = g->qkv;
     }
     if (pk)
-        RUN(e2mi_pool_l2_packed(s, rows, g->seq_start, g->seq_len, B, S, g->dout, g->pool_ws, g->out));
+        RUN("pool", e2mi_pool_l2_packed(s, rows, g->seq_start, g->seq_len, B, S, g->dout, g->pool_ws, g->out));
     else
-        RUN(e2mi_pool_l2(s, rows, g->valid, B, S, g->dout, g->pool_ws, g->out));
+        RUN("pool", e2mi_pool_l2(s, rows, g->valid, B, S, g->dout, g->pool_ws, g->out));
 #undef RUN
     return k + 1;  // the pool is two launches
 }
 
 static int run_shape(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s) {
-    if (!g->use_graph) {
+    if (!g->use_graph || g->prof_rec) {
         const int k = enqueue(g, B, S, Mp, pk, s);
         if (k < 0) return -1;
         g->kernels_last = k;
@@ -545,6 +583,7 @@ static int set_attention_i8(e2mi_engine *g, bool on) {
 extern "C" void e2mi_destroy(e2mi_engine *g) {
     if (!g) return;
     if (g->stream) (void)hipStreamSynchronize(g->stream);
+    for (const ProfEv &e : g->pev) (void)hipEventDestroy(e.a), (void)hipEventDestroy(e.b);
     for (auto &kv : g->graphs) (void)hipGraphExecDestroy(kv.second);
     for (void *p : g->allocs) (void)hipFree(p);
     if (g->h_ids) (void)hipHostFree(g->h_ids);
@@ -583,6 +622,14 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
     g->use_graph = !(ng && ng[0] && ng[0] != '0');
     const char *nf = getenv("E2MI_NOFUSE");
     g->fuse_qkv = !(nf && nf[0] && nf[0] != '0');
+    const char *pf = getenv("E2MI_PROFILE");
+    g->prof_on = pf && pf[0] && pf[0] != '0';
+    const char *dd = getenv("E2MI_DUMP");
+    if (dd && dd[0]) {
+        g->dump_dir = dd;
+        const char *dc = getenv("E2MI_DUMP_CALL");
+        g->dump_call = dc && atol(dc) > 0 ? atol(dc) : 1;
+    }
     auto fail = [&]() -> e2mi_engine * {
         e2mi_destroy(g);
         return nullptr;
@@ -687,6 +734,101 @@ namespace e2mi {
 // a call on stream s first drains the previous call's stream when it is another one (the calls
 // share the workspace and the pinned staging arrays), and reads the id flag an asynchronous device
 // call left behind
+// the profiled call's event pairs, after its stream has synchronized: per-stage totals into the
+// report (stages in order of first launch)
+static void prof_flush(e2mi_engine *g) {
+    if (g->pev.empty()) return;
+    std::vector<std::string> names;
+    std::vector<double> ms;
+    std::vector<long> n;
+    for (const ProfEv &e : g->pev) {
+        float t = 0.f;
+        if (hipEventElapsedTime(&t, e.a, e.b) != hipSuccess) t = 0.f;
+        (void)hipEventDestroy(e.a);
+        (void)hipEventDestroy(e.b);
+        size_t i = 0;
+        while (i < names.size() && names[i] != e.name) i++;
+        if (i == names.size()) {
+            names.push_back(e.name);
+            ms.push_back(0.0);
+            n.push_back(0);
+        }
+        ms[i] += t;
+        n[i]++;
+    }
+    g->pev.clear();
+    double total = 0.0;
+    for (double t : ms) total += t;
+    char line[256];
+    snprintf(line, sizeof line, "[e2mi] kernel profile, one call (ms, total %.3f):\n", total);
+    std::string text = line;
+    for (size_t i = 0; i < names.size(); i++) {
+        snprintf(line, sizeof line, "[e2mi]   %-20s %9.3f ms %6ld calls %8.4f ms/call %5.1f%%\n", names[i].c_str(),
+                 ms[i], n[i], ms[i] / n[i], total > 0 ? 100.0 * ms[i] / total : 0.0);
+        text += line;
+    }
+    g->prof_text += text;
+    fputs(text.c_str(), stderr);
+}
+
+static int dump_file(const std::string &dir, const char *name, const void *dptr, size_t bytes) {
+    if (!dptr || !bytes) return 0;
+    std::vector<unsigned char> h(bytes);
+    if (check_hip(hipMemcpy(h.data(), dptr, bytes, hipMemcpyDeviceToHost), "dump copy")) return -1;
+    const std::string path = dir + "/" + name;
+    FILE *f = fopen(path.c_str(), "wb");
+    if (!f) {
+        set_error("dump: cannot write %s", path.c_str());
+        return -1;
+    }
+    const size_t w = fwrite(h.data(), 1, bytes, f);
+    fclose(f);
+    if (w != bytes) {
+        set_error("dump: short write to %s", path.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+// the workspace of the last chunk after a call (its last layer's values; e2mi_set_layer_limit
+// picks the layer): residual x, final-normed rows xn, the attention's f16 inputs, the quantized
+// context and its scales, the last GEMM output tmp, the embeddings, and for packed batches each
+// row's position and source index. File names carry the element type.
+static int dump_workspace(e2mi_engine *g, hipStream_t s) {
+    if (check_hip(hipStreamSynchronize(s), "dump sync")) return -1;
+    const e2_config &c = g->cfg;
+    const LayerGeom &L = g->layers[g->last_layer].geo;
+    const size_t M = (size_t)g->last_M, qd = (size_t)c.n_heads * L.D, kvd = (size_t)L.KV * L.D;
+    const std::string &d = g->dump_dir;
+    int rc = dump_file(d, "e2mi_x.f32", g->x, M * c.hidden * 4) || dump_file(d, "e2mi_xn.f32", g->xn, M * c.hidden * 4) ||
+             dump_file(d, "e2mi_tmp.f32", g->tmp, M * c.hidden * 4) || dump_file(d, "e2mi_q16.f16", g->q16, M * qd * 2) ||
+             dump_file(d, "e2mi_k16.f16", g->k16, M * kvd * 2) || dump_file(d, "e2mi_vt16.f16", g->vt16, M * kvd * 2) ||
+             dump_file(d, "e2mi_ctx_q.i8", g->cq, M * qd) || dump_file(d, "e2mi_ctx_s.f32", g->cs, M * (qd / 128) * 4) ||
+             dump_file(d, "e2mi_out.f32", g->out, (size_t)g->last_B * g->dout * 4);
+    if (!rc && g->last_pk) {
+        // positions as the kernels read them; the row map of the last chunk's plan (host staging)
+        rc = dump_file(d, "e2mi_pos.i32", g->pos, M * 4);
+        FILE *f = rc ? nullptr : fopen((d + "/e2mi_rowmap.i32").c_str(), "wb");
+        if (!rc && (!f || fwrite(g->h_rowmap, 4, M, f) != M)) {
+            set_error("dump: cannot write %s/e2mi_rowmap.i32", d.c_str());
+            rc = -1;
+        }
+        if (f) fclose(f);
+    }
+    return rc ? -1 : 0;
+}
+
+// after a call's last chunk: the profile (first call) and the dump (call E2MI_DUMP_CALL)
+static int end_call(e2mi_engine *g, hipStream_t s) {
+    if (g->prof_rec) {
+        if (check_hip(hipStreamSynchronize(s), "profile sync")) return -1;
+        prof_flush(g);
+        g->prof_rec = false;
+    }
+    if (!g->dump_dir.empty() && g->calls == g->dump_call) return dump_workspace(g, s);
+    return 0;
+}
+
 static int begin_call(e2mi_engine *g, hipStream_t s) {
     if (g->last_stream && g->last_stream != s && check_hip(hipStreamSynchronize(g->last_stream), "previous call sync"))
         return -1;
@@ -702,6 +844,9 @@ static int begin_call(e2mi_engine *g, hipStream_t s) {
         }
     }
     g->last_stream = s;
+    for (const ProfEv &e : g->pev) (void)hipEventDestroy(e.a), (void)hipEventDestroy(e.b);  // a failed call's
+    g->pev.clear();
+    g->prof_rec = g->prof_on && g->calls == 0;
     return 0;
 }
 }  // namespace e2mi
@@ -747,7 +892,7 @@ extern "C" int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const u
     }
     g->calls++;
     g->last_ms = now_ms() - t0;
-    return 0;
+    return end_call(g, g->stream);
 }
 
 extern "C" int e2mi_text_embed(e2mi_engine *g, const int32_t *ids, int n_ids, float *out) {
@@ -827,7 +972,7 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
     }
     g->calls++;
     g->last_ms = now_ms() - t0;
-    return 0;
+    return end_call(g, s);
 }
 
 // ------------------------------------------------------------------ e2.h text entries
@@ -882,6 +1027,8 @@ extern "C" int e2mi_set_attention(e2mi_engine *g, int kind) {
     if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
     return set_attention_i8(g, kind == E2_ATTN_I8);
 }
+
+extern "C" const char *e2mi_profile_text(const e2mi_engine *g) { return g ? g->prof_text.c_str() : ""; }
 
 extern "C" int e2mi_stats(e2mi_engine *g, long *calls, long *kernels_last, double *last_ms) {
     if (!g) {

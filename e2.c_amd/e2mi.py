@@ -113,6 +113,7 @@ SIGNATURES = {
     "e2mi_text_embed_batch": (_I, [_P, _P, _P, _I, _I, _P]),
     "e2mi_text_embed_batch_device": (_I, [_P, _P, _P, _I, _I, _P, _P]),
     "e2mi_stats": (_I, [_P, C.POINTER(C.c_long), C.POINTER(C.c_long), C.POINTER(C.c_double)]),
+    "e2mi_profile_text": (C.c_char_p, [_P]),
     "e2mi_set_layer_limit": (_I, [_P, _I]),
     "e2mi_set_packing": (_I, [_P, _I]),
     "e2mi_set_attention": (_I, [_P, _I]),

@@ -315,6 +315,16 @@ int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, const uint8
                                  int batch, int seq_len, float *out, e2mi_stream stream);
 /* Calls served, kernels launched by the last forward, wall time of the last call (e2_hip_stats). */
 int e2mi_stats(e2mi_engine *g, long *calls, long *kernels_last, double *last_ms);
+/* Diagnostics set by the environment at e2mi_create, as the reference's HIP backend reads
+ * E2_HIP_PROFILE and E2_HIP_DUMP (src/gpu/hip/hip.c:51-108,121,138-139): E2MI_PROFILE=1 runs the
+ * engine's first call without a graph, one event pair per launch, and reports per-stage times
+ * (printed to stderr as e2h_prof_report prints them, hip.c:88-100); E2MI_DUMP=<dir> writes the
+ * workspace of call number E2MI_DUMP_CALL (default 1, its last chunk, its last layer: see
+ * e2mi_set_layer_limit) to <dir>/e2mi_<name>.<f32|f16|i8|i32> (forward.c:725-759: x, xn, tmp, q16,
+ * k16, vt16, ctx_q, ctx_s, out, and for packed batches pos and rowmap). e2mi_profile_text returns the
+ * report of the profiled call ("" before it or without E2MI_PROFILE); the text lives as long as the
+ * engine. No reference counterpart for the accessor (the reference only prints). */
+const char *e2mi_profile_text(const e2mi_engine *g);
 /* Run only the first n layers (0: all) before the final norm and pooling: the reference's
  * E2_HIP_LAYERS bisection knob (forward.c:359-366), for parity checks layer by layer. */
 int e2mi_set_layer_limit(e2mi_engine *g, int n_layers);
