@@ -841,6 +841,20 @@ def main():
     q_t = time_calls(torch, lambda: e2mi.quantize(cases[0]["x"], q=cases[0]["qa"],
                                                   scales=cases[0]["as_"]), 10)
     q_bytes = M * 768 * (4 + 1) + M * 6 * 4
+    # config 5 end to end: the per-token quantizer (f32 activations -> int8 + one scale per row)
+    # for each K, and quantize + f32 GEMM per step (the quantizer's output feeds the GEMM)
+    tok_quant = {}
+    for K in sorted({c["K"] for c in cases}):
+        c = next(c for c in cases if c["K"] == K)
+        t = time_calls(torch, lambda c=c: e2mi.quantize(c["x"], block=c["K"], q=c["qt"], scales=c["st"]), 10)
+        tok_quant[f"65536x{K}"] = {"us": round(t * 1e6, 2), "GB/s": round(M * (K * 5 + 4) / t / 1e9, 1)}
+
+    def quant_gemm(c):
+        e2mi.quantize(c["x"], block=c["K"], q=c["qt"], scales=c["st"], stream=stream)
+        gemm_tok(c)
+    qg_sweep = sweep(quant_gemm)
+    qg_sweep["note"] = ("per-token quantize of the f32 activations + the f32 GEMM, per shape; tops counts "
+                        "the GEMM's 2 M N K over both launches")
 
     # roofline: the dominant launch of the step (longest average duration)
     dom = int(np.argmax(per_launch))
@@ -901,6 +915,8 @@ def main():
                           "once; int32 accumulators exact, f32 within 1e-4 rel of the reference order",
         "vendor_int_mm": vendor,
         "quantize_65536x768": {"us": round(q_t * 1e6, 2), "GB/s": round(q_bytes / q_t / 1e9, 1)},
+        "per_token_quantize": tok_quant,
+        "per_token_quantize_plus_gemm": qg_sweep,
         "roofline": roofline,
     }
     out["vision_projections"] = vision_bench(torch, e2mi)

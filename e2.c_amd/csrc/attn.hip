@@ -38,8 +38,11 @@ struct AttnArgs {
     float *c32;             // optional [M][H*D] f32 context
     // packed batches: sequence b is rows [seq_start[b], seq_start[b] + seq_len[b]), all valid
     const int32_t *seq_start, *seq_len;
-    // packed batches, optional: one (sequence | head << 16 | query block << 24) per workgroup of a
-    // 1-D grid, longest sequences first; negative entries are no work
+    // packed batches, optional: one work entry per workgroup of a 1-D grid, longest sequences
+    // first; negative entries are no work. Entry = sequence | head << 16 | part << 20 |
+    // (parts - 1) << 22 | query block << 24 (see work_entry): with parts > 1 the block's key tiles
+    // are split into that many consecutive ranges, one workgroup each, which leave unnormalised
+    // partial states in part_o / part_ml for k_attn_merge
     const int32_t *work;
     int B, S, H, KV;
     float scale;
@@ -47,7 +50,18 @@ struct AttnArgs {
     // pos [M] is each row's position in its padded sequence (null: the packed index)
     int window;
     const int32_t *pos;
+    // split key ranges (head_dim 256): part p of row r, head h holds the context sum o (before the
+    // division by the softmax sum) at part_o[(p * part_rows + r) * H * D + h * D ..] and its row max
+    // and sum at part_ml[((p * part_rows + r) * H + h) * 2 + 0 | 1]
+    float *part_o, *part_ml;
+    int part_rows;
 };
+
+// the packed work entry (AttnArgs::work); h < 16, parts <= 4, query block < 128
+__host__ __device__ inline int work_entry(int b, int h, int part, int parts, int qb) {
+    return b | (h << 16) | (part << 20) | ((parts - 1) << 22) | (qb << 24);
+}
+constexpr int kMaxParts = 4;
 
 __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     __shared__ __align__(16) _Float16 Ks[kKT * kKP];
@@ -273,12 +287,14 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
     constexpr int NQ = D / 16, NO = D / 32, NLK = D / 64, NLV = D / 64;
     constexpr int RPI = 512 / D, LPR = D / 8;  // K rows per load, lanes per K row
     extern __shared__ __align__(16) unsigned char pk_smem[];
-    int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z, part = 0, parts = 1;
     if (a.work) {
         const int item = a.work[blockIdx.x];
         if (item < 0) return;
         b = item & 0xffff;
-        h = (item >> 16) & 0xff;
+        h = (item >> 16) & 0xf;
+        part = (item >> 20) & 3;
+        parts = ((item >> 22) & 3) + 1;
         qb = item >> 24;
     }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5;
@@ -307,6 +323,11 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
         pq0 = a.pos ? a.pos[row0 + q0] : q0;
         pq1 = a.pos ? a.pos[row0 + q1] : q1;
         pqi = a.pos ? a.pos[row0 + qc] : qc;
+    }
+    if (parts > 1) {  // this workgroup's share of the block's key tiles
+        const int n = kt1 - kt0, t0 = kt0;
+        kt0 = t0 + n * part / parts;
+        kt1 = t0 + n * (part + 1) / parts;
     }
     // wait for the Q loads here, with a wait the compiler's wait-count pass sees: otherwise it
     // waits for them inside the tile loop, where the count would also cover the tile loads in
@@ -445,6 +466,20 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     const float ltot = lrun + __shfl_xor(lrun, 32);
+    if (parts > 1) {
+        // a partial state: the context sum, the row max and the row sum (mrun is the pair's)
+        if (qi >= Sk) return;
+        const size_t prow = (size_t)part * a.part_rows + row0 + qi;
+        float *po = a.part_o + prow * HD + h * D;
+#pragma unroll
+        for (int t = 0; t < NO; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *(float4 *)(po + 32 * t + 8 * g + 4 * half) =
+                    make_float4(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]);
+        if (half == 0) *(float2 *)(a.part_ml + (prow * a.H + h) * 2) = make_float2(mrun, ltot);
+        return;
+    }
     const float inv = (qvalid && ltot > 0.f) ? __fdiv_rn(1.0f, ltot) : 0.f;
 #pragma unroll
     for (int t = 0; t < NO; t++) o[t] *= inv;
@@ -501,7 +536,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
         const int item = a.work[blockIdx.x];
         if (item < 0) return;
         b = item & 0xffff;
-        h = (item >> 16) & 0xff;
+        h = (item >> 16) & 0xf;  // (one part: work_entry(b, h, 0, 1, qb))
         qb = item >> 24;
     }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5;
@@ -692,6 +727,71 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
     }
 }
 
+// Merge of split key ranges (k_attn_packed with parts > 1; head_dim 256), for the entries of the
+// merge list (work_entry with part 0 and the block's part count): per query row, M = max_p m_p,
+// w_p = e^(m_p - M), ctx = (sum_p w_p o_p) * RN(1 / sum_p w_p l_p), parts in order, then the
+// per-128 quantization of k_attn_packed's epilogue. Four workgroups per entry, 32 rows each, 8 rows
+// per wave with all their loads issued before any is used; a lane holds 4 dims (lanes 0-31 the
+// first 128-dim block, 32-63 the second).
+__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a, const int32_t *merge) {
+    constexpr int D = 256, RW = 8;  // rows per wave, their loads issued together
+    const int item = merge[blockIdx.x >> 2];
+    if (item < 0) return;
+    const int b = item & 0xffff, h = (item >> 16) & 0xf, parts = ((item >> 22) & 3) + 1, qb = item >> 24;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, half = lane >> 5, d = 4 * lane;
+    const int HD = a.H * D;
+    const size_t row0 = (size_t)a.seq_start[b];
+    const int Sk = a.seq_len[b];
+    // workgroup blockIdx.x % 4 takes rows 32 (blockIdx.x % 4) .. + 31 of the block; wave w 8 of them
+    const int q0 = qb * 128 + (blockIdx.x & 3) * 32 + w * RW;
+    float mp[RW][kMaxParts], lp[RW][kMaxParts];
+    float4 op[RW][kMaxParts];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const size_t row = row0 + min(q0 + r, Sk - 1);
+#pragma unroll
+        for (int p = 0; p < kMaxParts; p++) {
+            if (p < parts) {
+                const size_t prow = (size_t)p * a.part_rows + row;
+                const float2 ml = *(const float2 *)(a.part_ml + (prow * a.H + h) * 2);
+                mp[r][p] = ml.x;
+                lp[r][p] = ml.y;
+                op[r][p] = *(const float4 *)(a.part_o + prow * HD + h * D + d);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const int qi = q0 + r;
+        if (qi >= Sk) break;
+        const size_t row = row0 + qi;
+        float M = -INFINITY;
+#pragma unroll
+        for (int p = 0; p < kMaxParts; p++)
+            if (p < parts) M = fmaxf(M, mp[r][p]);
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int p = 0; p < kMaxParts; p++) {
+                if (p >= parts) break;
+                const float wp = mp[r][p] == -INFINITY ? 0.f : __expf(mp[r][p] - M);
+                const float4 v = op[r][p];
+                L += wp * lp[r][p];
+                o = make_float4(o.x + wp * v.x, o.y + wp * v.y, o.z + wp * v.z, o.w + wp * v.w);
+            }
+        }
+        const float inv = L > 0.f ? __fdiv_rn(1.0f, L) : 0.f;
+        o = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+        const float am = group_max<32>(fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+        const QScale qs = qscale(am);
+        *(uint32_t *)(a.cq + row * HD + h * D + d) =
+            pack4(qbyte(o.x, qs.inv), qbyte(o.y, qs.inv), qbyte(o.z, qs.inv), qbyte(o.w, qs.inv));
+        if (a.c32) *(float4 *)(a.c32 + row * HD + h * D + d) = o;
+        if ((lane & 31) == 0) a.cs[row * (HD / kQBlock) + h * 2 + half] = qs.sc;
+    }
+}
+
 template <int D, bool WIN>
 static int attn_packed_attr() {
     static bool done = false;
@@ -731,7 +831,8 @@ static int attention_packed(const char *who, e2mi_stream stream, const uint16_t 
                             const uint16_t *k16, const uint16_t *vt16, int M, const int32_t *seq_start,
                             const int32_t *seq_len, const int32_t *pos, int B, int max_len, int H,
                             int KV, int D, float scale, int window, int8_t *ctx_q, float *ctx_s,
-                            float *ctx32, const int32_t *work, int n_work) {
+                            float *ctx32, const int32_t *work, int n_work, const int32_t *merge = nullptr,
+                            int n_merge = 0, float *part = nullptr, int part_rows = 0) {
     if ((D != 256 && D != 512) || B <= 0 || M <= 0 || max_len <= 0 || H <= 0 || KV <= 0 || H % KV ||
         window < 0) {
         set_error("%s: needs head_dim 256 or 512, H %% KV == 0 and window >= 0 (B=%d M=%d H=%d KV=%d D=%d)",
@@ -744,12 +845,22 @@ static int attention_packed(const char *who, e2mi_stream stream, const uint16_t 
         set_error("%s: null or misaligned pointer", who);
         return -1;
     }
-    if (work && (n_work <= 0 || B > 0xffff || H > 0xff || (max_len + 127) / 128 > 127)) {
-        set_error("%s: work list needs n_work > 0, B < 65536, H < 256, max_len < 16257", who);
+    if (work && (n_work <= 0 || B > 0xffff || H > 15 || (max_len + 127) / 128 > 127)) {
+        set_error("%s: work list needs n_work > 0, B < 65536, H < 16, max_len < 16257", who);
+        return -1;
+    }
+    if (merge && (D != 256 || !work || n_merge <= 0 || !part || part_rows < M || !aligned16(part))) {
+        set_error("%s: split key ranges need head_dim 256, a work list, n_merge > 0 and a 16-byte aligned "
+                  "partial workspace of at least M rows", who);
         return -1;
     }
     AttnArgs a = {q16, k16, vt16, nullptr, ctx_q, ctx_s, ctx32, seq_start, seq_len, work, B, M, H, KV, scale,
                   window, pos};
+    if (merge) {
+        a.part_o = part;
+        a.part_ml = part + (size_t)kMaxParts * part_rows * H * D;
+        a.part_rows = part_rows;
+    }
     // the direct-to-LDS kernel needs 4-byte-aligned V^T rows and 32-bit offsets into the V^T slab
     // and the K rows; every sequence must start on an even row (the engine starts them on
     // multiples of 8)
@@ -779,6 +890,14 @@ static int attention_packed(const char *who, e2mi_stream stream, const uint16_t 
         set_error("%s: head_dim 512 or a window needs an even M, 4-byte-aligned V^T and slabs under 2 GiB", who);
         return -1;
     }
+    if (merge) {
+        if (!direct) {
+            set_error("%s: split key ranges need the direct-to-LDS kernel (even M, aligned V^T)", who);
+            return -1;
+        }
+        if (check_hip(hipGetLastError(), "attention launch")) return -1;
+        hipLaunchKernelGGL(k_attn_merge, dim3(4 * n_merge), dim3(256), 0, (hipStream_t)stream, a, merge);
+    }
     return check_hip(hipGetLastError(), "attention launch");
 }
 
@@ -793,6 +912,26 @@ extern "C" int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, co
     }
     return attention_packed("attention_packed", stream, q16, k16, vt16, M, seq_start, seq_len, nullptr, B,
                             max_len, H, KV, D, scale, 0, ctx_q, ctx_s, ctx32, work, n_work);
+}
+
+extern "C" size_t e2mi_attention_part_bytes(int part_rows, int H, int D) {
+    if (part_rows <= 0 || H <= 0 || D != 256) return 0;
+    return (size_t)kMaxParts * part_rows * H * ((size_t)D + 2) * 4;
+}
+
+extern "C" int e2mi_attention_packed_split(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
+                                           const uint16_t *vt16, int M, const int32_t *seq_start,
+                                           const int32_t *seq_len, const int32_t *pos, int B, int max_len, int H,
+                                           int KV, int D, float scale, int window, int8_t *ctx_q, float *ctx_s,
+                                           float *ctx32, const int32_t *work, int n_work, const int32_t *merge,
+                                           int n_merge, float *part, int part_rows) {
+    if (!merge || !part) {
+        set_error("attention_packed_split: null merge list or partial workspace");
+        return -1;
+    }
+    return attention_packed("attention_packed_split", stream, q16, k16, vt16, M, seq_start, seq_len, pos, B,
+                            max_len, H, KV, D, scale, window, ctx_q, ctx_s, ctx32, work, n_work, merge, n_merge,
+                            part, part_rows);
 }
 
 extern "C" int e2mi_attention_packed_window(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,

@@ -152,7 +152,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
         const int item = a.work[blockIdx.x];
         if (item < 0) return;
         b = item & 0xffff;
-        h = (item >> 16) & 0xff;
+        h = (item >> 16) & 0xf;  // (one part: work_entry(b, h, 0, 1, qb))
         qb = item >> 24;
     }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5;

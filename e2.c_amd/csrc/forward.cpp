@@ -104,8 +104,16 @@ struct e2mi_engine {
     // per sequence its first row and length (device copies at fixed addresses for the graphs)
     int32_t *rowmap = nullptr, *pos = nullptr, *seq_start = nullptr, *seq_len = nullptr;
     int32_t *h_rowmap = nullptr, *h_pos = nullptr, *h_start = nullptr, *h_len = nullptr;
-    // attention work list (longest sequences first), a fixed number of slots per (sequences, rows)
+    // attention work list (longest sequences first), a fixed number of slots per (sequences, rows):
+    // with split key ranges (head_dim-256 layers) split_factor times the unsplit slots, the merge
+    // list, the partial states, and an unsplit list for the head_dim-512 layers
     int32_t *work = nullptr, *h_work = nullptr;
+    int split_factor = 1;  // the most parts a block of this geometry can take (1: never split)
+    int split_mode = 2;    // 0 never, 1 always, 2 when a chunk's blocks fill less than half the device
+    bool split_now = false;  // the planned chunk splits (part of the graph key)
+    int slots_device = 512;  // attention workgroups the device runs at once (2 per CU)
+    int32_t *mwork = nullptr, *h_mwork = nullptr, *work_full = nullptr, *h_work_full = nullptr;
+    float *part = nullptr;
     // the int8 attention (text.c:638-700) when the selection surface picks it: sequences of at
     // least kI8MinKeys keys go to its own work list, f32 q/k/v feed it (packed batches only)
     bool attn_i8 = false;
@@ -294,6 +302,26 @@ constexpr int kI8MinKeys = 32;
 // attention workgroups of a packed chunk of n sequences in M rows: at most H (M / 128 + n)
 static int work_slots(const e2mi_engine *g, int n, int M) { return g->cfg.n_heads * (M / 128 + n); }
 
+// split key ranges: a 128-query block whose keys span more than kAttnPartTiles 32-key tiles is
+// split into ceil(tiles / kAttnPartTiles) parts (at most kMaxParts), so the longest blocks no longer
+// set the attention's time alone; the parts depend only on the sequence's own length and the window
+constexpr int kAttnPartTiles = 8, kMaxAttnParts = 4;
+static int attn_parts(const e2mi_engine *g, int L, int q) {
+    if (!g->split_now || g->split_factor <= 1) return 1;
+    const int W = g->cfg.window;
+    int t0 = 0, t1 = (L + 31) / 32;
+    if (W > 0) {
+        const int q0 = q * 128, q1 = std::min(q0 + 127, L - 1);
+        t0 = std::max(q0 - W, 0) / 32;
+        t1 = std::min(std::min(q1 + W, L - 1) / 32 + 1, t1);
+    }
+    const int n = t1 - t0;
+    return std::max(1, std::min({g->split_factor, (n + kAttnPartTiles - 1) / kAttnPartTiles, n}));
+}
+static int32_t work_item(int b, int h, int part, int parts, int qb) {
+    return b | (h << 16) | (part << 20) | ((parts - 1) << 22) | (qb << 24);
+}
+
 // every kernel of one forward over B sequences of S tokens (M rows: B * S padded, or the packed
 // row count), on stream s; returns the launch count or -1
 static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s) {
@@ -354,9 +382,20 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s)
             if (!L.qkv_fused)
                 RUN("qkv_norm_rope", e2mi_qkv_norm_rope_packed(s, g->qkv, M, g->pos, H, KV, D, L.q_norm, L.k_norm, eps, cs, sn,
                                               g->q16, g->k16, g->vt16, g->q32, g->k32, g->v32));
-            RUN("attention", e2mi_attention_packed_window(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len, g->pos,
-                                             B, S, H, KV, D, c.attn_scale, L.geo.window, g->cq, g->cs,
-                                             nullptr, g->work, work_slots(g, B, M)));
+            if (D == 256 && g->split_now) {
+                RUN("attention", e2mi_attention_packed_split(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len,
+                                                             g->pos, B, S, H, KV, D, c.attn_scale, L.geo.window,
+                                                             g->cq, g->cs, nullptr, g->work,
+                                                             work_slots(g, B, M) * g->split_factor, g->mwork,
+                                                             work_slots(g, B, M), g->part, g->R));
+                k++;  // the merge
+            } else {
+                RUN("attention", e2mi_attention_packed_window(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len,
+                                                              g->pos, B, S, H, KV, D, c.attn_scale, L.geo.window,
+                                                              g->cq, g->cs, nullptr,
+                                                              g->work_full ? g->work_full : g->work,
+                                                              work_slots(g, B, M)));
+            }
             if (g->attn_i8)
                 RUN("attention_i8", e2mi_attention_i8_packed(s, g->q32, g->k32, g->v32, M, g->seq_start, g->seq_len, B, S,
                                              H, KV, D, g->i8ws, g->cq, g->cs, nullptr, g->work8,
@@ -411,7 +450,7 @@ static int run_shape(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t 
         g->kernels_last = k;
         return 0;
     }
-    auto key = std::make_tuple(B, S, Mp, pk ? 1 : 0);
+    auto key = std::make_tuple(B, S, Mp, (pk ? 1 : 0) | (pk && g->split_now ? 2 : 0));
     auto it = g->graphs.find(key);
     if (it == g->graphs.end()) {
         // the first call of a shape runs eagerly (kernel attributes get set outside any capture),
@@ -491,7 +530,15 @@ static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
     for (int b = 0; b < n; b++) order[b] = b;
     std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return g->h_len[x] > g->h_len[y]; });
     const int H = g->cfg.n_heads, slots = work_slots(g, n, Mp);
-    int k = 0, k8 = 0;
+    // split long blocks' keys only where the unsplit blocks leave most of the device idle (few
+    // sequences): a full batch's blocks already fill it, and the parts' partial states then cost
+    // more than they balance (config 4: 9460 -> 8115 embeddings/s split; one 2048-token sequence at
+    // the reference geometry: 5.77 -> 4.87 ms)
+    long blocks = 0;
+    for (int b = 0; b < n; b++) blocks += (long)H * ((g->h_len[b] + 127) / 128);
+    g->split_now = g->split_factor > 1 && (g->split_mode == 1 || (g->split_mode == 2 && 2 * blocks <= g->slots_device));
+    int k = 0, k8 = 0, km = 0, kf = 0;
+    bool any_split = false;
     for (int b : order) {
         // text.c:873-875: shorter sequences, and sequences with padding inside (all rows of the
         // trimmed sequence must be valid), take the f32 path there, the f16 kernel here
@@ -499,12 +546,23 @@ static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
         const bool i8 = g->attn_i8 && L >= kI8MinKeys && g->h_pos[r0] == 0 && g->h_pos[r0 + L - 1] == L - 1;
         for (int h = 0; h < H; h++)
             for (int q = 0; q < (g->h_len[b] + 127) / 128; q++) {
-                const int32_t item = b | (h << 16) | (q << 24);
-                if (i8) g->h_work8[k8++] = item;
-                else g->h_work[k++] = item;
+                if (i8) {
+                    g->h_work8[k8++] = work_item(b, h, 0, 1, q);
+                    continue;
+                }
+                const int P = attn_parts(g, L, q);
+                for (int p = 0; p < P; p++) g->h_work[k++] = work_item(b, h, p, P, q);
+                if (P > 1) g->h_mwork[km++] = work_item(b, h, 0, P, q);
+                any_split |= P > 1;
+                if (g->h_work_full) g->h_work_full[kf++] = work_item(b, h, 0, 1, q);
             }
     }
-    while (k < slots) g->h_work[k++] = -1;
+    g->split_now = any_split;  // no block long enough: the unsplit kernel, no merge launch
+    while (k < slots * g->split_factor) g->h_work[k++] = -1;
+    if (g->h_mwork)
+        while (km < slots) g->h_mwork[km++] = -1;
+    if (g->h_work_full)
+        while (kf < slots) g->h_work_full[kf++] = -1;
     if (g->attn_i8)
         while (k8 < slots) g->h_work8[k8++] = -1;
     return Mp;
@@ -539,8 +597,12 @@ static int upload_pack(e2mi_engine *g, int n, int Mp, const int32_t *host_ids, h
         check_hip(hipMemcpyAsync(g->pos, g->h_pos, (size_t)Mp * 4, hipMemcpyHostToDevice, s), "pos H2D") ||
         check_hip(hipMemcpyAsync(g->seq_start, g->h_start, (size_t)n * 4, hipMemcpyHostToDevice, s), "start H2D") ||
         check_hip(hipMemcpyAsync(g->seq_len, g->h_len, (size_t)n * 4, hipMemcpyHostToDevice, s), "len H2D") ||
-        check_hip(hipMemcpyAsync(g->work, g->h_work, (size_t)work_slots(g, n, Mp) * 4, hipMemcpyHostToDevice, s),
-                  "work H2D") ||
+        check_hip(hipMemcpyAsync(g->work, g->h_work, (size_t)work_slots(g, n, Mp) * g->split_factor * 4,
+                                 hipMemcpyHostToDevice, s), "work H2D") ||
+        (g->mwork && check_hip(hipMemcpyAsync(g->mwork, g->h_mwork, (size_t)work_slots(g, n, Mp) * 4,
+                                              hipMemcpyHostToDevice, s), "merge work H2D")) ||
+        (g->work_full && check_hip(hipMemcpyAsync(g->work_full, g->h_work_full, (size_t)work_slots(g, n, Mp) * 4,
+                                                  hipMemcpyHostToDevice, s), "full-layer work H2D")) ||
         (g->attn_i8 && check_hip(hipMemcpyAsync(g->work8, g->h_work8, (size_t)work_slots(g, n, Mp) * 4,
                                                 hipMemcpyHostToDevice, s), "int8 work H2D")))
         return -1;
@@ -589,7 +651,7 @@ extern "C" void e2mi_destroy(e2mi_engine *g) {
     if (g->h_ids) (void)hipHostFree(g->h_ids);
     if (g->h_valid) (void)hipHostFree(g->h_valid);
     if (g->h_out) (void)hipHostFree(g->h_out);
-    for (int32_t *p : {g->h_rowmap, g->h_pos, g->h_start, g->h_len, g->h_work, g->h_work8})
+    for (int32_t *p : {g->h_rowmap, g->h_pos, g->h_start, g->h_len, g->h_work, g->h_work8, g->h_mwork, g->h_work_full})
         if (p) (void)hipHostFree(p);
     if (g->h_mask) (void)hipHostFree(g->h_mask);
     if (g->h_bad) (void)hipHostFree(g->h_bad);
@@ -622,6 +684,14 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
     g->use_graph = !(ng && ng[0] && ng[0] != '0');
     const char *nf = getenv("E2MI_NOFUSE");
     g->fuse_qkv = !(nf && nf[0] && nf[0] != '0');
+    const char *ns = getenv("E2MI_SPLIT");  // 0 | 1 | auto (default)
+    if (ns && ns[0]) g->split_mode = ns[0] == '0' ? 0 : ns[0] == '1' ? 1 : 2;
+    {
+        // the most key tiles a query block can span: the sequence, or the window around the block
+        int tiles = (c.max_seq + 31) / 32;
+        if (c.window > 0) tiles = std::min(tiles, (128 + 2 * c.window) / 32 + 2);
+        g->split_factor = std::max(1, std::min(kMaxAttnParts, (tiles + kAttnPartTiles - 1) / kAttnPartTiles));
+    }
     const char *pf = getenv("E2MI_PROFILE");
     g->prof_on = pf && pf[0] && pf[0] != '0';
     const char *dd = getenv("E2MI_DUMP");
@@ -637,6 +707,7 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
     if (check_hip(hipGetDevice(&g->dev), "get device")) return fail();
     hipDeviceProp_t prop;
     if (check_hip(hipGetDeviceProperties(&prop, g->dev), "device properties")) return fail();
+    g->slots_device = 2 * prop.multiProcessorCount;  // k_attn_packed<256>: two workgroups per CU
     snprintf(g->devname, sizeof g->devname, "%s (%s, %d CUs)", prop.name, prop.gcnArchName,
              prop.multiProcessorCount);
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
@@ -696,7 +767,11 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         (c.ple_dim > 0 && dalloc(g, &g->ple32, R * c.n_layers * c.ple_dim)) ||
         dalloc(g, &g->rowmap, R) || dalloc(g, &g->pos, R) || dalloc(g, &g->seq_start, (size_t)g->bmax) ||
         dalloc(g, &g->seq_len, (size_t)g->bmax) ||
-        dalloc(g, &g->work, (size_t)c.n_heads * (R / 128 + g->bmax)) || dalloc(g, &g->d_bad, 1))
+        dalloc(g, &g->work, (size_t)c.n_heads * (R / 128 + g->bmax) * g->split_factor) || dalloc(g, &g->d_bad, 1) ||
+        (g->split_factor > 1 &&
+         (dalloc(g, &g->mwork, (size_t)c.n_heads * (R / 128 + g->bmax)) ||
+          dalloc(g, &g->part, e2mi_attention_part_bytes(R, c.n_heads, 256) / 4 + 64) ||
+          (c.full_period > 0 && dalloc(g, &g->work_full, (size_t)c.n_heads * (R / 128 + g->bmax))))))
         return fail();
     if (check_hip(hipHostMalloc((void **)&g->h_ids, R * 4), "pinned ids") ||
         check_hip(hipHostMalloc((void **)&g->h_valid, R), "pinned valid") ||
@@ -705,7 +780,12 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         check_hip(hipHostMalloc((void **)&g->h_pos, R * 4), "pinned pos") ||
         check_hip(hipHostMalloc((void **)&g->h_start, (size_t)g->bmax * 4), "pinned start") ||
         check_hip(hipHostMalloc((void **)&g->h_len, (size_t)g->bmax * 4), "pinned len") ||
-        check_hip(hipHostMalloc((void **)&g->h_work, (size_t)c.n_heads * (R / 128 + g->bmax) * 4), "pinned work") ||
+        check_hip(hipHostMalloc((void **)&g->h_work, (size_t)c.n_heads * (R / 128 + g->bmax) * g->split_factor * 4),
+                  "pinned work") ||
+        (g->mwork && check_hip(hipHostMalloc((void **)&g->h_mwork, (size_t)c.n_heads * (R / 128 + g->bmax) * 4),
+                               "pinned merge work")) ||
+        (g->work_full && check_hip(hipHostMalloc((void **)&g->h_work_full, (size_t)c.n_heads * (R / 128 + g->bmax) * 4),
+                                   "pinned full-layer work")) ||
         check_hip(hipHostMalloc((void **)&g->h_bad, 4), "pinned flag"))
         return fail();
     *g->h_bad = 0;
@@ -1029,6 +1109,17 @@ extern "C" int e2mi_set_attention(e2mi_engine *g, int kind) {
 }
 
 extern "C" const char *e2mi_profile_text(const e2mi_engine *g) { return g ? g->prof_text.c_str() : ""; }
+
+extern "C" int e2mi_set_attention_split(e2mi_engine *g, int mode) {
+    if (!g || mode < 0 || mode > 2) {
+        set_error("set_attention_split: null engine or mode %d (0 never, 1 always, 2 auto)", mode);
+        return -1;
+    }
+    if (g->stream) (void)hipStreamSynchronize(g->stream);
+    if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
+    g->split_mode = mode;
+    return 0;
+}
 
 extern "C" int e2mi_stats(e2mi_engine *g, long *calls, long *kernels_last, double *last_ms) {
     if (!g) {

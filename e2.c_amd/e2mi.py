@@ -75,6 +75,9 @@ SIGNATURES = {
     "e2mi_attention_packed": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _I]),
     "e2mi_attention_packed_window": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P,
                                           _P, _I]),
+    "e2mi_attention_part_bytes": (C.c_size_t, [_I, _I, _I]),
+    "e2mi_attention_packed_split": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P,
+                                         _P, _I, _P, _I, _P, _I]),
     "e2mi_add_norm_scale_quant": (_I, [_P, _P, _P, _P, _F, _P, _F, _I, _I, _P, _P, _P, _P]),
     "e2mi_scale_norm": (_I, [_P, _P, _I, _I, _F, _P, _F, _P]),
     "e2mi_i8_gemm_gelu_mul": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(Q8W), _I, _P, _I]),
@@ -114,6 +117,7 @@ SIGNATURES = {
     "e2mi_text_embed_batch_device": (_I, [_P, _P, _P, _I, _I, _P, _P]),
     "e2mi_stats": (_I, [_P, C.POINTER(C.c_long), C.POINTER(C.c_long), C.POINTER(C.c_double)]),
     "e2mi_profile_text": (C.c_char_p, [_P]),
+    "e2mi_set_attention_split": (_I, [_P, _I]),
     "e2mi_set_layer_limit": (_I, [_P, _I]),
     "e2mi_set_packing": (_I, [_P, _I]),
     "e2mi_set_attention": (_I, [_P, _I]),
@@ -481,13 +485,61 @@ def qkv_norm_rope_packed(qkv, pos, H, KV, q_gamma, k_gamma, cos_tab, sin_tab, ep
     return q16, k16, vt16, q32, k32, v32
 
 
+def work_entry(b, h, part, parts, qb):
+    """An attention work entry (include/e2mi.h, e2mi_attention_packed_split)."""
+    return b | (h << 16) | (part << 20) | ((parts - 1) << 22) | (qb << 24)
+
+
 def attention_work(lens, H):
-    """The engine's attention work list for packed sequences of these lengths: (b | h << 16 |
-    query_block << 24) per 128-query block, longest sequences first."""
+    """The engine's attention work list for packed sequences of these lengths: one entry per
+    128-query block, longest sequences first, keys unsplit."""
     import numpy as np
     order = sorted(range(len(lens)), key=lambda b: -int(lens[b]))
-    return np.asarray([b | (h << 16) | (q << 24) for b in order for h in range(H)
+    return np.asarray([work_entry(b, h, 0, 1, q) for b in order for h in range(H)
                        for q in range((int(lens[b]) + 127) // 128)], np.int32)
+
+
+def attention_split_work(lens, H, parts_of, window=0):
+    """Work and merge lists with split key ranges: parts_of(n_tiles) parts per query block (its
+    key tiles: all of the sequence, or those within the window by packed index, as the kernel
+    computes them)."""
+    import numpy as np
+    order = sorted(range(len(lens)), key=lambda b: -int(lens[b]))
+    work, merge = [], []
+    for b in order:
+        L = int(lens[b])
+        for h in range(H):
+            for q in range((L + 127) // 128):
+                t0, t1 = 0, (L + 31) // 32
+                if window > 0:
+                    q0, q1 = q * 128, min(q * 128 + 127, L - 1)
+                    t0, t1 = max(q0 - window, 0) // 32, min(min(q1 + window, L - 1) // 32 + 1, t1)
+                P = max(1, min(4, int(parts_of(t1 - t0)), t1 - t0))
+                work += [work_entry(b, h, p, P, q) for p in range(P)]
+                if P > 1:
+                    merge.append(work_entry(b, h, 0, P, q))
+    return np.asarray(work, np.int32), np.asarray(merge or [-1], np.int32)
+
+
+def attention_packed_split(q16, k16, vt16, start, lens, max_len, H, KV, work, merge, window=0, pos=None,
+                           scale=1.0, want_f32=True, stream=None):
+    """e2mi_attention_packed_split (head_dim 256) with work/merge lists from attention_split_work."""
+    import torch
+    M = q16.shape[0]
+    dev = q16.device
+    D = 256
+    cq = torch.zeros((M, H * D), dtype=torch.int8, device=dev)
+    cs = torch.zeros((M, H * D // 128), dtype=torch.float32, device=dev)
+    c32 = torch.zeros((M, H * D), dtype=torch.float32, device=dev) if want_f32 else None
+    nb = load().e2mi_attention_part_bytes(M, H, D)
+    part = torch.empty(nb // 4, dtype=torch.float32, device=dev)
+    wt = torch.from_numpy(work).to(dev)
+    mt = torch.from_numpy(merge).to(dev)
+    check(load().e2mi_attention_packed_split(stream_ptr(stream), ptr(q16), ptr(k16), ptr(vt16), M, ptr(start),
+                                             ptr(lens), ptr(pos), start.shape[0], max_len, H, KV, D, scale,
+                                             window, ptr(cq), ptr(cs), ptr(c32), ptr(wt), wt.shape[0], ptr(mt),
+                                             mt.shape[0], ptr(part), M), "attention_packed_split")
+    return cq, cs, c32
 
 
 def attention_packed(q16, k16, vt16, start, lens, max_len, H, KV, scale=1.0, want_f32=True,
@@ -704,6 +756,10 @@ class Engine:
     def set_packing(self, on: bool):
         """Packed batches (valid tokens only) on or off; off computes every padded row."""
         check(load().e2mi_set_packing(self.h, 1 if on else 0), "set_packing")
+
+    def set_split(self, mode: str):
+        """Split key ranges: "off", "on" or "auto" (e2mi_set_attention_split)."""
+        check(load().e2mi_set_attention_split(self.h, {"off": 0, "on": 1, "auto": 2}[mode]), "set_attention_split")
 
     def set_attention(self, kind: str):
         """Text attention kind: "f16" (default) or "i8" (the reference's int8 attention for

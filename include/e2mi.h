@@ -239,6 +239,23 @@ int e2mi_attention_packed_window(e2mi_stream stream, const uint16_t *q16, const 
                                  const int32_t *seq_len, const int32_t *pos, int B, int max_len,
                                  int H, int KV, int D, float scale, int window, int8_t *ctx_q,
                                  float *ctx_s, float *ctx32, const int32_t *work, int n_work);
+/* The same with long query blocks' keys split over several workgroups (head_dim 256): the reference
+ * walks a query block's keys in one sequence (text.c:702-741); here a work entry may carry a part p
+ * of P <= 4 (entry = b | h << 16 | p << 20 | (P - 1) << 22 | query_block << 24, h < 16), each part
+ * taking a consecutive share of the block's key tiles and leaving its context sum, row max and row
+ * sum in part (e2mi_attention_part_bytes(part_rows, H, 256) bytes, part_rows >= M); then one
+ * workgroup per merge entry (b | h << 16 | (P - 1) << 22 | query_block << 24, negative: idle)
+ * combines the parts, ctx = sum_p e^(m_p - M) o_p / sum_p e^(m_p - M) l_p, and quantizes ctx as the
+ * unsplit kernel does. Entries with P = 1 run as in e2mi_attention_packed_window. Split and unsplit
+ * results differ by the f16 rounding of the probabilities (each part's exponentials are taken
+ * against its own running max) and the order of the sums. */
+size_t e2mi_attention_part_bytes(int part_rows, int H, int D);
+int e2mi_attention_packed_split(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
+                                const uint16_t *vt16, int M, const int32_t *seq_start,
+                                const int32_t *seq_len, const int32_t *pos, int B, int max_len, int H,
+                                int KV, int D, float scale, int window, int8_t *ctx_q, float *ctx_s,
+                                float *ctx32, const int32_t *work, int n_work, const int32_t *merge,
+                                int n_merge, float *part, int part_rows);
 /* The reference's int8 attention (text.c:638-700 attb_i8; dispatch.c:51 selects it for long
  * sequences on AVX-512) for packed batches: q32 [M][H*D], k32/v32 [M][KV*D] f32 after q/k norm and
  * RoPE (e2mi_qkv_norm_rope_packed's optional f32 outputs), sequences as for
@@ -325,6 +342,15 @@ int e2mi_stats(e2mi_engine *g, long *calls, long *kernels_last, double *last_ms)
  * report of the profiled call ("" before it or without E2MI_PROFILE); the text lives as long as the
  * engine. No reference counterpart for the accessor (the reference only prints). */
 const char *e2mi_profile_text(const e2mi_engine *g);
+/* Split key ranges in the engine's attention (head_dim-256 layers; e2mi_attention_packed_split): a
+ * 128-query block whose keys span more than 8 tiles of 32 is shared out over up to 4 workgroups and
+ * merged. mode 0 never, 1 always, 2 (default; E2MI_SPLIT=0|1|auto at creation) only for chunks whose
+ * unsplit blocks fill at most half of the device's attention workgroups (few sequences: a single
+ * 2048-token document at the reference geometry 5.77 -> 4.87 ms; a full config-4 batch would lose
+ * 14 %). Split results differ from unsplit ones by f16 rounding, so with mode 2 a long sequence's
+ * embedding can differ between a small batch and a large one; mode 0 keeps them bit-identical. No
+ * reference counterpart (the reference has no split). */
+int e2mi_set_attention_split(e2mi_engine *g, int mode);
 /* Run only the first n layers (0: all) before the final norm and pooling: the reference's
  * E2_HIP_LAYERS bisection knob (forward.c:359-366), for parity checks layer by layer. */
 int e2mi_set_layer_limit(e2mi_engine *g, int n_layers);

@@ -191,7 +191,9 @@ def test_config4_full_size_properties(gpu, rng):
     depth (random-init stacks at scale 1.0 are chaotic, see above); size-independent properties
     instead: every embedding finite and unit-norm, packed and padded-rows forwards bit-identical,
     graph replays bit-identical to the eager first call, and a sample of sequences embedded alone
-    bit-identical to their batch rows."""
+    bit-identical to their batch rows (with split key ranges off: a lone long sequence would have
+    its keys split by the default rule, the full batch does not). Split and unsplit attention agree
+    to cosine 0.9999 after one layer, and the default rule splits a lone long sequence."""
     import torch
     import e2mi
     cfg = small_config(e2mi, n_layers=24, vocab=262144)
@@ -201,7 +203,7 @@ def test_config4_full_size_properties(gpu, rng):
     ids = rng.integers(0, cfg.vocab, (B, S)).astype(np.int32)
     lens = rng.integers(64, S + 1, B)
     valid = (np.arange(S)[None, :] < lens[:, None]).astype(np.uint8)
-    first = eng.embed_batch(ids, valid)                 # eager + graph record
+    first = eng.embed_batch(ids, valid)                 # eager + graph record (blocks fill the device)
     assert np.all(np.isfinite(first))
     assert np.abs(np.linalg.norm(first.astype(np.float64), axis=1) - 1).max() < 1e-5
     dev = torch.device("cuda:0")
@@ -210,6 +212,8 @@ def test_config4_full_size_properties(gpu, rng):
         eng.embed_batch_device(_t(ids, dev), _t(valid, dev), out)
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy(), first)
+    eng.set_split("off")
+    assert np.array_equal(eng.embed_batch(ids, valid), first)
     eng.set_packing(False)
     try:
         padded = eng.embed_batch(ids, valid)
@@ -220,3 +224,16 @@ def test_config4_full_size_properties(gpu, rng):
         L = int(lens[b])
         single = eng.embed_batch(ids[b:b + 1, :L], None)
         assert np.array_equal(single[0], first[b]), b
+    # one layer: split against unsplit over the whole batch; the default rule on a lone sequence
+    eng.set_layer_limit(1)
+    one_unsplit = eng.embed_batch(ids, valid)
+    eng.set_split("on")
+    one_split = eng.embed_batch(ids, valid)
+    cos = (one_split * one_unsplit).sum(1) / (np.linalg.norm(one_split, axis=1) * np.linalg.norm(one_unsplit, axis=1))
+    assert cos.min() >= 0.9999, cos.min()
+    assert not np.array_equal(one_split, one_unsplit)  # sequences over 256 tokens did split
+    b = int(np.argmax(lens))
+    lone_on = eng.embed_batch(ids[b:b + 1, :int(lens[b])], None)
+    eng.set_split("auto")
+    assert np.array_equal(eng.embed_batch(ids[b:b + 1, :int(lens[b])], None), lone_on)
+    eng.set_layer_limit(0)
