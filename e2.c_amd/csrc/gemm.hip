@@ -742,24 +742,52 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
         const unsigned char *spb = sscale + ((g + kPSlots - 1) % kPSlots) * SSLOT;
         const float *sp = (const float *)spb;
         read_ws(spb);  // the folded step's tile
+        // The A fragment and the first W fragment of sub-step kk + 1 are read during sub-step kk,
+        // so its first MFMA does not wait for a fresh LDS read; each fold unit's VALU work comes
+        // before its MFMA and covers the remaining reads' latency (C5 sweep and encoder shapes:
+        // 4-5 % faster than reading every fragment at the sub-step's start and folding after the
+        // MFMA). The fused q|k|v epilogue keeps the plain order: its registers leave no room for
+        // the 8 extra fragment registers.
+        constexpr bool PREF = EPI != EPI_QKV;
+        v4i apf[2], bpf[2];
+        if constexpr (PREF) {
+            apf[0] = *(const v4i *)(sb + offa[0]);
+            bpf[0] = *(const v4i *)(sb + offb[0]);
+        }
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             issue_part(is_next, kk);
-            const v4i af = *(const v4i *)(sb + offa[kk]);
-            v4i bf[4];
+            v4i af, bf[4];
+            if constexpr (PREF) {
+                af = apf[kk & 1];
+                bf[0] = bpf[kk & 1];
 #pragma unroll
-            for (int t = 0; t < 4; t++) bf[t] = *(const v4i *)(sb + offb[kk] + t * 4096);
+                for (int t = 1; t < 4; t++) bf[t] = *(const v4i *)(sb + offb[kk] + t * 4096);
+                if (kk < 3) {
+                    apf[(kk + 1) & 1] = *(const v4i *)(sb + offa[kk + 1]);
+                    bpf[(kk + 1) & 1] = *(const v4i *)(sb + offb[kk + 1]);
+                }
+            } else {
+                af = *(const v4i *)(sb + offa[kk]);
+#pragma unroll
+                for (int t = 0; t < 4; t++) bf[t] = *(const v4i *)(sb + offb[kk] + t * 4096);
+            }
 #pragma unroll
             for (int tn = 0; tn < 4; tn++)
                 cur[tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[tn], kk == 0 ? zero : cur[tn], 0, 0, 0);
 #pragma unroll
             for (int u = kk * 4; u < kk * 4 + 4; u++) fold_unit(prev, u, sp);
-            // 5 fragment reads + 1 scale read, then 1 MFMA : 1 fold unit
+            // 5 fragment reads + 1 scale read, then per MFMA its fold unit (before it when PREF)
             __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, XACT ? 12 : 8, 0);
+                if constexpr (PREF) {
+                    __builtin_amdgcn_sched_group_barrier(0x002, XACT ? 12 : 8, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                } else {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, XACT ? 12 : 8, 0);
+                }
             }
         }
         if (tile_start) {
