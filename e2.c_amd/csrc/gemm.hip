@@ -1019,33 +1019,35 @@ __global__ __launch_bounds__(512, 1) void k_gemm_t(GemmArgs p, int tiles_n, int 
 // Per-token GEMM with the f32 epilogue overlapped (k_gemm_tv): the per-token f32 contract at
 // K = 128 NB, N a multiple of 128, no bias or clamp (the config-5 sweep). Its time is the f32
 // output's HBM write, so the design keeps that write stream running while the MFMAs go on:
-//   - one 256-thread workgroup per CU, one wave per SIMD (512 registers: 256 accumulators, two
-//     sets of 64 x 128, 8 tiles of v_mfma_i32_32x32x32_i8 each); tile j's MFMAs accumulate into
-//     one set while the previous tile's epilogue is converted and stored from the other;
-//   - 256 x 128 output tiles (N = 1152 = 9 x 128 divides evenly), the M-major tile list cut into
-//     one contiguous chunk per XCD as in k_gemm_p;
+//   - one 512-thread workgroup per CU, 8 waves (4 x 2) of 64 x 64 over a 256 x 128 output tile,
+//     two waves per SIMD; each wave holds two accumulator sets of 2 x 2 v_mfma_i32_32x32x32_i8
+//     tiles (128 registers): tile j's MFMAs accumulate into one set while the previous tile's
+//     epilogue is converted and stored from the other, and the other wave of the SIMD covers the
+//     fragment waits (one wave per SIMD with 64 x 128 waves, two sets of 256 registers, measured
+//     3-6 % slower on the sweep);
+//   - the M-major tile list cut into one contiguous chunk per XCD as in k_gemm_p (N = 1152 =
+//     9 x 128 divides evenly);
 //   - three 48 KB A|W stages, loads two steps ahead; the barrier sits after the third of a step's
 //     four 32-deep sub-steps, once the step's last fragments are in registers, so the next step's
 //     first fragments are read under the fourth sub-step's MFMAs;
-//   - the loop is fully unrolled per tile into slots of one MFMA each, fenced by sched_barrier:
-//     the sub-step's six fragment reads sit at its first slot, one of the next-but-one step's 14
-//     direct-to-LDS loads at each of the step's first 14 slots (a wave that issues a burst of
-//     them stalls on the texture path with no other wave on its SIMD to keep the MFMAs busy), and
-//     the previous tile's 128 output elements per lane are spread over the first NB - 1 steps,
-//     one conversion fma((float)acc, RN(as * ws), 0) and one non-temporal dword store each (a
-//     store writes two full 128-byte rows); stores and loads share the in-order vmcnt counter, so
-//     the barrier's wait counts exactly the operations issued after the awaited loads.
+//   - the loop is fully unrolled per tile into slots of one MFMA each (16 per step), fenced by
+//     sched_barrier: a sub-step's four fragment reads (for the next sub-step) at its first slot,
+//     one of the next-but-one step's 7 direct-to-LDS loads at each of the step's first 7 slots,
+//     and the previous tile's 64 output elements per lane spread over the first NB - 1 steps, one
+//     conversion fma((float)acc, RN(as * ws), 0) and one non-temporal dword store each (a store
+//     writes two full 128-byte rows); stores and loads share the in-order vmcnt counter, so the
+//     barrier's wait counts exactly the operations issued after the awaited loads.
 namespace tv {
-constexpr int BM = 256, BN = 128, NW = 4, STAGES = 3, NSLOT = 3;
-constexpr int TILE = (BM + BN) * 128;   // A | W of one 128-deep step
-constexpr int SLOT = 2 * NW * 256;      // as | ws of one tile
+constexpr int BM = 256, BN = 128, NW = 8, STAGES = 3, NSLOT = 3;
+constexpr int TILE = (BM + BN) * 128;
+constexpr int SLOT = 2048;                     // as (256 floats) | ws (128 floats) of one tile
 constexpr int LDS = STAGES * TILE + NSLOT * SLOT;
-constexpr int L = BM / 8 / NW + BN / 8 / NW + 2;  // loads per wave per step: 8 A, 4 W, as, ws
-constexpr int NMICRO = 128;             // epilogue elements per lane and tile
+constexpr int L = BM / 8 / NW + BN / 8 / NW + 1;  // loads per wave per step: 4 A, 2 W, as or ws
+constexpr int NMICRO = 64;                     // epilogue elements per lane and tile
+constexpr int SPS = 16;                        // MFMA slots per step
 static_assert(LDS <= 160 * 1024, "LDS budget");
-// epilogue element u of a tile goes to slot micro_slot(u) of the next tile (first NB - 1 steps)
 template <int NB>
-constexpr int micro_slot(int u) { return u * (32 * (NB - 1)) / NMICRO; }
+constexpr int micro_slot(int u) { return u * (SPS * (NB - 1)) / NMICRO; }
 template <int NB>
 constexpr int stores_in(int s0, int s1) {
     int n = 0;
@@ -1055,19 +1057,18 @@ constexpr int stores_in(int s0, int s1) {
 }  // namespace tv
 
 template <int NB>
-__global__ __launch_bounds__(256, 1) void k_gemm_tv(GemmArgs p, int tiles_n, int tiles) {
+__global__ __launch_bounds__(512, 1) void k_gemm_tv(GemmArgs p, int tiles_n, int tiles) {
     using namespace tv;
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
     const int hi = lane >> 5, r32 = lane & 31;
 
     const int nx = (gridDim.x % 8 == 0) ? 8 : 1;
     const int grp = blockIdx.x % nx, li = blockIdx.x / nx, per = gridDim.x / nx;
     const int c0 = (int)((long)tiles * grp / nx), c1 = (int)((long)tiles * (grp + 1) / nx);
     const int ntile = (c1 - c0 > li) ? (c1 - c0 - li + per - 1) / per : 0;
-    const int G = ntile * NB;
-    // tile j of this workgroup is c0 + li + j per; (m block, n tile) advanced without division
     const int per_m = per / tiles_n, per_n = per % tiles_n;
     struct TC {
         int mb, nt;
@@ -1091,28 +1092,29 @@ __global__ __launch_bounds__(256, 1) void k_gemm_tv(GemmArgs p, int tiles_n, int
         __builtin_amdgcn_make_buffer_rsrc(p.Y, 0, (int)min((long)p.M * p.ldy * 4, 0x7fffffffL), 0x00020000);
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)smem);
 
-    // load i of a wave fills rows (i * 4 + wave) * 8 + lane / 8 of its tile (A: i < 8, W: i < 12),
-    // 16-byte chunk (lane % 8) ^ swzk(row), which is the same for every i (see k_gemm_p)
+    // load i of a wave fills rows (i * 8 + wave) * 8 + lane / 8 of its tile (A: i < 4, W: i < 6),
+    // 16-byte chunk (lane % 8) ^ swzk(row), the same for every i (see k_gemm_p); load 6: waves 0-3
+    // the activation scales of rows 64 wave .. + 63, waves 4-7 the weight scales of columns
+    // 64 (wave % 2) .. + 63 (waves 6 and 7 repeat 4 and 5: the same bytes to the same place)
     const int swl = ((lane & 7) ^ ((wave & 1) * 4 + ((lane >> 4) & 3))) << 4;
     const uint32_t vla = (uint32_t)(lane >> 3) * (uint32_t)p.lda + swl;
     const uint32_t vlb = (uint32_t)(lane >> 3) * (uint32_t)p.ldw + swl;
     const uint32_t vl4 = (uint32_t)lane * 4;
-    const uint32_t sta = 32u * (uint32_t)p.lda, stw = 32u * (uint32_t)p.ldw;  // 32 rows
+    const uint32_t sta = 64u * (uint32_t)p.lda, stw = 64u * (uint32_t)p.ldw;  // 64 rows
 
-    // ---- loads of step ig (tile itc, K block ikb) into stage ig % 3, the tile's scales into slot
     int ig = 0, ikb = 0, islot = 0;
     TC itc = tc0;
     struct Issue {
         uint32_t st, sl, ko;
         int m0, n0;
     };
-    uint32_t sa = 0, sw = 0;  // running scalar offsets of the step's A and W loads
+    uint32_t sa = 0, sw = 0;
     auto issue_prep = [&]() {
         Issue is;
         is.m0 = itc.mb * BM;
         is.n0 = itc.nt * BN;
         is.st = lds0 + (uint32_t)((ig % STAGES) * TILE) + (uint32_t)wave * 1024u;
-        is.sl = lds0 + (uint32_t)(STAGES * TILE + islot * SLOT) + (uint32_t)wave * 256u;
+        is.sl = lds0 + (uint32_t)(STAGES * TILE + islot * SLOT);
         is.ko = (uint32_t)(ikb * kQBlock);
         ++ig;
         if (++ikb == NB) {
@@ -1124,70 +1126,69 @@ __global__ __launch_bounds__(256, 1) void k_gemm_tv(GemmArgs p, int tiles_n, int
     };
     auto issue_load = [&](const Issue &is, int i) {
         if (i == 0) sa = (uint32_t)(is.m0 + wave * 8) * (uint32_t)p.lda + is.ko;
-        if (i == 8) sw = (uint32_t)(is.n0 + wave * 8) * (uint32_t)p.ldw + is.ko;
-        if (i < 8) {
+        if (i == 4) sw = (uint32_t)(is.n0 + wave * 8) * (uint32_t)p.ldw + is.ko;
+        if (i < 4) {
             dma16(rA, is.st + i * NW * 1024, vla, sa);
             sa += sta;
-        } else if (i < 12) {
-            dma16(rW, is.st + BM * 128 + (i - 8) * NW * 1024, vlb, sw);
+        } else if (i < 6) {
+            dma16(rW, is.st + BM * 128 + (i - 4) * NW * 1024, vlb, sw);
             sw += stw;
-        } else if (i == 12) {
-            dma4(rS, is.sl, vl4, (uint32_t)(is.m0 + wave * 64) * 4);
+        } else if (wave < 4) {
+            dma4(rS, is.sl + wave * 256, vl4, (uint32_t)(is.m0 + wave * 64) * 4);
         } else {
-            dma4(rV, is.sl + NW * 256, vl4, (uint32_t)(is.n0 + min(wave * 64, BN - 64)) * 4);
+            dma4(rV, is.sl + 1024 + (wave & 1) * 256, vl4, (uint32_t)(is.n0 + (wave & 1) * 64) * 4);
         }
     };
 
-    // ---- fragments of 32-deep sub-step kk: row r32 of a 32-row tile, 16-byte chunk 2 kk + hi
+    // fragments of 32-deep sub-step kk: row r32 of a 32-row tile, 16-byte chunk 2 kk + hi
     int fo[4];
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) fo[kk] = swz(r32, 2 * kk + hi);
     struct Frags {
-        v4i a[2], w[4];
+        v4i a[2], w[2];
     };
     auto read_frags = [&](int stage, int kk, Frags &f) {
         const unsigned char *sb = smem + stage * TILE + fo[kk];
 #pragma unroll
-        for (int h = 0; h < 2; h++) f.a[h] = *(const v4i *)(sb + (wave * 64 + h * 32) * 128);
+        for (int h = 0; h < 2; h++) f.a[h] = *(const v4i *)(sb + (wm * 64 + h * 32) * 128);
 #pragma unroll
-        for (int t = 0; t < 4; t++) f.w[t] = *(const v4i *)(sb + BM * 128 + t * 32 * 128);
+        for (int t = 0; t < 2; t++) f.w[t] = *(const v4i *)(sb + BM * 128 + (wn * 64 + t * 32) * 128);
     };
 
-    // ---- epilogue of the previous tile: lane holds column 32t + r32 and rows 32h + 8g + 4hi + r
-    // of the wave's 64 x 128 block
+    // epilogue of the previous tile: lane holds column 64 wn + 32 t + r32 and rows
+    // 64 wm + 32 h + 8 g + 4 hi + r
     struct Epi {
-        f32x4 a4[2][4];   // as of the lane's rows (h, g)
-        float w1[4];      // ws of the lane's column in tile t
-        uint32_t vy[4];   // per-lane output offset of row r (tile's n0 included)
-        uint32_t srow;    // the tile's first row offset
-        uint32_t so;      // the current (h, g) row group's offset
+        f32x4 a4[2][4];
+        float w1[2];
+        uint32_t vy[4];
+        uint32_t srow;
+        uint32_t so;
     } ep;
     auto epi_begin = [&](TC tc, int slot) {
         const unsigned char *sl = smem + STAGES * TILE + slot * SLOT;
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int g = 0; g < 4; g++) ep.a4[h][g] = *(const f32x4 *)(sl + wave * 256 + (h * 32 + g * 8 + hi * 4) * 4);
+            for (int g = 0; g < 4; g++)
+                ep.a4[h][g] = *(const f32x4 *)(sl + (wm * 64 + h * 32 + g * 8 + hi * 4) * 4);
 #pragma unroll
-        for (int t = 0; t < 4; t++) ep.w1[t] = *(const float *)(sl + NW * 256 + (t * 32 + r32) * 4);
-        const int n0 = tc.nt * BN;
+        for (int t = 0; t < 2; t++) ep.w1[t] = *(const float *)(sl + 1024 + (wn * 64 + t * 32 + r32) * 4);
+        const int n0 = tc.nt * BN + wn * 64;
 #pragma unroll
-        for (int r = 0; r < 4; r++) ep.vy[r] = (uint32_t)(((wave * 64 + hi * 4 + r) * p.ldy + n0 + r32) * 4);
+        for (int r = 0; r < 4; r++) ep.vy[r] = (uint32_t)(((wm * 64 + hi * 4 + r) * p.ldy + n0 + r32) * 4);
         ep.srow = (uint32_t)(tc.mb * BM) * (uint32_t)p.ldy * 4u;
     };
-    // element u = (h, g, t, r): the (h, g) row group's scalar offset once per group, t in the
-    // instruction's immediate offset
-    auto micro = [&](v16i (&acc)[2][4], auto U) {
+    auto micro = [&](v16i (&acc)[2][2], auto U) {
         constexpr int u = decltype(U)::value;
-        constexpr int h = u / 64, g = (u / 16) % 4, t = (u / 4) % 4, r = u % 4;
+        constexpr int h = u / 32, g = (u / 8) % 4, t = (u / 4) % 2, r = u % 4;
         if constexpr (t == 0 && r == 0) ep.so = ep.srow + (uint32_t)((h * 32 + g * 8) * p.ldy * 4);
         const float y = __builtin_fmaf((float)acc[h][t][4 * g + r], __fmul_rn(ep.a4[h][g][r], ep.w1[t]), 0.f);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, ep.vy[r] + t * 128, ep.so,
                                               kStoreNT);
     };
 
-    // ---- prologue: steps 0 and 1 in flight, step 0's first fragments read
     Frags F[2];
+    const int G = ntile * NB;
     if (G > 0) {
         Issue is = issue_prep();
 #pragma unroll
@@ -1201,23 +1202,22 @@ __global__ __launch_bounds__(256, 1) void k_gemm_tv(GemmArgs p, int tiles_n, int
     }
     const v16i zero = {};
 
-    int g = 0;  // step being computed
+    int g = 0;
     TC ctc = tc0, etc = tc0;
     int cslot = 0, eslot = 0;
-    // one tile: MFMAs into cur, the previous tile's epilogue from prev (when EON)
-    auto tile = [&](v16i (&cur)[2][4], v16i (&prev)[2][4], auto EON) {
+    auto tile = [&](v16i (&cur)[2][2], v16i (&prev)[2][2], auto EON) {
         constexpr bool EPI_ON = decltype(EON)::value;
         if constexpr (EPI_ON) epi_begin(etc, eslot);
         Issue is;
         [&]<int... S>(std::integer_sequence<int, S...>) {
             (
                 [&] {
-                    constexpr int s = S;        // slot of the tile
-                    constexpr int st = s / 32;  // step
-                    constexpr int ss = s % 32;  // slot of the step
-                    constexpr int kk = ss / 8;  // sub-step
-                    constexpr int i = ss % 8;   // MFMA of the sub-step
-                    constexpr int h = i / 4, t = i % 4;
+                    constexpr int s = S;          // slot of the tile
+                    constexpr int st = s / SPS;   // step
+                    constexpr int ss = s % SPS;   // slot of the step
+                    constexpr int kk = ss / 4;    // sub-step
+                    constexpr int i = ss % 4;     // MFMA of the sub-step
+                    constexpr int h = i / 2, t = i % 2;
                     if constexpr (ss == 0) is = issue_prep();
                     const Frags &f = F[kk % 2];
                     cur[h][t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h], f.w[t],
@@ -1232,40 +1232,38 @@ __global__ __launch_bounds__(256, 1) void k_gemm_tv(GemmArgs p, int tiles_n, int
                             ((micro_slot<NB>(U) == s ? micro(prev, std::integral_constant<int, U>{}) : void()), ...);
                         }(std::make_integer_sequence<int, NMICRO>{});
                     }
-                    if constexpr (ss == 23) {
+                    if constexpr (ss == 11) {
                         // every wave has read stage g % 3 and step g + 1's loads have landed:
-                        // besides them, the wave's vector-memory queue holds the stores of slots
-                        // L-1..31 of step g - 1 and 0..23 of step g and the L loads of step g + 2
-                        // (a tile's last step stores nothing, so step 0 has no term for the
-                        // previous tile)
+                        // besides them, the queue holds the stores of slots L-1..15 of step g - 1
+                        // and 0..11 of step g and the L loads of step g + 2
                         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                         constexpr int after =
-                            L + (EPI_ON ? stores_in<NB>(st * 32, st * 32 + 24) +
-                                              (st > 0 ? stores_in<NB>(st * 32 - 33 + L, st * 32) : 0)
+                            L + (EPI_ON ? stores_in<NB>(st * SPS, st * SPS + 12) +
+                                              (st > 0 ? stores_in<NB>(st * SPS - SPS - 1 + L, st * SPS) : 0)
                                         : 0);
                         static_assert(after <= 63, "vmcnt range");
                         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(after) : "memory");
                         __builtin_amdgcn_s_barrier();
                     }
-                    if constexpr (ss == 31) ++g;
+                    if constexpr (ss == SPS - 1) ++g;
                     __builtin_amdgcn_sched_barrier(0);
                 }(),
                 ...);
-        }(std::make_integer_sequence<int, 32 * NB>{});
+        }(std::make_integer_sequence<int, SPS * NB>{});
         etc = ctc;
         eslot = cslot;
         ctc = tc_next(ctc);
         cslot = cslot == NSLOT - 1 ? 0 : cslot + 1;
     };
-    static_assert(stores_in<NB>(32 * (NB - 1), 32 * NB) == 0, "the last step of a tile stores nothing");
-    auto final_epi = [&](v16i (&acc)[2][4]) {
+    static_assert(stores_in<NB>(SPS * (NB - 1), SPS * NB) == 0, "the last step of a tile stores nothing");
+    auto final_epi = [&](v16i (&acc)[2][2]) {
         epi_begin(etc, eslot);
         [&]<int... U>(std::integer_sequence<int, U...>) {
             (micro(acc, std::integral_constant<int, U>{}), ...);
         }(std::make_integer_sequence<int, NMICRO>{});
     };
 
-    v16i accA[2][4], accB[2][4];
+    v16i accA[2][2], accB[2][2];
     if (ntile > 0) {
         tile(accA, accB, std::false_type{});
         int j = 1;
@@ -1280,7 +1278,6 @@ __global__ __launch_bounds__(256, 1) void k_gemm_tv(GemmArgs p, int tiles_n, int
             final_epi(accA);
         }
     }
-    // the last steps issued loads past the end of the list: they land before the LDS is released
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
@@ -1360,10 +1357,9 @@ static int launch_tv(hipStream_t s, const GemmArgs &p) {
         return -1;
     }
     const int grid = (int)min(tiles, (long)num_cus());
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), tv::LDS, s, p, tiles_n, (int)tiles);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), tv::LDS, s, p, tiles_n, (int)tiles);
     return check_hip(hipGetLastError(), "gemm launch");
 }
-
 // the overlapped per-token f32 kernel: N a multiple of 128, no bias or clamp, K = 768 or 1152 (the
 // unrolled instantiations); every other per-token call takes k_gemm_t
 static bool use_tv(const GemmArgs &p) {
