@@ -588,7 +588,7 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmA
 
 // 8 waves of 32 x 128 (one 32-row MFMA tile by four 32-column ones): NWM x NWN waves, BM = 32 NWM,
 // BN = 128 NWN
-template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, bool NT = false>
 __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(GemmArgs p, int tiles_n, int tiles) {
     constexpr int NWAVE = NWM * NWN;
     static_assert(BM == 32 * NWM && BN == 128 * NWN && (NWAVE == 8 || NWAVE == 4), "8 or 4 waves of 32x128");
@@ -796,14 +796,14 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
             // refilled only by the next step's loads, issued after that step's barrier.
             const int pm0 = tile_m0(cj - 1), pn0 = tile_n0(cj - 1);
             if constexpr (EPI == EPI_F32) {
-                p_epilogue_f32<POST, FAST>(p, f, wsr, pm0, pn0, wm, wn, lane);
+                p_epilogue_f32<POST, FAST, NT>(p, f, wsr, pm0, pn0, wm, wn, lane);
             } else if constexpr (EPI == EPI_QKV) {
                 __syncthreads();
                 p_epilogue_qkv<FAST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
                                      (float *)(smem + (g % kPStages) * TILE));
             } else {
                 __syncthreads();
-                p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
+                p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST, NT>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
                                                                 (float *)(smem + (g % kPStages) * TILE));
             }
 #pragma unroll
@@ -837,12 +837,12 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
         }
         const int pm0 = tile_m0(ntile - 1), pn0 = tile_n0(ntile - 1);
         if constexpr (EPI == EPI_F32)
-            p_epilogue_f32<POST, FAST>(p, f, wsr, pm0, pn0, wm, wn, lane);
+            p_epilogue_f32<POST, FAST, NT>(p, f, wsr, pm0, pn0, wm, wn, lane);
         else if constexpr (EPI == EPI_QKV)
             p_epilogue_qkv<FAST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
                                  (float *)(smem + ((G - 1) % kPStages) * TILE));
         else
-            p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
+            p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST, NT>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
                                                             (float *)(smem + ((G - 1) % kPStages) * TILE));
     }
     // the last steps issued loads past the end of the list: they must land before the workgroup's
@@ -1291,14 +1291,14 @@ static int num_cus() {
     return cus;
 }
 
-template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, bool NT = false>
 static int launch_p1(hipStream_t s, const GemmArgs &p) {
     constexpr size_t lds = p_lds_bytes<BM, BN, NWM * NWN>();
     static_assert(lds <= 160 * 1024, "LDS budget");
     static_assert(EPI == EPI_F32 || EPI == EPI_QKV ||
                       NWM * NWN * (8 * ((EPI == EPI_GEGLU ? 64 : 128) + 4) + 32) * 4 <= (BM + BN) * 128,
                   "epilogue scratch fits a stage");
-    auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST>;
+    auto kern = k_gemm_p<BM, BN, NWM, NWN, EPI, FAST, POST, NT>;
     static bool attr = false;
     if (!attr) {
         if (check_hip(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
@@ -1374,14 +1374,28 @@ static int launch_t(hipStream_t s, const GemmArgs &p) {
     return post ? launch_t1<EPI, 3>(s, p) : launch_t1<EPI, 0>(s, p);
 }
 
+// f32 outputs of 128 MB or more go out with non-temporal stores: at M = 65536 the default
+// policy's write-allocation of a 200-335 MB output evicts the A and W tiles every step re-reads
+// from L2, and the loads then queue behind the writes (C5 768x1280: 155-163 -> 135-142 us).
+// Smaller outputs keep the default: in the encoder's forward the next kernel reads them at once,
+// from the caches. The requantizing epilogue's int8 outputs (84 MB at C5) measured slower
+// streamed and keep the default.
+constexpr size_t kStreamOutBytes = (size_t)128 << 20;
+template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST>
+static int launch_p2(hipStream_t s, const GemmArgs &p) {
+    if constexpr (EPI == EPI_F32 && BM == 256) {
+        if ((size_t)p.M * (size_t)p.N * 4 >= kStreamOutBytes) return launch_p1<BM, BN, NWM, NWN, EPI, FAST, POST, true>(s, p);
+    }
+    return launch_p1<BM, BN, NWM, NWN, EPI, FAST, POST>(s, p);
+}
 // POST: bit 0 adds a bias, bit 1 clamps to [lo, hi]; only "none" and "both" are instantiated (the
 // bias pointer may be null and an absent clamp is +-1e31)
 template <int BM, int BN, int NWM, int NWN, int EPI>
 static int launch_p(hipStream_t s, const GemmArgs &p) {
     const bool post = p.bias != nullptr || p.lo > -1e30f || p.hi < 1e30f;
     if (fold_fast())
-        return post ? launch_p1<BM, BN, NWM, NWN, EPI, true, 3>(s, p) : launch_p1<BM, BN, NWM, NWN, EPI, true, 0>(s, p);
-    return post ? launch_p1<BM, BN, NWM, NWN, EPI, false, 3>(s, p) : launch_p1<BM, BN, NWM, NWN, EPI, false, 0>(s, p);
+        return post ? launch_p2<BM, BN, NWM, NWN, EPI, true, 3>(s, p) : launch_p2<BM, BN, NWM, NWN, EPI, true, 0>(s, p);
+    return post ? launch_p2<BM, BN, NWM, NWN, EPI, false, 3>(s, p) : launch_p2<BM, BN, NWM, NWN, EPI, false, 0>(s, p);
 }
 
 static int launch_dump(hipStream_t s, const GemmArgs &p) {
