@@ -808,6 +808,27 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
 
 extern "C" e2mi_engine *e2mi_create(const e2_model *m) { return e2mi_create_rows(m, 0); }
 
+// the engine straight from an E8CQ cache, for a caller that links only the e2mi_* names (a backend
+// inside the reference, whose own e2.h and library define e2_model, e2_free and e2_last_error)
+extern "C" e2mi_engine *e2mi_create_e8cq(const char *path, int geometry, int n_layers, int vocab,
+                                         int max_rows) {
+    if (!path || (geometry != 0 && geometry != 1) || n_layers < 0 || vocab < 0) {
+        set_error("create_e8cq: null path, geometry %d (0 baseline, 1 reference) or negative override",
+                  geometry);
+        return nullptr;
+    }
+    e2_config c;
+    if (geometry == 0) e2_config_baseline(&c);
+    else e2_config_reference(&c);
+    if (n_layers > 0) c.n_layers = n_layers;
+    if (vocab > 0) c.vocab = vocab;
+    e2_model *m = e2_load_e8cq(path, &c);
+    if (!m) return nullptr;
+    e2mi_engine *g = e2mi_create_rows(m, max_rows);
+    e2_free(m);  // the engine holds its own device copy
+    return g;
+}
+
 extern "C" const char *e2mi_device(e2mi_engine *g) { return g ? g->devname : ""; }
 
 namespace e2mi {

@@ -110,6 +110,7 @@ SIGNATURES = {
     # the encoder engine (include/e2mi.h)
     "e2mi_create": (_P, [_P]),
     "e2mi_create_rows": (_P, [_P, _I]),
+    "e2mi_create_e8cq": (_P, [C.c_char_p, _I, _I, _I, _I]),
     "e2mi_destroy": (None, [_P]),
     "e2mi_device": (C.c_char_p, [_P]),
     "e2mi_text_embed": (_I, [_P, _P, _I, _P]),

@@ -302,6 +302,14 @@ typedef struct e2mi_engine e2mi_engine;
 e2mi_engine *e2mi_create(const e2_model *m);
 /* Same with an explicit workspace capacity in token rows (>= the model's max_seq). */
 e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows);
+/* The engine straight from an E8CQ cache (q8cache.c:242-385 format), for a backend built into the
+ * reference, whose own e2.h and library already define e2_model, e2_free and e2_last_error: with
+ * lib/libe2mi_backend.so, which exports only the e2mi_* names, the caller needs nothing else.
+ * geometry 0: BASELINE encoder (e2_config_baseline), 1: the reference checkpoint's (e2_config_
+ * reference); n_layers and vocab > 0 override the preset's. Replaces e2_hip_create(e2_model *)
+ * (e2hip.h:34) for callers that hold the cache path (E2_Q8_WRITE, e2.c:276-292). NULL with
+ * e2mi_last_error when the file does not match the geometry or there is no gfx950 device. */
+e2mi_engine *e2mi_create_e8cq(const char *path, int geometry, int n_layers, int vocab, int max_rows);
 void e2mi_destroy(e2mi_engine *g);
 /* Device name, architecture and CU count, for logging (e2_hip_device). */
 const char *e2mi_device(e2mi_engine *g);

@@ -44,3 +44,42 @@ def test_errors_are_reported_without_a_gpu():
     assert lib.e2mi_quantize(None, None, None, None, 4, 100, 100, 128) == -1
     assert "quantize" in e2mi.last_error()
     assert lib.e2mi_interleave_gate_up(None, None, None, None, None, None, 100, 8) == -1
+
+
+def _exports(path):
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True,
+                         text=True).stdout
+    return {f[2] for f in (l.split() for l in out.splitlines()) if len(f) == 3 and f[1] in "TWDBR"}
+
+
+def test_backend_library_exports_only_engine_names():
+    """lib/libe2mi_backend.so is what links into the reference: every e2mi_* entry point and no
+    e2_* name, which the reference's own library defines (e2_free, e2_last_error, e2_text_embed*,
+    the dispatch functions)."""
+    import e2mi
+    path = os.path.join(os.path.dirname(e2mi.LIB_PATH), "libe2mi_backend.so")
+    names = _exports(path)
+    want = {n for n in declared_symbols() if n.startswith("e2mi_")}
+    assert want - names == set(), sorted(want - names)
+    stray = sorted(n for n in names if not n.startswith("e2mi_"))
+    assert not stray, f"backend library exports non-engine names: {stray}"
+    # the full library does export the model API a caller of include/e2.h uses
+    assert {"e2_free", "e2_last_error", "e2_text_embed_batch"} <= _exports(e2mi.LIB_PATH)
+
+
+def test_integration_adapter_compiles_and_links(tmp_path):
+    """The reference-side adapter shown in the integration guide builds against include/e2mi.h
+    alone and resolves every symbol from lib/libe2mi_backend.so."""
+    import subprocess
+    import e2mi
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    sec = text[text.index("## 1."):text.index("## 2.")]
+    code = re.search(r"```c\n(.*?)```", sec, flags=re.S).group(1)
+    assert '#include "e2mi.h"' in code and '"e2.h"' not in code
+    src = tmp_path / "e2mi_adapter.c"
+    src.write_text(code)
+    libdir = os.path.dirname(e2mi.LIB_PATH)
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Wextra", "-Werror", "-fPIC", "-shared",
+                    "-I" + os.path.join(ROOT, "include"), str(src), "-L" + libdir, "-le2mi_backend",
+                    "-Wl,--no-undefined", "-o", str(tmp_path / "adapter.so")], check=True)
