@@ -63,6 +63,38 @@ __host__ __device__ inline int work_entry(int b, int h, int part, int parts, int
 }
 constexpr int kMaxParts = 4;
 
+// One key tile of the online softmax for the 16 logits a lane holds (its partner lane ^ 32 holds
+// the other 16 of the same query); every f16 attention kernel here calls it, so padded and packed
+// batches stay bit-identical. Logits are kept in base-2 units, t = s * c with c = scale * log2(e)
+// > 0 (the entry points refuse other scales), and p = 2^(t - m); masked keys arrive as s = -inf and
+// give p = 0. The running max m only moves when the tile's max exceeds it by more than kTau, so
+// p <= 2^kTau (f16 holds it, f32 sums too) and the context's rescale by alpha = 2^(m_old - m_new)
+// is skipped on most tiles: the result is the same softmax, normalised at the end by the same sum l.
+// Returns alpha (1 when m did not move).
+constexpr float kTau = 8.f;
+__device__ __forceinline__ float softmax_tile(const float (&s)[16], float c, float &mrun, float &lrun, h8 (&pb)[2]) {
+    float mloc = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, s[r]);
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    const float mc = mloc * c;
+    float alpha = 1.f;
+    if (mc > mrun + kTau) {
+        alpha = __builtin_amdgcn_exp2f(mrun - mc);
+        mrun = mc;
+    }
+    const float ms = mrun == -INFINITY ? 0.f : mrun;  // no key yet: every p is 0
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -ms));
+        psum += pr;
+        pb[r >> 3][r & 7] = (_Float16)pr;
+    }
+    lrun = lrun * alpha + psum;
+    return alpha;
+}
+
 __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     __shared__ __align__(16) _Float16 Ks[kKT * kKP];
     __shared__ __align__(16) _Float16 Vs[kD * kVP];
@@ -107,6 +139,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < 8; t++) o[t] = (f16v){};
     float mrun = -INFINITY, lrun = 0.f;
+    const float c2 = a.scale * 1.44269504088896341f;  // logits in base-2 units
 
     const bool block_live = qb * 128 < Sb;
     const int ntiles = block_live ? (Sb + kKT - 1) / kKT : 0;
@@ -158,41 +191,19 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
         // 16 (r / 8) + 8 half + 4 ((r / 4) % 2) + r % 4: registers 8 j .. 8 j + 7 hold the
         // consecutive keys 16 j + 8 half .. + 7, the PV MFMA's k order
         float tv[16];
-        float mloc = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int key = 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
-            tv[r] = vk[key] ? st[r] * a.scale : -INFINITY;
-            mloc = fmaxf(mloc, tv[r]);
+            tv[r] = vk[key] ? st[r] : -INFINITY;
         }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        const float mnew = fmaxf(mrun, mloc);
-        float alpha = 1.f;
-        float psum = 0.f;
-        _Float16 ph[16];
-        if (mnew == -INFINITY) {
+        h8 pb[2];
+        const float alpha = softmax_tile(tv, c2, mrun, lrun, pb);
+        if (__any(alpha != 1.f)) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) ph[r] = (_Float16)0.f;
-        } else {
-            alpha = __expf(mrun - mnew);
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const float pr = tv[r] == -INFINITY ? 0.f : __expf(tv[r] - mnew);
-                psum += pr;
-                ph[r] = (_Float16)pr;
-            }
+            for (int t = 0; t < 8; t++) o[t] *= alpha;
         }
-        lrun = lrun * alpha + psum;
-        mrun = mnew;
-#pragma unroll
-        for (int t = 0; t < 8; t++) o[t] *= alpha;
         // O^T += V^T P^T: MFMA #j covers the keys of registers 8j..8j+7, i.e. keys
         // 16 j + 8 half + 0..7; V^T is read in that order
-        h8 pb[2];
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) pb[j][e] = ph[8 * j + e];
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const _Float16 *vp = Vs + (32 * t + (lane & 31)) * kVP + 8 * half;
@@ -337,6 +348,7 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
 #pragma unroll
     for (int t = 0; t < NO; t++) o[t] = (f16v){};
     float mrun = -INFINITY, lrun = 0.f;
+    const float c2 = a.scale * 1.44269504088896341f;  // logits in base-2 units
 
     // sources: K rows of this kv head (row pitch KV*D halves), V^T slab [D][S] of this kv head
     const uint32_t rowB = (uint32_t)a.KV * D * 2;
@@ -404,56 +416,40 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
             st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
             if ((s & 1) && (s >> 1) < NLK + NLV && next) issue_load(kt + 1, s >> 1);
         }
-        // window: a tile inside the window of every query of the block needs no per-key test
-        bool edge = false;
+        // keys past the sequence, and with a window those out of range, get s = -inf; a tile inside
+        // the sequence (and, with a window, inside the window of every query of the block) needs no
+        // per-key test
+        float tv[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) tv[r] = st[r];
+        bool edge = k0 + kKT > Sk;
         if constexpr (WIN) {
             const int ka = k0, kb = min(k0 + kKT, Sk) - 1;
             const int pka = a.pos ? a.pos[row0 + ka] : ka, pkb = a.pos ? a.pos[row0 + kb] : kb;
-            edge = pkb - pq0 > W || pq1 - pka > W;
+            edge = edge || pkb - pq0 > W || pq1 - pka > W;
         }
-        float tv[16];
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            // S^T row 8 (r / 4) + 4 half + r % 4 of this register holds key swap23(row)
-            const int key = 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
-            bool keep = k0 + key < Sk;
-            if (edge && keep) {
-                const int pk = a.pos ? a.pos[row0 + k0 + key] : k0 + key;
-                keep = pk - pqi <= W && pqi - pk <= W;
-            }
-            tv[r] = keep ? st[r] * a.scale : -INFINITY;
-            mloc = fmaxf(mloc, tv[r]);
-        }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        const float mnew = fmaxf(mrun, mloc);
-        float alpha = 1.f;
-        float psum = 0.f;
-        _Float16 ph[16];
-        if (mnew == -INFINITY) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) ph[r] = (_Float16)0.f;
-        } else {
-            alpha = __expf(mrun - mnew);
+        if (edge) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const float pr = tv[r] == -INFINITY ? 0.f : __expf(tv[r] - mnew);
-                psum += pr;
-                ph[r] = (_Float16)pr;
+                // S^T row 8 (r / 4) + 4 half + r % 4 of this register holds key swap23(row)
+                const int key = 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
+                bool keep = k0 + key < Sk;
+                if constexpr (WIN) {
+                    if (keep) {
+                        const int pk = a.pos ? a.pos[row0 + k0 + key] : k0 + key;
+                        keep = pk - pqi <= W && pqi - pk <= W;
+                    }
+                }
+                if (!keep) tv[r] = -INFINITY;
             }
         }
-        lrun = lrun * alpha + psum;
-        mrun = mnew;
-        // the running max rarely moves after the first tiles: skip the rescale when no lane's did
+        h8 pb[2];
+        const float alpha = softmax_tile(tv, c2, mrun, lrun, pb);
+        // the running max moves on few tiles: skip the rescale when no lane's did
         if (__any(alpha != 1.f)) {
 #pragma unroll
             for (int t = 0; t < NO; t++) o[t] *= alpha;
         }
-        h8 pb[2];
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) pb[j][e] = ph[8 * j + e];
 #pragma unroll
         for (int t = 0; t < NO; t++) {
 #pragma unroll
@@ -571,6 +567,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < 8; t++) o[t] = (f16v){};
     float mrun = -INFINITY, lrun = 0.f;
+    const float c2 = a.scale * 1.44269504088896341f;  // logits in base-2 units
 
     const uint32_t rowB = (uint32_t)a.KV * D * 2;
     const v4u rK = rsrc_words(a.k + row0 * a.KV * D + kvh * D, (uint32_t)Sk * rowB);
@@ -637,53 +634,31 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
             sfull[r + 2] = st[r + 2] + x.z;
             sfull[r + 3] = st[r + 3] + x.w;
         }
-        bool edge = false;
+        bool edge = k0 + kKT > Sk;
         if (W > 0) {
             const int ka = k0, kb = min(k0 + kKT, Sk) - 1;
             const int pka = a.pos ? a.pos[row0 + ka] : ka, pkb = a.pos ? a.pos[row0 + kb] : kb;
-            edge = pkb - pq0 > W || pq1 - pka > W;
+            edge = edge || pkb - pq0 > W || pq1 - pka > W;
         }
-        float tv[16];
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int key = 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
-            bool keep = k0 + key < Sk;
-            if (edge && keep) {
-                const int pk = a.pos ? a.pos[row0 + k0 + key] : k0 + key;
-                keep = pk - pqi <= W && pqi - pk <= W;
-            }
-            tv[r] = keep ? sfull[r] * a.scale : -INFINITY;
-            mloc = fmaxf(mloc, tv[r]);
-        }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        const float mnew = fmaxf(mrun, mloc);
-        float alpha = 1.f;
-        float psum = 0.f;
-        _Float16 ph[16];
-        if (mnew == -INFINITY) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) ph[r] = (_Float16)0.f;
-        } else {
-            alpha = __expf(mrun - mnew);
+        if (edge) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const float pr = tv[r] == -INFINITY ? 0.f : __expf(tv[r] - mnew);
-                psum += pr;
-                ph[r] = (_Float16)pr;
+                const int key = 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
+                bool keep = k0 + key < Sk;
+                if (W > 0 && keep) {
+                    const int pk = a.pos ? a.pos[row0 + k0 + key] : k0 + key;
+                    keep = pk - pqi <= W && pqi - pk <= W;
+                }
+                if (!keep) sfull[r] = -INFINITY;
             }
         }
-        lrun = lrun * alpha + psum;
-        mrun = mnew;
+        // waves w and w + 4 hold the same sums and take the same steps
+        h8 pb[2];
+        const float alpha = softmax_tile(sfull, c2, mrun, lrun, pb);
         if (__any(alpha != 1.f)) {
 #pragma unroll
             for (int t = 0; t < 8; t++) o[t] *= alpha;
         }
-        h8 pb[2];
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) pb[j][e] = ph[8 * j + e];
 #pragma unroll
         for (int t = 0; t < 8; t++) {
 #pragma unroll
@@ -729,7 +704,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
 
 // Merge of split key ranges (k_attn_packed with parts > 1; head_dim 256), for the entries of the
 // merge list (work_entry with part 0 and the block's part count): per query row, M = max_p m_p,
-// w_p = e^(m_p - M), ctx = (sum_p w_p o_p) * RN(1 / sum_p w_p l_p), parts in order, then the
+// w_p = 2^(m_p - M) (row maxima in base-2 units, see softmax_tile), ctx = (sum_p w_p o_p) * RN(1 / sum_p w_p l_p), parts in order, then the
 // per-128 quantization of k_attn_packed's epilogue. Four workgroups per entry, 32 rows each, 8 rows
 // per wave with all their loads issued before any is used; a lane holds 4 dims (lanes 0-31 the
 // first 128-dim block, 32-63 the second).
@@ -775,7 +750,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a, const int32_t *m
 #pragma unroll
             for (int p = 0; p < kMaxParts; p++) {
                 if (p >= parts) break;
-                const float wp = mp[r][p] == -INFINITY ? 0.f : __expf(mp[r][p] - M);
+                const float wp = mp[r][p] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp[r][p] - M);
                 const float4 v = op[r][p];
                 L += wp * lp[r][p];
                 o = make_float4(o.x + wp * v.x, o.y + wp * v.y, o.z + wp * v.z, o.w + wp * v.w);
@@ -812,9 +787,9 @@ extern "C" int e2mi_attention(e2mi_stream stream, const uint16_t *q16, const uin
                               const uint16_t *vt16, const uint8_t *valid, int B, int S, int H,
                               int KV, int D, float scale, int8_t *ctx_q, float *ctx_s,
                               float *ctx32) {
-    if (D != kD || B <= 0 || S <= 0 || H <= 0 || KV <= 0 || H % KV) {
-        set_error("attention: needs head_dim 256 and H %% KV == 0 (B=%d S=%d H=%d KV=%d D=%d)", B, S,
-                  H, KV, D);
+    if (D != kD || B <= 0 || S <= 0 || H <= 0 || KV <= 0 || H % KV || !(scale > 0.f) || !(scale < INFINITY)) {
+        set_error("attention: needs head_dim 256, H %% KV == 0 and a finite scale > 0 (B=%d S=%d H=%d KV=%d D=%d "
+                  "scale=%g)", B, S, H, KV, D, (double)scale);
         return -1;
     }
     if (!q16 || !k16 || !vt16 || !valid || !ctx_q || !ctx_s || !aligned16(q16) || !aligned16(k16) ||
@@ -834,9 +809,9 @@ static int attention_packed(const char *who, e2mi_stream stream, const uint16_t 
                             float *ctx32, const int32_t *work, int n_work, const int32_t *merge = nullptr,
                             int n_merge = 0, float *part = nullptr, int part_rows = 0) {
     if ((D != 256 && D != 512) || B <= 0 || M <= 0 || max_len <= 0 || H <= 0 || KV <= 0 || H % KV ||
-        window < 0) {
-        set_error("%s: needs head_dim 256 or 512, H %% KV == 0 and window >= 0 (B=%d M=%d H=%d KV=%d D=%d)",
-                  who, B, M, H, KV, D);
+        window < 0 || !(scale > 0.f) || !(scale < INFINITY)) {
+        set_error("%s: needs head_dim 256 or 512, H %% KV == 0, window >= 0 and a finite scale > 0 (B=%d M=%d "
+                  "H=%d KV=%d D=%d scale=%g)", who, B, M, H, KV, D, (double)scale);
         return -1;
     }
     if (!q16 || !k16 || !vt16 || !seq_start || !seq_len || !ctx_q || !ctx_s || !aligned16(q16) ||

@@ -162,9 +162,9 @@ static bool config_ok(const e2_config &c) {
         (c.full_period > 0 && (c.full_kv_heads <= 0 || c.n_heads % c.full_kv_heads ||
                                (c.full_head_dim != 256 && c.full_head_dim != 512) ||
                                !(c.rope_theta_full > 0.f))) ||
-        (c.ple_dim > 0 && !(c.ple_scale > 0.f))) {
+        (c.ple_dim > 0 && !(c.ple_scale > 0.f)) || !(c.attn_scale > 0.f) || !(c.attn_scale < INFINITY)) {
         set_error("config: unsupported extras (ple_dim/out_dim multiples of 128 up to 1280, "
-                  "window >= 0, full layers with head_dim 256 or 512 and H %% kv == 0)");
+                  "window >= 0, full layers with head_dim 256 or 512 and H %% kv == 0, attn_scale > 0)");
         return false;
     }
     return true;

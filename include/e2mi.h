@@ -245,7 +245,8 @@ int e2mi_attention_packed_window(e2mi_stream stream, const uint16_t *q16, const 
  * taking a consecutive share of the block's key tiles and leaving its context sum, row max and row
  * sum in part (e2mi_attention_part_bytes(part_rows, H, 256) bytes, part_rows >= M); then one
  * workgroup per merge entry (b | h << 16 | (P - 1) << 22 | query_block << 24, negative: idle)
- * combines the parts, ctx = sum_p e^(m_p - M) o_p / sum_p e^(m_p - M) l_p, and quantizes ctx as the
+ * combines the parts, ctx = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p (m_p: row maxima of
+ * scale * log2(e) * q.k), and quantizes ctx as the
  * unsplit kernel does. Entries with P = 1 run as in e2mi_attention_packed_window. Split and unsplit
  * results differ by the f16 rounding of the probabilities (each part's exponentials are taken
  * against its own running max) and the order of the sums. */
@@ -286,7 +287,7 @@ int e2mi_gather_ids(e2mi_stream stream, const int32_t *ids, const int32_t *rowma
  * invalid query row, or one with no valid key, gets ctx = 0. f16 inputs from e2mi_qkv_norm_rope,
  * f32 softmax and accumulation. The context is quantized per 128 dims into ctx_q [B*S][H*D] /
  * ctx_s [B*S][H*D/128] (the O-projection's operand); ctx32 (optional) receives it in f32.
- * head_dim D must be 256. */
+ * head_dim D must be 256; scale finite and > 0 (every attention entry here). */
 int e2mi_attention(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
                    const uint16_t *vt16, const uint8_t *valid, int B, int S, int H, int KV, int D,
                    float scale, int8_t *ctx_q, float *ctx_s, float *ctx32);

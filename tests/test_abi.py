@@ -44,6 +44,13 @@ def test_errors_are_reported_without_a_gpu():
     assert lib.e2mi_quantize(None, None, None, None, 4, 100, 100, 128) == -1
     assert "quantize" in e2mi.last_error()
     assert lib.e2mi_interleave_gate_up(None, None, None, None, None, None, 100, 8) == -1
+    # the attention's softmax needs a positive, finite logit scale
+    for bad in (0.0, -0.5, float("inf"), float("nan")):
+        assert lib.e2mi_attention(None, None, None, None, None, 1, 128, 3, 1, 256, bad, None, None, None) == -1
+        assert "scale" in e2mi.last_error()
+        assert lib.e2mi_attention_packed_window(None, None, None, None, 8, None, None, None, 1, 8, 3, 1, 256,
+                                                bad, 0, None, None, None, None, 0) == -1
+        assert "scale" in e2mi.last_error()
 
 
 def _exports(path):

@@ -164,7 +164,8 @@ def test_e8cq_corruption_refused(e2mi_mod, model, tmp_path):
 
 
 def test_bad_configs_refused(e2mi_mod):
-    for over in (dict(head_dim=128), dict(hidden=700), dict(n_heads=3, n_kv_heads=2), dict(max_seq=4096)):
+    for over in (dict(head_dim=128), dict(hidden=700), dict(n_heads=3, n_kv_heads=2), dict(max_seq=4096),
+                 dict(attn_scale=0.0), dict(attn_scale=-1.0), dict(attn_scale=float("inf"))):
         with pytest.raises(e2mi_mod.E2MIError):
             e2mi_mod.Model.synthetic(e2mi_mod.baseline_config(n_layers=1, vocab=10, **over), 1)
 
