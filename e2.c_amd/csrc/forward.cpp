@@ -322,6 +322,62 @@ static int32_t work_item(int b, int h, int part, int parts, int qb) {
     return b | (h << 16) | (part << 20) | ((parts - 1) << 22) | (qb << 24);
 }
 
+// Workgroup i of a 1-D grid runs on XCD i % 8, and each XCD has its own L2. The attention work
+// items of one sequence read the same K and V^T, so they are dealt to one XCD: a sequence's
+// consecutive items are cut into chunks of at most 1/div of an XCD's share of the key tiles, each
+// chunk goes to the least-loaded XCD in list order (longest sequences first), and the XCD queues
+// are interleaved into the grid (a queue that runs dry is filled from the one with most items
+// left). Cost of an item: the key tiles it walks (its part of its block's range, window-aware).
+// Smaller chunks balance the XCDs better, larger ones share more K and V^T in L2: the f16 kernels
+// take div 2 at head_dim 256 (one chunk per sequence at config 4) and 4 at head_dim 512 (one
+// workgroup per CU, fewer slots to balance). The order changes no result: items are independent.
+constexpr int kXcds = 8;
+static int item_tiles(int32_t it, const int32_t *len, int window) {
+    const int b = it & 0xffff, part = (it >> 20) & 3, parts = ((it >> 22) & 3) + 1, q = it >> 24, L = len[b];
+    int t0 = 0, t1 = (L + 31) / 32;
+    if (window > 0) {
+        const int q0 = q * 128, q1 = std::min(q0 + 127, L - 1);
+        t0 = std::max(q0 - window, 0) / 32;
+        t1 = std::min(std::min(q1 + window, L - 1) / 32 + 1, t1);
+    }
+    const int n = t1 - t0;
+    return std::max(1, n * (part + 1) / parts - n * part / parts);
+}
+static void xcd_deal(int32_t *w, int n, const int32_t *len, int window, int div) {
+    if (n <= kXcds) return;
+    long total = 0;
+    for (int i = 0; i < n; i++) total += item_tiles(w[i], len, window);
+    const long lim = std::max(1L, (total + (long)kXcds * div - 1) / ((long)kXcds * div));
+    std::vector<int32_t> q[kXcds];
+    long load[kXcds] = {};
+    for (int i = 0; i < n;) {
+        const int b = w[i] & 0xffff;
+        long c = 0;
+        int j = i;
+        for (; j < n && (w[j] & 0xffff) == b; j++) {
+            const int t = item_tiles(w[j], len, window);
+            if (j > i && c + t > lim) break;
+            c += t;
+        }
+        const int x = (int)(std::min_element(load, load + kXcds) - load);
+        q[x].insert(q[x].end(), w + i, w + j);
+        load[x] += c;
+        i = j;
+    }
+    size_t at[kXcds] = {};
+    for (int k = 0; k < n;) {
+        for (int x = 0; x < kXcds && k < n; x++) {
+            int y = x;
+            if (at[y] == q[y].size()) {
+                y = 0;
+                for (int z = 1; z < kXcds; z++)
+                    if (q[z].size() - at[z] > q[y].size() - at[y]) y = z;
+            }
+            w[k++] = q[y][at[y]++];
+        }
+    }
+}
+
 // every kernel of one forward over B sequences of S tokens (M rows: B * S padded, or the packed
 // row count), on stream s; returns the launch count or -1
 static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s) {
@@ -393,7 +449,7 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s)
                 RUN("attention", e2mi_attention_packed_window(s, g->q16, g->k16, g->vt16, M, g->seq_start, g->seq_len,
                                                               g->pos, B, S, H, KV, D, c.attn_scale, L.geo.window,
                                                               g->cq, g->cs, nullptr,
-                                                              g->work_full ? g->work_full : g->work,
+                                                              D == 512 && g->work_full ? g->work_full : g->work,
                                                               work_slots(g, B, M)));
             }
             if (g->attn_i8)
@@ -558,6 +614,9 @@ static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
             }
     }
     g->split_now = any_split;  // no block long enough: the unsplit kernel, no merge launch
+    xcd_deal(g->h_work, k, g->h_len, g->cfg.window, 2);
+    if (g->h_work_full) xcd_deal(g->h_work_full, kf, g->h_len, 0, 4);
+    if (g->attn_i8) xcd_deal(g->h_work8, k8, g->h_len, 0, 2);
     while (k < slots * g->split_factor) g->h_work[k++] = -1;
     if (g->h_mwork)
         while (km < slots) g->h_mwork[km++] = -1;

@@ -491,13 +491,69 @@ def work_entry(b, h, part, parts, qb):
     return b | (h << 16) | (part << 20) | ((parts - 1) << 22) | (qb << 24)
 
 
-def attention_work(lens, H):
+XCDS = 8
+
+
+def _item_tiles(it, lens, window):
+    b, part, parts, q = it & 0xffff, (it >> 20) & 3, ((it >> 22) & 3) + 1, it >> 24
+    L = int(lens[b])
+    t0, t1 = 0, (L + 31) // 32
+    if window > 0:
+        q0, q1 = q * 128, min(q * 128 + 127, L - 1)
+        t0, t1 = max(q0 - window, 0) // 32, min(min(q1 + window, L - 1) // 32 + 1, t1)
+    n = t1 - t0
+    return max(1, n * (part + 1) // parts - n * part // parts)
+
+
+def xcd_deal(work, lens, window=0, div=2):
+    """The engine's order of an attention work list (forward.cpp xcd_deal): workgroup i runs on XCD
+    i % 8, so each sequence's consecutive items, cut into chunks of at most 1/div of an XCD's share
+    of the key tiles, go to the least-loaded XCD, and the XCD queues are interleaved (a dry queue is
+    filled from the one with most items left). A permutation of `work`."""
+    import numpy as np
+    w = [int(x) for x in work]
+    n = len(w)
+    if n <= XCDS:
+        return np.asarray(w, np.int32)
+    cost = [_item_tiles(it, lens, window) for it in w]
+    lim = max(1, -(-sum(cost) // (XCDS * div)))
+    queues, load = [[] for _ in range(XCDS)], [0] * XCDS
+    i = 0
+    while i < n:
+        b, c, j = w[i] & 0xffff, 0, i
+        while j < n and (w[j] & 0xffff) == b:
+            if j > i and c + cost[j] > lim:
+                break
+            c += cost[j]
+            j += 1
+        x = min(range(XCDS), key=lambda z: (load[z], z))
+        queues[x] += w[i:j]
+        load[x] += c
+        i = j
+    at, out = [0] * XCDS, []
+    while len(out) < n:
+        for x in range(XCDS):
+            if len(out) == n:
+                break
+            y = x
+            if at[y] == len(queues[y]):
+                y = 0
+                for z in range(1, XCDS):
+                    if len(queues[z]) - at[z] > len(queues[y]) - at[y]:
+                        y = z
+            out.append(queues[y][at[y]])
+            at[y] += 1
+    return np.asarray(out, np.int32)
+
+
+def attention_work(lens, H, window=0, div=2):
     """The engine's attention work list for packed sequences of these lengths: one entry per
-    128-query block, longest sequences first, keys unsplit."""
+    128-query block, longest sequences first, keys unsplit, dealt to the XCDs (xcd_deal; the
+    engine takes div 4 for head_dim 512)."""
     import numpy as np
     order = sorted(range(len(lens)), key=lambda b: -int(lens[b]))
-    return np.asarray([work_entry(b, h, 0, 1, q) for b in order for h in range(H)
-                       for q in range((int(lens[b]) + 127) // 128)], np.int32)
+    return xcd_deal([work_entry(b, h, 0, 1, q) for b in order for h in range(H)
+                     for q in range((int(lens[b]) + 127) // 128)], lens, window, div)
 
 
 def attention_split_work(lens, H, parts_of, window=0):
@@ -519,7 +575,7 @@ def attention_split_work(lens, H, parts_of, window=0):
                 work += [work_entry(b, h, p, P, q) for p in range(P)]
                 if P > 1:
                     merge.append(work_entry(b, h, 0, P, q))
-    return np.asarray(work, np.int32), np.asarray(merge or [-1], np.int32)
+    return xcd_deal(work, lens, window), np.asarray(merge or [-1], np.int32)
 
 
 def attention_packed_split(q16, k16, vt16, start, lens, max_len, H, KV, work, merge, window=0, pos=None,
