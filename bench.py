@@ -662,6 +662,48 @@ def summarize_counters(fetch_csv, write_csv, mfma_csv, trace_csv):
     return text
 
 
+def summarize_ktrace(trace_csv, steps=20, warmup=5):
+    """Per-kernel statistics of a rocprofv3 --kernel-trace CSV of a default bench run, and the
+    per-shape split of the headline kernel k_gemm_tv: its last launches in the trace are the
+    timed region (`steps` steps of the four shapes in SHAPES order) followed by `steps` back-to-back
+    launches of each shape (the per-launch durations the roofline uses)."""
+    import csv
+    import collections
+    rows = list(csv.DictReader(open(trace_csv)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    by = collections.defaultdict(list)
+    for r in rows:
+        name = r["Kernel_Name"].replace("void ", "").split("(")[0]
+        by[(name, r["Grid_Size_X"], r["Workgroup_Size_X"])].append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = ["| kernel | grid | block | calls | avg us | min us | max us | total ms |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for (name, grid, blk), d in sorted(by.items(), key=lambda kv: -sum(kv[1]))[:16]:
+        lines.append(f"| `{name[:90]}` | {grid} | {blk} | {len(d)} | {np.mean(d):.1f} | {min(d):.1f} | "
+                     f"{max(d):.1f} | {sum(d) / 1e3:.2f} |")
+    tv = [r for r in rows if "k_gemm_tv" in r["Kernel_Name"]]
+    n = len(SHAPES)
+    tail = tv[-2 * steps * n:]
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    timed, per = tail[:steps * n], tail[steps * n:]
+    lines += ["", "| (K,N) | kernel | timed-region launches | avg us | back-to-back launches | avg us | span us per launch |",
+              "|---|---|---:|---:|---:|---:|---:|"]
+    for i, (K, N) in enumerate(SHAPES):
+        t = [dur(r) for r in timed[i::n]]
+        b = per[i * steps:(i + 1) * steps]
+        span = (int(b[-1]["End_Timestamp"]) - int(b[0]["Start_Timestamp"])) / 1e3 / len(b)
+        kn = "k_gemm_tv<%d>" % (K // 128)
+        assert all(kn in r["Kernel_Name"] for r in timed[i::n] + b), "launch order differs from the bench's"
+        lines.append(f"| {K}x{N} | `{kn}` | {len(t)} | {np.mean(t):.2f} | {len(b)} | "
+                     f"{np.mean([dur(r) for r in b]):.2f} | {span:.2f} |")
+    step_span = (int(timed[-1]["End_Timestamp"]) - int(timed[0]["Start_Timestamp"])) / 1e3 / steps
+    lines.append("")
+    lines.append(f"timed region in the trace: {step_span:.1f} us per step (first launch start to last launch end)")
+    text = "\n".join(lines) + "\n"
+    print(text)
+    return text
+
+
 # ------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -684,10 +726,16 @@ def main():
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "MFMA_CSV", "TRACE_CSV"),
                     help="turn the counter CSVs and the kernel trace of --probe-all runs into "
                          "profiles/counters_probe_all.md")
+    ap.add_argument("--summarize-ktrace", metavar="TRACE_CSV",
+                    help="per-kernel statistics and the headline kernel's per-shape split from a "
+                         "rocprofv3 --kernel-trace CSV of a default-step bench run")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn FETCH_SIZE / WRITE_SIZE counter CSVs of a --probe run into "
                          "profiles/gemm_tok_traffic.json")
     args = ap.parse_args()
+    if args.summarize_ktrace:
+        summarize_ktrace(args.summarize_ktrace, args.steps, args.warmup)
+        return
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
         return
@@ -793,31 +841,18 @@ def main():
         print("probe done")
         return
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    # timed region: exactly K steps, synchronised on both sides; per-launch HIP events on the
-    # launching stream give each kernel's average duration for the roofline
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in cases] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        for i, c in enumerate(cases):
-            ev[s][i][0].record(stream)
-            gemm_tok(c)
-            ev[s][i][1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per_launch = [np.mean([ev[s][i][0].elapsed_time(ev[s][i][1]) * 1e-3 for s in range(args.steps)])
-                  for i in range(len(cases))]
-    ops = [2.0 * M * c["N"] * c["K"] for c in cases]
-    ms_per_step = wall / args.steps * 1e3
-    value = sum(ops) / (wall / args.steps) / 1e12
-
-    # the other contracts on the same activations: per-token with the fused requantizing epilogue;
-    # per-128 scales (exact and fast fold, f32 and requant); the vendor int8 GEMM for scale
+    # the other contracts on the same activations, measured first (so the headline below runs on a
+    # GPU at its working clocks): per-token with the fused requantizing epilogue; per-128 scales
+    # (exact and fast fold, f32 and requant); the vendor int8 GEMM for scale
     reps = max(3, args.steps // 2)
+    ops = [2.0 * M * c["N"] * c["K"] for c in cases]
+    # untimed: about 0.3 s of the step's launches before the first measured leg, so that no leg
+    # is measured on a GPU still at idle clocks (the first leg of a fresh process measured 5-10 %
+    # slower than the same leg a few hundred milliseconds later)
+    t_w = time.perf_counter()
+    while time.perf_counter() - t_w < 0.3:
+        step()
+        torch.cuda.synchronize()
 
     def sweep(fn):
         for c in cases:  # first calls (library heuristics, attribute set-up) stay untimed
@@ -856,6 +891,28 @@ def main():
     qg_sweep["note"] = ("per-token quantize of the f32 activations + the f32 GEMM, per shape; tops counts "
                         "the GEMM's 2 M N K over both launches")
 
+    # the timed region: W warmup steps, then exactly K steps of the four launches, synchronised on
+    # both sides, nothing else on the stream (a HIP event pair recorded around every launch, as
+    # earlier builds did, cost about 12 % of the sweep's throughput in same-box A/B runs); one event
+    # pair spans the region as a cross-check of the host clock
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev_span = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    t0 = time.perf_counter()
+    ev_span[0].record(stream)
+    for s in range(args.steps):
+        step()
+    ev_span[1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    span_ms = ev_span[0].elapsed_time(ev_span[1]) / args.steps
+    ms_per_step = wall / args.steps * 1e3
+    value = sum(ops) / (wall / args.steps) / 1e12
+    # each kernel's average launch duration (the roofline's): K back-to-back launches of one shape
+    # between a HIP event pair on the launching stream
+    per_launch = [time_calls(torch, lambda c=c: gemm_tok(c), args.steps) for c in cases]
+
     # roofline: the dominant launch of the step (longest average duration)
     dom = int(np.argmax(per_launch))
     c = cases[dom]
@@ -886,7 +943,25 @@ def main():
                      "mfma_TOPS": round(ach, 2), "mfma_frac": round(ach / PEAK_INT8_TOPS, 4),
                      "note": "algorithmic roofline max(t_mfma, t_hbm) at the spec peaks (int8 ops "
                              "counted as TFLOP/s); achieved = algorithmic bytes (or ops) / the "
-                             "launch's average duration from HIP events on its stream"})
+                             "launch's average duration from HIP events around back-to-back launches "
+                             "on its stream"})
+    # the write roof measured on this box: the HIP runtime's 32-bit fill of the same f32 output
+    # (hipMemsetD32Async, nothing read), against which the launch's output stream is compared
+    yb = c["yf"].numel() * 4
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemsetD32Async.restype = C.c_int
+    hip.hipMemsetD32Async.argtypes = [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p]
+
+    def fill():
+        if hip.hipMemsetD32Async(c["yf"].data_ptr(), 0, c["yf"].numel(), sp) != 0:
+            raise RuntimeError("hipMemsetD32Async failed")
+    fill()
+    t_fill = time_calls(torch, fill, args.steps)
+    roofline["measured_write_roof"] = {
+        "GB/s": round(yb / t_fill / 1e9, 1), "fill_us": round(t_fill * 1e6, 2),
+        "fill_time_over_launch_time": round(t_fill / per_launch[dom], 4),
+        "note": "hipMemsetD32Async of the launch's f32 output (the same bytes written, nothing read), "
+                "HIP events around back-to-back fills"}
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -895,6 +970,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "event_span_ms_per_step": round(span_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
