@@ -704,6 +704,60 @@ def summarize_ktrace(trace_csv, steps=20, warmup=5):
     return text
 
 
+def summarize_enc_ktrace(trace_csv):
+    """Per-kernel statistics of a rocprofv3 --kernel-trace CSV of `bench.py --encoder-only` and the
+    per-forward / per-layer stage times of its f16-attention forwards: a forward is the launches
+    from the embedding kernel (k_rows<1, ...>) to k_pool_finish; the first (eager) one is left out."""
+    import csv
+    import collections
+    rows = list(csv.DictReader(open(trace_csv)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    name = lambda r: r["Kernel_Name"].replace("void ", "").split("(")[0]
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    by = collections.defaultdict(list)
+    for r in rows:
+        by[(name(r), r["Grid_Size_X"], r["Workgroup_Size_X"])].append(dur(r))
+    lines = ["| kernel | grid | block | calls | avg us | min us | max us | total ms |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for (n, grid, blk), d in sorted(by.items(), key=lambda kv: -sum(kv[1]))[:18]:
+        lines.append(f"| `{n[:80]}` | {grid} | {blk} | {len(d)} | {np.mean(d):.1f} | {min(d):.1f} | "
+                     f"{max(d):.1f} | {sum(d) / 1e3:.2f} |")
+    fwd, cur = [], None
+    for r in rows:
+        n = name(r)
+        if n.startswith("e2mi::k_rows<1"):
+            cur = [r]
+        elif cur is not None:
+            cur.append(r)
+            if "k_pool_finish" in n:
+                fwd.append(cur)
+                cur = None
+    f16 = [f for f in fwd[1:] if not any("k_attn_i8" in name(r) for r in f)]
+    i8 = [f for f in fwd if any("k_attn_i8" in name(r) for r in f)]
+    stage = collections.defaultdict(list)
+    for f in f16:
+        per = collections.defaultdict(float)
+        for r in f:
+            per[name(r)] += dur(r)
+        for k, v in per.items():
+            stage[k].append(v)
+    nl = sum(1 for r in f16[0] if "k_attn_packed" in name(r)) if f16 else 0
+    lines += ["", f"f16-attention forwards: {len(f16)} (after the eager one), {len(f16[0]) if f16 else 0} "
+              f"launches each, {nl} layers; int8-attention forwards: {len(i8)}", "",
+              "| kernel | per forward us | per layer us |", "|---|---:|---:|"]
+    for k, v in sorted(stage.items(), key=lambda kv: -np.mean(kv[1])):
+        lines.append(f"| `{k[:80]}` | {np.mean(v):.1f} | {np.mean(v) / max(nl, 1):.1f} |")
+    if f16:
+        kern = [sum(dur(r) for r in f) for f in f16]
+        span = [(int(f[-1]["End_Timestamp"]) - int(f[0]["Start_Timestamp"])) / 1e3 for f in f16]
+        lines.append("")
+        lines.append(f"per forward: kernels {np.mean(kern) / 1e3:.3f} ms, first launch start to last "
+                     f"launch end {np.mean(span) / 1e3:.3f} ms")
+    text = "\n".join(lines) + "\n"
+    print(text)
+    return text
+
+
 # ------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -729,10 +783,16 @@ def main():
     ap.add_argument("--summarize-ktrace", metavar="TRACE_CSV",
                     help="per-kernel statistics and the headline kernel's per-shape split from a "
                          "rocprofv3 --kernel-trace CSV of a default-step bench run")
+    ap.add_argument("--summarize-enc-ktrace", metavar="TRACE_CSV",
+                    help="per-kernel statistics and per-layer stage times from a rocprofv3 "
+                         "--kernel-trace CSV of an --encoder-only run")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn FETCH_SIZE / WRITE_SIZE counter CSVs of a --probe run into "
                          "profiles/gemm_tok_traffic.json")
     args = ap.parse_args()
+    if args.summarize_enc_ktrace:
+        summarize_enc_ktrace(args.summarize_enc_ktrace)
+        return
     if args.summarize_ktrace:
         summarize_ktrace(args.summarize_ktrace, args.steps, args.warmup)
         return
