@@ -1432,10 +1432,23 @@ static int check_args(const GemmArgs &p, const char *who) {
     return 0;
 }
 
-// fewer 256 x 128 tiles than CUs (the vision tower's 2520-patch projections, small batches):
-// 128 x 128 tiles of 4 waves, two workgroups per CU, four times the tiles
-static bool small_grid(const GemmArgs &p) {
-    return (long)((p.M + 255) / 256) * ((p.N + 127) / 128) < num_cus();
+// 128 x 128 tiles of 4 waves, two workgroups per CU, instead of 256 x 128 tiles of 8 waves, one
+// per CU, where they take fewer rounds of the device: with fewer 256 x 128 tiles than CUs (the
+// vision tower's 2520-patch projections, small batches), and where the 256 x 128 tiles need a last
+// round that only a few CUs work on (the reference geometry's N = 512 projections at 17408 rows:
+// 272 tiles, two rounds for 1.06 rounds of work). In units of one 256 x 128 tile's time on a CU:
+// 256 x 128 tiles take ceil(tiles / CUs) rounds; 128 x 128 tiles take one unit per full round of
+// two workgroups on every CU, and a last partial round of at most one workgroup per CU about 0.6
+// (a 128 x 128 workgroup alone on its CU).
+static bool half_tiles(const GemmArgs &p) {
+    const long C = num_cus();
+    const long t256 = (long)((p.M + 255) / 256) * ((p.N + 127) / 128);
+    if (t256 < C) return true;
+    const long t128 = (long)((p.M + 127) / 128) * ((p.N + 127) / 128);
+    const long full = t128 / (2 * C), rem = t128 % (2 * C);
+    const double r128 = (double)full + (rem == 0 ? 0.0 : rem <= C ? 0.6 : 1.0);
+    const double r256 = (double)((t256 + C - 1) / C);
+    return r128 <= r256 - 0.3;
 }
 
 int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump, bool tok = false) {
@@ -1452,7 +1465,7 @@ int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump, bool tok = false) {
         return launch_dump(s, p);
     }
     if (tok) return launch_t<EPI_F32>(s, p);
-    if (small_grid(p)) return launch_p<128, 128, 4, 1, EPI_F32>(s, p);
+    if (half_tiles(p)) return launch_p<128, 128, 4, 1, EPI_F32>(s, p);
     return launch_p<256, 128, 8, 1, EPI_F32>(s, p);
 }
 
@@ -1464,7 +1477,7 @@ int launch_gemm_i8q(hipStream_t s, GemmArgs p, bool tok = false) {
         return -1;
     }
     if (tok) return launch_t<EPI_I8Q>(s, p);
-    if (small_grid(p)) return launch_p<128, 128, 4, 1, EPI_I8Q>(s, p);
+    if (half_tiles(p)) return launch_p<128, 128, 4, 1, EPI_I8Q>(s, p);
     return launch_p<256, 128, 8, 1, EPI_I8Q>(s, p);
 }
 
@@ -1476,7 +1489,7 @@ int launch_gemm_gelumul(hipStream_t s, GemmArgs p) {
         set_error("i8_gemm_gelu_mul: N must be a multiple of 128; outputs and multiplier 16-byte aligned");
         return -1;
     }
-    if (small_grid(p)) return launch_p<128, 128, 4, 1, EPI_GELUMUL>(s, p);
+    if (half_tiles(p)) return launch_p<128, 128, 4, 1, EPI_GELUMUL>(s, p);
     return launch_p<256, 128, 8, 1, EPI_GELUMUL>(s, p);
 }
 

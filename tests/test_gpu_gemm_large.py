@@ -211,3 +211,24 @@ def test_config5_end_to_end(gpu, oracle, rng, K, N):
     q2, s2 = oracle.quantize(yo)
     assert np.array_equal(yq.cpu().numpy()[rows], q2)
     assert np.array_equal(ys.cpu().numpy()[rows].view(np.uint32), s2.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K", [(17408, 1024), (17408, 2048), (22912, 512)])
+def test_gemm_half_tiles_rounds_bit_exact(gpu, oracle, rng, exact_fold, M, K):
+    """N = 512 at the reference geometry's packed row counts: 256 x 128 tiles would need a second,
+    nearly empty round on 256 CUs (272 and 360 tiles), so the launcher takes 128 x 128 tiles, two
+    workgroups per CU (gemm.hip half_tiles). Same fold, same bits: f32 and requantized outputs
+    against the oracle on sampled rows, the partial last tile among them."""
+    import e2mi
+    N = 512
+    qa, as_, w, ws = _case(rng, M, N, K)
+    W = e2mi.DeviceWeight.from_rowmajor(w, ws)
+    y = e2mi.i8_gemm(_t(qa, gpu), _t(as_, gpu), W).cpu().numpy()
+    yq, ys = e2mi.i8_gemm_q(_t(qa, gpu), _t(as_, gpu), W)
+    yq, ys = yq.cpu().numpy(), ys.cpu().numpy()
+    rows = _rows(rng, M)
+    yo = oracle.i8_gemm(qa[rows], as_[rows], w, ws)
+    assert np.array_equal(y[rows].view(np.uint32), yo.view(np.uint32))
+    qo, so = oracle.quantize(yo)
+    assert np.array_equal(yq[rows], qo)
+    assert np.array_equal(ys[rows].view(np.uint32), so.view(np.uint32))
