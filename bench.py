@@ -705,9 +705,10 @@ def summarize_ktrace(trace_csv, steps=20, warmup=5):
 
 
 def summarize_enc_ktrace(trace_csv):
-    """Per-kernel statistics of a rocprofv3 --kernel-trace CSV of `bench.py --encoder-only` and the
-    per-forward / per-layer stage times of its f16-attention forwards: a forward is the launches
-    from the embedding kernel (k_rows<1, ...>) to k_pool_finish; the first (eager) one is left out."""
+    """Per-kernel statistics of a rocprofv3 --kernel-trace CSV of `bench.py --encoder-only` or
+    `--reference-only` and the per-forward / per-layer stage times of its f16-attention forwards,
+    per batch shape: a forward is the launches from the embedding kernel (k_rows<1, ...>) to
+    k_pool_finish; the first (eager) one of each shape is left out."""
     import csv
     import collections
     rows = list(csv.DictReader(open(trace_csv)))
@@ -732,27 +733,35 @@ def summarize_enc_ktrace(trace_csv):
             if "k_pool_finish" in n:
                 fwd.append(cur)
                 cur = None
-    f16 = [f for f in fwd[1:] if not any("k_attn_i8" in name(r) for r in f)]
-    i8 = [f for f in fwd if any("k_attn_i8" in name(r) for r in f)]
-    stage = collections.defaultdict(list)
-    for f in f16:
-        per = collections.defaultdict(float)
-        for r in f:
-            per[name(r)] += dur(r)
-        for k, v in per.items():
-            stage[k].append(v)
-    nl = sum(1 for r in f16[0] if "k_attn_packed" in name(r)) if f16 else 0
-    lines += ["", f"f16-attention forwards: {len(f16)} (after the eager one), {len(f16[0]) if f16 else 0} "
-              f"launches each, {nl} layers; int8-attention forwards: {len(i8)}", "",
-              "| kernel | per forward us | per layer us |", "|---|---:|---:|"]
-    for k, v in sorted(stage.items(), key=lambda kv: -np.mean(kv[1])):
-        lines.append(f"| `{k[:80]}` | {np.mean(v):.1f} | {np.mean(v) / max(nl, 1):.1f} |")
-    if f16:
+    # forwards grouped by their row count (the embedding kernel's grid): one batch shape each;
+    # the first forward of each group (eager, before the graph) is left out
+    groups = collections.OrderedDict()
+    for f in fwd:
+        groups.setdefault(f[0]["Grid_Size_X"], []).append(f)
+    for grid, fl in groups.items():
+        f16 = [f for f in fl[1:] if not any("k_attn_i8" in name(r) for r in f)]
+        i8 = [f for f in fl if any("k_attn_i8" in name(r) for r in f)]
+        if not f16:
+            continue
+        stage = collections.defaultdict(list)
+        for f in f16:
+            per = collections.defaultdict(float)
+            for r in f:
+                per[name(r)] += dur(r)
+            for k, v in per.items():
+                stage[k].append(v)
+        nl = sum(1 for r in f16[0] if "k_attn_packed" in name(r))
         kern = [sum(dur(r) for r in f) for f in f16]
         span = [(int(f[-1]["End_Timestamp"]) - int(f[0]["Start_Timestamp"])) / 1e3 for f in f16]
-        lines.append("")
-        lines.append(f"per forward: kernels {np.mean(kern) / 1e3:.3f} ms, first launch start to last "
-                     f"launch end {np.mean(span) / 1e3:.3f} ms")
+        lines += ["", f"forwards of {int(grid) // 64} rows (embedding grid {grid}): {len(f16)} f16-attention "
+                  f"forwards after the eager one, {len(f16[0])} launches each, {nl} layers; int8-attention "
+                  f"forwards: {len(i8)}; per forward: kernels {np.mean(kern) / 1e3:.3f} ms, first launch "
+                  f"start to last launch end {np.mean(span) / 1e3:.3f} ms", "",
+                  "| kernel | per forward us | % | per layer us |", "|---|---:|---:|---:|"]
+        tot = sum(np.mean(v) for v in stage.values())
+        for k, v in sorted(stage.items(), key=lambda kv: -np.mean(kv[1])):
+            lines.append(f"| `{k[:80]}` | {np.mean(v):.1f} | {100 * np.mean(v) / tot:.1f} | "
+                         f"{np.mean(v) / max(nl, 1):.1f} |")
     text = "\n".join(lines) + "\n"
     print(text)
     return text
