@@ -1281,6 +1281,320 @@ __global__ __launch_bounds__(512, 1) void k_gemm_tv(GemmArgs p, int tiles_n, int
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// Per-token GEMM with the requantizing epilogue overlapped (k_gemm_tq): the per-token requant
+// contract (e2mi_i8_gemm_tok_q) at K = 128 NB, N a multiple of 128, no bias or clamp. The pipeline
+// of k_gemm_tv (256 x 128 output tiles, one 512-thread workgroup per CU, three 48 KB A|W stages
+// with loads two steps ahead, slots of one MFMA each, two accumulator sets, the previous tile's
+// epilogue spread over the current tile's slots), with the waves laid out for the requantization:
+//   - 8 waves of 32 x 128 (all of the tile's 128 columns, one quantization block), four MFMA tiles
+//     each; a wave owns whole blocks, so a row's maximum needs no other wave;
+//   - W's 128 rows of a tile are fetched into LDS in the order rho -> 4 (rho % 32) + rho / 32, so
+//     MFMA tile t leaves lane c (of 32) the output column 4 c + t: every lane holds four
+//     consecutive columns of each of its 16 rows, one int8 dword, and a store instruction writes
+//     two rows' 128 bytes whole;
+//   - epilogue of the previous tile, spread over the slots: (A) 64 conversions
+//     y = fma((float)acc, RN(as * ws), 0) in place, with the lane's running row maxima; (B) the
+//     rows' maxima over the 32 lanes of each half by a transposing halving exchange (each lane
+//     pair ends with one row's maximum), the quantizer's scale and inverse for that row, its scale
+//     stored, the 16 inverses fetched back by lane permutes; (C) 16 packs and dword stores.
+// Bytes and scales equal k_gemm_t's requantizing epilogue (the same conversion, maximum and
+// quantizer arithmetic).
+namespace tq {
+constexpr int BM = 256, BN = 128, NW = 8, STAGES = 3, NSLOT = 3;
+constexpr int TILE = (BM + BN) * 128;
+constexpr int SLOT = 2048;                     // as (256 floats) | ws (128 floats) of one tile
+constexpr int LDS = STAGES * TILE + NSLOT * SLOT;
+constexpr int L = BM / 8 / NW + BN / 8 / NW + 1;  // loads per wave per step: 4 A, 2 W, as or ws
+constexpr int SPS = 16;                        // MFMA slots per step
+constexpr int NA = 64, NC = 16;                // phase A conversions, phase C packs per lane
+static_assert(LDS <= 160 * 1024, "LDS budget");
+// slots of the phases within a tile (the epilogue of the previous tile): A over the first slots,
+// B right after the last A, C in the last NC slots before the tile's last step
+template <int NB>
+constexpr int slot_c(int r) { return SPS * (NB - 1) - NC + r; }
+template <int NB>
+constexpr int slot_a(int u) { return u * (slot_c<NB>(0) - 1) / NA; }
+template <int NB>
+constexpr int slot_b() { return slot_a<NB>(NA - 1); }
+// stores issued in slots [s0, s1): one for the scales at B, one per C slot
+template <int NB>
+constexpr int stores_in(int s0, int s1) {
+    int n = (slot_b<NB>() >= s0 && slot_b<NB>() < s1) ? 1 : 0;
+    for (int r = 0; r < NC; r++) n += (slot_c<NB>(r) >= s0 && slot_c<NB>(r) < s1) ? 1 : 0;
+    return n;
+}
+}  // namespace tq
+
+template <int X>
+__device__ inline float swz_xor_max(float v) { return fmaxf(v, swz_xor<X>(v)); }
+template <int X, int N>
+__device__ inline void halve_max(const float (&v)[2 * N], float (&o)[N], bool up) {
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float keep = up ? v[i + N] : v[i], give = up ? v[i] : v[i + N];
+        o[i] = fmaxf(keep, swz_xor<X>(give));
+    }
+}
+
+template <int NB>
+__global__ __launch_bounds__(512, 1) void k_gemm_tq(GemmArgs p, int tiles_n, int tiles) {
+    using namespace tq;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = lane >> 5, r32 = lane & 31;
+
+    const int nx = (gridDim.x % 8 == 0) ? 8 : 1;
+    const int grp = blockIdx.x % nx, li = blockIdx.x / nx, per = gridDim.x / nx;
+    const int c0 = (int)((long)tiles * grp / nx), c1 = (int)((long)tiles * (grp + 1) / nx);
+    const int ntile = (c1 - c0 > li) ? (c1 - c0 - li + per - 1) / per : 0;
+    const int per_m = per / tiles_n, per_n = per % tiles_n;
+    struct TC {
+        int mb, nt;
+    };
+    auto tc_next = [&](TC t) {
+        t.mb += per_m;
+        t.nt += per_n;
+        if (t.nt >= tiles_n) {
+            t.nt -= tiles_n;
+            t.mb += 1;
+        }
+        return t;
+    };
+    const TC tc0 = {(c0 + li) / tiles_n, (c0 + li) % tiles_n};
+
+    const v4u rA = rsrc_words(p.A, (uint32_t)((size_t)p.M * p.lda));
+    const v4u rW = rsrc_words(p.W, (uint32_t)((size_t)p.N * p.ldw));
+    const v4u rS = rsrc_words(p.as, (uint32_t)((size_t)p.M * 4));
+    const v4u rV = rsrc_words(p.ws, (uint32_t)((size_t)p.N * 4));
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(p.Yq, 0, (int)min((long)p.M * p.ldyq, 0x7fffffffL), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(p.ys, 0, (int)min((long)p.M * p.ldys * 4, 0x7fffffffL), 0x00020000);
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)smem);
+
+    // A loads as in k_gemm_tv. W load ii (0, 1) of a wave fills LDS rows rho = 64 ii + 8 wave +
+    // lane / 8 with W row 4 (rho % 32) + rho / 32 = 32 (wave % 4) + 2 ii + wave / 4 + 4 (lane / 8)
+    // of the tile: the lane part 4 (lane / 8) rows, the rest a scalar row; the 16-byte chunk
+    // swizzle depends on the LDS row only, as for A
+    const int swl = ((lane & 7) ^ ((wave & 1) * 4 + ((lane >> 4) & 3))) << 4;
+    const uint32_t vla = (uint32_t)(lane >> 3) * (uint32_t)p.lda + swl;
+    const uint32_t vlb = (uint32_t)(lane >> 3) * 4u * (uint32_t)p.ldw + swl;
+    const uint32_t vl4 = (uint32_t)lane * 4;
+    const uint32_t sta = 64u * (uint32_t)p.lda;
+
+    int ig = 0, ikb = 0, islot = 0;
+    TC itc = tc0;
+    struct Issue {
+        uint32_t st, sl, ko;
+        int m0, n0;
+    };
+    uint32_t sa = 0;
+    auto issue_prep = [&]() {
+        Issue is;
+        is.m0 = itc.mb * BM;
+        is.n0 = itc.nt * BN;
+        is.st = lds0 + (uint32_t)((ig % STAGES) * TILE) + (uint32_t)wave * 1024u;
+        is.sl = lds0 + (uint32_t)(STAGES * TILE + islot * SLOT);
+        is.ko = (uint32_t)(ikb * kQBlock);
+        ++ig;
+        if (++ikb == NB) {
+            ikb = 0;
+            itc = tc_next(itc);
+            islot = islot == NSLOT - 1 ? 0 : islot + 1;
+        }
+        return is;
+    };
+    auto issue_load = [&](const Issue &is, int i) {
+        if (i == 0) sa = (uint32_t)(is.m0 + wave * 8) * (uint32_t)p.lda + is.ko;
+        if (i < 4) {
+            dma16(rA, is.st + i * NW * 1024, vla, sa);
+            sa += sta;
+        } else if (i < 6) {
+            const uint32_t wr = (uint32_t)(is.n0 + 32 * (wave & 3) + 2 * (i - 4) + (wave >> 2));
+            dma16(rW, is.st + BM * 128 + (i - 4) * NW * 1024, vlb, wr * (uint32_t)p.ldw + is.ko);
+        } else if (wave < 4) {
+            dma4(rS, is.sl + wave * 256, vl4, (uint32_t)(is.m0 + wave * 64) * 4);
+        } else {
+            dma4(rV, is.sl + 1024 + (wave & 1) * 256, vl4, (uint32_t)(is.n0 + (wave & 1) * 64) * 4);
+        }
+    };
+
+    // fragments of 32-deep sub-step kk: row r32 of a 32-row tile, 16-byte chunk 2 kk + hi
+    int fo[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) fo[kk] = swz(r32, 2 * kk + hi);
+    struct Frags {
+        v4i a, w[4];
+    };
+    auto read_frags = [&](int stage, int kk, Frags &f) {
+        const unsigned char *sb = smem + stage * TILE + fo[kk];
+        f.a = *(const v4i *)(sb + (wave * 32) * 128);
+#pragma unroll
+        for (int t = 0; t < 4; t++) f.w[t] = *(const v4i *)(sb + BM * 128 + (t * 32) * 128);
+    };
+
+    // epilogue state of the previous tile: register r of tile t holds row
+    // 32 wave + 8 (r / 4) + 4 hi + r % 4 and column 4 r32 + t
+    struct Epi {
+        f32x4 a4[4];  // activation scales of the lane's 16 rows
+        f32x4 w4;     // weight scales of its 4 columns
+        float m[16];  // running row maxima, then the rows' inverse scales
+        uint32_t row0;  // first row of the wave (of the tile being written)
+        uint32_t col;   // the lane's first column
+    } ep;
+    auto epi_begin = [&](TC tc, int slot) {
+        const unsigned char *sl = smem + STAGES * TILE + slot * SLOT;
+#pragma unroll
+        for (int g = 0; g < 4; g++) ep.a4[g] = *(const f32x4 *)(sl + (wave * 32 + g * 8 + hi * 4) * 4);
+        ep.w4 = *(const f32x4 *)(sl + 1024 + (4 * r32) * 4);
+        ep.row0 = (uint32_t)(tc.mb * BM + wave * 32);
+        ep.col = (uint32_t)(tc.nt * BN + 4 * r32);
+    };
+    // phase A, element u: tile t = u % 4 of register r = u / 4
+    auto phase_a = [&](v16i (&acc)[4], auto U) {
+        constexpr int u = decltype(U)::value;
+        constexpr int t = u % 4, r = u / 4;
+        const float y = __builtin_fmaf((float)acc[t][r], __fmul_rn(ep.a4[r >> 2][r & 3], ep.w4[t]), 0.f);
+        acc[t][r] = __builtin_bit_cast(int, y);
+        ep.m[r] = t == 0 ? fabsf(y) : fmaxf(ep.m[r], fabsf(y));
+    };
+    // phase B: per-row maxima over the half-wave, scale and inverse, the scales stored, the lane's
+    // 16 rows' inverses back in ep.m
+    auto phase_b = [&]() {
+        float m8[8], m4[4], m2[2], m1[1];
+        halve_max<16, 8>(ep.m, m8, lane & 16);
+        halve_max<8, 4>(m8, m4, lane & 8);
+        halve_max<4, 2>(m4, m2, lane & 4);
+        halve_max<2, 1>(m2, m1, lane & 2);
+        const float amax = swz_xor_max<1>(m1[0]);
+        // this lane pair holds register j's row
+        const int j = ((lane >> 4) & 1) * 8 + ((lane >> 3) & 1) * 4 + ((lane >> 2) & 1) * 2 + ((lane >> 1) & 1);
+        const QScale qs = qscale(amax);
+        const uint32_t row = ep.row0 + (uint32_t)(8 * (j >> 2) + 4 * hi + (j & 3));
+        // one lane per row writes its scale; the others point past the descriptor's range
+        const uint32_t so = (lane & 1) == 0 ? (row * (uint32_t)p.ldys + (ep.col - 4 * r32) / 128) * 4 : 0x80000000u;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, qs.sc), rs, so, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int src = (lane & 0x20) | (((r >> 3) & 1) << 4) | (((r >> 2) & 1) << 3) | (((r >> 1) & 1) << 2) |
+                            ((r & 1) << 1);
+            ep.m[r] = __shfl(qs.inv, src);
+        }
+    };
+    // phase C, register r: the four columns' bytes, one dword store
+    auto phase_c = [&](v16i (&acc)[4], auto R) {
+        constexpr int r = decltype(R)::value;
+        // the elements go through plain ints first: __builtin_bit_cast of a vector element lvalue
+        // reads the vector's first element in this compiler (its address is the vector's)
+        const int b0 = acc[0][r], b1 = acc[1][r], b2 = acc[2][r], b3 = acc[3][r];
+        const uint32_t w = pack4_magic(__builtin_bit_cast(float, b0), __builtin_bit_cast(float, b1),
+                                       __builtin_bit_cast(float, b2), __builtin_bit_cast(float, b3), ep.m[r]);
+        const uint32_t row = ep.row0 + (uint32_t)(8 * (r >> 2) + 4 * hi + (r & 3));
+        __builtin_amdgcn_raw_buffer_store_b32(w, rq, row * (uint32_t)p.ldyq + ep.col, 0, 0);
+    };
+
+    Frags F[2];
+    const int G = ntile * NB;
+    if (G > 0) {
+        Issue is = issue_prep();
+#pragma unroll
+        for (int i = 0; i < L; i++) issue_load(is, i);
+        is = issue_prep();
+#pragma unroll
+        for (int i = 0; i < L; i++) issue_load(is, i);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
+        __syncthreads();
+        read_frags(0, 0, F[0]);
+    }
+    const v16i zero = {};
+
+    int g = 0;
+    TC ctc = tc0, etc = tc0;
+    int cslot = 0, eslot = 0;
+    auto tile = [&](v16i (&cur)[4], v16i (&prev)[4], auto EON) {
+        constexpr bool EPI_ON = decltype(EON)::value;
+        if constexpr (EPI_ON) epi_begin(etc, eslot);
+        Issue is;
+        [&]<int... S>(std::integer_sequence<int, S...>) {
+            (
+                [&] {
+                    constexpr int s = S;          // slot of the tile
+                    constexpr int st = s / SPS;   // step
+                    constexpr int ss = s % SPS;   // slot of the step
+                    constexpr int kk = ss / 4;    // sub-step
+                    constexpr int t = ss % 4;     // MFMA (output tile) of the sub-step
+                    if constexpr (ss == 0) is = issue_prep();
+                    const Frags &f = F[kk % 2];
+                    cur[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a, f.w[t], (st == 0 && kk == 0) ? zero : cur[t],
+                                                                    0, 0, 0);
+                    if constexpr (t == 0) {
+                        if constexpr (kk < 3) read_frags(g % STAGES, kk + 1, F[(kk + 1) % 2]);
+                        else read_frags((g + 1) % STAGES, 0, F[0]);
+                    }
+                    if constexpr (ss < L) issue_load(is, ss);
+                    if constexpr (EPI_ON) {
+                        [&]<int... U>(std::integer_sequence<int, U...>) {
+                            ((slot_a<NB>(U) == s ? phase_a(prev, std::integral_constant<int, U>{}) : void()), ...);
+                        }(std::make_integer_sequence<int, NA>{});
+                        if constexpr (slot_b<NB>() == s) phase_b();
+                        [&]<int... R>(std::integer_sequence<int, R...>) {
+                            ((slot_c<NB>(R) == s ? phase_c(prev, std::integral_constant<int, R>{}) : void()), ...);
+                        }(std::make_integer_sequence<int, NC>{});
+                    }
+                    if constexpr (ss == 11) {
+                        // every wave has read stage g % 3 and step g + 1's loads have landed:
+                        // besides them, the queue holds the stores of slots L-1..15 of step g - 1
+                        // and 0..11 of step g and the L loads of step g + 2
+                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                        constexpr int after =
+                            L + (EPI_ON ? stores_in<NB>(st * SPS, st * SPS + 12) +
+                                              (st > 0 ? stores_in<NB>(st * SPS - SPS - 1 + L, st * SPS) : 0)
+                                        : 0);
+                        static_assert(after <= 63, "vmcnt range");
+                        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(after) : "memory");
+                        __builtin_amdgcn_s_barrier();
+                    }
+                    if constexpr (ss == SPS - 1) ++g;
+                    __builtin_amdgcn_sched_barrier(0);
+                }(),
+                ...);
+        }(std::make_integer_sequence<int, SPS * NB>{});
+        etc = ctc;
+        eslot = cslot;
+        ctc = tc_next(ctc);
+        cslot = cslot == NSLOT - 1 ? 0 : cslot + 1;
+    };
+    static_assert(stores_in<NB>(SPS * (NB - 1), SPS * NB) == 0, "the last step of a tile stores nothing");
+    auto final_epi = [&](v16i (&acc)[4]) {
+        epi_begin(etc, eslot);
+        [&]<int... U>(std::integer_sequence<int, U...>) {
+            (phase_a(acc, std::integral_constant<int, U>{}), ...);
+        }(std::make_integer_sequence<int, NA>{});
+        phase_b();
+        [&]<int... R>(std::integer_sequence<int, R...>) {
+            (phase_c(acc, std::integral_constant<int, R>{}), ...);
+        }(std::make_integer_sequence<int, NC>{});
+    };
+
+    v16i accA[4], accB[4];
+    if (ntile > 0) {
+        tile(accA, accB, std::false_type{});
+        int j = 1;
+        for (; j + 1 < ntile; j += 2) {
+            tile(accB, accA, std::true_type{});
+            tile(accA, accB, std::true_type{});
+        }
+        if (j < ntile) {
+            tile(accB, accA, std::true_type{});
+            final_epi(accB);
+        } else {
+            final_epi(accA);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 static int num_cus() {
     static int cus = 0;
     if (!cus) {
@@ -1360,6 +1674,26 @@ static int launch_tv(hipStream_t s, const GemmArgs &p) {
     hipLaunchKernelGGL(kern, dim3(grid), dim3(512), tv::LDS, s, p, tiles_n, (int)tiles);
     return check_hip(hipGetLastError(), "gemm launch");
 }
+template <int NB>
+static int launch_tq(hipStream_t s, const GemmArgs &p) {
+    auto kern = k_gemm_tq<NB>;
+    static bool attr = false;
+    if (!attr) {
+        if (check_hip(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, tq::LDS),
+                      "gemm lds attribute"))
+            return -1;
+        attr = true;
+    }
+    const int tiles_n = p.N / tq::BN;
+    const long tiles = (long)((p.M + tq::BM - 1) / tq::BM) * tiles_n;
+    if (tiles > (1L << 30)) {
+        set_error("gemm: too many tiles");
+        return -1;
+    }
+    const int grid = (int)min(tiles, (long)num_cus());
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), tq::LDS, s, p, tiles_n, (int)tiles);
+    return check_hip(hipGetLastError(), "gemm launch");
+}
 // the overlapped per-token f32 kernel: N a multiple of 128, no bias or clamp, K = 768 or 1152 (the
 // unrolled instantiations); every other per-token call takes k_gemm_t
 static bool use_tv(const GemmArgs &p) {
@@ -1367,9 +1701,20 @@ static bool use_tv(const GemmArgs &p) {
     return !post && p.N % tv::BN == 0 && (p.K == 6 * kQBlock || p.K == 9 * kQBlock);
 }
 
+// E2MI_TQ=0 keeps the per-token requantizing calls on k_gemm_t (A/B measurements)
+static bool use_tq() {
+    static int on = -1;
+    if (on < 0) {
+        const char *e = getenv("E2MI_TQ");
+        on = (e && e[0] == '0') ? 0 : 1;
+    }
+    return on == 1;
+}
+
 template <int EPI>
 static int launch_t(hipStream_t s, const GemmArgs &p) {
     if (EPI == EPI_F32 && use_tv(p)) return p.K == 6 * kQBlock ? launch_tv<6>(s, p) : launch_tv<9>(s, p);
+    if (EPI == EPI_I8Q && use_tv(p) && use_tq()) return p.K == 6 * kQBlock ? launch_tq<6>(s, p) : launch_tq<9>(s, p);
     const bool post = p.bias != nullptr || p.lo > -1e30f || p.hi < 1e30f;
     return post ? launch_t1<EPI, 3>(s, p) : launch_t1<EPI, 0>(s, p);
 }
