@@ -232,3 +232,26 @@ def test_gemm_half_tiles_rounds_bit_exact(gpu, oracle, rng, exact_fold, M, K):
     qo, so = oracle.quantize(yo)
     assert np.array_equal(yq[rows], qo)
     assert np.array_equal(ys[rows].view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,K", [(30000, 1152, 768), (40003, 768, 1152), (20000, 1280, 768),
+                                   (9000, 2304, 1152), (300, 128, 768)])
+def test_gemm_per_token_requant_overlapped(gpu, oracle, rng, M, N, K):
+    """The per-token requantizing kernel that converts, reduces and stores a tile while computing
+    the next (k_gemm_tq: N a multiple of 128, K = 768 or 1152, no bias or clamp), at tile counts that
+    do not divide over the CUs (workgroups walk odd and even numbers of tiles, the last tile's
+    epilogue after the loop), a partial last row block and a single tile: sampled rows' bytes and
+    scales bit-exact with the oracle, rows with outlier scales among them."""
+    import e2mi
+    qa = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    as_ = rng.uniform(0.001, 0.05, (M, 1)).astype(np.float32)
+    as_[rng.integers(0, M, 16)] *= 40.0
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    W = e2mi.DeviceWeight.from_rowmajor(w, ws)
+    yq, ys = e2mi.i8_gemm_tok_q(_t(qa, gpu), _t(as_, gpu), W)
+    rows = _rows(rng, M) if M > 400 else np.arange(M)
+    yo = oracle.i8_gemm(qa[rows], as_[rows], w, ws, block=K)
+    qo, so = oracle.quantize(yo)
+    assert np.array_equal(yq.cpu().numpy()[rows], qo)
+    assert np.array_equal(ys.cpu().numpy()[rows].view(np.uint32), so.view(np.uint32))
