@@ -48,6 +48,65 @@ __global__ __launch_bounds__(256) void k_quant_row(int8_t *__restrict__ q, float
     if (l == 0) sc[m] = s.sc;
 }
 
+// per-128 blocks with one wave per row (K <= 256 NCH): chunk i of lane l holds elements
+// 4 (l + 64 i) .. + 3, i.e. block 2 i + l / 32, so each block's maximum is one half-wave reduction;
+// 16-byte loads, 4-byte stores of whole 128-byte block rows per half-wave
+template <int NCH>
+__global__ __launch_bounds__(256) void k_quant128_r(int8_t *__restrict__ q, float *__restrict__ sc,
+                                                    const float *__restrict__ x, int M, int K,
+                                                    int ldx, int ldq) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (m >= M) return;
+    const float *xr = x + (size_t)m * ldx;
+    const int nb = K / kQBlock;
+    float4 v[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const int k = l * 4 + 256 * i;
+        v[i] = k < K ? *(const float4 *)(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const int k = l * 4 + 256 * i;
+        float a = fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
+        a = group_max<32>(a);
+        if (k < K) {
+            const QScale s = qscale(a);
+            *(uint32_t *)(q + (size_t)m * ldq + k) =
+                pack4(qbyte(v[i].x, s.inv), qbyte(v[i].y, s.inv), qbyte(v[i].z, s.inv), qbyte(v[i].w, s.inv));
+            if ((l & 31) == 0) sc[(size_t)m * nb + 2 * i + (l >> 5)] = s.sc;
+        }
+    }
+}
+
+// the same with the row held in registers (K <= 256 NCH): one read of x instead of two
+template <int NCH>
+__global__ __launch_bounds__(256) void k_quant_row_r(int8_t *__restrict__ q, float *__restrict__ sc,
+                                                     const float *__restrict__ x, int M, int K,
+                                                     int ldx, int ldq) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (m >= M) return;
+    const float *xr = x + (size_t)m * ldx;
+    float4 v[NCH];
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const int k = l * 4 + 256 * i;
+        v[i] = k < K ? *(const float4 *)(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        a = fmaxf(a, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
+    a = group_max<64>(a);
+    const QScale s = qscale(a);
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const int k = l * 4 + 256 * i;
+        if (k < K)
+            *(uint32_t *)(q + (size_t)m * ldq + k) =
+                pack4(qbyte(v[i].x, s.inv), qbyte(v[i].y, s.inv), qbyte(v[i].z, s.inv), qbyte(v[i].w, s.inv));
+    }
+    if (l == 0) sc[m] = s.sc;
+}
+
 int launch_quantize(hipStream_t s, int8_t *q, int ldq, float *scales, const float *x, int M,
                     int K, int ldx, int block) {
     if (M <= 0 || K <= 0 || K % 128 || ldx < K || ldq < K || ldx % 4 || ldq % 4) {
@@ -61,11 +120,22 @@ int launch_quantize(hipStream_t s, int8_t *q, int ldq, float *scales, const floa
     }
     if (block == kQBlock) {
         const long items = (long)M * (K / kQBlock);
-        hipLaunchKernelGGL(k_quant128, dim3((unsigned)((items + 7) / 8)), dim3(256), 0, s, q,
-                           scales, x, M, K, ldx, ldq);
+        const dim3 g((unsigned)((M + 3) / 4));
+        if (K <= 768)
+            hipLaunchKernelGGL(k_quant128_r<3>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq);
+        else if (K <= 1280)
+            hipLaunchKernelGGL(k_quant128_r<5>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq);
+        else
+            hipLaunchKernelGGL(k_quant128, dim3((unsigned)((items + 7) / 8)), dim3(256), 0, s, q,
+                               scales, x, M, K, ldx, ldq);
     } else if (block == K) {
-        hipLaunchKernelGGL(k_quant_row, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, s, q, scales,
-                           x, M, K, ldx, ldq);
+        const dim3 g((unsigned)((M + 3) / 4));
+        if (K <= 768)
+            hipLaunchKernelGGL(k_quant_row_r<3>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq);
+        else if (K <= 1280)
+            hipLaunchKernelGGL(k_quant_row_r<5>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq);
+        else
+            hipLaunchKernelGGL(k_quant_row, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq);
     } else {
         set_error("quantize: block must be 128 or K (got %d, K=%d)", block, K);
         return -1;
