@@ -448,8 +448,10 @@ extern "C" int e2mi_attention_i8_packed(e2mi_stream stream, const float *q32, co
         set_error("attention_i8_packed: too many rows");
         return -1;
     }
-    if (work && (n_work <= 0 || B > 0xffff || H > 0xff || (max_len + 127) / 128 > 127)) {
-        set_error("attention_i8_packed: work list needs n_work > 0, B < 65536, H < 256, max_len < 16257");
+    // a work entry holds the head in 4 bits (b | h << 16 | part << 20 | parts - 1 << 22 | qb << 24,
+    // the f16 kernels' encoding)
+    if (work && (n_work <= 0 || B > 0xffff || H > 0xf || (max_len + 127) / 128 > 127)) {
+        set_error("attention_i8_packed: work list needs n_work > 0, B < 65536, H < 16, max_len < 16257");
         return -1;
     }
     const I8Ws wo = i8_ws(M, B, max_len, H, KV);

@@ -45,6 +45,7 @@
 #include "../../include/e2_dispatch.h"
 #include "common.h"
 #include "model_internal.h"
+#include "plan.h"
 
 namespace e2mi {
 
@@ -109,7 +110,9 @@ struct e2mi_engine {
     // list, the partial states, and an unsplit list for the head_dim-512 layers
     int32_t *work = nullptr, *h_work = nullptr;
     int split_factor = 1;  // the most parts a block of this geometry can take (1: never split)
-    int split_mode = 2;    // 0 never, 1 always, 2 when a chunk's blocks fill less than half the device
+    // 0 never (the default: a sequence's embedding does not depend on its batch-mates, as on the
+    // reference's CPU path), 1 always, 2 when a chunk's blocks fill less than half the device
+    int split_mode = 0;
     bool split_now = false;  // the planned chunk splits (part of the graph key)
     int slots_device = 512;  // attention workgroups the device runs at once (2 per CU)
     int32_t *mwork = nullptr, *h_mwork = nullptr, *work_full = nullptr, *h_work_full = nullptr;
@@ -302,81 +305,11 @@ constexpr int kI8MinKeys = 32;
 // attention workgroups of a packed chunk of n sequences in M rows: at most H (M / 128 + n)
 static int work_slots(const e2mi_engine *g, int n, int M) { return g->cfg.n_heads * (M / 128 + n); }
 
-// split key ranges: a 128-query block whose keys span more than kAttnPartTiles 32-key tiles is
-// split into ceil(tiles / kAttnPartTiles) parts (at most kMaxParts), so the longest blocks no longer
-// set the attention's time alone; the parts depend only on the sequence's own length and the window
+// split key ranges: a 128-query block whose keys span more than 8 tiles of 32 is split into
+// ceil(tiles / 8) parts (at most kMaxAttnParts), so the longest blocks no longer set the
+// attention's time alone; the parts depend only on the sequence's own length and the window
+// (block_parts, plan.cpp). The attention work lists are dealt to the XCDs (xcd_deal, plan.cpp).
 constexpr int kAttnPartTiles = 8, kMaxAttnParts = 4;
-static int attn_parts(const e2mi_engine *g, int L, int q) {
-    if (!g->split_now || g->split_factor <= 1) return 1;
-    const int W = g->cfg.window;
-    int t0 = 0, t1 = (L + 31) / 32;
-    if (W > 0) {
-        const int q0 = q * 128, q1 = std::min(q0 + 127, L - 1);
-        t0 = std::max(q0 - W, 0) / 32;
-        t1 = std::min(std::min(q1 + W, L - 1) / 32 + 1, t1);
-    }
-    const int n = t1 - t0;
-    return std::max(1, std::min({g->split_factor, (n + kAttnPartTiles - 1) / kAttnPartTiles, n}));
-}
-static int32_t work_item(int b, int h, int part, int parts, int qb) {
-    return b | (h << 16) | (part << 20) | ((parts - 1) << 22) | (qb << 24);
-}
-
-// Workgroup i of a 1-D grid runs on XCD i % 8, and each XCD has its own L2. The attention work
-// items of one sequence read the same K and V^T, so they are dealt to one XCD: a sequence's
-// consecutive items are cut into chunks of at most 1/div of an XCD's share of the key tiles, each
-// chunk goes to the least-loaded XCD in list order (longest sequences first), and the XCD queues
-// are interleaved into the grid (a queue that runs dry is filled from the one with most items
-// left). Cost of an item: the key tiles it walks (its part of its block's range, window-aware).
-// Smaller chunks balance the XCDs better, larger ones share more K and V^T in L2: the f16 kernels
-// take div 2 at head_dim 256 (one chunk per sequence at config 4) and 4 at head_dim 512 (one
-// workgroup per CU, fewer slots to balance). The order changes no result: items are independent.
-constexpr int kXcds = 8;
-static int item_tiles(int32_t it, const int32_t *len, int window) {
-    const int b = it & 0xffff, part = (it >> 20) & 3, parts = ((it >> 22) & 3) + 1, q = it >> 24, L = len[b];
-    int t0 = 0, t1 = (L + 31) / 32;
-    if (window > 0) {
-        const int q0 = q * 128, q1 = std::min(q0 + 127, L - 1);
-        t0 = std::max(q0 - window, 0) / 32;
-        t1 = std::min(std::min(q1 + window, L - 1) / 32 + 1, t1);
-    }
-    const int n = t1 - t0;
-    return std::max(1, n * (part + 1) / parts - n * part / parts);
-}
-static void xcd_deal(int32_t *w, int n, const int32_t *len, int window, int div) {
-    if (n <= kXcds) return;
-    long total = 0;
-    for (int i = 0; i < n; i++) total += item_tiles(w[i], len, window);
-    const long lim = std::max(1L, (total + (long)kXcds * div - 1) / ((long)kXcds * div));
-    std::vector<int32_t> q[kXcds];
-    long load[kXcds] = {};
-    for (int i = 0; i < n;) {
-        const int b = w[i] & 0xffff;
-        long c = 0;
-        int j = i;
-        for (; j < n && (w[j] & 0xffff) == b; j++) {
-            const int t = item_tiles(w[j], len, window);
-            if (j > i && c + t > lim) break;
-            c += t;
-        }
-        const int x = (int)(std::min_element(load, load + kXcds) - load);
-        q[x].insert(q[x].end(), w + i, w + j);
-        load[x] += c;
-        i = j;
-    }
-    size_t at[kXcds] = {};
-    for (int k = 0; k < n;) {
-        for (int x = 0; x < kXcds && k < n; x++) {
-            int y = x;
-            if (at[y] == q[y].size()) {
-                y = 0;
-                for (int z = 1; z < kXcds; z++)
-                    if (q[z].size() - at[z] > q[y].size() - at[y]) y = z;
-            }
-            w[k++] = q[y][at[y]++];
-        }
-    }
-}
 
 // every kernel of one forward over B sequences of S tokens (M rows: B * S padded, or the packed
 // row count), on stream s; returns the launch count or -1
@@ -553,70 +486,28 @@ static int validate_batch(const e2mi_engine *g, const int32_t *ids, int batch, i
     return 0;
 }
 
-// rows one sequence takes in a packed chunk: its valid tokens, rounded up to a multiple of 8
-static int seq_rows(const uint8_t *valid, int S) {
-    int len = 0;
-    for (int i = 0; i < S; i++) len += valid ? (valid[i] != 0) : 1;
-    return (len + 7) & ~7;
-}
-
 // the packed layout of n sequences of S tokens (valid: host mask, null = all valid) into the
-// engine's host staging arrays; returns the row count
+// engine's host staging arrays, and the attention work lists; returns the row count
 static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
-    int r = 0;
-    for (int b = 0; b < n; b++) {
-        g->h_start[b] = r;
-        int len = 0;
-        for (int i = 0; i < S; i++)
-            if (!valid || valid[(size_t)b * S + i]) {
-                g->h_rowmap[r + len] = b * S + i;
-                g->h_pos[r + len] = i;
-                len++;
-            }
-        g->h_len[b] = len;
-        const int end = (r + len + 7) & ~7;
-        for (int i = r + len; i < end; i++) g->h_rowmap[i] = -1, g->h_pos[i] = 0;
-        r = end;
-    }
-    const int Mp = (r + 255) & ~255;
-    for (int i = r; i < Mp; i++) g->h_rowmap[i] = -1, g->h_pos[i] = 0;
-    // attention work, longest sequences first: the grid holds more workgroups than the CUs can run
-    // at once, and the last to start should be the short ones
-    std::vector<int> order(n);
-    for (int b = 0; b < n; b++) order[b] = b;
-    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return g->h_len[x] > g->h_len[y]; });
+    const int Mp = pack_rows(valid, n, S, g->h_rowmap, g->h_pos, g->h_start, g->h_len);
     const int H = g->cfg.n_heads, slots = work_slots(g, n, Mp);
     // split long blocks' keys only where the unsplit blocks leave most of the device idle (few
-    // sequences): a full batch's blocks already fill it, and the parts' partial states then cost
-    // more than they balance (config 4: 9460 -> 8115 embeddings/s split; one 2048-token sequence at
-    // the reference geometry: 5.77 -> 4.87 ms)
+    // sequences; mode 2): a full batch's blocks already fill it, and the parts' partial states then
+    // cost more than they balance (config 4: 9460 -> 8115 embeddings/s split; one 2048-token
+    // sequence at the reference geometry: 5.77 -> 4.87 ms)
     long blocks = 0;
     for (int b = 0; b < n; b++) blocks += (long)H * ((g->h_len[b] + 127) / 128);
-    g->split_now = g->split_factor > 1 && (g->split_mode == 1 || (g->split_mode == 2 && 2 * blocks <= g->slots_device));
-    int k = 0, k8 = 0, km = 0, kf = 0;
-    bool any_split = false;
-    for (int b : order) {
-        // text.c:873-875: shorter sequences, and sequences with padding inside (all rows of the
-        // trimmed sequence must be valid), take the f32 path there, the f16 kernel here
-        const int L = g->h_len[b], r0 = g->h_start[b];
-        const bool i8 = g->attn_i8 && L >= kI8MinKeys && g->h_pos[r0] == 0 && g->h_pos[r0 + L - 1] == L - 1;
-        for (int h = 0; h < H; h++)
-            for (int q = 0; q < (g->h_len[b] + 127) / 128; q++) {
-                if (i8) {
-                    g->h_work8[k8++] = work_item(b, h, 0, 1, q);
-                    continue;
-                }
-                const int P = attn_parts(g, L, q);
-                for (int p = 0; p < P; p++) g->h_work[k++] = work_item(b, h, p, P, q);
-                if (P > 1) g->h_mwork[km++] = work_item(b, h, 0, P, q);
-                any_split |= P > 1;
-                if (g->h_work_full) g->h_work_full[kf++] = work_item(b, h, 0, 1, q);
-            }
-    }
-    g->split_now = any_split;  // no block long enough: the unsplit kernel, no merge launch
-    xcd_deal(g->h_work, k, g->h_len, g->cfg.window, 2);
-    if (g->h_work_full) xcd_deal(g->h_work_full, kf, g->h_len, 0, 4);
-    if (g->attn_i8) xcd_deal(g->h_work8, k8, g->h_len, 0, 2);
+    const bool split = g->split_factor > 1 &&
+                       (g->split_mode == 1 || (g->split_mode == 2 && 2 * blocks <= g->slots_device));
+    AttnParams p{H, g->cfg.window, split ? g->split_factor : 1, g->attn_i8, kI8MinKeys, 2};
+    AttnLists o;
+    o.work = g->h_work;
+    o.merge = g->h_mwork;
+    o.work_full = g->h_work_full;
+    o.work8 = g->attn_i8 ? g->h_work8 : nullptr;
+    attention_lists(p, g->h_len, g->h_start, g->h_pos, n, o);
+    g->split_now = o.n_merge > 0;  // no block long enough: the unsplit kernel, no merge launch
+    int k = o.n_work, km = o.n_merge, kf = o.n_full, k8 = o.n_work8;
     while (k < slots * g->split_factor) g->h_work[k++] = -1;
     if (g->h_mwork)
         while (km < slots) g->h_mwork[km++] = -1;
@@ -743,7 +634,7 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
     g->use_graph = !(ng && ng[0] && ng[0] != '0');
     const char *nf = getenv("E2MI_NOFUSE");
     g->fuse_qkv = !(nf && nf[0] && nf[0] != '0');
-    const char *ns = getenv("E2MI_SPLIT");  // 0 | 1 | auto (default)
+    const char *ns = getenv("E2MI_SPLIT");  // 0 (default) | 1 | auto
     if (ns && ns[0]) g->split_mode = ns[0] == '0' ? 0 : ns[0] == '1' ? 1 : 2;
     {
         // the most key tiles a query block can span: the sequence, or the window around the block
@@ -867,24 +758,48 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
 
 extern "C" e2mi_engine *e2mi_create(const e2_model *m) { return e2mi_create_rows(m, 0); }
 
+// the geometry presets of the entries that take no e2_config (callers inside the reference, whose
+// own e2.h defines e2_model and e2_config differently): 0 the BASELINE encoder, 1 the reference
+// checkpoint's; n_layers and vocab > 0 override the preset's
+static int preset_config(const char *who, int geometry, int n_layers, int vocab, e2_config *c) {
+    if ((geometry != 0 && geometry != 1) || n_layers < 0 || vocab < 0) {
+        set_error("%s: geometry %d (0 baseline, 1 reference) or negative override", who, geometry);
+        return -1;
+    }
+    if (geometry == 0) e2_config_baseline(c);
+    else e2_config_reference(c);
+    if (n_layers > 0) c->n_layers = n_layers;
+    if (vocab > 0) c->vocab = vocab;
+    return 0;
+}
+
 // the engine straight from an E8CQ cache, for a caller that links only the e2mi_* names (a backend
 // inside the reference, whose own e2.h and library define e2_model, e2_free and e2_last_error)
 extern "C" e2mi_engine *e2mi_create_e8cq(const char *path, int geometry, int n_layers, int vocab,
                                          int max_rows) {
-    if (!path || (geometry != 0 && geometry != 1) || n_layers < 0 || vocab < 0) {
-        set_error("create_e8cq: null path, geometry %d (0 baseline, 1 reference) or negative override",
-                  geometry);
+    e2_config c;
+    if (!path) {
+        set_error("create_e8cq: null path");
         return nullptr;
     }
-    e2_config c;
-    if (geometry == 0) e2_config_baseline(&c);
-    else e2_config_reference(&c);
-    if (n_layers > 0) c.n_layers = n_layers;
-    if (vocab > 0) c.vocab = vocab;
+    if (preset_config("create_e8cq", geometry, n_layers, vocab, &c)) return nullptr;
     e2_model *m = e2_load_e8cq(path, &c);
     if (!m) return nullptr;
     e2mi_engine *g = e2mi_create_rows(m, max_rows);
     e2_free(m);  // the engine holds its own device copy
+    return g;
+}
+
+// the engine from tensors the caller holds in memory (the reference's e2_model walked by its
+// adapter, e2_hip_create's upload of m->layers[l].q8_* as they are, forward.c:121-183)
+extern "C" e2mi_engine *e2mi_create_tensors(const e2mi_tensor *tensors, int n_tensors, int geometry,
+                                            int n_layers, int vocab, int max_rows) {
+    e2_config c;
+    if (preset_config("create_tensors", geometry, n_layers, vocab, &c)) return nullptr;
+    e2_model *m = model_from_tensors(tensors, n_tensors, c);
+    if (!m) return nullptr;
+    e2mi_engine *g = e2mi_create_rows(m, max_rows);
+    e2_free(m);  // borrowed views only: the engine holds its own device copy
     return g;
 }
 

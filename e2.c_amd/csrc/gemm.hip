@@ -1866,6 +1866,13 @@ int launch_gemm_qkv(hipStream_t s, GemmArgs p) {
         set_error("i8_gemm_qkv: null gamma/table/output pointer or V^T not 8-byte aligned");
         return -1;
     }
+    // the epilogue's buffer-store offsets are 32-bit byte offsets into each output
+    const long widest = (long)p.M * (p.qH > p.qKV ? p.qH : p.qKV) * 256 * ((p.q32 || p.k32 || p.v32) ? 4 : 2);
+    if (widest > 0x7fffffffL) {
+        set_error("i8_gemm_qkv: %d rows of %d heads exceed 2^31 bytes of one output", p.M,
+                  p.qH > p.qKV ? p.qH : p.qKV);
+        return -1;
+    }
     // 128 x 256 tiles: a tile is one head of 128 rows
     return launch_p<128, 256, 4, 2, EPI_QKV>(s, p);
 }

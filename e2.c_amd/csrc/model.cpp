@@ -15,10 +15,11 @@
 #include <vector>
 
 #include "../../include/e2.h"
+#include "../../include/e2mi.h"
 #include "common.h"
 #include "model_internal.h"
 
-struct e2_model {
+struct e2mi_model {
     e2_config cfg;
     std::map<std::string, e2mi::HostQ8W> q8;
     std::map<std::string, e2mi::F32T> f32;
@@ -157,6 +158,11 @@ static bool config_ok(const e2_config &c) {
                   "head_dim 256, H %% KV == 0, 1 <= max_seq <= 2048)");
         return false;
     }
+    // the attention work lists carry the head in 4 bits (b | h << 16 | part << 20 | ... | qb << 24)
+    if (c.n_heads > 15) {
+        set_error("config: at most 15 query heads (the attention work entries hold the head in 4 bits)");
+        return false;
+    }
     if (c.ple_dim < 0 || c.ple_dim % 128 || c.ple_dim > 1280 || c.out_dim < 0 || c.out_dim % 128 ||
         c.out_dim > 1280 || c.window < 0 || c.full_period < 0 || (long)c.n_layers * c.ple_dim > (1 << 20) ||
         (c.full_period > 0 && (c.full_kv_heads <= 0 || c.n_heads % c.full_kv_heads ||
@@ -182,53 +188,66 @@ struct Entry {  // 152 bytes, the reference's q8c_entry
 };
 static_assert(sizeof(Entry) == 152, "E8CQ index entry is 152 bytes");
 
-static bool entry_ok(const Entry &e, uint64_t idx_off, const char *path) {
-    if (!memchr(e.name, 0, sizeof e.name) || !e.name[0]) {
-        set_error("%s: entry with an unterminated or empty name", path);
-        return false;
+// The payload an index entry's kind and dims imply, in bytes (the format: kinds 1 and 2 are dense
+// bf16 / f32 arrays of the product of their dims; kind 3 is a packed int8 weight whose dims are
+// {N, K, blocks of 128 along K, N rounded up to 8} and whose payload is the interleaved bytes
+// [Npad][ceil(K/4) * 4], then Npad f32 scales, then blocks x Npad int32 sums). 0 with a reason when
+// the dims are not those of any valid tensor of that kind.
+static uint64_t implied_bytes(const Entry &e, const char **why) {
+    if (e.kind == KIND_Q8W) {
+        const int64_t N = e.dims[0], K = e.dims[1];
+        const bool shape = N > 0 && K > 0 && N <= (1 << 30) && K <= (1 << 30) &&
+                           e.dims[2] == (K + kQBlock - 1) / kQBlock && e.dims[3] == ((N + 7) & ~7ll);
+        if (!shape) {
+            *why = "packed int8 dims are not {N, K, ceil(K/128), ceil8(N)} with 0 < N, K <= 2^30";
+            return 0;
+        }
+        const uint64_t rows = (uint64_t)e.dims[3], quads = (uint64_t)(K + 3) / 4;
+        return rows * quads * 4 + rows * 4 + (uint64_t)e.dims[2] * rows * 4;
     }
-    if (e.kind < KIND_BF16 || e.kind > KIND_Q8W || e.ndim > 4 || (e.kind == KIND_Q8W && e.ndim != 4)) {
-        set_error("%s: %.64s: bad kind/rank", path, e.name);
-        return false;
-    }
-    for (uint32_t d = 0; d < e.ndim; d++)
+    uint64_t n = e.kind == KIND_BF16 ? 2 : 4;
+    for (uint32_t d = 0; d < e.ndim; d++) {
         if (e.dims[d] < 0) {
-            set_error("%s: %.64s: negative dimension", path, e.name);
-            return false;
+            *why = "a dimension is negative";
+            return 0;
         }
-    if (e.off < 16 || (e.off & 15) || e.off > idx_off || e.nbytes > idx_off - e.off) {
-        set_error("%s: %.64s: blob outside the data area", path, e.name);
+        if (__builtin_mul_overflow(n, (uint64_t)e.dims[d], &n)) {
+            *why = "the dims multiply past 64 bits";
+            return 0;
+        }
+    }
+    return n;
+}
+
+// One index entry, checked before anything reads through it: a usable name, a known kind and rank,
+// a payload placed inside the data area (16-byte aligned, after the header, before the index) and
+// sized exactly as its kind and dims imply.
+static bool entry_ok(const Entry &e, uint64_t idx_off, const char *path) {
+    const void *nul = memchr(e.name, 0, sizeof e.name);
+    if (!nul || nul == e.name) {
+        set_error("%s: index entry without a NUL-terminated name", path);
         return false;
     }
-    if (e.kind != KIND_Q8W) {
-        uint64_t want = e.kind == KIND_BF16 ? 2 : 4;
-        for (uint32_t d = 0; d < e.ndim; d++) {
-            if (e.dims[d] == 0) { want = 0; continue; }
-            if (want > UINT64_MAX / (uint64_t)e.dims[d]) {
-                set_error("%s: %.64s: element count overflows", path, e.name);
-                return false;
-            }
-            want *= (uint64_t)e.dims[d];
-        }
-        if (e.nbytes != want) {
-            set_error("%s: %.64s: blob size is not its element count", path, e.name);
-            return false;
-        }
-        return true;
-    }
-    const int64_t N = e.dims[0], K = e.dims[1];
-    if (N <= 0 || K <= 0 || N > (1 << 30) || K > (1 << 30)) {
-        set_error("%s: %.64s: bad shape", path, e.name);
+    const bool rank_ok = e.kind == KIND_Q8W ? e.ndim == 4 : e.ndim <= 4;
+    if (e.kind < KIND_BF16 || e.kind > KIND_Q8W || !rank_ok) {
+        set_error("%s: %.64s: kind %u with %u dims is not a tensor this format stores", path, e.name, e.kind, e.ndim);
         return false;
     }
-    const int64_t nb = (K + kQBlock - 1) / kQBlock, Npad = (N + 7) & ~7ll;
-    if (e.dims[2] != nb || e.dims[3] != Npad) {
-        set_error("%s: %.64s: packed for another block size/Npad", path, e.name);
+    const uint64_t end = e.off + e.nbytes;
+    if (e.off % 16 || e.off < 16 || end < e.off || end > idx_off) {
+        set_error("%s: %.64s: payload [%llu, +%llu) is not a 16-byte aligned range of the data area", path,
+                  e.name, (unsigned long long)e.off, (unsigned long long)e.nbytes);
         return false;
     }
-    const uint64_t want = (uint64_t)Npad * ((K + 3) / 4) * 4 + (uint64_t)Npad * 4 + (uint64_t)nb * Npad * 4;
+    const char *why = nullptr;
+    const uint64_t want = implied_bytes(e, &why);
+    if (why) {
+        set_error("%s: %.64s: %s", path, e.name, why);
+        return false;
+    }
     if (e.nbytes != want) {
-        set_error("%s: %.64s: blob size mismatch", path, e.name);
+        set_error("%s: %.64s: %llu payload bytes where the dims call for %llu", path, e.name,
+                  (unsigned long long)e.nbytes, (unsigned long long)want);
         return false;
     }
     return true;
@@ -478,6 +497,44 @@ static float bf16f(uint16_t v) {
     return f;
 }
 
+// Every tensor the text tower of geometry `cf` reads is present with its shape (e2.c:306-402 names,
+// q8_shape / norm_len sizes); `who` prefixes the message.
+static bool geometry_ok(const e2_model *m, const e2_config &cf, const char *who) {
+    auto need_f32 = [&](const std::string &name, size_t count) {
+        auto it = m->f32.find(name);
+        if (it == m->f32.end() || it->second.count() != count) {
+            set_error("%s: %s missing or mis-shaped", who, name.c_str());
+            return false;
+        }
+        return true;
+    };
+    auto need_q8 = [&](const std::string &name, int N, int K) {
+        auto it = m->q8.find(name);
+        if (it == m->q8.end() || it->second.N != N || it->second.K != K) {
+            set_error("%s: %s missing or mis-shaped", who, name.c_str());
+            return false;
+        }
+        return true;
+    };
+    if (!need_f32(kEmbed, (size_t)cf.vocab * cf.hidden) || !need_f32(kFinalNorm, (size_t)cf.hidden))
+        return false;
+    if (cf.ple_dim > 0 && (!need_q8(kPleModel, cf.n_layers * cf.ple_dim, cf.hidden) ||
+                           !need_f32(kPleNorm, (size_t)cf.ple_dim)))
+        return false;
+    if (cf.out_dim > 0 && !need_q8(kEmbedProj, cf.out_dim, cf.hidden)) return false;
+    for (int l = 0; l < cf.n_layers; l++) {
+        for (int s = 0; s < n_q8(cf); s++) {
+            int N, K;
+            q8_shape(cf, l, s, &N, &K);
+            if (!need_q8(layer_name(l, kQ8Suffix[s]), N, K)) return false;
+        }
+        for (int s = 0; s < n_norm(cf); s++)
+            if (!need_f32(layer_name(l, kNormSuffix[s]), (size_t)norm_len(cf, l, s))) return false;
+        if (cf.ple_dim > 0 && !need_f32(layer_name(l, kLayerScalar), 1)) return false;
+    }
+    return true;
+}
+
 extern "C" e2_model *e2_load_e8cq(const char *path, const e2_config *c) {
     if (!path || !c || !config_ok(*c)) {
         if (!path || !c) set_error("load_e8cq: null argument");
@@ -554,42 +611,104 @@ extern "C" e2_model *e2_load_e8cq(const char *path, const e2_config *c) {
             }
         }
     }
-    // every tensor of the configured geometry must be present with its shape
-    const e2_config &cf = *c;
-    auto need_f32 = [&](const std::string &name, size_t count) {
-        auto it = m->f32.find(name);
-        if (it == m->f32.end() || it->second.count() != count) {
-            set_error("%s: %s missing or mis-shaped", path, name.c_str());
-            return false;
+    if (!geometry_ok(m, *c, path)) return fail();
+    return m;
+}
+
+namespace e2mi {
+// A model over tensors the caller holds in memory (e2mi_create_tensors): int8 weights and f32
+// tensors are borrowed for the engine's upload, bf16 ones widened to f32 (exact: a bf16 value is the
+// high half of its f32). Checked like a cache: every tensor of the geometry present with its shape.
+e2_model *model_from_tensors(const e2mi_tensor *t, int n, const e2_config &c) {
+    if (!config_ok(c)) return nullptr;
+    if (!t || n <= 0) {
+        set_error("create_tensors: no tensors");
+        return nullptr;
+    }
+    e2_model *m = new (std::nothrow) e2_model();
+    if (!m) {
+        set_error("oom: model");
+        return nullptr;
+    }
+    m->cfg = c;
+    // bf16 tensors are widened only once every shape has been checked: nothing past a shape the
+    // geometry does not expect is ever read
+    std::vector<std::pair<F32T *, const uint16_t *>> widen;
+    try {
+        for (int i = 0; i < n; i++) {
+            const e2mi_tensor &x = t[i];
+            if (!x.name || !x.name[0] || !x.data) {
+                set_error("create_tensors: tensor %d has no name or no data", i);
+                e2_free(m);
+                return nullptr;
+            }
+            if (m->q8.count(x.name) || m->f32.count(x.name)) {
+                set_error("create_tensors: %s given twice", x.name);
+                e2_free(m);
+                return nullptr;
+            }
+            if (x.kind == E2MI_TENSOR_Q8W) {
+                if (x.N <= 0 || x.K <= 0 || x.Npad != ((x.N + 7) & ~7) || !x.scale) {
+                    set_error("create_tensors: %s: int8 weight with N %d, K %d, Npad %d or no scales", x.name,
+                              x.N, x.K, x.Npad);
+                    e2_free(m);
+                    return nullptr;
+                }
+                HostQ8W &w = m->q8[x.name];
+                w.N = x.N;
+                w.K = x.K;
+                w.nb = x.nblocks;
+                w.Npad = x.Npad;
+                w.w = (const int8_t *)x.data;
+                w.scale = x.scale;
+                w.bsq = x.bsq;
+            } else if (x.kind == E2MI_TENSOR_F32 || x.kind == E2MI_TENSOR_BF16) {
+                if (x.N <= 0 || x.K <= 0) {
+                    set_error("create_tensors: %s: %d x %d", x.name, x.N, x.K);
+                    e2_free(m);
+                    return nullptr;
+                }
+                F32T &f = m->f32[x.name];
+                f.ndim = 2;
+                f.dims[0] = x.N;
+                f.dims[1] = x.K;
+                if (x.kind == E2MI_TENSOR_F32) f.p = (const float *)x.data;
+                else widen.push_back({&f, (const uint16_t *)x.data});
+            } else {
+                set_error("create_tensors: %s: kind %d (bf16 1, f32 2, q8w 3)", x.name, x.kind);
+                e2_free(m);
+                return nullptr;
+            }
         }
-        return true;
-    };
-    auto need_q8 = [&](const std::string &name, int N, int K) {
-        auto it = m->q8.find(name);
-        if (it == m->q8.end() || it->second.N != N || it->second.K != K) {
-            set_error("%s: %s missing or mis-shaped", path, name.c_str());
-            return false;
+    } catch (...) {
+        e2_free(m);
+        set_error("oom: create_tensors");
+        return nullptr;
+    }
+    if (!geometry_ok(m, c, "create_tensors")) {
+        e2_free(m);
+        return nullptr;
+    }
+    try {
+        for (auto &w : widen) {
+            F32T &f = *w.first;
+            f.own.resize(f.count());
+            const uint16_t *src = w.second;
+            float *dst = f.own.data();
+            const long cols = (long)f.dims[1];
+            parallel_rows((long)f.dims[0], [=](long r) {
+                for (long j = 0; j < cols; j++) dst[r * cols + j] = bf16f(src[r * cols + j]);
+            });
+            f.p = dst;
         }
-        return true;
-    };
-    if (!need_f32(kEmbed, (size_t)cf.vocab * cf.hidden) || !need_f32(kFinalNorm, (size_t)cf.hidden))
-        return fail();
-    if (cf.ple_dim > 0 && (!need_q8(kPleModel, cf.n_layers * cf.ple_dim, cf.hidden) ||
-                           !need_f32(kPleNorm, (size_t)cf.ple_dim)))
-        return fail();
-    if (cf.out_dim > 0 && !need_q8(kEmbedProj, cf.out_dim, cf.hidden)) return fail();
-    for (int l = 0; l < cf.n_layers; l++) {
-        for (int s = 0; s < n_q8(cf); s++) {
-            int N, K;
-            q8_shape(cf, l, s, &N, &K);
-            if (!need_q8(layer_name(l, kQ8Suffix[s]), N, K)) return fail();
-        }
-        for (int s = 0; s < n_norm(cf); s++)
-            if (!need_f32(layer_name(l, kNormSuffix[s]), (size_t)norm_len(cf, l, s))) return fail();
-        if (cf.ple_dim > 0 && !need_f32(layer_name(l, kLayerScalar), 1)) return fail();
+    } catch (...) {
+        e2_free(m);
+        set_error("oom: create_tensors");
+        return nullptr;
     }
     return m;
 }
+}  // namespace e2mi
 
 // ------------------------------------------------------------------ accessors for the engine
 namespace e2mi {

@@ -1,6 +1,7 @@
 // model_internal.h — the host model's tensor records, shared by model.cpp and forward.cpp.
 #pragma once
 
+#include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -8,6 +9,7 @@
 #include <vector>
 
 #include "../../include/e2.h"
+#include "../../include/e2mi.h"
 
 namespace e2mi {
 
@@ -64,6 +66,9 @@ const char *ple_model_name();
 const char *ple_norm_name();
 const char *embed_proj_name();
 const char *layer_scalar_suffix();
+
+// a model over caller-held tensors (e2mi_create_tensors); NULL with the error set
+e2_model *model_from_tensors(const e2mi_tensor *t, int n, const e2_config &c);
 
 // the engine e2_text_embed* created for a model, owned by it: e2_free calls the destructor
 void **model_engine_slot(e2_model *m);

@@ -44,6 +44,12 @@ class TensorView(C.Structure):
                 ("bsq", _P), ("nbytes", C.c_size_t)]
 
 
+class E2MITensor(C.Structure):
+    """e2mi_tensor (include/e2mi.h): one caller-held tensor under the reference's name."""
+    _fields_ = [("name", C.c_char_p), ("kind", _I), ("N", _I), ("K", _I), ("nblocks", _I), ("Npad", _I),
+                ("data", _P), ("scale", _P), ("bsq", _P)]
+
+
 # name -> (restype, argtypes); every symbol include/*.h declares appears here
 SIGNATURES = {
     "e2mi_last_error": (C.c_char_p, []),
@@ -111,6 +117,9 @@ SIGNATURES = {
     "e2mi_create": (_P, [_P]),
     "e2mi_create_rows": (_P, [_P, _I]),
     "e2mi_create_e8cq": (_P, [C.c_char_p, _I, _I, _I, _I]),
+    "e2mi_create_tensors": (_P, [C.POINTER(E2MITensor), _I, _I, _I, _I, _I]),
+    "e2mi_plan_pack": (_I, [_P, _I, _I, _P, _P, _P, _P]),
+    "e2mi_plan_attention": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, C.POINTER(_I)]),
     "e2mi_destroy": (None, [_P]),
     "e2mi_device": (C.c_char_p, [_P]),
     "e2mi_text_embed": (_I, [_P, _P, _I, _P]),
@@ -446,27 +455,18 @@ def attention(q16, k16, vt16, valid, B, S, H, KV, scale=1.0, want_f32=True, stre
 
 # ---- packed batches (valid tokens only, sequence b in rows [start[b], start[b] + len[b]))
 def pack_plan(valid):
-    """The engine's packed layout of a [B, S] mask: each sequence's valid tokens in order from a
-    row that is a multiple of 8, the total rounded up to 256. Returns (rowmap, pos, start, len, M):
-    rowmap[r] = b * S + s of packed row r (-1 for filler rows), pos[r] = s."""
+    """The engine's packed layout of a [B, S] mask (e2mi_plan_pack): each sequence's valid tokens in
+    order from a row that is a multiple of 8, the total rounded up to 256. Returns (rowmap, pos,
+    start, len, M): rowmap[r] = b * S + s of packed row r (-1 for filler rows), pos[r] = s."""
     import numpy as np
-    valid = np.asarray(valid).astype(bool)
+    valid = np.ascontiguousarray(np.asarray(valid) != 0, np.uint8)
     B, S = valid.shape
-    rowmap, pos, start, lens = [], [], [], []
-    for b in range(B):
-        idx = np.nonzero(valid[b])[0]
-        start.append(len(rowmap))
-        lens.append(len(idx))
-        rowmap += list(b * S + idx)
-        pos += list(idx)
-        pad = (-len(rowmap)) % 8
-        rowmap += [-1] * pad
-        pos += [0] * pad
-    pad = (-len(rowmap)) % 256
-    rowmap += [-1] * pad
-    pos += [0] * pad
-    i32 = lambda v: np.asarray(v, np.int32)
-    return i32(rowmap), i32(pos), i32(start), i32(lens), len(rowmap)
+    cap = B * ((S + 7) & ~7) + 256
+    rowmap, pos = np.empty(cap, np.int32), np.empty(cap, np.int32)
+    start, lens = np.empty(B, np.int32), np.empty(B, np.int32)
+    M = load().e2mi_plan_pack(ptr(valid), B, S, ptr(rowmap), ptr(pos), ptr(start), ptr(lens))
+    check(0 if M > 0 else -1, "plan_pack")
+    return rowmap[:M].copy(), pos[:M].copy(), start, lens, M
 
 
 def qkv_norm_rope_packed(qkv, pos, H, KV, q_gamma, k_gamma, cos_tab, sin_tab, eps=1e-6,
@@ -491,91 +491,33 @@ def work_entry(b, h, part, parts, qb):
     return b | (h << 16) | (part << 20) | ((parts - 1) << 22) | (qb << 24)
 
 
-XCDS = 8
-
-
-def _item_tiles(it, lens, window):
-    b, part, parts, q = it & 0xffff, (it >> 20) & 3, ((it >> 22) & 3) + 1, it >> 24
-    L = int(lens[b])
-    t0, t1 = 0, (L + 31) // 32
-    if window > 0:
-        q0, q1 = q * 128, min(q * 128 + 127, L - 1)
-        t0, t1 = max(q0 - window, 0) // 32, min(min(q1 + window, L - 1) // 32 + 1, t1)
-    n = t1 - t0
-    return max(1, n * (part + 1) // parts - n * part // parts)
-
-
-def xcd_deal(work, lens, window=0, div=2):
-    """The engine's order of an attention work list (forward.cpp xcd_deal): workgroup i runs on XCD
-    i % 8, so each sequence's consecutive items, cut into chunks of at most 1/div of an XCD's share
-    of the key tiles, go to the least-loaded XCD, and the XCD queues are interleaved (a dry queue is
-    filled from the one with most items left). A permutation of `work`."""
+def plan_attention(lens, H, window=0, max_parts=1, div=2):
+    """The engine's attention work list (e2mi_plan_attention): returns (work, merge) as int32 arrays
+    (merge empty when nothing is split)."""
     import numpy as np
-    w = [int(x) for x in work]
-    n = len(w)
-    if n <= XCDS:
-        return np.asarray(w, np.int32)
-    cost = [_item_tiles(it, lens, window) for it in w]
-    lim = max(1, -(-sum(cost) // (XCDS * div)))
-    queues, load = [[] for _ in range(XCDS)], [0] * XCDS
-    i = 0
-    while i < n:
-        b, c, j = w[i] & 0xffff, 0, i
-        while j < n and (w[j] & 0xffff) == b:
-            if j > i and c + cost[j] > lim:
-                break
-            c += cost[j]
-            j += 1
-        x = min(range(XCDS), key=lambda z: (load[z], z))
-        queues[x] += w[i:j]
-        load[x] += c
-        i = j
-    at, out = [0] * XCDS, []
-    while len(out) < n:
-        for x in range(XCDS):
-            if len(out) == n:
-                break
-            y = x
-            if at[y] == len(queues[y]):
-                y = 0
-                for z in range(1, XCDS):
-                    if len(queues[z]) - at[z] > len(queues[y]) - at[y]:
-                        y = z
-            out.append(queues[y][at[y]])
-            at[y] += 1
-    return np.asarray(out, np.int32)
+    lens = np.ascontiguousarray(lens, np.int32)
+    blocks = int(sum((int(L) + 127) // 128 for L in lens))
+    work = np.empty(max(1, H * blocks * max_parts), np.int32)
+    merge = np.empty(max(1, H * blocks), np.int32)
+    nm = C.c_int(0)
+    n = load().e2mi_plan_attention(ptr(lens), len(lens), H, window, max_parts, div, ptr(work), ptr(merge),
+                                   C.byref(nm))
+    check(0 if n >= 0 else -1, "plan_attention")
+    return work[:n].copy(), merge[:nm.value].copy()
 
 
 def attention_work(lens, H, window=0, div=2):
-    """The engine's attention work list for packed sequences of these lengths: one entry per
-    128-query block, longest sequences first, keys unsplit, dealt to the XCDs (xcd_deal; the
-    engine takes div 4 for head_dim 512)."""
-    import numpy as np
-    order = sorted(range(len(lens)), key=lambda b: -int(lens[b]))
-    return xcd_deal([work_entry(b, h, 0, 1, q) for b in order for h in range(H)
-                     for q in range((int(lens[b]) + 127) // 128)], lens, window, div)
+    """The engine's unsplit attention work list for packed sequences of these lengths (one entry per
+    128-query block, longest sequences first, dealt to the XCDs; div 4 at head_dim 512)."""
+    return plan_attention(lens, H, window, 1, div)[0]
 
 
-def attention_split_work(lens, H, parts_of, window=0):
-    """Work and merge lists with split key ranges: parts_of(n_tiles) parts per query block (its
-    key tiles: all of the sequence, or those within the window by packed index, as the kernel
-    computes them)."""
+def attention_split_work(lens, H, max_parts=4, window=0):
+    """Work and merge lists with split key ranges (e2mi_attention_packed_split): merge is [-1] when
+    no block is split."""
     import numpy as np
-    order = sorted(range(len(lens)), key=lambda b: -int(lens[b]))
-    work, merge = [], []
-    for b in order:
-        L = int(lens[b])
-        for h in range(H):
-            for q in range((L + 127) // 128):
-                t0, t1 = 0, (L + 31) // 32
-                if window > 0:
-                    q0, q1 = q * 128, min(q * 128 + 127, L - 1)
-                    t0, t1 = max(q0 - window, 0) // 32, min(min(q1 + window, L - 1) // 32 + 1, t1)
-                P = max(1, min(4, int(parts_of(t1 - t0)), t1 - t0))
-                work += [work_entry(b, h, p, P, q) for p in range(P)]
-                if P > 1:
-                    merge.append(work_entry(b, h, 0, P, q))
-    return xcd_deal(work, lens, window), np.asarray(merge or [-1], np.int32)
+    work, merge = plan_attention(lens, H, window, max_parts)
+    return work, (merge if len(merge) else np.asarray([-1], np.int32))
 
 
 def attention_packed_split(q16, k16, vt16, start, lens, max_len, H, KV, work, merge, window=0, pos=None,
@@ -707,6 +649,58 @@ def gather_ids(ids, rowmap, stream=None):
 
 
 # ---- model container and encoder engine
+Q8_SUFFIXES = ("self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+               "self_attn.o_proj.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight",
+               "ple_block.per_layer_input_gate.weight", "ple_block.per_layer_projection.weight")
+NORM_SUFFIXES = ("input_layernorm.weight", "post_attention_layernorm.weight", "pre_feedforward_layernorm.weight",
+                 "post_feedforward_layernorm.weight", "self_attn.q_norm.weight", "self_attn.k_norm.weight",
+                 "ple_block.post_per_layer_input_norm.weight")
+
+
+def tensor_names(cfg):
+    """The reference's names (e2.c:306-402) of every tensor the text tower of `cfg` reads."""
+    ple = cfg.ple_dim > 0
+    names = ["language_model.embed_tokens.weight", "language_model.norm.weight"]
+    if ple:
+        names += ["language_model.ple.per_layer_model_projection.weight",
+                  "language_model.ple.per_layer_projection_norm.weight"]
+    if cfg.out_dim > 0:
+        names.append("language_model.embedding_projection.weight")
+    for l in range(cfg.n_layers):
+        pre = f"language_model.layers.{l}."
+        names += [pre + s for s in Q8_SUFFIXES[:9 if ple else 7]]
+        names += [pre + s for s in NORM_SUFFIXES[:7 if ple else 6]]
+        if ple:
+            names.append(pre + "layer_scalar")
+    return names
+
+
+def model_tensors(model, table=None):
+    """e2mi_tensor records viewing `model`'s own buffers (no copies; keep the model alive while they
+    are used). `table`, a uint16 bf16 array [vocab][hidden], replaces the f32 token table (the
+    reference holds it in bf16)."""
+    cfg = model.config
+    recs, keep = [], []
+    for name in tensor_names(cfg):
+        v = TensorView()
+        check(load().e2_model_tensor(model.h, name.encode(), C.byref(v)), "model_tensor")
+        bname = name.encode()
+        keep.append(bname)
+        if v.kind == 3:
+            N, K, nb, Npad = (int(d) for d in v.dims)
+            recs.append(E2MITensor(bname, 3, N, K, nb, Npad, v.data, v.scale, v.bsq))
+        elif name == "language_model.embed_tokens.weight" and table is not None:
+            keep.append(table)
+            recs.append(E2MITensor(bname, 1, table.shape[0], table.shape[1], 0, 0, table.ctypes.data, None, None))
+        else:
+            n = v.nbytes // 4
+            rows = int(v.dims[0]) if v.ndim == 2 else 1
+            recs.append(E2MITensor(bname, 2, rows, n // rows, 0, 0, v.data, None, None))
+    arr = (E2MITensor * len(recs))(*recs)
+    arr._keep = keep
+    return arr
+
+
 def baseline_config(**over):
     c = E2Config()
     load().e2_config_baseline(C.byref(c))
@@ -773,14 +767,23 @@ class Model:
 class Engine:
     """An e2mi_engine (include/e2mi.h) on the current device; destroyed with the object."""
 
-    def __init__(self, model: Model, max_rows: int = 0):
-        h = load().e2mi_create_rows(model.h, max_rows)
+    def __init__(self, model: Model, max_rows: int = 0, _handle=None, _cfg=None):
+        h = _handle if _handle is not None else load().e2mi_create_rows(model.h, max_rows)
         if not h:
             raise E2MIError(f"create: {last_error()}")
         self.h = C.c_void_p(h)
-        cfg = model.config
+        cfg = _cfg if _cfg is not None else model.config
         self.hidden = cfg.hidden
         self.dim = cfg.out_dim if cfg.out_dim > 0 else cfg.hidden  # embedding width
+
+    @classmethod
+    def from_tensors(cls, tensors, cfg, geometry: int, max_rows: int = 0):
+        """e2mi_create_tensors over e2mi_tensor records (model_tensors); cfg gives n_layers, vocab
+        and the embedding width."""
+        h = load().e2mi_create_tensors(tensors, len(tensors), geometry, cfg.n_layers, cfg.vocab, max_rows)
+        if not h:
+            raise E2MIError(f"create_tensors: {last_error()}")
+        return cls(None, _handle=h, _cfg=cfg)
 
     @property
     def device(self) -> str:

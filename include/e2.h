@@ -24,7 +24,11 @@
 extern "C" {
 #endif
 
-typedef struct e2_model e2_model;
+/* The reference's handle name over this repository's own model struct (tag e2mi_model, the one
+ * include/e2mi.h names): the reference's struct e2_model (src/model.h:113) is a different layout,
+ * and the engine's entry points take e2mi_model, so a reference model cannot be handed to them by
+ * mistake. A caller holding the reference's model uses e2mi_create_tensors (e2mi.h). */
+typedef struct e2mi_model e2_model;
 
 typedef struct {
     int n_layers;      /* 24 */

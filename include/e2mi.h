@@ -218,12 +218,34 @@ int e2mi_qkv_norm_rope_packed(e2mi_stream stream, const float *qkv, int M, const
                               uint16_t *k16, uint16_t *vt16, float *q32, float *k32, float *v32);
 /* (qkv_norm_rope_packed takes head_dim 256 or 512: the reference checkpoint's full-attention
  * layers have 512, text.c:476.) */
+/* The engine's host-side plan of a packed batch, for callers that run the packed kernels with
+ * their own forward (no reference counterpart: the reference computes every padded row,
+ * text.c:1015-1024). e2mi_plan_pack: sequence b's valid tokens (valid [B][S], nonzero keeps a token,
+ * NULL: all valid) in order in rows [start[b], start[b] + len[b]), each sequence starting on a
+ * multiple of 8 rows, the total rounded up to 256; rowmap[r] = b * S + s of packed row r (-1 for a
+ * filler row), pos[r] = s (0 for fillers). rowmap and pos hold B * ceil8(S) + 256 entries, start
+ * and len B. Returns the packed row count M. */
+int e2mi_plan_pack(const uint8_t *valid, int B, int S, int32_t *rowmap, int32_t *pos, int32_t *start,
+                   int32_t *len);
+/* The attention work list of packed sequences of lengths len[B] (the engine's own list): sequences
+ * longest first, every head h < H, every 128-query block; with max_parts > 1 a block whose key
+ * tiles of 32 (all of the sequence, or those within `window` of the block by packed index) number
+ * n > 8 is split into min(max_parts, ceil(n / 8), n) parts and gets a merge entry (the lists of
+ * e2mi_attention_packed_split; max_parts <= 4). The entries are dealt to the 8 XCDs: a sequence's
+ * consecutive entries, cut into chunks of at most 1/div of an XCD's share of the key tiles, go to
+ * the least-loaded XCD, and workgroup i of the grid runs on XCD i % 8 (the engine: div 2 at
+ * head_dim 256, 4 at 512). work holds H * sum(ceil(len / 128)) * max_parts entries, merge (needed
+ * when max_parts > 1) H * sum(ceil(len / 128)). Returns the number of work entries and sets
+ * *n_merge (may be NULL when max_parts is 1). */
+int e2mi_plan_attention(const int32_t *len, int B, int H, int window, int max_parts, int div,
+                        int32_t *work, int32_t *merge, int *n_merge);
 /* attention of each packed sequence over its own rows (all valid); vt16 [KV][D][M] from
  * e2mi_qkv_norm_rope_packed, seq_len[b] <= max_len, every seq_start a multiple of 8 (the
  * e2mi.pack_plan layout); rows outside every sequence are not written. work (optional, device):
- * n_work entries b | h << 16 | query_block << 24 (128 queries per block), one workgroup each, in
- * the order given (longest sequences first balances the grid), negative entries idle; NULL runs a
- * (query block, head, sequence) grid over max_len. */
+ * n_work entries b | h << 16 | query_block << 24 (128 queries per block; b < 65536, the head in
+ * 4 bits so H < 16 with a work list, query_block < 128), one workgroup each, in the order given
+ * (longest sequences first balances the grid), negative entries idle; NULL runs a (query block,
+ * head, sequence) grid over max_len. */
 int e2mi_attention_packed(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
                           const uint16_t *vt16, int M, const int32_t *seq_start,
                           const int32_t *seq_len, int B, int max_len, int H, int KV, int D,
@@ -264,8 +286,9 @@ int e2mi_attention_packed_split(e2mi_stream stream, const uint16_t *q16, const u
  * (row, head, 128 dims), K per key row and V^T per (sequence, kv head, dim) with the reference's
  * quantizers, scores and context are int8 GEMMs folded per 128-block in the reference's order,
  * the probabilities are quantized per 128-key block. Outputs as e2mi_attention_packed (context
- * quantized per 128 dims for the O projection, optional f32 copy). workspace: device memory of
- * e2mi_attention_i8_workspace_bytes(M, B, max_len, H, KV) bytes, 256-byte aligned. */
+ * quantized per 128 dims for the O projection, optional f32 copy; work entries as there, H < 16).
+ * workspace: device memory of e2mi_attention_i8_workspace_bytes(M, B, max_len, H, KV) bytes,
+ * 256-byte aligned. */
 size_t e2mi_attention_i8_workspace_bytes(int M, int B, int max_len, int H, int KV);
 int e2mi_attention_i8_packed(e2mi_stream stream, const float *q32, const float *k32,
                              const float *v32, int M, const int32_t *seq_start,
@@ -294,15 +317,51 @@ int e2mi_attention(e2mi_stream stream, const uint16_t *q16, const uint16_t *k16,
 
 /* ---- the encoder on the device (e2hip.h:34-64) */
 
-typedef struct e2_model e2_model; /* e2.h */
+/* This repository's model container (include/e2.h names it e2_model there). It is not the
+ * reference's struct e2_model (src/model.h:113): a caller holding the reference's model hands its
+ * tensors over with e2mi_create_tensors below. */
+typedef struct e2mi_model e2mi_model;
 typedef struct e2mi_engine e2mi_engine;
 
 /* Upload the model (int8 weights re-laid out for MFMA, q|k|v concatenated, gate|up interleaved)
  * and allocate a workspace for 32768 token rows (e2_hip_create, hip.c:112-167). `m` may be freed
- * afterwards. NULL (and e2mi_last_error) when there is no gfx950 device or the model is invalid. */
-e2mi_engine *e2mi_create(const e2_model *m);
+ * afterwards. NULL (and e2mi_last_error) when there is no gfx950 device or the model is invalid.
+ * Exported by lib/libe2mi.so only (the backend library exports the two entries below instead). */
+e2mi_engine *e2mi_create(const e2mi_model *m);
 /* Same with an explicit workspace capacity in token rows (>= the model's max_seq). */
-e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows);
+e2mi_engine *e2mi_create_rows(const e2mi_model *m, int max_rows);
+
+/* One tensor of a model held in memory by the caller, under the reference's tensor name
+ * (e2.c:306-402, e.g. "language_model.layers.3.self_attn.q_proj.weight"). kind:
+ *   E2MI_TENSOR_Q8W  the reference's e2_q8w (int8.h:79-92) as it is: data = w, the quad-interleaved
+ *                    [Npad/8][K/4][8][4] bytes (int8.h:14-22); scale = the per-row scales [Npad];
+ *                    N, K, Npad (= N rounded up to 8) and nblocks its fields; bsq is not read (this
+ *                    backend stores activations signed, so no weight-sum correction) and may be NULL;
+ *   E2MI_TENSOR_F32  data = float[rows * cols] (norm scales, the layer scalar: rows = 1);
+ *   E2MI_TENSOR_BF16 data = uint16 bf16[rows * cols] (the token table, e2.c:311-317).
+ * For F32 and BF16, N = rows and K = cols. Same codes as the E8CQ kinds (q8cache.c:1-13). */
+enum { E2MI_TENSOR_BF16 = 1, E2MI_TENSOR_F32 = 2, E2MI_TENSOR_Q8W = 3 };
+typedef struct {
+    const char *name;
+    int kind;
+    int N, K;
+    int nblocks, Npad;
+    const void *data;
+    const float *scale;
+    const int32_t *bsq;
+} e2mi_tensor;
+
+/* The engine from a model held in memory: e2_hip_create(e2_model *m) (e2hip.h:31-35, hip.c:112-167;
+ * forward.c:121-183 uploads m->layers[l].q8_* as they are). The reference-side adapter
+ * (e2.c_amd/integration/e2hip_mi.c) walks its e2_model and lists every text-tower tensor here by
+ * name; the engine
+ * uploads them and borrows nothing, so the arrays may be freed when the call returns (the
+ * reference's create borrows `m` for the engine's life). geometry, n_layers, vocab and max_rows as
+ * in e2mi_create_e8cq. Every tensor of the geometry must be present with its shape (names not
+ * used by the text tower are ignored); NULL with e2mi_last_error otherwise, or when there is no
+ * gfx950 device. */
+e2mi_engine *e2mi_create_tensors(const e2mi_tensor *tensors, int n_tensors, int geometry, int n_layers,
+                                 int vocab, int max_rows);
 /* The engine straight from an E8CQ cache (q8cache.c:242-385 format), for a backend built into the
  * reference, whose own e2.h and library already define e2_model, e2_free and e2_last_error: with
  * lib/libe2mi_backend.so, which exports only the e2mi_* names, the caller needs nothing else.
@@ -353,12 +412,13 @@ int e2mi_stats(e2mi_engine *g, long *calls, long *kernels_last, double *last_ms)
 const char *e2mi_profile_text(const e2mi_engine *g);
 /* Split key ranges in the engine's attention (head_dim-256 layers; e2mi_attention_packed_split): a
  * 128-query block whose keys span more than 8 tiles of 32 is shared out over up to 4 workgroups and
- * merged. mode 0 never, 1 always, 2 (default; E2MI_SPLIT=0|1|auto at creation) only for chunks whose
- * unsplit blocks fill at most half of the device's attention workgroups (few sequences: a single
- * 2048-token document at the reference geometry 5.77 -> 4.87 ms; a full config-4 batch would lose
- * 14 %). Split results differ from unsplit ones by f16 rounding, so with mode 2 a long sequence's
- * embedding can differ between a small batch and a large one; mode 0 keeps them bit-identical. No
- * reference counterpart (the reference has no split). */
+ * merged. mode 0 never (the default), 1 always, 2 only for chunks whose unsplit blocks fill at most
+ * half of the device's attention workgroups (few sequences: a single 2048-token document at the
+ * reference geometry 5.77 -> 4.87 ms; a full config-4 batch would lose 14 %). E2MI_SPLIT=0|1|auto
+ * sets it at creation. Split results differ from unsplit ones by f16 rounding, so under mode 2 a
+ * long sequence's embedding depends on its batch-mates (alone it may split, in a full batch it does
+ * not); modes 0 and 1 keep every sequence's embedding independent of the batch, as the reference's
+ * CPU path is. No reference counterpart (the reference has no split). */
 int e2mi_set_attention_split(e2mi_engine *g, int mode);
 /* Run only the first n layers (0: all) before the final norm and pooling: the reference's
  * E2_HIP_LAYERS bisection knob (forward.c:359-366), for parity checks layer by layer. */

@@ -189,5 +189,13 @@ int rt_identity_layer(int l) {
  * valid (text.c:873-876). */
 int rt_attn_i8(int S) { return e2_attn_pick(e2_cpu_backend(), E2_TOWER_TEXT, S) == E2_ATTN_I8; }
 
+/* Force the reference's text attention kind (e2_attn_override, dispatch.c:139-142): 0 f32, 2 int8,
+ * -1 back to the rule table. */
+void rt_attn_text(int kind) { e2_attn_override(E2_TOWER_TEXT, kind); }
+
+/* The reference's model built by rt_open, for the reference-side adapter (e2hip_mi.c), which walks
+ * it as e2_hip_create does. NULL before rt_open. */
+e2_model *rt_model(void) { return g_m; }
+
 int rt_threads(void) { return e2_nthreads(); }
 const char *rt_cpu(void) { return e2_cpu_name(); }

@@ -22,11 +22,24 @@ def _np(t):
     return t.cpu().numpy()
 
 
-def _engine_rule(n):
-    return -(-n // 8)  # ceil(n / 8): 8 key tiles (256 keys) per part, at most 4 (attention_split_work)
+def _split_work(e2mi, lens, H, parts, window):
+    """The engine's lists (e2mi_plan_attention: ceil(tiles / 8) parts, at most 4), or every block in
+    min(parts, tiles) parts (window 0; the order of the entries changes no result)."""
+    if parts == "engine":
+        return e2mi.attention_split_work(lens, H, 4, window=window)
+    assert window == 0
+    work, merge = [], []
+    for b, L in enumerate(int(x) for x in lens):
+        for h in range(H):
+            for q in range((L + 127) // 128):
+                P = max(1, min(parts, (L + 31) // 32))
+                work += [e2mi.work_entry(b, h, p, P, q) for p in range(P)]
+                if P > 1:
+                    merge.append(e2mi.work_entry(b, h, 0, P, q))
+    return np.asarray(work, np.int32), np.asarray(merge or [-1], np.int32)
 
 
-def _case(gpu, oracle, rng, valid, H, KV, window, scale, parts_of):
+def _case(gpu, oracle, rng, valid, H, KV, window, scale, parts):
     import e2mi
     D = 256
     B, S = valid.shape
@@ -37,7 +50,7 @@ def _case(gpu, oracle, rng, valid, H, KV, window, scale, parts_of):
     q16, k16, v16 = (_t(a, gpu).half() for a in (q, k, v))
     vt16 = v16.reshape(M, KV, D).permute(1, 2, 0).contiguous()
     sd, ld, pd = _t(start, gpu), _t(lens, gpu), _t(pos, gpu)
-    work, merge = e2mi.attention_split_work(lens, H, parts_of, window=window)
+    work, merge = _split_work(e2mi, lens, H, parts, window)
     assert len(merge) > 0 and merge[0] >= 0, "the case must split some block"
     work = np.concatenate([work, np.full(5, -1, np.int32)])
     merge = np.concatenate([merge, np.full(3, -1, np.int32)])
@@ -81,8 +94,7 @@ def test_split_baseline_heads(gpu, oracle, rng, parts):
     valid = np.zeros((6, 512), np.uint8)
     for b, L in enumerate((512, 300, 257, 129, 33, 1)):
         valid[b, :L] = 1
-    rule = _engine_rule if parts == "engine" else (lambda n, P=parts: P)
-    frac = _case(gpu, oracle, rng, valid, 3, 1, 0, 1.0, rule)
+    frac = _case(gpu, oracle, rng, valid, 3, 1, 0, 1.0, parts)
     assert frac > 0.3
 
 
@@ -95,4 +107,4 @@ def test_split_sliding_window(gpu, oracle, rng, holes):
     if holes:
         valid[0, 200:260] = 0
         valid[1, rng.random(S) < 0.2] = 0
-    _case(gpu, oracle, rng, valid, 4, 2, 512, 1.0 / 16, _engine_rule)
+    _case(gpu, oracle, rng, valid, 4, 2, 512, 1.0 / 16, "engine")

@@ -191,9 +191,9 @@ def test_config4_full_size_properties(gpu, rng):
     depth (random-init stacks at scale 1.0 are chaotic, see above); size-independent properties
     instead: every embedding finite and unit-norm, packed and padded-rows forwards bit-identical,
     graph replays bit-identical to the eager first call, and a sample of sequences embedded alone
-    bit-identical to their batch rows (with split key ranges off: a lone long sequence would have
-    its keys split by the default rule, the full batch does not). Split and unsplit attention agree
-    to cosine 0.9999 after one layer, and the default rule splits a lone long sequence."""
+    bit-identical to their batch rows (the default: split key ranges off, so no embedding depends on
+    its batch-mates). Split and unsplit attention agree to cosine 0.9999 after one layer, and the
+    opt-in "auto" rule splits a lone long sequence."""
     import torch
     import e2mi
     cfg = small_config(e2mi, n_layers=24, vocab=262144)
@@ -212,8 +212,6 @@ def test_config4_full_size_properties(gpu, rng):
         eng.embed_batch_device(_t(ids, dev), _t(valid, dev), out)
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy(), first)
-    eng.set_split("off")
-    assert np.array_equal(eng.embed_batch(ids, valid), first)
     eng.set_packing(False)
     try:
         padded = eng.embed_batch(ids, valid)

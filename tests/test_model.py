@@ -165,7 +165,8 @@ def test_e8cq_corruption_refused(e2mi_mod, model, tmp_path):
 
 def test_bad_configs_refused(e2mi_mod):
     for over in (dict(head_dim=128), dict(hidden=700), dict(n_heads=3, n_kv_heads=2), dict(max_seq=4096),
-                 dict(attn_scale=0.0), dict(attn_scale=-1.0), dict(attn_scale=float("inf"))):
+                 dict(attn_scale=0.0), dict(attn_scale=-1.0), dict(attn_scale=float("inf")),
+                 dict(n_heads=16, n_kv_heads=1)):
         with pytest.raises(e2mi_mod.E2MIError):
             e2mi_mod.Model.synthetic(e2mi_mod.baseline_config(n_layers=1, vocab=10, **over), 1)
 
@@ -219,3 +220,43 @@ def test_reference_geometry_tensors_and_e8cq(e2mi_mod, tmp_path):
     # the extras draw from their own streams: the shared tensors match a BASELINE-extras-free model
     plain = e2mi_mod.Model.synthetic(e2mi_mod.reference_config(n_layers=6, vocab=100, ple_dim=0, out_dim=0), 9)
     assert np.array_equal(plain.tensor(lname(2, Q8[4]))[0], m.tensor(lname(2, Q8[4]))[0])
+
+
+def test_tensor_entry_refusals(e2mi_mod):
+    """e2mi_create_tensors checks the caller's tensors before any device work: a missing tensor, a
+    mis-shaped or duplicated one, a bad kind, a null pointer or an unknown geometry is refused with a
+    message (no GPU needed: nothing reaches the device)."""
+    from model_util import reference_small_config
+    e2mi = e2mi_mod
+    m = e2mi.Model.synthetic(reference_small_config(e2mi, n_layers=1, vocab=64), 3)
+    cfg = m.config
+    t = e2mi.model_tensors(m)
+    lib = e2mi.load()
+    q = next(i for i in range(len(t)) if t[i].kind == 3)
+
+    def refused(arr, n, what, geometry=1):
+        assert not lib.e2mi_create_tensors(arr, n, geometry, cfg.n_layers, cfg.vocab, 0)
+        assert what in e2mi.last_error(), e2mi.last_error()
+
+    refused(t, len(t) - 1, "missing")
+    t[q].N += 8
+    t[q].Npad += 8
+    refused(t, len(t), "mis-shaped")
+    t[q].N -= 8
+    refused(t, len(t), "Npad")
+    t[q].Npad -= 8
+    t[q].kind = 7
+    refused(t, len(t), "kind")
+    t[q].kind = 3
+    scale = t[q].scale
+    t[q].scale = None
+    refused(t, len(t), "no scales")
+    t[q].scale = scale
+    dup = (e2mi.E2MITensor * (len(t) + 1))(*t, t[0])
+    refused(dup, len(dup), "twice")
+    refused(t, len(t), "geometry", geometry=5)
+    refused(None, 0, "no tensors")
+    # the complete list passes the checks; without a gfx950 device the engine itself then fails
+    t2 = e2mi.model_tensors(m)
+    if not lib.e2mi_create_tensors(t2, len(t2), 1, cfg.n_layers, cfg.vocab, 0):
+        assert "create_tensors" not in e2mi.last_error(), e2mi.last_error()
