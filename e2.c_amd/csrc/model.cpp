@@ -518,9 +518,17 @@ static bool geometry_ok(const e2_model *m, const e2_config &cf, const char *who)
     };
     if (!need_f32(kEmbed, (size_t)cf.vocab * cf.hidden) || !need_f32(kFinalNorm, (size_t)cf.hidden))
         return false;
-    if (cf.ple_dim > 0 && (!need_q8(kPleModel, cf.n_layers * cf.ple_dim, cf.hidden) ||
-                           !need_f32(kPleNorm, (size_t)cf.ple_dim)))
-        return false;
+    // the PLE projection holds ple_dim rows per layer of the checkpoint; a model run on its first
+    // n_layers layers (the reference's n_layers below 24) reads the first n_layers slices
+    if (cf.ple_dim > 0) {
+        auto it = m->q8.find(kPleModel);
+        if (it == m->q8.end() || it->second.K != cf.hidden || it->second.N % cf.ple_dim ||
+            it->second.N < cf.n_layers * cf.ple_dim) {
+            set_error("%s: %s missing or mis-shaped", who, kPleModel);
+            return false;
+        }
+        if (!need_f32(kPleNorm, (size_t)cf.ple_dim)) return false;
+    }
     if (cf.out_dim > 0 && !need_q8(kEmbedProj, cf.out_dim, cf.hidden)) return false;
     for (int l = 0; l < cf.n_layers; l++) {
         for (int s = 0; s < n_q8(cf); s++) {
