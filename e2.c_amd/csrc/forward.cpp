@@ -647,8 +647,8 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
     const char *dd = getenv("E2MI_DUMP");
     if (dd && dd[0]) {
         g->dump_dir = dd;
-        const char *dc = getenv("E2MI_DUMP_CALL");
-        g->dump_call = dc && atol(dc) > 0 ? atol(dc) : 1;
+        const char *dc = getenv("E2MI_DUMP_CALL");  // a call number (default 1), or "all"
+        g->dump_call = dc && !strcmp(dc, "all") ? -1 : dc && atol(dc) > 0 ? atol(dc) : 1;
     }
     auto fail = [&]() -> e2mi_engine * {
         e2mi_destroy(g);
@@ -900,7 +900,7 @@ static int end_call(e2mi_engine *g, hipStream_t s) {
         prof_flush(g);
         g->prof_rec = false;
     }
-    if (!g->dump_dir.empty() && g->calls == g->dump_call) return dump_workspace(g, s);
+    if (!g->dump_dir.empty() && (g->dump_call < 0 || g->calls == g->dump_call)) return dump_workspace(g, s);
     return 0;
 }
 

@@ -404,7 +404,8 @@ int e2mi_stats(e2mi_engine *g, long *calls, long *kernels_last, double *last_ms)
  * E2_HIP_PROFILE and E2_HIP_DUMP (src/gpu/hip/hip.c:51-108,121,138-139): E2MI_PROFILE=1 runs the
  * engine's first call without a graph, one event pair per launch, and reports per-stage times
  * (printed to stderr as e2h_prof_report prints them, hip.c:88-100); E2MI_DUMP=<dir> writes the
- * workspace of call number E2MI_DUMP_CALL (default 1, its last chunk, its last layer: see
+ * workspace of call number E2MI_DUMP_CALL (default 1; "all": after every call, overwriting; its
+ * last chunk, its last layer: see
  * e2mi_set_layer_limit) to <dir>/e2mi_<name>.<f32|f16|i8|i32> (forward.c:725-759: x, xn, tmp, q16,
  * k16, vt16, ctx_q, ctx_s, out, and for packed batches pos and rowmap). e2mi_profile_text returns the
  * report of the profiled call ("" before it or without E2MI_PROFILE); the text lives as long as the

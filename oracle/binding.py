@@ -70,6 +70,7 @@ class Oracle:
             "or_i8_gemm_acc": (None, [_P, _P, _I, _I, _I, _I, _P]),
             "or_i8_gemm_scalar": (None, [_P, _P, _P, _P, _I, _I, _I, _P]),
             "or_i8_gemm_mt": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _P, _I]),
+            "or_i8_gemm_mt_block": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I]),
             "or_gelu_tanh": (_F, [_F]),
             "or_gelu_mul_quant": (None, [_P, _I, _P, _I, _I, _I, _I, _P, _P]),
             "or_rmsnorm": (None, [_P, _I, _I, _P, _F]),
@@ -158,15 +159,16 @@ class Oracle:
         self.lib.or_i8_gemm_scalar(_ptr(qa), _ptr(as_), _ptr(w), _ptr(ws), M, N, K, _ptr(y))
         return y
 
-    def i8_gemm_mt(self, qa, as_, w, ws, bias=None, nthreads=8):
+    def i8_gemm_mt(self, qa, as_, w, ws, bias=None, nthreads=8, block=128):
+        """The threaded VNNI form of i8_gemm (same fold): blocks of 128, or block = K (per token)."""
         M, K = qa.shape
         N = w.shape[0]
-        if K % 128:
-            raise ValueError("K must be a multiple of 128")
+        if K % block or block % 4:
+            raise ValueError("K must be a multiple of the block, the block of 4")
         y = np.empty((M, N), np.float32)
-        self.lib.or_i8_gemm_mt(_ptr(_need(qa, np.int8)), _ptr(_need(as_, np.float32)),
-                               _ptr(_need(w, np.int8)), _ptr(_need(ws, np.float32)), _ptr(bias),
-                               M, N, K, _ptr(y), nthreads)
+        self.lib.or_i8_gemm_mt_block(_ptr(_need(qa, np.int8)), _ptr(_need(as_, np.float32)),
+                                     _ptr(_need(w, np.int8)), _ptr(_need(ws, np.float32)), _ptr(bias),
+                                     M, N, K, block, _ptr(y), nthreads)
         return y
 
     def quantize_mt(self, x, nthreads=8):

@@ -236,7 +236,7 @@ typedef struct {
     const int32_t *bz;   /* [nb][Np] */
     const float *ws, *bias;
     float *y;
-    int M, N, K, Np, nb;
+    int M, N, K, Np, nb, bq; /* bq: 4-byte groups per activation block (32: blocks of 128) */
 } vnni_task;
 
 static void vnni_cols16(void *arg, int item) {
@@ -252,7 +252,7 @@ static void vnni_cols16(void *arg, int item) {
         for (int b = 0; b < t->nb; b++) {
             __m512i acc[8];
             for (int i = 0; i < 8; i++) acc[i] = _mm512_setzero_si512();
-            for (int k4 = b * 32; k4 < b * 32 + 32; k4++) {
+            for (int k4 = b * t->bq; k4 < b * t->bq + t->bq; k4++) {
                 const __m512i wv = _mm512_loadu_si512(t->wp + ((size_t)k4 * t->Np + n0) * 4);
                 for (int i = 0; i < mm; i++) {
                     int32_t a4;
@@ -273,9 +273,9 @@ static void vnni_cols16(void *arg, int item) {
     }
 }
 
-void or_i8_gemm_mt(const int8_t *qa, const float *as, const int8_t *w, const float *ws,
-                   const float *bias, int M, int N, int K, float *y, int nthreads) {
-    const int Np = (N + 15) & ~15, nb = K / 128;
+void or_i8_gemm_mt_block(const int8_t *qa, const float *as, const int8_t *w, const float *ws,
+                         const float *bias, int M, int N, int K, int block, float *y, int nthreads) {
+    const int Np = (N + 15) & ~15, nb = K / block;
     uint8_t *ab = malloc((size_t)M * K);
     int8_t *wp = calloc((size_t)K * Np, 1);
     int32_t *bz = calloc((size_t)nb * Np, sizeof(int32_t));
@@ -285,13 +285,18 @@ void or_i8_gemm_mt(const int8_t *qa, const float *as, const int8_t *w, const flo
         for (int k = 0; k < K; k++) {
             const int8_t v = w[(size_t)n * K + k];
             wp[((size_t)(k >> 2) * Np + n) * 4 + (k & 3)] = v;
-            bz[(size_t)(k >> 7) * Np + n] += v;
+            bz[(size_t)(k / block) * Np + n] += v;
         }
-    vnni_task t = { ab, as, wp, bz, ws, bias, y, M, N, K, Np, nb };
+    vnni_task t = { ab, as, wp, bz, ws, bias, y, M, N, K, Np, nb, block / 4 };
     or_parallel(vnni_cols16, &t, Np / 16, nthreads);
     free(ab);
     free(wp);
     free(bz);
+}
+
+void or_i8_gemm_mt(const int8_t *qa, const float *as, const int8_t *w, const float *ws,
+                   const float *bias, int M, int N, int K, float *y, int nthreads) {
+    or_i8_gemm_mt_block(qa, as, w, ws, bias, M, N, K, 128, y, nthreads);
 }
 
 typedef struct {

@@ -81,6 +81,10 @@ void or_embed(const float *table, const int32_t *ids, int n, int D, float scale,
 /* ---- a6 at scale: threaded GEMM driver (text.c:275-421) for the CPU baseline */
 void or_i8_gemm_mt(const int8_t *qa, const float *as, const int8_t *w, const float *ws,
                    const float *bias, int M, int N, int K, float *y, int nthreads);
+/* the same with one activation scale per `block` columns (K % block == 0, block % 4 == 0): block = K
+ * is the per-token fold (int8.h:61-70, E2_I8_BLOCK = K) */
+void or_i8_gemm_mt_block(const int8_t *qa, const float *as, const int8_t *w, const float *ws,
+                         const float *bias, int M, int N, int K, int block, float *y, int nthreads);
 void or_quantize_mt(const float *x, int M, int K, int8_t *q, float *scales, int nthreads);
 
 /* ---- a9/a12 + text_forward (text.c:817-984): the BASELINE geometry, or the reference

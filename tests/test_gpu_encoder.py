@@ -126,17 +126,19 @@ def _t(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
-def test_config3_attention_sublayer(setup, rng):
-    """BASELINE config 3 shape family (B x S with padding, QKV 768->1280, q/k norm, RoPE, GQA 3:1,
-    O 768->768), composed from the kernel entry points, vs the oracle's attention sublayer."""
+@pytest.mark.parametrize("B", [4, 32])
+def test_config3_attention_sublayer(setup, rng, B):
+    """BASELINE config 3 (B x S with padding, QKV 768->1280, q/k norm, RoPE, GQA 3:1, O 768->768),
+    composed from the kernel entry points, vs the oracle's attention sublayer; B = 32 x S = 512 with
+    lengths U[64, 512] is the configuration as stated."""
     import torch
     e2mi, o, m, eng, om = setup
     dev = torch.device("cuda:0")
-    B, S = 4, 512
+    S = 512
     x = rng.standard_normal((B * S, 768)).astype(np.float32)
     ids, valid = random_batch(rng, B, S, 1000, min_len=64)
     valid = valid.reshape(-1)
-    want = om.attention_sublayer(0, x, valid, B, S)
+    want = om.attention_sublayer(0, x, valid, B, S, nthreads=16)
     L = om._keep[0][0]
     Wqkv = e2mi.DeviceWeight.from_rowmajor(L["wqkv"], L["sqkv"])
     Wo = e2mi.DeviceWeight.from_rowmajor(L["wo"], L["so"])

@@ -1,5 +1,6 @@
 """Oracle functions pinned by mathematics (closed forms and double-precision evaluation)."""
 import numpy as np
+import pytest
 
 
 def test_rope_table_closed_form(oracle):
@@ -172,3 +173,18 @@ def test_attention_i8_oracle_uniform_closed_form(oracle, rng):
             want[d] = f
         for h in range(H):
             assert np.allclose(got[:, h * D:(h + 1) * D], want[None, :], rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("K,block", [(768, 128), (768, 768), (1152, 1152), (1152, 128)])
+def test_threaded_gemm_equals_scalar_fold(oracle, rng, K, block):
+    """The oracle's threaded VNNI GEMM (the every-row checker at M = 65536) gives the scalar
+    restatement's bits for blocks of 128 and for one block per row, partial row and column tiles
+    included."""
+    M, N = 37, 200
+    qa = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    as_ = rng.uniform(0.001, 0.05, (M, K // block)).astype(np.float32)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    a = oracle.i8_gemm(qa, as_, w, ws, block=block)
+    b = oracle.i8_gemm_mt(qa, as_, w, ws, block=block, nthreads=4)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
