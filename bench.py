@@ -20,6 +20,7 @@ reference's packed (E8CQ-style) blobs and re-laid out on the device at load.
 from __future__ import annotations
 
 import argparse
+import subprocess
 import ctypes as C
 import json
 import os
@@ -177,30 +178,48 @@ def physical_cores():
     return max(1, min(len(cores), 16))
 
 
+def lscpu_summary():
+    """Model name, sockets, cores per socket, threads per core and NUMA nodes from lscpu."""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    keep = ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "CPU(s)", "NUMA node(s)",
+            "CPU max MHz")
+    info = {}
+    for line in out.splitlines():
+        k, _, v = line.partition(":")
+        if k.strip() in keep and k.strip() not in info:
+            info[k.strip()] = v.strip()
+    return info
+
+
 def cpu_baseline(budget_s=12.0):
-    """The reference's e2_i8_gemm_avx512 (oracle/_ref, built from its sources with one activation
-    block per row, E2_I8_BLOCK = K, int8.h:61-70: per-token scales, like the timed sweep) on the
-    host cores, N-split across threads like text.c's gemm_segs, over a bounded sample of the same
-    sweep: M_s = 2048 rows of each shape, f32 output."""
+    """The reference's e2_i8_gemm_avx512 (e2_i8_gemm_vnni without AVX-512 VNNI) on the reference's
+    own worker pool (e2_pool_global_init / e2_parallel, threads.c:143-160,261-282; its thread policy:
+    physical cores within the affinity and cgroup budget), columns claimed in tiles from a shared
+    counter as text.c's GEMM regions do (text.c:297-318,341-406), one region per GEMM: the harness
+    oracle/ref_gemm_pool.c, built with the reference's sources and flags, one activation block per row
+    (E2_I8_BLOCK = K, int8.h:61-70: per-token scales, like the timed sweep). A bounded sample of the
+    sweep: M_s = 2048 rows of each shape, f32 output; 3 warm-up passes, then best and median."""
     sys.path.insert(0, ROOT)
-    from oracle.binding import Oracle, Ref, Q8W
+    from oracle.binding import Oracle, RefGemmPool, Q8W
     flags = cpu_flags()
-    threads = physical_cores()
     Ms = 2048
     rng = np.random.default_rng(7)
-    have_ref = all(os.path.exists(Ref.per_row_path(K)) for K, _ in SHAPES)
-    use_ref = have_ref and {"avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512_vnni"} <= flags
-    kind, which = ("reference", "avx512") if use_ref else ("port", None)
-    if not use_ref and have_ref and "avx_vnni" in flags:
-        kind, which = "reference", "vnni_range"
-    refs = {K: Ref.per_row(K) for K in {k for k, _ in SHAPES}} if kind == "reference" else None
-    orc = Oracle() if refs is None else None
+    have_ref = all(RefGemmPool.available(K) for K, _ in SHAPES)
+    avx512 = {"avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512_vnni"} <= flags
+    use_ref = have_ref and (avx512 or "avx_vnni" in flags)
+    which = 0 if avx512 else 1
+    pools = {K: RefGemmPool(K) for K in {k for k, _ in SHAPES}} if use_ref else None
+    orc = None if use_ref else Oracle()
+    threads = next(iter(pools.values())).threads if pools else physical_cores()
     work = []
     for K, N in SHAPES:
         qa = rng.integers(-127, 128, (Ms, K), dtype=np.int8)
         qb = (qa.view(np.uint8) ^ 0x80).view(np.int8).copy()
         w, ws, wq = packed_weight(rng, N, K)
-        if refs is None:  # the threaded port has per-128 blocks only
+        if not use_ref:  # the threaded port has per-128 blocks only
             as_ = rng.uniform(0.001, 0.05, (Ms, K // 128)).astype(np.float32)
             bsq = np.zeros(1, np.int32)
         else:
@@ -211,78 +230,71 @@ def cpu_baseline(budget_s=12.0):
         wsp[:N] = ws
         wqp = np.concatenate([wq, np.zeros(4 * K * 8, np.int8)])
         y = np.zeros((Ms, N), np.float32)
-        work.append((K, N, qa, qb, as_, w, ws, wqp, wsp, bsq, y))
-
-    def run_shape(item):
-        K, N, qa, qb, as_, w, ws, wqp, wsp, bsq, y = item
-        if refs is None:
-            orc.i8_gemm_mt(qa, as_, w, ws, nthreads=threads)
-            return
         q = Q8W(wqp.ctypes.data, bsq.ctypes.data, wsp.ctypes.data, N, K, 1, N, -1e31, 1e31, 1)
-        fn = getattr(refs[K].lib, f"e2_i8_gemm_{which}")
-        tile = max(16, (N // (threads * 2)) // 16 * 16)
-        ranges = [(a, min(N, a + tile)) for a in range(0, N, tile)]
-        nxt = [0]
-        lock = threading.Lock()
+        work.append((K, N, qa, qb, as_, w, ws, wqp, wsp, bsq, y, q))
 
-        def worker():
-            while True:
-                with lock:
-                    i = nxt[0]
-                    nxt[0] += 1
-                if i >= len(ranges):
-                    return
-                fn(y.ctypes.data_as(C.c_void_p), qb.ctypes.data_as(C.c_void_p),
-                   as_.ctypes.data_as(C.c_void_p), C.byref(q), Ms, N, ranges[i][0], ranges[i][1])
+    def shape_time(item, nthreads=None):
+        K, N, qa, qb, as_, w, ws, wqp, wsp, bsq, y, q = item
+        if pools is None:
+            t0 = time.perf_counter()
+            orc.i8_gemm_mt(qa, as_, w, ws, nthreads=nthreads or threads)
+            return time.perf_counter() - t0
+        return pools[K].timed(which, y, qb, as_, q)
 
-        ts = [threading.Thread(target=worker) for _ in range(threads)]
-        for t in ts:
-            t.start()
-        for t in ts:
-            t.join()
+    def one_pass(nthreads=None):
+        return sum(shape_time(item, nthreads) for item in work)
 
-    for _ in range(3):  # three warm-up passes (text_bench.c:52-80)
-        for item in work:
-            run_shape(item)
+    # shape by shape: each K is its own build of the reference (E2_I8_BLOCK = K) with its own pool,
+    # so one pool works while the other sleeps; a pass is the sum over the four shapes
     ops_per_pass = sum(2.0 * Ms * N * K for K, N, *_ in work)
-    times = []
-    t_start = time.time()
-    while len(times) < 5 or (time.time() - t_start < budget_s and len(times) < 200):
-        t0 = time.perf_counter()
-        for item in work:
-            run_shape(item)
-        times.append(time.perf_counter() - t0)
-    best = min(times)
+    best, med, times = 0.0, 0.0, []
+    for item in work:
+        for _ in range(3):  # three warm-ups (text_bench.c:52-80)
+            shape_time(item)
+        ts, t_start = [], time.time()
+        while len(ts) < 5 or (time.time() - t_start < budget_s / len(work) and len(ts) < 200):
+            ts.append(shape_time(item))
+        best += min(ts)
+        med += float(np.median(ts))
+        times.append(len(ts))
+    if pools:
+        for p in pools.values():
+            p.close()
 
-    def one_core():  # one thread, pinned: the same pass over the four shapes, best of 3
-        nonlocal threads
-        saved, threads = threads, 1
+    def one_core():  # one worker, pinned: the same pass over the four shapes, best of 3
+        if pools is None:
+            return min(one_pass(1) for _ in range(3))
+        ones = {K: RefGemmPool(K, nthreads=1) for K in pools}
+        saved = dict(pools)
+        pools.update(ones)
         try:
-            ts = []
-            for _ in range(3):
-                t0 = time.perf_counter()
-                for item in work:
-                    run_shape(item)
-                ts.append(time.perf_counter() - t0)
-            return min(ts)
+            one_pass()
+            return min(one_pass() for _ in range(3))
         finally:
-            threads = saved
+            pools.update(saved)
+            for p in ones.values():
+                p.close()
     t1, cpu = pinned_one_core(one_core)
+    kernel = ("e2_i8_gemm_avx512" if which == 0 else "e2_i8_gemm_vnni") if pools else "or_i8_gemm_mt"
     return {
         "value": round(ops_per_pass / best / 1e12, 4),
         "unit": "TOPS",
         "cores": threads,
-        "kind": kind,
+        "kind": "reference" if pools else "port",
         "sample": (f"the config-5 sweep on M={Ms} rows per shape (of 65536), f32 output, "
-                   + ("per-token scales (the reference built with E2_I8_BLOCK=K) " if refs else
-                      "per-128 scales (the threaded port; no AVX-512 VNNI per-row build here) ")
-                   + f"(e2_i8_gemm_{which or 'port'} N-split over {threads} threads); best of "
-                   f"{len(times)} passes; median {ops_per_pass / float(np.median(times)) / 1e12:.4f} TOPS"),
-        "kernel": f"e2_i8_gemm_{which}" if which else "or_i8_gemm_mt",
+                   + ("per-token scales (the reference built with E2_I8_BLOCK=K), " if pools else
+                      "per-128 scales (the threaded port: no reference build or no VNNI here), ")
+                   + f"{kernel} on the reference's own pool of {threads} workers, columns claimed in tiles "
+                   f"as text.c's regions do; per shape 3 warm-ups, then best and median of {times} "
+                   "calls, summed over the four shapes"),
+        "best_TOPS": round(ops_per_pass / best / 1e12, 4),
+        "median_TOPS": round(ops_per_pass / med / 1e12, 4),
+        "kernel": kernel,
         "cpu_avx512_vnni": "avx512_vnni" in flags,
         "cpu_model": cpu_model(),
+        "lscpu": lscpu_summary(),
         "single_core": {"value": round(ops_per_pass / t1 / 1e12, 4), "unit": "TOPS",
-                        "sample": f"the same pass on one thread pinned to cpu {cpu}, best of 3"},
+                        "sample": f"the same pass with a one-worker pool pinned to cpu {cpu}, best of 3"},
     }
 
 
@@ -489,28 +501,6 @@ def reference_text_cpu_baseline(model, ids, valid, nseq=8, budget_s=25.0):
                             "sample": f"sequence 0 (length {int(valid_s[0].sum())}), pinned to cpu {cpu}, "
                                       "one-thread pool"},
             "cpu_model": cpu_model(), "unit_norm_ok": unit_ok}
-
-
-def encoder_cpu_baseline(model, ids, valid, nseq=24):
-    """The oracle's text recipe (oracle/e2_oracle_model.c, a C port: VNNI int8 GEMMs, fp32 row-wise
-    attention) on the host cores, over the first nseq sequences of the benchmark batch."""
-    sys.path.insert(0, ROOT)
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    from oracle.binding import Oracle
-    from model_util import oracle_model
-    threads = physical_cores()
-    om = oracle_model(Oracle(), model)
-    t0 = time.perf_counter()
-    om.encode(np.ascontiguousarray(ids[:nseq]), np.ascontiguousarray(valid[:nseq]), nthreads=threads)
-    dt = time.perf_counter() - t0
-    return {"value": round(nseq / dt, 4), "unit": "embeddings/s", "cores": threads, "kind": "port",
-            "sample": f"{nseq} of the {ENC_B} benchmark sequences (lengths {valid[:nseq].sum(1).tolist()}), "
-                      f"24 layers, {dt:.1f} s",
-            "cpu_model": cpu_model(),
-            "note": "the reference's text.c is hard-wired to its checkpoint's geometry (four heads, "
-                    "PLE, embed_proj; text.c:467-478, 906-984), so config 4's geometry runs only in "
-                    "this port (scalar-order int8 GEMMs, f32 row-wise attention); the reference's "
-                    "own CPU path is timed at its geometry under reference_geometry"}
 
 
 # ------------------------------------------------------------------ HBM traffic from PMC runs
@@ -1071,7 +1061,12 @@ def main():
         out["encoder"] = enc
         out["embeddings_per_s"] = enc["embeddings_per_s"]
         if not args.no_cpu_baseline:
-            out["encoder_cpu_baseline"] = encoder_cpu_baseline(model, eids, evalid)
+            out["encoder_cpu_baseline"] = {
+                "see": "reference_geometry.config4_64x512.cpu_baseline",
+                "note": "the reference's text.c is hard-wired to its checkpoint's geometry (four heads, "
+                        "PLE, embed_proj; text.c:467-478, 906-984) and cannot run config 4's; its own "
+                        "CPU path (e2_text_embed_batch on its pool) is timed at its geometry on the same "
+                        "64 x 512 batch shape, beside this engine at that geometry"}
         del model
         out["reference_geometry"] = reference_geometry_bench(
             torch, e2mi, max(5, args.steps // 2), args.warmup, cpu_sample=0 if args.no_cpu_baseline else 8)

@@ -444,6 +444,52 @@ class Ref:
         return out
 
 
+class RefGemmPool:
+    """The reference's int8 GEMM (e2_i8_gemm_avx512, or e2_i8_gemm_vnni without AVX-512 VNNI) on the
+    reference's own worker pool, columns claimed in tiles as text.c's GEMM regions claim them
+    (oracle/ref_gemm_pool.c, built with E2_I8_BLOCK = K: one activation scale per row). One pool
+    per block size; nthreads 0 takes the reference's thread policy (threads.c:177-261)."""
+
+    def __init__(self, K, nthreads=0):
+        path = os.path.join(HERE, "_ref", f"b{K}", "libgemmpool.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        L = self.lib = C.CDLL(path)
+        L.rg_init.argtypes = [_I]
+        L.rg_init.restype = _I
+        L.rg_close.restype = None
+        L.rg_gemm.argtypes = [_I, _P, _P, _P, C.POINTER(Q8W), _I, _I]
+        L.rg_gemm.restype = _I
+        L.rg_pass.argtypes = [_I, _I, _P, _P, _P, _P, _P, _P]
+        L.rg_pass.restype = C.c_double
+        self.K = K
+        self.threads = L.rg_init(nthreads)
+
+    @staticmethod
+    def available(K):
+        return os.path.exists(os.path.join(HERE, "_ref", f"b{K}", "libgemmpool.so"))
+
+    def gemm(self, kind, y, qa_biased, as_, q8w):
+        M, N = y.shape
+        if self.lib.rg_gemm(kind, _ptr(y), _ptr(qa_biased), _ptr(as_), C.byref(q8w), M, N):
+            raise RuntimeError("rg_gemm")
+
+    def timed(self, kind, y, qa_biased, as_, q8w):
+        """Seconds of one GEMM region, timed inside the library."""
+        M, N = y.shape
+        ys, qs, ss = (C.c_void_p * 1)(y.ctypes.data), (C.c_void_p * 1)(qa_biased.ctypes.data), \
+            (C.c_void_p * 1)(as_.ctypes.data)
+        ws = (C.POINTER(Q8W) * 1)(C.pointer(q8w))
+        Ms, Ns = (C.c_int * 1)(M), (C.c_int * 1)(N)
+        t = self.lib.rg_pass(kind, 1, ys, qs, ss, ws, Ms, Ns)
+        if t < 0:
+            raise RuntimeError("rg_pass")
+        return t
+
+    def close(self):
+        self.lib.rg_close()
+
+
 class RefText:
     """The reference's own text tower (text.c, with the rest of the reference library) driven by
     oracle/ref_text.c on a model read from an E8CQ cache of the reference geometry. One model per
