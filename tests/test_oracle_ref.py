@@ -153,3 +153,35 @@ def test_per_row_build_bit_exact(oracle, rng, K):
     # and it differs from the per-128 build's result (the block is really K)
     y128 = oracle.i8_gemm(*oracle.quantize(x), w, ws)
     assert not np.array_equal(y128, y_or)
+
+
+@pytest.mark.parametrize("K,N", [(768, 1152), (1152, 768)])
+def test_pool_harness_matches_oracle(oracle, rng, K, N):
+    """The CPU baseline's harness (oracle/ref_gemm_pool.c: the reference's e2_i8_gemm_avx512 on its
+    own pool, columns claimed in tiles) computes the per-token GEMM the oracle restates, bit for bit,
+    on a partial column tile and a row count the reference pads to 8."""
+    from oracle.binding import Q8W, RefGemmPool
+    if not RefGemmPool.available(K):
+        pytest.skip("oracle/_ref not built")
+    import bench
+    if "avx512_vnni" not in bench.cpu_flags():
+        pytest.skip("no AVX-512 VNNI on this host")
+    M = 136
+    pool = RefGemmPool(K, nthreads=4)
+    try:
+        qa = rng.integers(-127, 128, (M, K), dtype=np.int8)
+        qb = (qa.view(np.uint8) ^ 0x80).view(np.int8).copy()
+        as_ = rng.uniform(0.001, 0.05, (M, 1)).astype(np.float32)
+        w, ws, wq = bench.packed_weight(rng, N, K)
+        bsq = np.zeros(N + 32, np.int32)
+        bsq[:N] = w.astype(np.int32).sum(1)
+        wsp = np.zeros(N + 32, np.float32)
+        wsp[:N] = ws
+        wqp = np.concatenate([wq, np.zeros(4 * K * 8, np.int8)])
+        q = Q8W(wqp.ctypes.data, bsq.ctypes.data, wsp.ctypes.data, N, K, 1, N, -1e31, 1e31, 1)
+        y = np.zeros((M, N), np.float32)
+        pool.gemm(0, y, qb, as_, q)
+        yo = oracle.i8_gemm(qa, as_, w, ws, block=K)
+        assert np.array_equal(y.view(np.uint32), yo.view(np.uint32))
+    finally:
+        pool.close()
