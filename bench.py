@@ -211,7 +211,9 @@ def cpu_baseline(budget_s=12.0):
     avx512 = {"avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512_vnni"} <= flags
     use_ref = have_ref and (avx512 or "avx_vnni" in flags)
     which = 0 if avx512 else 1
-    pools = {K: RefGemmPool(K) for K in {k for k, _ in SHAPES}} if use_ref else None
+    # one worker per physical core, within this box's share (the reference's own policy would also
+    # count cores outside it)
+    pools = {K: RefGemmPool(K, nthreads=physical_cores()) for K in {k for k, _ in SHAPES}} if use_ref else None
     orc = None if use_ref else Oracle()
     threads = next(iter(pools.values())).threads if pools else physical_cores()
     work = []
