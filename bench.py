@@ -768,6 +768,28 @@ def summarize_enc_ktrace(trace_csv):
         for k, v in sorted(stage.items(), key=lambda kv: -np.mean(kv[1])):
             lines.append(f"| `{k[:80]}` | {np.mean(v):.1f} | {100 * np.mean(v) / tot:.1f} | "
                          f"{np.mean(v) / max(nl, 1):.1f} |")
+    # device-entry calls (e2mi_text_embed_batch_device): each starts with the id check (k_check_ids);
+    # before its forward's first kernel: mask read-back, host planning, plan upload, graph launch;
+    # after the forward's last kernel until the next call's id check: output copy, flag read-back,
+    # return to the caller (consecutive calls only: the next one within 2 ms)
+    t = lambda r, k: int(r[k]) / 1e3
+    starts = [i for i, r in enumerate(rows) if "k_check_ids" in name(r)]
+    pre, post = [], []
+    for c, i in enumerate(starts):
+        emb = next((j for j in range(i, len(rows)) if name(rows[j]).startswith("e2mi::k_rows<1")), None)
+        end = next((j for j in range(i, len(rows)) if "k_pool_finish" in name(rows[j])), None)
+        if emb is None or end is None:
+            continue
+        pre.append(t(rows[emb], "Start_Timestamp") - t(rows[i], "Start_Timestamp"))
+        if c + 1 < len(starts):
+            g = t(rows[starts[c + 1]], "Start_Timestamp") - t(rows[end], "End_Timestamp")
+            if 0 <= g < 2000:
+                post.append(g)
+    if pre:
+        q = lambda v: f"median {np.median(v):.0f}, min {min(v):.0f}, max {max(v):.0f}"
+        lines += ["", f"device-entry calls: {len(pre)}; id check to the forward's first kernel (us): {q(pre)}; "
+                  f"forward's last kernel to the next call's id check (us, {len(post)} consecutive pairs): "
+                  + (q(post) if post else "none")]
     text = "\n".join(lines) + "\n"
     print(text)
     return text
