@@ -102,7 +102,11 @@ struct e2mi_engine {
     uint8_t *h_valid = nullptr;
     float *h_out = nullptr;
     // packed batches: per packed row its source index in the chunk (-1 filler) and RoPE position,
-    // per sequence its first row and length (device copies at fixed addresses for the graphs)
+    // per sequence its first row and length, and the attention work lists: regions of one device
+    // buffer (d_plan) and of its pinned staging twin (h_plan), laid out per (sequences, rows) by
+    // plan_layout, so one copy uploads a chunk's plan and every graph of a shape reads it at the
+    // same addresses
+    int32_t *d_plan = nullptr, *h_plan = nullptr;
     int32_t *rowmap = nullptr, *pos = nullptr, *seq_start = nullptr, *seq_len = nullptr;
     int32_t *h_rowmap = nullptr, *h_pos = nullptr, *h_start = nullptr, *h_len = nullptr;
     // attention work list (longest sequences first), a fixed number of slots per (sequences, rows):
@@ -128,8 +132,9 @@ struct e2mi_engine {
     // the stream of the previous call: a call on another stream first waits for it (the calls share
     // the workspace and the pinned staging arrays)
     hipStream_t last_stream = nullptr;
-    // device-side id check of the device entry: the embedding kernel raises d_bad for an id outside
-    // the vocabulary; h_bad is its pinned copy, read once the call's stream has drained
+    // device-side id check of the device entry: the id check and the embedding kernel raise the
+    // flag for an id outside the vocabulary, writing pinned host memory (h_bad; d_bad is its device
+    // address) that the host reads once the call's stream has drained and clears itself
     int *d_bad = nullptr, *h_bad = nullptr;
     bool bad_pending = false;  // a previous asynchronous call's flag still to be read
     bool packed = true;
@@ -160,7 +165,6 @@ int launch_embed_checked(hipStream_t s, const float *table, int vocab, const int
                          const float *gamma, float eps, int M, int D, float *x_out, int8_t *q, float *qs,
                          int *bad_id);
 int launch_zero_f32(hipStream_t s, float *p, long n);
-int launch_zero_flag(hipStream_t s, int *p);
 int launch_check_ids(hipStream_t s, const int32_t *ids, long n, int vocab, int *flag);
 
 template <class T>
@@ -486,9 +490,49 @@ static int validate_batch(const e2mi_engine *g, const int32_t *ids, int batch, i
     return 0;
 }
 
+// The plan's regions for n sequences in Mp packed rows, in int32 units from the start of d_plan /
+// h_plan (each region 256-byte aligned): positions, sequence starts and lengths, the f16 work list
+// (split_factor times the slots), the merge list, the head_dim-512 list, the int8 list, and last the
+// row map (uploaded only by the device entry).
+struct PlanLayout {
+    size_t pos, start, len, work, mwork, work_full, work8, rowmap, end;
+};
+static bool has_full_list(const e2mi_engine *g) { return g->split_factor > 1 && g->cfg.full_period > 0; }
+static PlanLayout plan_layout(const e2mi_engine *g, int n, int Mp) {
+    auto up = [](size_t x) { return (x + 63) & ~(size_t)63; };
+    const size_t slots = (size_t)work_slots(g, n, Mp);
+    PlanLayout L;
+    size_t o = 0;
+    L.pos = o, o = up(o + (size_t)Mp);
+    L.start = o, o = up(o + (size_t)n);
+    L.len = o, o = up(o + (size_t)n);
+    L.work = o, o = up(o + slots * (size_t)g->split_factor);
+    L.mwork = o, o = up(o + (g->split_factor > 1 ? slots : 0));
+    L.work_full = o, o = up(o + (has_full_list(g) ? slots : 0));
+    L.work8 = o, o = up(o + slots);
+    L.rowmap = o, o = up(o + (size_t)Mp);
+    L.end = o;
+    return L;
+}
+static void plan_bind(e2mi_engine *g, const PlanLayout &L) {
+    int32_t *d = g->d_plan, *h = g->h_plan;
+    g->pos = d + L.pos, g->h_pos = h + L.pos;
+    g->seq_start = d + L.start, g->h_start = h + L.start;
+    g->seq_len = d + L.len, g->h_len = h + L.len;
+    g->work = d + L.work, g->h_work = h + L.work;
+    g->mwork = g->split_factor > 1 ? d + L.mwork : nullptr, g->h_mwork = g->split_factor > 1 ? h + L.mwork : nullptr;
+    g->work_full = has_full_list(g) ? d + L.work_full : nullptr;
+    g->h_work_full = has_full_list(g) ? h + L.work_full : nullptr;
+    g->work8 = d + L.work8, g->h_work8 = h + L.work8;
+    g->rowmap = d + L.rowmap, g->h_rowmap = h + L.rowmap;
+}
+
 // the packed layout of n sequences of S tokens (valid: host mask, null = all valid) into the
 // engine's host staging arrays, and the attention work lists; returns the row count
 static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
+    long rows = 0;
+    for (int b = 0; b < n; b++) rows += seq_rows(valid ? valid + (size_t)b * S : nullptr, S);
+    plan_bind(g, plan_layout(g, n, (int)((rows + 255) & ~255L)));
     const int Mp = pack_rows(valid, n, S, g->h_rowmap, g->h_pos, g->h_start, g->h_len);
     const int H = g->cfg.n_heads, slots = work_slots(g, n, Mp);
     // split long blocks' keys only where the unsplit blocks leave most of the device idle (few
@@ -538,25 +582,17 @@ static int chunk_size(const e2mi_engine *g, const uint8_t *valid, int b0, int ba
     return n;
 }
 
-// upload the chunk's packing tables (and, from host ids, its packed ids) on stream s
+// upload the chunk's plan on stream s in one copy (and, from host ids, its packed ids in a second):
+// every region but the row map for host ids, the whole plan for device ids
 static int upload_pack(e2mi_engine *g, int n, int Mp, const int32_t *host_ids, hipStream_t s) {
-    if (host_ids)
+    const PlanLayout L = plan_layout(g, n, Mp);
+    if (host_ids) {
         for (int r = 0; r < Mp; r++) g->h_ids[r] = g->h_rowmap[r] >= 0 ? host_ids[g->h_rowmap[r]] : 0;
-    if ((host_ids && check_hip(hipMemcpyAsync(g->ids, g->h_ids, (size_t)Mp * 4, hipMemcpyHostToDevice, s), "ids H2D")) ||
-        (!host_ids && check_hip(hipMemcpyAsync(g->rowmap, g->h_rowmap, (size_t)Mp * 4, hipMemcpyHostToDevice, s), "rowmap H2D")) ||
-        check_hip(hipMemcpyAsync(g->pos, g->h_pos, (size_t)Mp * 4, hipMemcpyHostToDevice, s), "pos H2D") ||
-        check_hip(hipMemcpyAsync(g->seq_start, g->h_start, (size_t)n * 4, hipMemcpyHostToDevice, s), "start H2D") ||
-        check_hip(hipMemcpyAsync(g->seq_len, g->h_len, (size_t)n * 4, hipMemcpyHostToDevice, s), "len H2D") ||
-        check_hip(hipMemcpyAsync(g->work, g->h_work, (size_t)work_slots(g, n, Mp) * g->split_factor * 4,
-                                 hipMemcpyHostToDevice, s), "work H2D") ||
-        (g->mwork && check_hip(hipMemcpyAsync(g->mwork, g->h_mwork, (size_t)work_slots(g, n, Mp) * 4,
-                                              hipMemcpyHostToDevice, s), "merge work H2D")) ||
-        (g->work_full && check_hip(hipMemcpyAsync(g->work_full, g->h_work_full, (size_t)work_slots(g, n, Mp) * 4,
-                                                  hipMemcpyHostToDevice, s), "full-layer work H2D")) ||
-        (g->attn_i8 && check_hip(hipMemcpyAsync(g->work8, g->h_work8, (size_t)work_slots(g, n, Mp) * 4,
-                                                hipMemcpyHostToDevice, s), "int8 work H2D")))
-        return -1;
-    return 0;
+        if (check_hip(hipMemcpyAsync(g->ids, g->h_ids, (size_t)Mp * 4, hipMemcpyHostToDevice, s), "ids H2D"))
+            return -1;
+    }
+    const size_t count = host_ids ? L.rowmap : L.end;
+    return check_hip(hipMemcpyAsync(g->d_plan, g->h_plan, count * 4, hipMemcpyHostToDevice, s), "plan H2D");
 }
 
 // switch the int8 attention on or off; its buffers (f32 q/k/v, the quantized operands, a second
@@ -578,9 +614,7 @@ static int set_attention_i8(e2mi_engine *g, bool on) {
         const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
         const size_t wsb = e2mi_attention_i8_workspace_bytes(g->R, g->bmax, c.max_seq, c.n_heads, c.n_kv_heads);
         if (dalloc(g, &g->q32, R * qd) || dalloc(g, &g->k32, R * kvd) || dalloc(g, &g->v32, R * kvd) ||
-            dalloc(g, &g->i8ws, wsb) || dalloc(g, &g->work8, (size_t)c.n_heads * (R / 128 + g->bmax)) ||
-            check_hip(hipHostMalloc((void **)&g->h_work8, (size_t)c.n_heads * (R / 128 + g->bmax) * 4),
-                      "pinned int8 work"))
+            dalloc(g, &g->i8ws, wsb))
             return -1;
     }
     g->attn_i8 = on;
@@ -601,8 +635,7 @@ extern "C" void e2mi_destroy(e2mi_engine *g) {
     if (g->h_ids) (void)hipHostFree(g->h_ids);
     if (g->h_valid) (void)hipHostFree(g->h_valid);
     if (g->h_out) (void)hipHostFree(g->h_out);
-    for (int32_t *p : {g->h_rowmap, g->h_pos, g->h_start, g->h_len, g->h_work, g->h_work8, g->h_mwork, g->h_work_full})
-        if (p) (void)hipHostFree(p);
+    if (g->h_plan) (void)hipHostFree(g->h_plan);
     if (g->h_mask) (void)hipHostFree(g->h_mask);
     if (g->h_bad) (void)hipHostFree(g->h_bad);
     if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
@@ -715,31 +748,18 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         dalloc(g, &g->ids, R) || dalloc(g, &g->valid, R) || dalloc(g, &g->out, R * g->dout) ||
         dalloc(g, &g->pool_ws, (R / 64 + R + 64) * (size_t)(g->dout + 1)) ||
         (c.ple_dim > 0 && dalloc(g, &g->ple32, R * c.n_layers * c.ple_dim)) ||
-        dalloc(g, &g->rowmap, R) || dalloc(g, &g->pos, R) || dalloc(g, &g->seq_start, (size_t)g->bmax) ||
-        dalloc(g, &g->seq_len, (size_t)g->bmax) ||
-        dalloc(g, &g->work, (size_t)c.n_heads * (R / 128 + g->bmax) * g->split_factor) || dalloc(g, &g->d_bad, 1) ||
-        (g->split_factor > 1 &&
-         (dalloc(g, &g->mwork, (size_t)c.n_heads * (R / 128 + g->bmax)) ||
-          dalloc(g, &g->part, e2mi_attention_part_bytes(R, c.n_heads, 256) / 4 + 64) ||
-          (c.full_period > 0 && dalloc(g, &g->work_full, (size_t)c.n_heads * (R / 128 + g->bmax))))))
+        dalloc(g, &g->d_plan, plan_layout(g, g->bmax, (int)R).end) ||
+        (g->split_factor > 1 && dalloc(g, &g->part, e2mi_attention_part_bytes(R, c.n_heads, 256) / 4 + 64)))
         return fail();
     if (check_hip(hipHostMalloc((void **)&g->h_ids, R * 4), "pinned ids") ||
         check_hip(hipHostMalloc((void **)&g->h_valid, R), "pinned valid") ||
         check_hip(hipHostMalloc((void **)&g->h_out, (size_t)g->bmax * g->dout * 4), "pinned out") ||
-        check_hip(hipHostMalloc((void **)&g->h_rowmap, R * 4), "pinned rowmap") ||
-        check_hip(hipHostMalloc((void **)&g->h_pos, R * 4), "pinned pos") ||
-        check_hip(hipHostMalloc((void **)&g->h_start, (size_t)g->bmax * 4), "pinned start") ||
-        check_hip(hipHostMalloc((void **)&g->h_len, (size_t)g->bmax * 4), "pinned len") ||
-        check_hip(hipHostMalloc((void **)&g->h_work, (size_t)c.n_heads * (R / 128 + g->bmax) * g->split_factor * 4),
-                  "pinned work") ||
-        (g->mwork && check_hip(hipHostMalloc((void **)&g->h_mwork, (size_t)c.n_heads * (R / 128 + g->bmax) * 4),
-                               "pinned merge work")) ||
-        (g->work_full && check_hip(hipHostMalloc((void **)&g->h_work_full, (size_t)c.n_heads * (R / 128 + g->bmax) * 4),
-                                   "pinned full-layer work")) ||
-        check_hip(hipHostMalloc((void **)&g->h_bad, 4), "pinned flag"))
+        check_hip(hipHostMalloc((void **)&g->h_plan, plan_layout(g, g->bmax, (int)R).end * 4), "pinned plan") ||
+        check_hip(hipHostMalloc((void **)&g->h_bad, 4, hipHostMallocMapped | hipHostMallocCoherent), "pinned flag") ||
+        check_hip(hipHostGetDevicePointer((void **)&g->d_bad, g->h_bad, 0), "flag device address"))
         return fail();
     *g->h_bad = 0;
-    if (launch_zero_flag(g->stream, g->d_bad)) return fail();
+    plan_bind(g, plan_layout(g, g->bmax, (int)R));
     // filler rows of packed batches read contexts that no attention writes: start them at zero
     if (check_hip(hipMemsetAsync(g->cq, 0, R * qd, g->stream), "clear ctx") ||
         check_hip(hipMemsetAsync(g->cs, 0, R * (qd / 128) * 4, g->stream), "clear ctx scales"))
@@ -988,7 +1008,7 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
     // ids are checked on the device, masked positions included (the embedding kernel also raises
     // the flag); the flag is read once the stream drains: at the end of this call, or at the next
     // call when the caller passes a stream
-    if (launch_zero_flag(s, g->d_bad) || launch_check_ids(s, ids, (long)rows, g->cfg.vocab, g->d_bad)) return -1;
+    if (launch_check_ids(s, ids, (long)rows, g->cfg.vocab, g->d_bad)) return -1;
     if (!g->packed) {
         if ((long)batch * seq_len > g->R) {
             set_error("text_embed_batch_device: %d x %d rows exceed the engine's %d-row workspace",
@@ -1033,7 +1053,6 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
             if (b0 < batch && check_hip(hipStreamSynchronize(s), "chunk sync")) return -1;
         }
     }
-    if (check_hip(hipMemcpyAsync(g->h_bad, g->d_bad, 4, hipMemcpyDeviceToHost, s), "flag D2H")) return -1;
     if (stream) {
         g->bad_pending = true;
     } else {

@@ -404,7 +404,6 @@ __global__ __launch_bounds__(256) void k_pool_finish(const float *__restrict__ p
 __global__ __launch_bounds__(256) void k_zero_f32(float *__restrict__ p, long n) {
     for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) p[i] = 0.f;
 }
-__global__ void k_zero_i32(int *p) { *p = 0; }
 // raise *flag when any of n ids lies outside [0, vocab) (masked positions included, e2.h:31-32)
 __global__ __launch_bounds__(256) void k_check_ids(const int32_t *__restrict__ ids, long n, int vocab, int *flag) {
     bool bad = false;
@@ -562,10 +561,6 @@ int launch_check_ids(hipStream_t s, const int32_t *ids, long n, int vocab, int *
     const long blocks = std::min((n + 255) / 256, 1024L);
     hipLaunchKernelGGL(k_check_ids, dim3((unsigned)blocks), dim3(256), 0, s, ids, n, vocab, flag);
     return check_hip(hipGetLastError(), "id check launch");
-}
-int launch_zero_flag(hipStream_t s, int *p) {
-    hipLaunchKernelGGL(k_zero_i32, dim3(1), dim3(1), 0, s, p);
-    return check_hip(hipGetLastError(), "flag clear launch");
 }
 }  // namespace e2mi
 
