@@ -320,26 +320,34 @@ __global__ __launch_bounds__(256) void k_gelu_mul_quant(float *__restrict__ gate
 }
 
 // ---- masked mean pool + L2: partial sums per (sequence, 64-row chunk), then a finishing pass
+// rows are added in order, r0 .. r1 - 1, eight at a time: the eight loads are issued before the
+// first addition, so a thread keeps eight 16-byte loads in flight instead of one
+constexpr int kPoolBatch = 8;
 __global__ __launch_bounds__(256) void k_pool_partial(const float *__restrict__ x,
                                                       const uint8_t *__restrict__ valid, int S,
                                                       int D, int chunks, float *__restrict__ part,
                                                       int *__restrict__ cnt) {
     const int b = blockIdx.x / chunks, ch = blockIdx.x % chunks;
     const int r0 = ch * 64, r1 = min(S, r0 + 64);
-    int n = 0;
     for (int c = threadIdx.x; c < D / 4; c += blockDim.x) {
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        n = 0;
-        for (int r = r0; r < r1; r++) {
-            if (!valid[(size_t)b * S + r]) continue;
-            const float4 v = ld4(x + ((size_t)b * S + r) * D + 4 * c);
-            acc = make_float4(acc.x + v.x, acc.y + v.y, acc.z + v.z, acc.w + v.w);
-            n++;
+        for (int rb = r0; rb < r1; rb += kPoolBatch) {
+            float4 v[kPoolBatch];
+            bool keep[kPoolBatch];
+#pragma unroll
+            for (int i = 0; i < kPoolBatch; i++) {
+                const int r = rb + i;
+                keep[i] = r < r1 && valid[(size_t)b * S + r];
+                v[i] = keep[i] ? ld4(x + ((size_t)b * S + r) * D + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int i = 0; i < kPoolBatch; i++)
+                if (keep[i]) acc = make_float4(acc.x + v[i].x, acc.y + v[i].y, acc.z + v[i].z, acc.w + v[i].w);
         }
         st4(part + ((size_t)b * chunks + ch) * D + 4 * c, acc);
     }
     if (threadIdx.x == 0) {
-        n = 0;
+        int n = 0;
         for (int r = r0; r < r1; r++) n += valid[(size_t)b * S + r] != 0;
         cnt[b * chunks + ch] = n;
     }
@@ -357,9 +365,14 @@ __global__ __launch_bounds__(256) void k_pool_partial_packed(const float *__rest
     const size_t base = (size_t)start[b];
     for (int c = threadIdx.x; c < D / 4; c += blockDim.x) {
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int r = r0; r < r1; r++) {
-            const float4 v = ld4(x + (base + r) * D + 4 * c);
-            acc = make_float4(acc.x + v.x, acc.y + v.y, acc.z + v.z, acc.w + v.w);
+        for (int rb = r0; rb < r1; rb += kPoolBatch) {
+            float4 v[kPoolBatch];
+#pragma unroll
+            for (int i = 0; i < kPoolBatch; i++)
+                v[i] = rb + i < r1 ? ld4(x + (base + rb + i) * D + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int i = 0; i < kPoolBatch; i++)
+                if (rb + i < r1) acc = make_float4(acc.x + v[i].x, acc.y + v[i].y, acc.z + v[i].z, acc.w + v[i].w);
         }
         st4(part + ((size_t)b * chunks + ch) * D + 4 * c, acc);
     }
