@@ -451,18 +451,31 @@ __device__ inline float rms_inv256(float ss, float eps) {
 //  3. q/k: x = (y * inv) * gamma, then a' = a c - b s, b' = b c + a s (products rounded, then the
 //     sum; kernels.c:112-126), f16; v: y * inv, f16, stored transposed per sequence.
 // scr: 3 x 8 x 32 words of the step's free A|W stage (partial sums, inverse rms, positions).
+// The kernel's own GemmArgs (its first argument, at the start of the kernel-argument segment), read
+// through a pointer the compiler cannot follow back to the kernel's entry: the fields read through it
+// are loaded (s_load) where they are used instead of being held in SGPRs across the K loop. The
+// fused q|k|v kernel needs eleven pointers and five scalars in its epilogue only; held for the
+// whole kernel they pushed it past the SGPR file (41 SGPRs spilled).
+typedef const __attribute__((address_space(4))) GemmArgs *KernArgs;
+__device__ __attribute__((always_inline)) inline KernArgs kernel_args() {
+    KernArgs a = (KernArgs)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(a));
+    return a;
+}
+
 template <bool FAST>
-__device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmArgs &p, float (&f)[4][16],
+__device__ __attribute__((always_inline)) inline void p_epilogue_qkv(KernArgs pa, float (&f)[4][16],
                                                                      const float (&wsr)[4], int m0, int n0,
                                                                      int wave, int wm, int wn, int lane,
                                                                      float *scr) {
+    const KernArgs p = pa;
     if constexpr (FAST) {
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int r = 0; r < 16; r++) f[t][r] = __fmul_rn(f[t][r], wsr[t]);
     }
-    const int hd = n0 >> 8, nqk = p.qH + p.qKV;
+    const int hd = n0 >> 8, nqk = p->qH + p->qKV;
     const int hh = lane >> 5, c = lane & 31;
     // 1. register r = 4 g + j holds row 8 g + 4 hh + j of the wave's 32
     float s16[16], s8[8], s4[4], s2[2], s1[1];
@@ -484,7 +497,7 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmA
     if ((lane & 1) == 0) xs[wave * 32 + rw] = part;
     __syncthreads();
     // 2. the two waves add the same two partial sums (addition commutes: both get the same inv)
-    const float inv = rms_inv256(part + xs[(wm * 2 + (wn ^ 1)) * 32 + rw], p.eps);
+    const float inv = rms_inv256(part + xs[(wm * 2 + (wn ^ 1)) * 32 + rw], p->eps);
     if ((lane & 1) == 0) xi[wave * 32 + rw] = inv;
     // 3. four rows at a time (registers 4 g .. 4 g + 3, rows rb + 8 g + 0..3), their inv read back
     // from LDS (LDS operations of one wave complete in order: the reads see this wave's writes);
@@ -492,14 +505,14 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmA
     const int rb = m0 + wm * 32 + 4 * hh;
     typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
     if (hd < nqk) {
-        const bool isq = hd < p.qH;
-        const int hq = isq ? hd : hd - p.qH, ld = (isq ? p.qH : p.qKV) * 256;
-        const float *gam = isq ? p.q_gamma : p.k_gamma;
+        const bool isq = hd < p->qH;
+        const int hq = isq ? hd : hd - p->qH, ld = (isq ? p->qH : p->qKV) * 256;
+        const float *gam = isq ? p->q_gamma : p->k_gamma;
         const __amdgpu_buffer_rsrc_t r16 =
-            __builtin_amdgcn_make_buffer_rsrc(isq ? p.q16 : p.k16, 0, (int)min((long)p.M * ld * 2, 0x7fffffffL), 0x00020000);
-        float *o32 = isq ? p.q32 : p.k32;
+            __builtin_amdgcn_make_buffer_rsrc(isq ? p->q16 : p->k16, 0, (int)min((long)p->M * ld * 2, 0x7fffffffL), 0x00020000);
+        float *o32 = isq ? p->q32 : p->k32;
         const __amdgpu_buffer_rsrc_t r32 =
-            __builtin_amdgcn_make_buffer_rsrc(o32, 0, o32 ? (int)min((long)p.M * ld * 4, 0x7fffffffL) : 0, 0x00020000);
+            __builtin_amdgcn_make_buffer_rsrc(o32, 0, o32 ? (int)min((long)p->M * ld * 4, 0x7fffffffL) : 0, 0x00020000);
         const int i0 = wn * 64 + c;  // tiles t = 0, 1: dimensions i0 + 32 t and i0 + 32 t + 128
         const float g00 = gam[i0], g01 = gam[i0 + 128], g10 = gam[i0 + 32], g11 = gam[i0 + 160];
         // the 16 rows' positions, then per group of 4 rows its 16 table entries, each batch of
@@ -508,8 +521,8 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmA
         // the wave's 32 row positions go through LDS (lane l < 32: row wm * 32 + l)
         int *xp = (int *)(scr + 2 * 8 * 32) + wave * 32;
         if (lane < 32) {
-            const int m = min(m0 + wm * 32 + lane, p.M - 1);
-            xp[lane] = p.pos ? p.pos[m] : m % p.qS;
+            const int m = min(m0 + wm * 32 + lane, p->M - 1);
+            xp[lane] = p->pos ? p->pos[m] : m % p->qS;
         }
 #pragma unroll
         for (int g = 0; g < 4; g++) {
@@ -521,8 +534,8 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmA
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
                     const size_t e = (size_t)pg[jj] * 256 + i0 + 32 * t;
-                    cv[jj][t] = p.cs[e];
-                    sv[jj][t] = p.sn[e];
+                    cv[jj][t] = p->cs[e];
+                    sv[jj][t] = p->sn[e];
                 }
             const float4 i4 = *(const float4 *)(xi + wave * 32 + 8 * g + 4 * hh);
             const float ivg[4] = {i4.x, i4.y, i4.z, i4.w};
@@ -546,11 +559,11 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmA
             }
         }
     } else {
-        const int vh = hd - nqk, S = p.qS, ld32 = p.qKV * 256;
+        const int vh = hd - nqk, S = p->qS, ld32 = p->qKV * 256;
         const bool fast = S % 4 == 0;
-        float *o32 = p.v32;
+        float *o32 = p->v32;
         const __amdgpu_buffer_rsrc_t r32 =
-            __builtin_amdgcn_make_buffer_rsrc(o32, 0, o32 ? (int)min((long)p.M * ld32 * 4, 0x7fffffffL) : 0, 0x00020000);
+            __builtin_amdgcn_make_buffer_rsrc(o32, 0, o32 ? (int)min((long)p->M * ld32 * 4, 0x7fffffffL) : 0, 0x00020000);
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             const float4 i4 = *(const float4 *)(xi + wave * 32 + 8 * g + 4 * hh);
@@ -562,17 +575,17 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(const GemmA
                 float x[4];
 #pragma unroll
                 for (int jj = 0; jj < 4; jj++) x[jj] = __fmul_rn(f[t][4 * g + jj], ivg[jj]);
-                if (fast && m + 3 < p.M) {
+                if (fast && m + 3 < p->M) {
                     // four consecutive positions of one sequence: one 8-byte store
-                    uint16_t *dst = p.vt16 + ((size_t)((m / S) * p.qKV + vh) * 256 + d) * S + m % S;
+                    uint16_t *dst = p->vt16 + ((size_t)((m / S) * p->qKV + vh) * 256 + d) * S + m % S;
                     *(u32x2v *)dst = (u32x2v){(uint32_t)f2h_rn(x[0]) | ((uint32_t)f2h_rn(x[1]) << 16),
                                               (uint32_t)f2h_rn(x[2]) | ((uint32_t)f2h_rn(x[3]) << 16)};
                 } else {
 #pragma unroll
                     for (int jj = 0; jj < 4; jj++) {
                         const int mm = m + jj;
-                        if (mm < p.M)
-                            p.vt16[((size_t)((mm / S) * p.qKV + vh) * 256 + d) * S + mm % S] = f2h_rn(x[jj]);
+                        if (mm < p->M)
+                            p->vt16[((size_t)((mm / S) * p->qKV + vh) * 256 + d) * S + mm % S] = f2h_rn(x[jj]);
                     }
                 }
                 if (o32) {
@@ -799,7 +812,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
                 p_epilogue_f32<POST, FAST, NT>(p, f, wsr, pm0, pn0, wm, wn, lane);
             } else if constexpr (EPI == EPI_QKV) {
                 __syncthreads();
-                p_epilogue_qkv<FAST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
+                p_epilogue_qkv<FAST>(kernel_args(), f, wsr, pm0, pn0, wave, wm, wn, lane,
                                      (float *)(smem + (g % kPStages) * TILE));
             } else {
                 __syncthreads();
@@ -839,7 +852,7 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
         if constexpr (EPI == EPI_F32)
             p_epilogue_f32<POST, FAST, NT>(p, f, wsr, pm0, pn0, wm, wn, lane);
         else if constexpr (EPI == EPI_QKV)
-            p_epilogue_qkv<FAST>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
+            p_epilogue_qkv<FAST>(kernel_args(), f, wsr, pm0, pn0, wave, wm, wn, lane,
                                  (float *)(smem + ((G - 1) % kPStages) * TILE));
         else
             p_epilogue_q<BM, BN, NWM, NWN, EPI, FAST, POST, NT>(p, f, wsr, pm0, pn0, wave, wm, wn, lane,
