@@ -120,6 +120,7 @@ SIGNATURES = {
     "e2mi_create_tensors": (_P, [C.POINTER(E2MITensor), _I, _I, _I, _I, _I]),
     "e2mi_plan_pack": (_I, [_P, _I, _I, _P, _P, _P, _P]),
     "e2mi_plan_attention": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, C.POINTER(_I)]),
+    "e2mi_plan_device": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "e2mi_destroy": (None, [_P]),
     "e2mi_device": (C.c_char_p, [_P]),
     "e2mi_text_embed": (_I, [_P, _P, _I, _P]),
@@ -510,6 +511,25 @@ def attention_work(lens, H, window=0, div=2):
     """The engine's unsplit attention work list for packed sequences of these lengths (one entry per
     128-query block, longest sequences first, dealt to the XCDs; div 4 at head_dim 512)."""
     return plan_attention(lens, H, window, 1, div)[0]
+
+
+def plan_device(valid, H, window=0, div=2, ids=None, n_slots=None, stream=None):
+    """The device planner (e2mi_plan_device) on a [B, S] device mask (uint8 tensor): returns
+    (rowmap, pos, start, len, M, work, ids_out) as device tensors, rowmap, pos and ids_out cut to M
+    rows, work to n_slots entries (default H (ceil(B S / 128) + B)); ids_out is None without ids."""
+    import torch
+    B, S = valid.shape
+    dev = valid.device
+    cap = B * ((S + 7) & ~7) + 256
+    n_slots = n_slots or H * ((B * S + 127) // 128 + B)
+    i32 = lambda n: torch.full((n,), -7, dtype=torch.int32, device=dev)
+    rowmap, pos, start, lens, work, rows = i32(cap), i32(cap), i32(B), i32(B), i32(n_slots), i32(1)
+    ids_out = i32(cap) if ids is not None else None
+    check(load().e2mi_plan_device(stream_ptr(stream), ptr(valid), ptr(ids), B, S, H, window, div, n_slots,
+                                  ptr(rowmap), ptr(pos), ptr(start), ptr(lens), ptr(ids_out), ptr(work),
+                                  ptr(rows)), "plan_device")
+    M = int(rows.item())
+    return (rowmap[:M], pos[:M], start, lens, M, work, None if ids_out is None else ids_out[:M])
 
 
 def attention_split_work(lens, H, max_parts=4, window=0):

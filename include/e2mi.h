@@ -239,6 +239,17 @@ int e2mi_plan_pack(const uint8_t *valid, int B, int S, int32_t *rowmap, int32_t 
  * *n_merge (may be NULL when max_parts is 1). */
 int e2mi_plan_attention(const int32_t *len, int B, int H, int window, int max_parts, int div,
                         int32_t *work, int32_t *merge, int *n_merge);
+/* The same plan built on the device from a device mask, by one single-workgroup kernel on `stream`
+ * (the engine's device entry plans this way; no counterpart in the reference, whose HIP path runs
+ * padded batches): rowmap, pos, start and len as e2mi_plan_pack gives them, *rows its row count M,
+ * and work as e2mi_plan_attention gives it unsplit (max_parts 1), followed by -1 up to n_slots
+ * entries; with ids [B][S] (device) ids_out gets each packed row's token (0 for filler rows).
+ * All pointers are device memory: rowmap, pos and ids_out of B * ceil8(S) + 256 entries, start and
+ * len of B, work of n_slots, rows one int. Needs 0 < B <= 1024, 0 < H < 16 and
+ * H * (ceil(B * S / 128) + B) <= n_slots <= 8192. Returns 0, or -1 with the error set. */
+int e2mi_plan_device(e2mi_stream stream, const uint8_t *valid, const int32_t *ids, int B, int S, int H,
+                     int window, int div, int n_slots, int32_t *rowmap, int32_t *pos, int32_t *start,
+                     int32_t *len, int32_t *ids_out, int32_t *work, int32_t *rows);
 /* attention of each packed sequence over its own rows (all valid); vt16 [KV][D][M] from
  * e2mi_qkv_norm_rope_packed, seq_len[b] <= max_len, every seq_start a multiple of 8 (the
  * e2mi.pack_plan layout); rows outside every sequence are not written. work (optional, device):
