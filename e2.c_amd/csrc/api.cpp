@@ -25,6 +25,11 @@ int check_hip(hipError_t e, const char *what) {
     return -1;
 }
 
+static thread_local DeviceRows t_rows;
+DeviceRows device_rows() { return t_rows; }
+DeviceRowsScope::DeviceRowsScope(const int *ptr, int mul) : prev_(t_rows) { t_rows = DeviceRows{ptr, mul}; }
+DeviceRowsScope::~DeviceRowsScope() { t_rows = prev_; }
+
 struct GemmArgs;
 int launch_quantize(hipStream_t s, int8_t *q, int ldq, float *scales, const float *x, int M,
                     int K, int ldx, int block);

@@ -25,6 +25,28 @@ int check_hip(hipError_t e, const char *what);
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// ---- the row count of a forward planned on the device (the engine's device entry): while the
+// engine enqueues such a forward, the row kernels, the quantizer, the q/k/v norm kernel and the
+// per-128 GEMMs launched from that thread read their row count from `ptr` (an int in device memory
+// that the planner writes, times `mul`), and the host row count they are given only sizes their
+// grids. Rows past the device count are never read by the rows before them, so the count prunes
+// work only. Unset (null) for every other launch.
+struct DeviceRows {
+    const int *ptr = nullptr;
+    int mul = 1;
+};
+DeviceRows device_rows();
+class DeviceRowsScope {
+  public:
+    DeviceRowsScope(const int *ptr, int mul = 1);
+    ~DeviceRowsScope();
+    DeviceRowsScope(const DeviceRowsScope &) = delete;
+    DeviceRowsScope &operator=(const DeviceRowsScope &) = delete;
+
+  private:
+    DeviceRows prev_;
+};
+
 }  // namespace e2mi
 
 // ---- device helpers

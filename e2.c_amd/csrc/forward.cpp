@@ -46,6 +46,7 @@
 #include "common.h"
 #include "model_internal.h"
 #include "plan.h"
+#include "plan_dev.h"
 
 namespace e2mi {
 
@@ -107,6 +108,10 @@ struct e2mi_engine {
     // plan_layout, so one copy uploads a chunk's plan and every graph of a shape reads it at the
     // same addresses
     int32_t *d_plan = nullptr, *h_plan = nullptr;
+    // the device entry plans on the device when the whole batch fits one chunk (device_plan_fits):
+    // the planner writes the packed row count here, and the forward's kernels read it
+    int32_t *d_rows = nullptr;
+    bool device_plan = true;  // E2MI_DEVICE_PLAN=0 / e2mi_set_device_plan(0): plan on the host
     int32_t *rowmap = nullptr, *pos = nullptr, *seq_start = nullptr, *seq_len = nullptr;
     int32_t *h_rowmap = nullptr, *h_pos = nullptr, *h_start = nullptr, *h_len = nullptr;
     // attention work list (longest sequences first), a fixed number of slots per (sequences, rows):
@@ -138,7 +143,8 @@ struct e2mi_engine {
     int *d_bad = nullptr, *h_bad = nullptr;
     bool bad_pending = false;  // a previous asynchronous call's flag still to be read
     bool packed = true;
-    std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;  // (sequences, seq_len, rows, packed)
+    // (sequences, seq_len, rows, bits: packed 1, split 2, planned on the device 4)
+    std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;
     bool use_graph = true;
     bool fuse_qkv = true;  // E2MI_NOFUSE=1: the q|k|v GEMM and the norm/RoPE kernel run separately
     int layer_limit = 0;
@@ -317,7 +323,9 @@ constexpr int kAttnPartTiles = 8, kMaxAttnParts = 4;
 
 // every kernel of one forward over B sequences of S tokens (M rows: B * S padded, or the packed
 // row count), on stream s; returns the launch count or -1
-static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s) {
+static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s, bool dev = false) {
+    // dev: planned on the device, Mp rows of capacity; the kernels read the planned count
+    const DeviceRowsScope dev_rows(dev ? g->d_rows : nullptr);
     const e2_config &c = g->cfg;
     const int M = pk ? Mp : B * S, Dm = c.hidden, H = c.n_heads, P = c.ple_dim;
     if (M <= 0 || M > g->R) {
@@ -359,6 +367,7 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s)
         const int NP = c.n_layers * P;
         RUN("ple_quant", e2mi_quantize(s, g->qg, g->gs, g->x, M, Dm, Dm, 128));
         RUN("ple_model", e2mi_i8_gemm(s, g->ple32, NP, g->qg, g->gs, &g->ple_model, M, 0, NP));
+        const DeviceRowsScope ple_rows(dev ? g->d_rows : nullptr, c.n_layers);  // n_layers slices per row
         RUN("ple_norm", e2mi_scale_norm(s, g->ple32, M * c.n_layers, P, c.ple_scale, g->ple_proj_norm, eps, g->ple32));
     }
     for (int l = 0; l < nl; l++) {
@@ -436,25 +445,25 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s)
     return k + 1;  // the pool is two launches
 }
 
-static int run_shape(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s) {
+static int run_shape(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s, bool dev = false) {
     if (!g->use_graph || g->prof_rec) {
-        const int k = enqueue(g, B, S, Mp, pk, s);
+        const int k = enqueue(g, B, S, Mp, pk, s, dev);
         if (k < 0) return -1;
         g->kernels_last = k;
         return 0;
     }
-    auto key = std::make_tuple(B, S, Mp, (pk ? 1 : 0) | (pk && g->split_now ? 2 : 0));
+    auto key = std::make_tuple(B, S, Mp, (pk ? 1 : 0) | (pk && g->split_now ? 2 : 0) | (dev ? 4 : 0));
     auto it = g->graphs.find(key);
     if (it == g->graphs.end()) {
         // the first call of a shape runs eagerly (kernel attributes get set outside any capture),
         // then the sequence is recorded for every later call
-        const int k = enqueue(g, B, S, Mp, pk, s);
+        const int k = enqueue(g, B, S, Mp, pk, s, dev);
         if (k < 0) return -1;
         g->kernels_last = k;
         hipGraph_t graph = nullptr;
         if (check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"))
             return -1;
-        const int k2 = enqueue(g, B, S, Mp, pk, s);
+        const int k2 = enqueue(g, B, S, Mp, pk, s, dev);
         const hipError_t e = hipStreamEndCapture(s, &graph);
         if (k2 < 0 || check_hip(e, "end capture")) {
             if (graph) (void)hipGraphDestroy(graph);
@@ -562,6 +571,18 @@ static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
     return Mp;
 }
 
+// The device entry plans on the device (plan_dev.hip) when the whole batch is one chunk whatever its
+// mask (every token valid: n ceil8(S) rows, rounded up to 256, within the workspace) and its lists fit
+// the planner's workgroup, with the unsplit f16 lists (no int8 attention, no split mode) and no
+// workspace dump (which writes the host plan). Returns the rows the forward is sized for, or 0.
+static int device_plan_rows(const e2mi_engine *g, int n, int S) {
+    if (!g->device_plan || !g->packed || g->attn_i8 || g->split_mode != 0 || !g->dump_dir.empty() || n > g->bmax)
+        return 0;
+    const long cap = ((long)n * ((S + 7) & ~7) + 255) & ~255L;
+    if (cap > g->R || !plan_device_fits(n, S, g->cfg.n_heads, work_slots(g, n, (int)cap))) return 0;
+    return (int)cap;
+}
+
 // sequences of the next chunk starting at b0: as many as fit the workspace rows (packed: rounded
 // up to 256), the staging arrays and the pooling workspace; at least one
 static int chunk_size(const e2mi_engine *g, const uint8_t *valid, int b0, int batch, int S) {
@@ -667,6 +688,8 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
     g->use_graph = !(ng && ng[0] && ng[0] != '0');
     const char *nf = getenv("E2MI_NOFUSE");
     g->fuse_qkv = !(nf && nf[0] && nf[0] != '0');
+    const char *dp = getenv("E2MI_DEVICE_PLAN");  // 1 (default) | 0
+    g->device_plan = !(dp && dp[0] == '0');
     const char *ns = getenv("E2MI_SPLIT");  // 0 (default) | 1 | auto
     if (ns && ns[0]) g->split_mode = ns[0] == '0' ? 0 : ns[0] == '1' ? 1 : 2;
     {
@@ -748,7 +771,7 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         dalloc(g, &g->ids, R) || dalloc(g, &g->valid, R) || dalloc(g, &g->out, R * g->dout) ||
         dalloc(g, &g->pool_ws, (R / 64 + R + 64) * (size_t)(g->dout + 1)) ||
         (c.ple_dim > 0 && dalloc(g, &g->ple32, R * c.n_layers * c.ple_dim)) ||
-        dalloc(g, &g->d_plan, plan_layout(g, g->bmax, (int)R).end) ||
+        dalloc(g, &g->d_plan, plan_layout(g, g->bmax, (int)R).end) || dalloc(g, &g->d_rows, 1) ||
         (g->split_factor > 1 && dalloc(g, &g->part, e2mi_attention_part_bytes(R, c.n_heads, 256) / 4 + 64)))
         return fail();
     if (check_hip(hipHostMalloc((void **)&g->h_ids, R * 4), "pinned ids") ||
@@ -760,8 +783,12 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         return fail();
     *g->h_bad = 0;
     plan_bind(g, plan_layout(g, g->bmax, (int)R));
-    // filler rows of packed batches read contexts that no attention writes: start them at zero
-    if (check_hip(hipMemsetAsync(g->cq, 0, R * qd, g->stream), "clear ctx") ||
+    // filler rows of packed batches read contexts that no attention writes: start them at zero; a
+    // device-planned forward writes its plan's rows only up to its row count, so the plan's rows
+    // past it hold earlier calls' entries or these zeros (valid positions and tokens)
+    if (check_hip(hipMemsetAsync(g->d_plan, 0, plan_layout(g, g->bmax, (int)R).end * 4, g->stream), "clear plan") ||
+        check_hip(hipMemsetAsync(g->ids, 0, R * 4, g->stream), "clear ids") ||
+        check_hip(hipMemsetAsync(g->cq, 0, R * qd, g->stream), "clear ctx") ||
         check_hip(hipMemsetAsync(g->cs, 0, R * (qd / 128) * 4, g->stream), "clear ctx scales"))
         return fail();
     const char *np = getenv("E2MI_NOPACK");
@@ -1021,6 +1048,33 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
             check_hip(hipMemcpyAsync(out, g->out, (size_t)batch * g->dout * 4, hipMemcpyDeviceToDevice, s),
                       "out D2D"))
             return -1;
+    } else if (const int cap = device_plan_rows(g, batch, seq_len)) {
+        // planned on the device: the call reads nothing back, and one recorded forward serves every
+        // mask of this batch shape (its kernels read the planned row count)
+        plan_bind(g, plan_layout(g, batch, cap));
+        g->split_now = false;
+        PlanDevArgs pa{};
+        pa.valid = valid;
+        pa.ids = ids;
+        pa.n = batch;
+        pa.S = seq_len;
+        pa.H = g->cfg.n_heads;
+        pa.window = g->cfg.window;
+        pa.div = 2;
+        pa.full_div = 4;
+        pa.slots = work_slots(g, batch, cap);
+        pa.rowmap = g->rowmap;
+        pa.pos = g->pos;
+        pa.start = g->seq_start;
+        pa.len = g->seq_len;
+        pa.ids_out = g->ids;
+        pa.work = g->work;
+        pa.work_full = g->work_full;
+        pa.rows = g->d_rows;
+        if (launch_plan_packed(s, pa) || run_shape(g, batch, seq_len, cap, true, s, true) ||
+            check_hip(hipMemcpyAsync(out, g->out, (size_t)batch * g->dout * 4, hipMemcpyDeviceToDevice, s),
+                      "out D2D"))
+            return -1;
     } else {
         // the packing is planned on the host from the mask: one synchronous copy of B*S bytes
         // (which also drains earlier work on the stream that used the staging arrays)
@@ -1108,6 +1162,17 @@ extern "C" int e2mi_set_packing(e2mi_engine *g, int on) {
     if (g->stream) (void)hipStreamSynchronize(g->stream);
     if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
     g->packed = on != 0;
+    return 0;
+}
+
+extern "C" int e2mi_set_device_plan(e2mi_engine *g, int on) {
+    if (!g) {
+        set_error("set_device_plan: null engine");
+        return -1;
+    }
+    if (g->stream) (void)hipStreamSynchronize(g->stream);
+    if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
+    g->device_plan = on != 0;
     return 0;
 }
 

@@ -60,6 +60,8 @@ struct GemmArgs {
     float *q32, *k32, *v32;
     int qH, qKV, qS;
     float eps;
+    // a device row count (a multiple of 256, at most M; k_gemm_p only), or null: M rows
+    const int *rows;
 };
 
 
@@ -615,6 +617,13 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned char *const sscale = smem + kPStages * TILE;
 
+    if (p.rows) {
+        // a forward planned on the device: its row count, a multiple of 256, from device memory; the
+        // host M sized the grid and, in the q|k|v epilogue (which reads the kernel's arguments
+        // again), bounds the stores of tiles that all lie below this count
+        p.M = min(p.M, *p.rows);
+        tiles = (p.M + BM - 1) / BM * tiles_n;
+    }
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / NWN, wn = wave % NWN;
@@ -1771,7 +1780,11 @@ static int launch_dump(hipStream_t s, const GemmArgs &p) {
     return check_hip(hipGetLastError(), "gemm launch");
 }
 
-static int check_args(const GemmArgs &p, const char *who) {
+static int check_args(const GemmArgs &p, const char *who, bool rows_ok = true) {
+    if (p.rows && !rows_ok) {
+        set_error("%s: a device row count is taken by the per-128 GEMMs only", who);
+        return -1;
+    }
     if (p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % kQBlock) {
         set_error("%s: bad geometry M=%d N=%d K=%d (K must be a positive multiple of 128)", who, p.M,
                   p.N, p.K);
@@ -1810,7 +1823,7 @@ static bool half_tiles(const GemmArgs &p) {
 }
 
 int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump, bool tok = false) {
-    if (check_args(p, "i8_gemm")) return -1;
+    if (check_args(p, "i8_gemm", !dump && !tok)) return -1;
     if (!p.Y || p.ldy < p.N) {
         set_error("i8_gemm: null output or ldy < N");
         return -1;
@@ -1828,7 +1841,7 @@ int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump, bool tok = false) {
 }
 
 int launch_gemm_i8q(hipStream_t s, GemmArgs p, bool tok = false) {
-    if (check_args(p, "i8_gemm_q")) return -1;
+    if (check_args(p, "i8_gemm_q", !tok)) return -1;
     if (p.N % 128 || !p.Yq || !p.ys || p.ldyq < p.N || p.ldyq % 16 || !aligned16(p.Yq) ||
         p.ldys < p.N / 128) {
         set_error("i8_gemm_q: N must be a multiple of 128 with a 16-byte aligned int8 output");
@@ -1919,6 +1932,7 @@ static GemmArgs make_args(const int8_t *qa, const float *as, const e2mi_q8w *w, 
     p.K = w->K;
     p.lo = w->out_min;
     p.hi = w->out_max;
+    p.rows = device_rows().ptr;
     return p;
 }
 

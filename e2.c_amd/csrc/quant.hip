@@ -12,11 +12,12 @@ namespace e2mi {
 // block == 128: a half-wave per (row, block); 8 blocks per 256-thread workgroup.
 __global__ __launch_bounds__(256) void k_quant128(int8_t *__restrict__ q, float *__restrict__ sc,
                                                   const float *__restrict__ x, int M, int K,
-                                                  int ldx, int ldq) {
+                                                  int ldx, int ldq, const int *rows) {
     const int nb = K / kQBlock;
     const long item = (long)blockIdx.x * 8 + (threadIdx.x >> 5);
     if (item >= (long)M * nb) return;
     const int m = (int)(item / nb), b = (int)(item % nb), l = threadIdx.x & 31;
+    if (rows && m >= *rows) return;
     const float4 v = *(const float4 *)(x + (size_t)m * ldx + b * kQBlock + l * 4);
     float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     a = group_max<32>(a);
@@ -29,9 +30,9 @@ __global__ __launch_bounds__(256) void k_quant128(int8_t *__restrict__ q, float 
 // block == K (the per-token variant, the reference rebuilt with -DE2_I8_BLOCK=K): one wave per row.
 __global__ __launch_bounds__(256) void k_quant_row(int8_t *__restrict__ q, float *__restrict__ sc,
                                                    const float *__restrict__ x, int M, int K,
-                                                   int ldx, int ldq) {
+                                                   int ldx, int ldq, const int *rows) {
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
-    if (m >= M) return;
+    if (m >= M || (rows && m >= *rows)) return;
     const float *xr = x + (size_t)m * ldx;
     float a = 0.f;
     for (int k = l * 4; k < K; k += 256) {
@@ -54,9 +55,9 @@ __global__ __launch_bounds__(256) void k_quant_row(int8_t *__restrict__ q, float
 template <int NCH>
 __global__ __launch_bounds__(256) void k_quant128_r(int8_t *__restrict__ q, float *__restrict__ sc,
                                                     const float *__restrict__ x, int M, int K,
-                                                    int ldx, int ldq) {
+                                                    int ldx, int ldq, const int *rows) {
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
-    if (m >= M) return;
+    if (m >= M || (rows && m >= *rows)) return;
     const float *xr = x + (size_t)m * ldx;
     const int nb = K / kQBlock;
     float4 v[NCH];
@@ -83,9 +84,9 @@ __global__ __launch_bounds__(256) void k_quant128_r(int8_t *__restrict__ q, floa
 template <int NCH>
 __global__ __launch_bounds__(256) void k_quant_row_r(int8_t *__restrict__ q, float *__restrict__ sc,
                                                      const float *__restrict__ x, int M, int K,
-                                                     int ldx, int ldq) {
+                                                     int ldx, int ldq, const int *rows) {
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
-    if (m >= M) return;
+    if (m >= M || (rows && m >= *rows)) return;
     const float *xr = x + (size_t)m * ldx;
     float4 v[NCH];
     float a = 0.f;
@@ -118,24 +119,25 @@ int launch_quantize(hipStream_t s, int8_t *q, int ldq, float *scales, const floa
         set_error("quantize: null or misaligned pointer (x 16-B, q 4-B aligned)");
         return -1;
     }
+    const int *rows = device_rows().ptr;
     if (block == kQBlock) {
         const long items = (long)M * (K / kQBlock);
         const dim3 g((unsigned)((M + 3) / 4));
         if (K <= 768)
-            hipLaunchKernelGGL(k_quant128_r<3>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq);
+            hipLaunchKernelGGL(k_quant128_r<3>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq, rows);
         else if (K <= 1280)
-            hipLaunchKernelGGL(k_quant128_r<5>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq);
+            hipLaunchKernelGGL(k_quant128_r<5>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq, rows);
         else
             hipLaunchKernelGGL(k_quant128, dim3((unsigned)((items + 7) / 8)), dim3(256), 0, s, q,
-                               scales, x, M, K, ldx, ldq);
+                               scales, x, M, K, ldx, ldq, rows);
     } else if (block == K) {
         const dim3 g((unsigned)((M + 3) / 4));
         if (K <= 768)
-            hipLaunchKernelGGL(k_quant_row_r<3>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq);
+            hipLaunchKernelGGL(k_quant_row_r<3>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq, rows);
         else if (K <= 1280)
-            hipLaunchKernelGGL(k_quant_row_r<5>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq);
+            hipLaunchKernelGGL(k_quant_row_r<5>, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq, rows);
         else
-            hipLaunchKernelGGL(k_quant_row, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq);
+            hipLaunchKernelGGL(k_quant_row, g, dim3(256), 0, s, q, scales, x, M, K, ldx, ldq, rows);
     } else {
         set_error("quantize: block must be 128 or K (got %d, K=%d)", block, K);
         return -1;

@@ -42,6 +42,8 @@ struct RowArgs {
     int M, D;
     float pre_scale = 1.f;   // PLAIN: rows scaled before the norm (the PLE inputs, text.c:930-931)
     float post_scale = 1.f;  // ADDNORM: x scaled after the add (layer_scalar, text.c:959)
+    const int *rows = nullptr;  // device row count (times rows_mul, at most M), or null: M
+    int rows_mul = 1;
 };
 
 __device__ inline float4 ld4(const float *p) { return *(const float4 *)p; }
@@ -63,7 +65,7 @@ __device__ inline float4 scale4(float4 v, float inv, float4 g) {
 template <int MODE, int NC>
 __global__ __launch_bounds__(256) void k_rows(RowArgs a) {
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
-    if (m >= a.M) return;
+    if (m >= a.M || (a.rows && m >= *a.rows * a.rows_mul)) return;
     const int D = a.D, nch = D / 4;
     float4 v[NC];
     const float *row;
@@ -151,6 +153,7 @@ struct QkvArgs {
     float *q32, *k32, *v32;    // optional f32 copies (parity tests), same layouts as q16/k16/[M][KV*D]
     const int32_t *pos;        // packed batches: RoPE position of each row (then S = M, B = 1)
     int M, S, H, KV;
+    const int *rows;           // device row count (at most M), or null: M
 };
 
 // f16 of an f32 value that is already rounded: the register barrier keeps the compiler from folding
@@ -187,6 +190,7 @@ __global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a, int nv) {
         __shared__ __align__(16) uint16_t vbuf[VR * D];
         const int vb = (int)blockIdx.x, nrb = (a.M + VR - 1) / VR;
         const int vh = vb / nrb, m0 = (vb % nrb) * VR, w = threadIdx.x >> 6;
+        if (a.rows && m0 >= *a.rows) return;  // the whole block (a packed row count is a multiple of 256)
         const int h = a.H + a.KV + vh;
         // wave w: rows 8 w .. 8 w + 7, four at a time (independent loads in flight)
 #pragma unroll
@@ -249,6 +253,7 @@ __global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a, int nv) {
     const long item = (long)(blockIdx.x - nv) * 4 + (threadIdx.x >> 6);
     if (item >= (long)a.M * qkh) return;
     const int m = (int)(item / qkh), h = (int)(item % qkh);
+    if (a.rows && m >= *a.rows) return;
     const int kind = h < a.H ? 0 : 1;  // q, k
     const float *src = a.qkv + (size_t)m * heads * D + h * D;
     float4 v[NCH];
@@ -444,13 +449,18 @@ static int row_launch(hipStream_t s, int mode, const RowArgs &a) {
     }
     const int nc = (a.D / 4 + 63) / 64;
     dim3 grid((a.M + 3) / 4), block(256);
+    RowArgs b = a;
+    if (!b.rows) {
+        b.rows = device_rows().ptr;
+        b.rows_mul = device_rows().mul;
+    }
 #define ROWK(MODE)                                                                          \
     switch (nc) {                                                                           \
-    case 1: hipLaunchKernelGGL((k_rows<MODE, 1>), grid, block, 0, s, a); break;             \
-    case 2: hipLaunchKernelGGL((k_rows<MODE, 2>), grid, block, 0, s, a); break;             \
-    case 3: hipLaunchKernelGGL((k_rows<MODE, 3>), grid, block, 0, s, a); break;             \
-    case 4: hipLaunchKernelGGL((k_rows<MODE, 4>), grid, block, 0, s, a); break;             \
-    default: hipLaunchKernelGGL((k_rows<MODE, 5>), grid, block, 0, s, a); break;            \
+    case 1: hipLaunchKernelGGL((k_rows<MODE, 1>), grid, block, 0, s, b); break;             \
+    case 2: hipLaunchKernelGGL((k_rows<MODE, 2>), grid, block, 0, s, b); break;             \
+    case 3: hipLaunchKernelGGL((k_rows<MODE, 3>), grid, block, 0, s, b); break;             \
+    case 4: hipLaunchKernelGGL((k_rows<MODE, 4>), grid, block, 0, s, b); break;             \
+    default: hipLaunchKernelGGL((k_rows<MODE, 5>), grid, block, 0, s, b); break;            \
     }
     if (mode == ROW_EMBED) { ROWK(ROW_EMBED) }
     else if (mode == ROW_ADDNORM) { ROWK(ROW_ADDNORM) }
@@ -462,7 +472,9 @@ static int row_launch(hipStream_t s, int mode, const RowArgs &a) {
 
 int launch_rows(hipStream_t s, int mode, const RowArgs &a) { return row_launch(s, mode, a); }
 
-int launch_qkv_norm_rope(hipStream_t s, const QkvArgs &a, int D) {
+int launch_qkv_norm_rope(hipStream_t s, const QkvArgs &qa, int D) {
+    QkvArgs a = qa;
+    if (!a.rows) a.rows = device_rows().ptr;
     const long nqk = ((long)a.M * (a.H + a.KV) + 3) / 4;
     const long nv = (long)a.KV * ((a.M + 31) / 32);
     if (nqk + nv > 0x7fffffffL) {

@@ -130,6 +130,7 @@ SIGNATURES = {
     "e2mi_profile_text": (C.c_char_p, [_P]),
     "e2mi_set_attention_split": (_I, [_P, _I]),
     "e2mi_set_layer_limit": (_I, [_P, _I]),
+    "e2mi_set_device_plan": (_I, [_P, _I]),
     "e2mi_set_packing": (_I, [_P, _I]),
     "e2mi_set_attention": (_I, [_P, _I]),
 }
@@ -836,6 +837,10 @@ class Engine:
     def set_packing(self, on: bool):
         """Packed batches (valid tokens only) on or off; off computes every padded row."""
         check(load().e2mi_set_packing(self.h, 1 if on else 0), "set_packing")
+
+    def set_device_plan(self, on: bool):
+        """The device entry's packed plan built on the device (default) or on the host."""
+        check(load().e2mi_set_device_plan(self.h, 1 if on else 0), "set_device_plan")
 
     def set_split(self, mode: str):
         """Split key ranges: "off", "on" or "auto" (e2mi_set_attention_split)."""

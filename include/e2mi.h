@@ -438,6 +438,14 @@ int e2mi_set_layer_limit(e2mi_engine *g, int n_layers);
 /* Packed batches on (1, the default; E2MI_NOPACK=1 turns it off at creation) or off (0: every
  * row of the padded batch is computed, as the reference does). No counterpart in the reference. */
 int e2mi_set_packing(e2mi_engine *g, int on);
+/* Where the device entry plans a packed batch: 1 (the default) on the device (e2mi_plan_device's
+ * kernel, whenever the whole batch fits the workspace at any mask, the plan fits the planner's
+ * workgroup, and neither the int8 attention, split key ranges nor E2MI_DUMP is on): the call reads
+ * nothing back and one recorded forward per (batch, seq_len) serves every mask, its kernels
+ * reading the planned row count from device memory; 0 on the host, as e2mi_text_embed_batch does
+ * (the mask read back, a forward recorded per packed row count). The embeddings are the same bit
+ * for bit. E2MI_DEVICE_PLAN=0 sets 0 at creation. No counterpart in the reference. */
+int e2mi_set_device_plan(e2mi_engine *g, int on);
 /* Text attention kind (the reference's E2_ATTN_TEXT / e2_attn_override, dispatch.h:34-41, read at
  * e2mi_create): E2_ATTN_F16 (1, the gfx950 rule's choice) or E2_ATTN_I8 (2: sequences of at least 32
  * valid tokens take the int8 attention of text.c:638-700, shorter ones the f16 kernel, as the

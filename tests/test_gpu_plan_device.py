@@ -85,3 +85,69 @@ def test_device_plan_refusals(gpu):
     assert lib.e2mi_plan_device(None, v.data_ptr(), None, 4, 64, 16, 0, 2, 4000, p, p, p, p, None, p, p) == -1
     # ids_out without ids
     assert lib.e2mi_plan_device(None, v.data_ptr(), None, 4, 64, 3, 0, 2, 18, p, p, p, p, p, p, p) == -1
+
+
+def _embed_both(eng, ids, valid, dev):
+    """The device entry's embeddings (device plan) and the host entry's (host plan)."""
+    import torch
+    out = torch.full((ids.shape[0], eng.dim), 7.0, device=dev)
+    eng.embed_batch_device(torch.from_numpy(ids).to(dev), torch.from_numpy(valid).to(dev), out)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), eng.embed_batch(ids, valid)
+
+
+def test_engine_device_plan_equals_host_plan(gpu):
+    """Masks of one shape whose packed row counts differ (so one recorded forward serves them all
+    and its kernels take the planned count): the device entry's embeddings equal the host entry's
+    bit for bit, an all-invalid batch (no rows) gives zero vectors, and two calls enqueued on a
+    stream without a wait in between (the second planner run follows the first forward) give each
+    call's own result."""
+    import torch
+    import e2mi
+    from model_util import random_batch, small_config
+    rng = np.random.default_rng(77)
+    cfg = small_config(e2mi, n_layers=3)
+    m = e2mi.Model.synthetic(cfg, 5)
+    eng = e2mi.Engine(m, max_rows=16 * 200)
+    B, S = 16, 200
+    masks = []
+    for k in range(4):
+        ids, valid = random_batch(rng, B, S, cfg.vocab, min_len=1, holes=k % 2 == 1)
+        if k == 2:
+            valid[3] = 0
+        masks.append((ids, valid))
+    masks.append((masks[0][0], np.zeros((B, S), np.uint8)))
+    for ids, valid in masks:
+        d, h = _embed_both(eng, ids, valid, gpu)
+        assert np.array_equal(d, h)
+        if not valid.any():
+            assert np.all(d == 0)
+    s = torch.cuda.Stream()
+    outs = [torch.empty((B, eng.dim), device=gpu) for _ in range(2)]
+    dev_in = [(torch.from_numpy(i).to(gpu), torch.from_numpy(v).to(gpu)) for i, v in masks[:2]]
+    torch.cuda.synchronize()
+    for (it, vt), o in zip(dev_in, outs):
+        eng.embed_batch_device(it, vt, o, stream=s)
+    s.synchronize()
+    for (ids, valid), o in zip(masks[:2], outs):
+        assert np.array_equal(o.cpu().numpy(), eng.embed_batch(ids, valid))
+    eng.set_device_plan(False)
+    d, h = _embed_both(eng, *masks[1], gpu)
+    assert np.array_equal(d, h)
+    eng.set_device_plan(True)
+
+
+def test_reference_geometry_device_plan(gpu):
+    """The reference checkpoint's geometry (windowed layers dealt with the window, the head_dim-512
+    layer's own list, the PLE norm over n_layers slices of each row): device plan == host plan."""
+    import e2mi
+    from model_util import random_batch, reference_small_config
+    rng = np.random.default_rng(78)
+    cfg = reference_small_config(e2mi, n_layers=6)
+    m = e2mi.Model.synthetic(cfg, 6)
+    B, S = 6, 1500
+    eng = e2mi.Engine(m, max_rows=B * 1504)
+    for k in range(2):
+        ids, valid = random_batch(rng, B, S, cfg.vocab, min_len=100, holes=k == 1)
+        d, h = _embed_both(eng, ids, valid, gpu)
+        assert np.array_equal(d, h)
