@@ -323,7 +323,10 @@ def encoder_bench(torch, e2mi, steps, warmup, cpu_sample=4, padded=True):
     dev = torch.device("cuda:0")
     ids_d, valid_d = torch.from_numpy(ids).to(dev), torch.from_numpy(valid).to(dev)
     out = torch.empty((ENC_B, cfg.hidden), device=dev)
-    stream = torch.cuda.current_stream()
+    # the caller's own stream (torch's default stream has handle 0, which the entry takes as "none"
+    # and then synchronises every call)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
     for _ in range(max(2, warmup)):  # the first call records the shape's graph
         eng.embed_batch_device(ids_d, valid_d, out, stream)
     torch.cuda.synchronize()
@@ -342,11 +345,32 @@ def encoder_bench(torch, e2mi, steps, warmup, cpu_sample=4, padded=True):
             torch.cuda.synchronize()
             ts.append(time.perf_counter() - t1)
         return ts
-    dev_ts, host_ts = [], []
+    # the device entry plans the packed batch on the device (the default); the same entry with the
+    # host planner (mask read back, plan uploaded) is timed in the same rounds
+    def host_planned():
+        eng.set_device_plan(False)
+        try:
+            eng.embed_batch_device(ids_d, valid_d, out, stream)
+        finally:
+            eng.set_device_plan(True)
+    dev_ts, host_ts, hplan_ts = [], [], []
     for _ in range(2):
         dev_ts += per_call(lambda: eng.embed_batch_device(ids_d, valid_d, out, stream), max(3, steps // 2))
         host_ts += per_call(lambda: eng.embed_batch(ids, valid), max(3, steps // 2))
+        hplan_ts += per_call(host_planned, max(3, steps // 2))
     dt = float(np.median(dev_ts))
+    # calls enqueued back to back on the caller's stream (a serving loop): four untimed calls bring
+    # the clocks back up after the host's pause, then npipe calls between two events on the stream
+    npipe = max(10, steps)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(4):
+        eng.embed_batch_device(ids_d, valid_d, out, stream)
+    e0.record(stream)
+    for _ in range(npipe):
+        eng.embed_batch_device(ids_d, valid_d, out, stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    dt_pipe = e0.elapsed_time(e1) / npipe / 1e3
     o = out.cpu().numpy()
     # the same batch with every padded row computed (the reference's way), for comparison
     dt_pad, o_pad = None, None
@@ -386,8 +410,12 @@ def encoder_bench(torch, e2mi, steps, warmup, cpu_sample=4, padded=True):
         "embeddings_per_s": round(ENC_B / dt, 2),
         "ms_per_batch": round(dt * 1e3, 3),
         "timing": (f"median of {len(dev_ts)} calls, each synchronised, after 0.5 s of warm forwards; "
-                   f"device entry mean {np.mean(dev_ts) * 1e3:.3f} ms, min {min(dev_ts) * 1e3:.3f} ms"),
+                   f"device entry mean {np.mean(dev_ts) * 1e3:.3f} ms, min {min(dev_ts) * 1e3:.3f} ms; "
+                   f"pipelined: {npipe} calls enqueued back to back after 4 untimed ones, stream events"),
         "tokens_per_s_valid": round(float(valid.sum()) / dt, 1),
+        "pipelined_embeddings_per_s": round(ENC_B / dt_pipe, 2),
+        "pipelined_ms_per_batch": round(dt_pipe * 1e3, 3),
+        "device_entry_host_plan_ms_per_batch": round(float(np.median(hplan_ts)) * 1e3, 3),
         "host_buffers_embeddings_per_s": round(ENC_B / hdt, 2),
         "host_buffers_ms_per_batch": round(hdt * 1e3, 3),
         "unit_norm_ok": bool(np.allclose(np.linalg.norm(o, axis=1), 1, atol=1e-4)),
@@ -427,7 +455,7 @@ def reference_geometry_bench(torch, e2mi, steps, warmup, cpu_sample=0):
     model = e2mi.Model.synthetic(cfg, 1004)
     t_model = time.perf_counter() - t0
     dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream()
+    stream = torch.cuda.Stream()  # the caller's own stream, as in the encoder leg
     eng = e2mi.Engine(model, max_rows=ENC_B * ENC_S)
     res = {"config": "reference checkpoint geometry, 24 layers, random-init int8 weights, vocab 262144",
            "model_build_s": round(t_model, 2)}
@@ -438,6 +466,7 @@ def reference_geometry_bench(torch, e2mi, steps, warmup, cpu_sample=0):
         valid = (np.arange(S)[None, :] < lens[:, None]).astype(np.uint8)
         ids_d, valid_d = torch.from_numpy(ids).to(dev), torch.from_numpy(valid).to(dev)
         out = torch.empty((B, cfg.out_dim), device=dev)
+        torch.cuda.synchronize()
         for _ in range(max(2, warmup)):
             eng.embed_batch_device(ids_d, valid_d, out, stream)
         torch.cuda.synchronize()
@@ -769,27 +798,38 @@ def summarize_enc_ktrace(trace_csv):
             lines.append(f"| `{k[:80]}` | {np.mean(v):.1f} | {100 * np.mean(v) / tot:.1f} | "
                          f"{np.mean(v) / max(nl, 1):.1f} |")
     # device-entry calls (e2mi_text_embed_batch_device): each starts with the id check (k_check_ids);
-    # before its forward's first kernel: mask read-back, host planning, plan upload, graph launch;
-    # after the forward's last kernel until the next call's id check: output copy, flag read-back,
-    # return to the caller (consecutive calls only: the next one within 2 ms)
+    # before its forward's first kernel: the device planner (k_plan_packed) and the graph launch, or
+    # with the host planner the mask read-back, host planning, plan upload and id gather; after the
+    # forward's last kernel until the next call's id check: output copy, flag read (synchronised
+    # calls), return to the caller (consecutive calls only: the next one within 2 ms)
     t = lambda r, k: int(r[k]) / 1e3
     starts = [i for i, r in enumerate(rows) if "k_check_ids" in name(r)]
-    pre, post = [], []
-    for c, i in enumerate(starts):
+    calls = []  # (check, first forward kernel, last forward kernel, planned on the device)
+    for i in starts:
         emb = next((j for j in range(i, len(rows)) if name(rows[j]).startswith("e2mi::k_rows<1")), None)
         end = next((j for j in range(i, len(rows)) if "k_pool_finish" in name(rows[j])), None)
-        if emb is None or end is None:
+        if emb is not None and end is not None:
+            calls.append((i, emb, end, any("k_plan_packed" in name(rows[j]) for j in range(i, emb))))
+    for dev in (True, False):
+        sel = [k for k, c in enumerate(calls) if c[3] == dev]
+        if not sel:
             continue
-        pre.append(t(rows[emb], "Start_Timestamp") - t(rows[i], "Start_Timestamp"))
-        if c + 1 < len(starts):
-            g = t(rows[starts[c + 1]], "Start_Timestamp") - t(rows[end], "End_Timestamp")
-            if 0 <= g < 2000:
-                post.append(g)
-    if pre:
+        pre = [t(rows[calls[k][1]], "Start_Timestamp") - t(rows[calls[k][0]], "Start_Timestamp") for k in sel]
+        # between one forward's last kernel and the next call's first forward kernel (consecutive
+        # calls of the same planner, within 2 ms): the span, and the part with no kernel running
+        span, idle = [], []
+        for k in sel:
+            if k + 1 < len(calls) and calls[k + 1][3] == dev:
+                e, b = calls[k][2], calls[k + 1][1]
+                g = t(rows[b], "Start_Timestamp") - t(rows[e], "End_Timestamp")
+                if 0 <= g < 2000:
+                    span.append(g)
+                    idle.append(g - sum(dur(rows[j]) for j in range(e + 1, b)))
         q = lambda v: f"median {np.median(v):.0f}, min {min(v):.0f}, max {max(v):.0f}"
-        lines += ["", f"device-entry calls: {len(pre)}; id check to the forward's first kernel (us): {q(pre)}; "
-                  f"forward's last kernel to the next call's id check (us, {len(post)} consecutive pairs): "
-                  + (q(post) if post else "none")]
+        lines += ["", f"device-entry calls planned on the {'device' if dev else 'host'}: {len(pre)}; id check to "
+                  f"the forward's first kernel (us): {q(pre)}; one forward's last kernel to the next's first "
+                  f"(us, {len(span)} consecutive pairs): " + (f"{q(span)}, of which no kernel running: {q(idle)}"
+                                                             if span else "none")]
     text = "\n".join(lines) + "\n"
     print(text)
     return text

@@ -35,6 +35,7 @@
 #include <time.h>
 
 #include <algorithm>
+#include <deque>
 #include <map>
 #include <string>
 #include <tuple>
@@ -137,11 +138,17 @@ struct e2mi_engine {
     // the stream of the previous call: a call on another stream first waits for it (the calls share
     // the workspace and the pinned staging arrays)
     hipStream_t last_stream = nullptr;
-    // device-side id check of the device entry: the id check and the embedding kernel raise the
-    // flag for an id outside the vocabulary, writing pinned host memory (h_bad; d_bad is its device
-    // address) that the host reads once the call's stream has drained and clears itself
-    int *d_bad = nullptr, *h_bad = nullptr;
-    bool bad_pending = false;  // a previous asynchronous call's flag still to be read
+    // device-side id check of the device entry: each call's check kernel raises its own flag for an
+    // id outside the vocabulary, one of kFlagSlots ints of mapped pinned host memory (h_flags;
+    // d_flags is its device address), used in turn; the slots of calls whose flags are still unread
+    // wait in `unread`, in call order, each with an event recorded after the call's check kernel. A
+    // call reads the flags of the earlier checks that have finished without waiting for the others,
+    // so calls on a caller stream are enqueued back to back.
+    static constexpr int kFlagSlots = 64;
+    int *d_flags = nullptr, *h_flags = nullptr;
+    hipEvent_t flag_ev[kFlagSlots] = {};
+    std::deque<int> unread;
+    int next_slot = 0;
     bool packed = true;
     // (sequences, seq_len, rows, bits: packed 1, split 2, planned on the device 4)
     std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;
@@ -362,7 +369,7 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s,
         }                                                                                          \
     } while (0)
     RUN("embed", launch_embed_checked(s, g->embed, c.vocab, g->ids, c.embed_scale, g->layers[0].ln_in, eps, M, Dm,
-                             g->x, g->qa, g->as, g->d_bad));
+                             g->x, g->qa, g->as, nullptr));
     if (P > 0) {  // the per-layer inputs from the scaled embeddings (text.c:929-932)
         const int NP = c.n_layers * P;
         RUN("ple_quant", e2mi_quantize(s, g->qg, g->gs, g->x, M, Dm, Dm, 128));
@@ -658,7 +665,9 @@ extern "C" void e2mi_destroy(e2mi_engine *g) {
     if (g->h_out) (void)hipHostFree(g->h_out);
     if (g->h_plan) (void)hipHostFree(g->h_plan);
     if (g->h_mask) (void)hipHostFree(g->h_mask);
-    if (g->h_bad) (void)hipHostFree(g->h_bad);
+    if (g->h_flags) (void)hipHostFree(g->h_flags);
+    for (hipEvent_t e : g->flag_ev)
+        if (e) (void)hipEventDestroy(e);
     if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
     if (g->stream) (void)hipStreamDestroy(g->stream);
     delete g;
@@ -778,10 +787,14 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         check_hip(hipHostMalloc((void **)&g->h_valid, R), "pinned valid") ||
         check_hip(hipHostMalloc((void **)&g->h_out, (size_t)g->bmax * g->dout * 4), "pinned out") ||
         check_hip(hipHostMalloc((void **)&g->h_plan, plan_layout(g, g->bmax, (int)R).end * 4), "pinned plan") ||
-        check_hip(hipHostMalloc((void **)&g->h_bad, 4, hipHostMallocMapped | hipHostMallocCoherent), "pinned flag") ||
-        check_hip(hipHostGetDevicePointer((void **)&g->d_bad, g->h_bad, 0), "flag device address"))
+        check_hip(hipHostMalloc((void **)&g->h_flags, e2mi_engine::kFlagSlots * 4,
+                                hipHostMallocMapped | hipHostMallocCoherent), "pinned flags") ||
+        check_hip(hipHostGetDevicePointer((void **)&g->d_flags, g->h_flags, 0), "flag device address"))
         return fail();
-    *g->h_bad = 0;
+    for (int k = 0; k < e2mi_engine::kFlagSlots; k++) {
+        g->h_flags[k] = 0;
+        if (check_hip(hipEventCreateWithFlags(&g->flag_ev[k], hipEventDisableTiming), "flag event")) return fail();
+    }
     plan_bind(g, plan_layout(g, g->bmax, (int)R));
     // filler rows of packed batches read contexts that no attention writes: start them at zero; a
     // device-planned forward writes its plan's rows only up to its row count, so the plan's rows
@@ -951,21 +964,45 @@ static int end_call(e2mi_engine *g, hipStream_t s) {
     return 0;
 }
 
+// Read the flags of earlier device-entry calls in call order: those whose work has finished, or,
+// with `wait` > 0, also waiting for the oldest `wait` calls. Stops at the first raised flag: returns
+// its slot (cleared) and leaves the later calls unread; -1 when none was raised, -2 on a HIP error.
+static int read_flags(e2mi_engine *g, int wait) {
+    while (!g->unread.empty()) {
+        const int k = g->unread.front();
+        if (wait > 0) {
+            if (check_hip(hipEventSynchronize(g->flag_ev[k]), "flag event")) return -2;
+            wait--;
+        } else {
+            const hipError_t e = hipEventQuery(g->flag_ev[k]);
+            if (e == hipErrorNotReady) break;
+            if (check_hip(e, "flag event")) return -2;
+        }
+        g->unread.pop_front();
+        if (g->h_flags[k]) {
+            g->h_flags[k] = 0;
+            return k;
+        }
+    }
+    return -1;
+}
+
+static int flag_error(e2mi_engine *g, int slot, int own) {
+    if (slot == -2) return -1;
+    if (slot == own)
+        set_error("text_embed_batch_device: a token id is outside [0,%d); the embeddings are not valid", g->cfg.vocab);
+    else
+        set_error("text_embed_batch_device: a previous asynchronous call had a token id outside [0,%d); its "
+                  "embeddings are not valid", g->cfg.vocab);
+    return -1;
+}
+
 static int begin_call(e2mi_engine *g, hipStream_t s) {
     if (g->last_stream && g->last_stream != s && check_hip(hipStreamSynchronize(g->last_stream), "previous call sync"))
         return -1;
-    if (g->bad_pending) {
-        if (check_hip(hipStreamSynchronize(g->last_stream ? g->last_stream : s), "previous call sync")) return -1;
-        g->bad_pending = false;
-        if (*g->h_bad) {
-            *g->h_bad = 0;
-            g->last_stream = s;
-            set_error("text_embed_batch_device: the previous asynchronous call had a token id outside [0,%d); "
-                      "its embeddings are not valid", g->cfg.vocab);
-            return -1;
-        }
-    }
     g->last_stream = s;
+    const int k = read_flags(g, 0);
+    if (k != -1) return flag_error(g, k, -1);
     for (const ProfEv &e : g->pev) (void)hipEventDestroy(e.a), (void)hipEventDestroy(e.b);  // a failed call's
     g->pev.clear();
     g->prof_rec = g->prof_on && g->calls == 0;
@@ -1032,10 +1069,21 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
     if (begin_call(g, s)) return -1;
     const size_t rows = (size_t)batch * seq_len;
     const double t0 = now_ms();
-    // ids are checked on the device, masked positions included (the embedding kernel also raises
-    // the flag); the flag is read once the stream drains: at the end of this call, or at the next
-    // call when the caller passes a stream
-    if (launch_check_ids(s, ids, (long)rows, g->cfg.vocab, g->d_bad)) return -1;
+    // ids are checked on the device, masked positions included, into this call's flag slot (only the
+    // check kernel writes it; an event after it marks the flag final); the flag is read at the end
+    // of this call, or, with a caller stream, by the first later call that finds the check finished
+    // (a full ring waits for its oldest call)
+    if ((int)g->unread.size() == e2mi_engine::kFlagSlots) {
+        const int k = read_flags(g, 1);
+        if (k != -1) return flag_error(g, k, -1);
+    }
+    const int slot = g->next_slot;
+    g->next_slot = (slot + 1) % e2mi_engine::kFlagSlots;
+    g->h_flags[slot] = 0;
+    if (launch_check_ids(s, ids, (long)rows, g->cfg.vocab, g->d_flags + slot) ||
+        check_hip(hipEventRecord(g->flag_ev[slot], s), "flag event record"))
+        return -1;
+    g->unread.push_back(slot);
     if (!g->packed) {
         if ((long)batch * seq_len > g->R) {
             set_error("text_embed_batch_device: %d x %d rows exceed the engine's %d-row workspace",
@@ -1107,16 +1155,10 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
             if (b0 < batch && check_hip(hipStreamSynchronize(s), "chunk sync")) return -1;
         }
     }
-    if (stream) {
-        g->bad_pending = true;
-    } else {
+    if (!stream) {
         if (check_hip(hipStreamSynchronize(s), "forward sync")) return -1;
-        if (*g->h_bad) {
-            *g->h_bad = 0;
-            set_error("text_embed_batch_device: a token id is outside [0,%d); the embeddings are not valid",
-                      g->cfg.vocab);
-            return -1;
-        }
+        const int k = read_flags(g, (int)g->unread.size());
+        if (k != -1) return flag_error(g, k, slot);
     }
     g->calls++;
     g->last_ms = now_ms() - t0;

@@ -25,9 +25,11 @@ struct PlanDevArgs {
 };
 
 // the plan of n sequences of S tokens with H heads fits one planner workgroup in `slots` entries
-// per list (at least the longest list, H (ceil(n S / 128) + n))
+// per list (at least the longest list, H (ceil(n S / 128) + n)); a work entry holds 127 query blocks
+// of a sequence at most (S <= 16256)
 inline bool plan_device_fits(int n, int S, int H, int slots) {
-    if (n <= 0 || n > kPlanMaxSeqs || S <= 0 || H <= 0 || H > 15 || slots > kPlanMaxItems) return false;
+    if (n <= 0 || n > kPlanMaxSeqs || S <= 0 || S > 16256 || H <= 0 || H > 15 || slots > kPlanMaxItems)
+        return false;
     const long need = (long)H * (((long)n * S + 127) / 128 + n);
     return slots >= need && (long)n * ((S + 7) & ~7) + 256 <= 0x7fffffffL;
 }

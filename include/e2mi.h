@@ -245,7 +245,7 @@ int e2mi_plan_attention(const int32_t *len, int B, int H, int window, int max_pa
  * and work as e2mi_plan_attention gives it unsplit (max_parts 1), followed by -1 up to n_slots
  * entries; with ids [B][S] (device) ids_out gets each packed row's token (0 for filler rows).
  * All pointers are device memory: rowmap, pos and ids_out of B * ceil8(S) + 256 entries, start and
- * len of B, work of n_slots, rows one int. Needs 0 < B <= 1024, 0 < H < 16 and
+ * len of B, work of n_slots, rows one int. Needs 0 < B <= 1024, 0 < S <= 16256, 0 < H < 16 and
  * H * (ceil(B * S / 128) + B) <= n_slots <= 8192. Returns 0, or -1 with the error set. */
 int e2mi_plan_device(e2mi_stream stream, const uint8_t *valid, const int32_t *ids, int B, int S, int H,
                      int window, int div, int n_slots, int32_t *rowmap, int32_t *pos, int32_t *start,
@@ -397,14 +397,18 @@ int e2mi_text_embed_batch(e2mi_engine *g, const int32_t *ids, const uint8_t *val
                           int seq_len, float *out);
 /* The same forward with DEVICE buffers already resident in HBM: ids [batch*seq_len], valid
  * [batch*seq_len], out [batch][hidden]. Enqueued on `stream` (NULL: the engine's own stream, then
- * synchronised). With packed batches the mask is first copied to the host (one synchronous copy of
- * batch*seq_len bytes) to plan the packing, and batches larger than the workspace run in chunks
- * (a chunk with no valid token is filled with zero vectors by a kernel, nothing else runs);
- * unpacked, batch*seq_len must fit the workspace.
+ * synchronised). Packed batches are planned on the device (e2mi_set_device_plan): nothing is read
+ * back, so calls on a caller stream are enqueued back to back; where that planner does not apply
+ * (a batch that could exceed the workspace, the int8 attention, split key ranges, E2MI_DUMP) the
+ * mask is copied to the host (one synchronous copy of batch*seq_len bytes) to plan the packing,
+ * and batches larger than the workspace run in chunks (a chunk with no valid token is filled with
+ * zero vectors by a kernel, nothing else runs); unpacked, batch*seq_len must fit the workspace.
  * Ids are checked on the device, masked positions included (text.c:1008-1013 checks them on the
  * host): an id outside [0, vocab) makes the call return -1 with e2mi_last_error set, and the
- * embeddings it wrote are not valid. With a caller stream the call returns before the forward
- * ends, so the check is reported by the engine's next call (which returns -1 and does no work).
+ * embeddings it wrote are not valid. With a caller stream the call returns before its check has
+ * run, so the check is reported by the first later call of the engine that finds it finished (a
+ * call after the stream was synchronised, or any call on another stream or with NULL, always
+ * does); that call returns -1 and does no work.
  * Calls on one engine are serialised: a call on a stream other than the previous call's first waits
  * for that stream (the calls share the workspace and the pinned staging arrays). */
 int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, const uint8_t *valid,

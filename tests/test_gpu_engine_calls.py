@@ -89,6 +89,27 @@ def test_device_entry_reports_out_of_range_ids(small_engine, rng):
     rc = lib.e2mi_text_embed_batch_device(eng.h, e2mi.ptr(_t(ids, dev)), e2mi.ptr(vt), 3, 64,
                                           e2mi.ptr(out), None)
     assert rc == -1 and "previous" in e2mi.last_error()
+    # on one caller stream: calls are enqueued back to back; once the stream is synchronised the next
+    # call reports the flagged one
+    rc = lib.e2mi_text_embed_batch_device(eng.h, e2mi.ptr(idt), e2mi.ptr(vt), 3, 64, e2mi.ptr(out),
+                                          e2mi.stream_ptr(s))
+    assert rc == 0
+    s.synchronize()
+    gd = _t(ids, dev)
+    rc = lib.e2mi_text_embed_batch_device(eng.h, e2mi.ptr(gd), e2mi.ptr(vt), 3, 64, e2mi.ptr(out),
+                                          e2mi.stream_ptr(s))
+    assert rc == -1 and "previous" in e2mi.last_error()
+    rc = lib.e2mi_text_embed_batch_device(eng.h, e2mi.ptr(gd), e2mi.ptr(vt), 3, 64, e2mi.ptr(out),
+                                          e2mi.stream_ptr(s))
+    assert rc == 0
+    s.synchronize()
+    assert np.array_equal(out.cpu().numpy(), good)
+    # more calls than the engine's 64 flag slots in flight on one stream, all good
+    for _ in range(70):
+        assert lib.e2mi_text_embed_batch_device(eng.h, e2mi.ptr(gd), e2mi.ptr(vt), 3, 64, e2mi.ptr(out),
+                                                e2mi.stream_ptr(s)) == 0
+    s.synchronize()
+    assert np.array_equal(out.cpu().numpy(), good)
     # the engine is usable again, with the right results
     eng.embed_batch_device(_t(ids, dev), vt, out)
     torch.cuda.synchronize()
