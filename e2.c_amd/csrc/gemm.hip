@@ -30,6 +30,8 @@
 #include <type_traits>
 #include <utility>
 
+#include <stddef.h>
+
 #include "common.h"
 
 namespace e2mi {
@@ -60,7 +62,8 @@ struct GemmArgs {
     float *q32, *k32, *v32;
     int qH, qKV, qS;
     float eps;
-    // a device row count (a multiple of 256, at most M; k_gemm_p only), or null: M rows
+    // a device row count (a multiple of 256, at most M; k_gemm_p only, which takes it as its own
+    // first argument), or null: M rows
     const int *rows;
 };
 
@@ -453,14 +456,21 @@ __device__ inline float rms_inv256(float ss, float eps) {
 //  3. q/k: x = (y * inv) * gamma, then a' = a c - b s, b' = b c + a s (products rounded, then the
 //     sum; kernels.c:112-126), f16; v: y * inv, f16, stored transposed per sequence.
 // scr: 3 x 8 x 32 words of the step's free A|W stage (partial sums, inverse rms, positions).
-// The kernel's own GemmArgs (its first argument, at the start of the kernel-argument segment), read
-// through a pointer the compiler cannot follow back to the kernel's entry: the fields read through it
-// are loaded (s_load) where they are used instead of being held in SGPRs across the K loop. The
-// fused q|k|v kernel needs eleven pointers and five scalars in its epilogue only; held for the
-// whole kernel they pushed it past the SGPR file (41 SGPRs spilled).
+// k_gemm_p's arguments as laid out in its kernel-argument segment: the device row count's pointer
+// first (preloaded into SGPRs: gemm.hip is built with -amdgpu-kernarg-preload-count=2, so the count
+// is loaded at once instead of after the argument segment), then the GemmArgs.
+struct PArgsLayout {
+    const int *rows;
+    GemmArgs p;
+};
+// The kernel's own GemmArgs, read through a pointer the compiler cannot follow back to the kernel's
+// entry: the fields read through it are loaded (s_load) where they are used instead of being held
+// in SGPRs across the K loop. The fused q|k|v kernel needs eleven pointers and five scalars in its
+// epilogue only; held for the whole kernel they pushed it past the SGPR file (41 SGPRs spilled).
 typedef const __attribute__((address_space(4))) GemmArgs *KernArgs;
 __device__ __attribute__((always_inline)) inline KernArgs kernel_args() {
-    KernArgs a = (KernArgs)__builtin_amdgcn_kernarg_segment_ptr();
+    KernArgs a = (KernArgs)((const __attribute__((address_space(4))) char *)__builtin_amdgcn_kernarg_segment_ptr() +
+                            offsetof(PArgsLayout, p));
     asm volatile("" : "+s"(a));
     return a;
 }
@@ -604,7 +614,8 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(KernArgs pa
 // 8 waves of 32 x 128 (one 32-row MFMA tile by four 32-column ones): NWM x NWN waves, BM = 32 NWM,
 // BN = 128 NWN
 template <int BM, int BN, int NWM, int NWN, int EPI, bool FAST, int POST, bool NT = false>
-__global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(GemmArgs p, int tiles_n, int tiles) {
+__global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(const int *rows, GemmArgs p, int tiles_n,
+                                                                               int tiles) {
     constexpr int NWAVE = NWM * NWN;
     static_assert(BM == 32 * NWM && BN == 128 * NWN && (NWAVE == 8 || NWAVE == 4), "8 or 4 waves of 32x128");
     constexpr int kPStages = p_stages<NWAVE>(), AHEAD = kPStages - 1;  // loads AHEAD steps ahead
@@ -617,11 +628,11 @@ __global__ __launch_bounds__(NWM * NWN * 64, 8 / (NWM * NWN)) void k_gemm_p(Gemm
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned char *const sscale = smem + kPStages * TILE;
 
-    if (p.rows) {
+    if (rows) {
         // a forward planned on the device: its row count, a multiple of 256, from device memory; the
         // host M sized the grid and, in the q|k|v epilogue (which reads the kernel's arguments
         // again), bounds the stores of tiles that all lie below this count
-        p.M = min(p.M, *p.rows);
+        p.M = min(p.M, *rows);
         tiles = (p.M + BM - 1) / BM * tiles_n;
     }
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1649,7 +1660,7 @@ static int launch_p1(hipStream_t s, const GemmArgs &p) {
         return -1;
     }
     const int grid = (int)min(tiles, (long)num_cus() * (8 / (NWM * NWN)));
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(NWM * NWN * 64), lds, s, p, tiles_n, (int)tiles);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NWM * NWN * 64), lds, s, p.rows, p, tiles_n, (int)tiles);
     return check_hip(hipGetLastError(), "gemm launch");
 }
 
