@@ -27,7 +27,7 @@ int check_hip(hipError_t e, const char *what) {
 
 static thread_local DeviceRows t_rows;
 DeviceRows device_rows() { return t_rows; }
-DeviceRowsScope::DeviceRowsScope(const int *ptr, int mul) : prev_(t_rows) { t_rows = DeviceRows{ptr, mul}; }
+DeviceRowsScope::DeviceRowsScope(const int *ptr, int mul, int est) : prev_(t_rows) { t_rows = DeviceRows{ptr, mul, est}; }
 DeviceRowsScope::~DeviceRowsScope() { t_rows = prev_; }
 
 struct GemmArgs;

@@ -30,15 +30,17 @@ inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 // per-128 GEMMs launched from that thread read their row count from `ptr` (an int in device memory
 // that the planner writes, times `mul`), and the host row count they are given only sizes their
 // grids. Rows past the device count are never read by the rows before them, so the count prunes
-// work only. Unset (null) for every other launch.
+// work only. `est` (> 0) is the host's estimate of that count, from which the GEMMs choose their
+// tile shape (the same results either way). Unset (null) for every other launch.
 struct DeviceRows {
     const int *ptr = nullptr;
     int mul = 1;
+    int est = 0;
 };
 DeviceRows device_rows();
 class DeviceRowsScope {
   public:
-    DeviceRowsScope(const int *ptr, int mul = 1);
+    DeviceRowsScope(const int *ptr, int mul = 1, int est = 0);
     ~DeviceRowsScope();
     DeviceRowsScope(const DeviceRowsScope &) = delete;
     DeviceRowsScope &operator=(const DeviceRowsScope &) = delete;

@@ -149,6 +149,13 @@ struct e2mi_engine {
     hipEvent_t flag_ev[kFlagSlots] = {};
     std::deque<int> unread;
     int next_slot = 0;
+    // a device-planned call's planner also writes its row count into its slot of h_rows (mapped
+    // pinned memory; 0 until written); when the host reads the slot of a finished call it keeps the
+    // count per (sequences, seq_len) in rows_seen, the estimate from which the next calls of that
+    // shape choose their GEMM tile shapes
+    int *d_rows_seen = nullptr, *h_rows = nullptr;
+    std::pair<int, int> slot_shape[kFlagSlots];
+    std::map<std::pair<int, int>, int> rows_seen;
     bool packed = true;
     // (sequences, seq_len, rows, bits: packed 1, split 2, planned on the device 4)
     std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;
@@ -179,6 +186,8 @@ int launch_embed_checked(hipStream_t s, const float *table, int vocab, const int
                          int *bad_id);
 int launch_zero_f32(hipStream_t s, float *p, long n);
 int launch_check_ids(hipStream_t s, const int32_t *ids, long n, int vocab, int *flag);
+// gemm.hip: whether a per-128 GEMM of M x N rows takes 128 x 128 tiles (else 256 x 128)
+bool gemm_half_tiles(int M, int N);
 
 template <class T>
 static int dalloc(e2mi_engine *g, T **p, size_t count) {
@@ -330,9 +339,10 @@ constexpr int kAttnPartTiles = 8, kMaxAttnParts = 4;
 
 // every kernel of one forward over B sequences of S tokens (M rows: B * S padded, or the packed
 // row count), on stream s; returns the launch count or -1
-static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s, bool dev = false) {
-    // dev: planned on the device, Mp rows of capacity; the kernels read the planned count
-    const DeviceRowsScope dev_rows(dev ? g->d_rows : nullptr);
+static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s, bool dev = false, int est = 0) {
+    // dev: planned on the device, Mp rows of capacity; the kernels read the planned count, the GEMMs
+    // choose their tiles for about `est` rows
+    const DeviceRowsScope dev_rows(dev ? g->d_rows : nullptr, 1, est);
     const e2_config &c = g->cfg;
     const int M = pk ? Mp : B * S, Dm = c.hidden, H = c.n_heads, P = c.ple_dim;
     if (M <= 0 || M > g->R) {
@@ -374,7 +384,7 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s,
         const int NP = c.n_layers * P;
         RUN("ple_quant", e2mi_quantize(s, g->qg, g->gs, g->x, M, Dm, Dm, 128));
         RUN("ple_model", e2mi_i8_gemm(s, g->ple32, NP, g->qg, g->gs, &g->ple_model, M, 0, NP));
-        const DeviceRowsScope ple_rows(dev ? g->d_rows : nullptr, c.n_layers);  // n_layers slices per row
+        const DeviceRowsScope ple_rows(dev ? g->d_rows : nullptr, c.n_layers, est);  // n_layers slices per row
         RUN("ple_norm", e2mi_scale_norm(s, g->ple32, M * c.n_layers, P, c.ple_scale, g->ple_proj_norm, eps, g->ple32));
     }
     for (int l = 0; l < nl; l++) {
@@ -452,25 +462,27 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s,
     return k + 1;  // the pool is two launches
 }
 
-static int run_shape(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s, bool dev = false) {
+// dev: planned on the device (est: the expected row count, sig: the GEMM tile shapes it gives)
+static int run_shape(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s, bool dev = false, int est = 0,
+                     int sig = 0) {
     if (!g->use_graph || g->prof_rec) {
-        const int k = enqueue(g, B, S, Mp, pk, s, dev);
+        const int k = enqueue(g, B, S, Mp, pk, s, dev, est);
         if (k < 0) return -1;
         g->kernels_last = k;
         return 0;
     }
-    auto key = std::make_tuple(B, S, Mp, (pk ? 1 : 0) | (pk && g->split_now ? 2 : 0) | (dev ? 4 : 0));
+    auto key = std::make_tuple(B, S, Mp, (pk ? 1 : 0) | (pk && g->split_now ? 2 : 0) | (dev ? 4 : 0) | sig << 3);
     auto it = g->graphs.find(key);
     if (it == g->graphs.end()) {
         // the first call of a shape runs eagerly (kernel attributes get set outside any capture),
         // then the sequence is recorded for every later call
-        const int k = enqueue(g, B, S, Mp, pk, s, dev);
+        const int k = enqueue(g, B, S, Mp, pk, s, dev, est);
         if (k < 0) return -1;
         g->kernels_last = k;
         hipGraph_t graph = nullptr;
         if (check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"))
             return -1;
-        const int k2 = enqueue(g, B, S, Mp, pk, s, dev);
+        const int k2 = enqueue(g, B, S, Mp, pk, s, dev, est);
         const hipError_t e = hipStreamEndCapture(s, &graph);
         if (k2 < 0 || check_hip(e, "end capture")) {
             if (graph) (void)hipGraphDestroy(graph);
@@ -578,6 +590,26 @@ static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
     return Mp;
 }
 
+// The GEMM tile shapes of a device-planned forward of about `est` rows: one bit per distinct output
+// width of the forward's GEMMs whose tile shape follows the row count (gemm_half_tiles)
+static int tile_signature(const e2mi_engine *g, int est) {
+    std::vector<int> ns;
+    for (const LayerDev &L : g->layers) {
+        ns.push_back(L.o.N);
+        ns.push_back(L.down.N);
+        if (!L.qkv_fused) ns.push_back(L.qkv.N);
+        if (g->cfg.ple_dim > 0) ns.push_back(L.ple_gate.N), ns.push_back(L.ple_proj.N);
+    }
+    if (g->cfg.ple_dim > 0) ns.push_back(g->ple_model.N);
+    if (g->cfg.out_dim > 0) ns.push_back(g->embed_proj.N);
+    std::sort(ns.begin(), ns.end());
+    ns.erase(std::unique(ns.begin(), ns.end()), ns.end());
+    int sig = 0;
+    for (size_t i = 0; i < ns.size(); i++)
+        if (gemm_half_tiles(est, ns[i])) sig |= 1 << i;
+    return sig;
+}
+
 // The device entry plans on the device (plan_dev.hip) when the whole batch is one chunk whatever its
 // mask (every token valid: n ceil8(S) rows, rounded up to 256, within the workspace) and its lists fit
 // the planner's workgroup, with the unsplit f16 lists (no int8 attention, no split mode) and no
@@ -666,6 +698,7 @@ extern "C" void e2mi_destroy(e2mi_engine *g) {
     if (g->h_plan) (void)hipHostFree(g->h_plan);
     if (g->h_mask) (void)hipHostFree(g->h_mask);
     if (g->h_flags) (void)hipHostFree(g->h_flags);
+    if (g->h_rows) (void)hipHostFree(g->h_rows);
     for (hipEvent_t e : g->flag_ev)
         if (e) (void)hipEventDestroy(e);
     if (g->last_stream) (void)hipStreamSynchronize(g->last_stream);
@@ -789,10 +822,14 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
         check_hip(hipHostMalloc((void **)&g->h_plan, plan_layout(g, g->bmax, (int)R).end * 4), "pinned plan") ||
         check_hip(hipHostMalloc((void **)&g->h_flags, e2mi_engine::kFlagSlots * 4,
                                 hipHostMallocMapped | hipHostMallocCoherent), "pinned flags") ||
-        check_hip(hipHostGetDevicePointer((void **)&g->d_flags, g->h_flags, 0), "flag device address"))
+        check_hip(hipHostGetDevicePointer((void **)&g->d_flags, g->h_flags, 0), "flag device address") ||
+        check_hip(hipHostMalloc((void **)&g->h_rows, e2mi_engine::kFlagSlots * 4,
+                                hipHostMallocMapped | hipHostMallocCoherent), "pinned row counts") ||
+        check_hip(hipHostGetDevicePointer((void **)&g->d_rows_seen, g->h_rows, 0), "row count device address"))
         return fail();
     for (int k = 0; k < e2mi_engine::kFlagSlots; k++) {
         g->h_flags[k] = 0;
+        g->h_rows[k] = 0;
         if (check_hip(hipEventCreateWithFlags(&g->flag_ev[k], hipEventDisableTiming), "flag event")) return fail();
     }
     plan_bind(g, plan_layout(g, g->bmax, (int)R));
@@ -979,6 +1016,7 @@ static int read_flags(e2mi_engine *g, int wait) {
             if (check_hip(e, "flag event")) return -2;
         }
         g->unread.pop_front();
+        if (g->h_rows[k] > 0) g->rows_seen[g->slot_shape[k]] = g->h_rows[k];
         if (g->h_flags[k]) {
             g->h_flags[k] = 0;
             return k;
@@ -1080,6 +1118,8 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
     const int slot = g->next_slot;
     g->next_slot = (slot + 1) % e2mi_engine::kFlagSlots;
     g->h_flags[slot] = 0;
+    g->h_rows[slot] = 0;
+    g->slot_shape[slot] = std::make_pair(batch, seq_len);
     if (launch_check_ids(s, ids, (long)rows, g->cfg.vocab, g->d_flags + slot) ||
         check_hip(hipEventRecord(g->flag_ev[slot], s), "flag event record"))
         return -1;
@@ -1119,7 +1159,13 @@ extern "C" int e2mi_text_embed_batch_device(e2mi_engine *g, const int32_t *ids, 
         pa.work = g->work;
         pa.work_full = g->work_full;
         pa.rows = g->d_rows;
-        if (launch_plan_packed(s, pa) || run_shape(g, batch, seq_len, cap, true, s, true) ||
+        pa.rows_host = g->d_rows_seen + slot;
+        // the GEMM tiles follow the row count of this shape's latest finished call (the capacity
+        // before one has finished): the same embeddings either way, one recorded forward per choice
+        const auto seen = g->rows_seen.find(std::make_pair(batch, seq_len));
+        const int est = seen != g->rows_seen.end() ? seen->second : cap;
+        if (launch_plan_packed(s, pa) ||
+            run_shape(g, batch, seq_len, cap, true, s, true, est, tile_signature(g, est)) ||
             check_hip(hipMemcpyAsync(out, g->out, (size_t)batch * g->dout * 4, hipMemcpyDeviceToDevice, s),
                       "out D2D"))
             return -1;

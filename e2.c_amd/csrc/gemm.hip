@@ -1822,15 +1822,20 @@ static int check_args(const GemmArgs &p, const char *who, bool rows_ok = true) {
 // 256 x 128 tiles take ceil(tiles / CUs) rounds; 128 x 128 tiles take one unit per full round of
 // two workgroups on every CU, and a last partial round of at most one workgroup per CU about 0.6
 // (a 128 x 128 workgroup alone on its CU).
-static bool half_tiles(const GemmArgs &p) {
+bool gemm_half_tiles(int M, int N) {
     const long C = num_cus();
-    const long t256 = (long)((p.M + 255) / 256) * ((p.N + 127) / 128);
+    const long t256 = (long)((M + 255) / 256) * ((N + 127) / 128);
     if (t256 < C) return true;
-    const long t128 = (long)((p.M + 127) / 128) * ((p.N + 127) / 128);
+    const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
     const long full = t128 / (2 * C), rem = t128 % (2 * C);
     const double r128 = (double)full + (rem == 0 ? 0.0 : rem <= C ? 0.6 : 1.0);
     const double r256 = (double)((t256 + C - 1) / C);
     return r128 <= r256 - 0.3;
+}
+// in a forward planned on the device, for the host's estimate of the planned row count
+static bool half_tiles(const GemmArgs &p) {
+    const int est = p.rows ? device_rows().est : 0;
+    return gemm_half_tiles(est > 0 && est < p.M ? est : p.M, p.N);
 }
 
 int launch_gemm_f32(hipStream_t s, GemmArgs p, bool dump, bool tok = false) {

@@ -22,6 +22,7 @@ struct PlanDevArgs {
     int32_t *ids_out;       // per packed row its token (0 for fillers), or null
     int32_t *work, *work_full;
     int32_t *rows;          // the packed row count
+    int32_t *rows_host;     // ... also written here (mapped host memory), or null
 };
 
 // the plan of n sequences of S tokens with H heads fits one planner workgroup in `slots` entries

@@ -260,7 +260,10 @@ __device__ void plan_lists(const PlanDevArgs &a, int *lds) {
     const int st = block_scan((L + 7) & ~7, misc, &rows8);
     const int M = (rows8 + 255) & ~255;
     if (tid < n) a.start[tid] = st;
-    if (tid == 0) *a.rows = M;
+    if (tid == 0) {
+        *a.rows = M;
+        if (a.rows_host) *a.rows_host = M;
+    }
     for (int r = rows8 + tid; r < M; r += kPlanThreads) {
         a.rowmap[r] = -1;
         a.pos[r] = 0;
