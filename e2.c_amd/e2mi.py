@@ -149,6 +149,14 @@ def load(path: str = LIB_PATH):
         return _lib
     if not os.path.exists(path):
         raise E2MIError(f"{path} is missing: the HIP backend was not built (run __graft_entry__.build())")
+    # torch (ROCm wheels) ships its own HIP runtime under the same soname as the system one this
+    # library links; loaded first, the library would pull in the system runtime and torch would
+    # then run against a second one. Import torch first so the process holds one runtime (torch's,
+    # to which the library's dependency then resolves).
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
