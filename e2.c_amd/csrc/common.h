@@ -49,6 +49,9 @@ class DeviceRowsScope {
     DeviceRows prev_;
 };
 
+// compute units of the current device (256 on the MI355X), cached after the first query
+int num_cus();
+
 }  // namespace e2mi
 
 // ---- device helpers
@@ -95,18 +98,50 @@ __device__ inline uint32_t pack4(int a, int b, int c, int d) {
            ((uint32_t)(d & 0xff) << 24);
 }
 
-// max over the 2^k lanes of a lane group (width <= 64), every lane gets the result
+// The value of lane l ^ O (O a power of two below 64). Within a 16-lane row by DPP, a VALU move
+// (xor 1 and 2 by quad permutes, 4 by the row shifts either way and a select, 8 by a rotation of
+// the row by half); xor 16 by ds_swizzle, xor 32 by ds_bpermute, which go through the LDS unit.
+template <int O>
+__device__ inline float xor_lane(float v) {
+    const int x = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (O == 1) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true);  // quad_perm [1, 0, 3, 2]
+    } else if constexpr (O == 2) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true);  // quad_perm [2, 3, 0, 1]
+    } else if constexpr (O == 4) {
+        const int up = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4, lane - 4
+        const int dn = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, true);  // row_shl:4, lane + 4
+        r = (threadIdx.x & 4) ? up : dn;
+    } else if constexpr (O == 8) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, true);  // row_ror:8
+    } else if constexpr (O == 16) {
+        r = __builtin_amdgcn_ds_swizzle(x, 0x1F | (16 << 10));  // bit mode, xor 16 within 32 lanes
+    } else {
+        static_assert(O == 32, "xor of 1 .. 32");
+        r = __builtin_amdgcn_ds_bpermute((int)((threadIdx.x & 63) ^ 32) << 2, x);
+    }
+    return __builtin_bit_cast(float, r);
+}
+template <int O, int W>
+__device__ inline float xor_max(float v) {
+    if constexpr (O == 0) return v;
+    else return xor_max<O / 2, W>(fmaxf(v, xor_lane<O>(v)));
+}
+template <int O, int W>
+__device__ inline float xor_sum(float v) {
+    if constexpr (O == 0) return v;
+    else return xor_sum<O / 2, W>(v + xor_lane<O>(v));
+}
+// max / sum over the 2^k lanes of a lane group (width <= 64) by the xor butterfly, partners W/2
+// apart first; every lane gets the same result (each step's two operands commute)
 template <int W>
 __device__ inline float group_max(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, W));
-    return v;
+    return xor_max<W / 2, W>(v);
 }
 template <int W>
 __device__ inline float group_sum(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, W);
-    return v;
+    return xor_sum<W / 2, W>(v);
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs; remap so each XCD walks a contiguous

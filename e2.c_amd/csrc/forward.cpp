@@ -60,6 +60,10 @@ struct LayerDev {
     // the q|k|v weight is stored in the fused GEMM's rotate-half pair order (head_dim 256 layers):
     // e2mi_i8_gemm_qkv runs the q/k/v norms and RoPE in its epilogue
     bool qkv_fused = false;
+    // the O (down) projection runs the norm_add after it in its epilogue (768-wide hidden size):
+    // e2mi_i8_gemm_add_norm_quant; the down projection of the PLE geometry keeps its own row kernel
+    // (its norm_add also scales x)
+    bool o_an = false, down_an = false;
 };
 
 static double now_ms() {
@@ -161,6 +165,7 @@ struct e2mi_engine {
     std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;
     bool use_graph = true;
     bool fuse_qkv = true;  // E2MI_NOFUSE=1: the q|k|v GEMM and the norm/RoPE kernel run separately
+    bool fuse_an = true;   // E2MI_NOFUSE_AN=1: the O and down GEMMs and their norm_add run separately
     int layer_limit = 0;
     long calls = 0, kernels_last = 0;
     double last_ms = 0.0;
@@ -188,6 +193,8 @@ int launch_zero_f32(hipStream_t s, float *p, long n);
 int launch_check_ids(hipStream_t s, const int32_t *ids, long n, int vocab, int *flag);
 // gemm.hip: whether a per-128 GEMM of M x N rows takes 128 x 128 tiles (else 256 x 128)
 bool gemm_half_tiles(int M, int N);
+// gemm_an.hip: the 16-row units per workgroup of e2mi_i8_gemm_add_norm_quant at a row count
+int gemm_an_units(int rows);
 
 template <class T>
 static int dalloc(e2mi_engine *g, T **p, size_t count) {
@@ -289,6 +296,8 @@ static int upload_layer(e2mi_engine *g, const e2_model *m, int l, LayerDev &L) {
     }
     if (check_hip(hipMemcpyAsync(L.gu.scale, gus.data(), gus.size() * 4, hipMemcpyHostToDevice, g->stream), "gu scale"))
         return -1;
+    L.o_an = g->fuse_an && c.hidden == 768;
+    L.down_an = L.o_an && c.ple_dim == 0;
     float **norms[7] = {&L.ln_in, &L.ln_attn, &L.ln_pre, &L.ln_ffn, &L.q_norm, &L.k_norm, &L.ple_norm};
     for (int s = 0; s < (c.ple_dim > 0 ? 7 : 6); s++) {
         const size_t n = (s == 4 || s == 5) ? (size_t)L.geo.D : (size_t)c.hidden;
@@ -426,13 +435,25 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s,
             RUN("attention", e2mi_attention(s, g->q16, g->k16, g->vt16, g->valid, B, S, H, KV, D, c.attn_scale,
                                g->cq, g->cs, nullptr));
         }
-        RUN("o_proj", e2mi_i8_gemm(s, g->tmp, Dm, g->cq, g->cs, &L.o, M, 0, Dm));
-        RUN("add_norm", e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_attn, L.ln_pre, eps, M, Dm, g->x, nullptr,
-                                g->qa, g->as));
+        if (L.o_an) {
+            RUN("o_proj+add_norm", e2mi_i8_gemm_add_norm_quant(s, g->cq, g->cs, &L.o, M, g->x, L.ln_attn, L.ln_pre, eps,
+                                                               g->x, nullptr, g->qa, g->as, nullptr));
+        } else {
+            RUN("o_proj", e2mi_i8_gemm(s, g->tmp, Dm, g->cq, g->cs, &L.o, M, 0, Dm));
+            RUN("add_norm", e2mi_add_norm_quant(s, g->tmp, g->x, L.ln_attn, L.ln_pre, eps, M, Dm, g->x, nullptr,
+                                                g->qa, g->as));
+        }
         RUN("gate_up_geglu", e2mi_i8_gemm_geglu(s, g->qg, g->gs, nullptr, g->qa, g->as, &L.gu, M));
-        RUN("down", e2mi_i8_gemm(s, g->tmp, Dm, g->qg, g->gs, &L.down, M, 0, Dm));
         const bool last = l + 1 == nl;
         const float *gnext = last ? g->final_norm : g->layers[l + 1].ln_in;
+        if (L.down_an) {
+            RUN("down+add_norm", e2mi_i8_gemm_add_norm_quant(s, g->qg, g->gs, &L.down, M, g->x, L.ln_ffn, gnext, eps, g->x,
+                                                             last ? g->xn : nullptr,
+                                                             !last || c.out_dim > 0 ? g->qa : nullptr,
+                                                             !last || c.out_dim > 0 ? g->as : nullptr, nullptr));
+            continue;
+        }
+        RUN("down", e2mi_i8_gemm(s, g->tmp, Dm, g->qg, g->gs, &L.down, M, 0, Dm));
         if (P > 0) {
             // post_ffn norm_add, x itself quantized for the PLE gate; the PLE block; layer scale
             RUN("add_norm", e2mi_add_norm_scale_quant(s, g->tmp, g->x, L.ln_ffn, 1.0f, nullptr, eps, M, Dm, g->x, nullptr,
@@ -595,8 +616,8 @@ static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
 static int tile_signature(const e2mi_engine *g, int est) {
     std::vector<int> ns;
     for (const LayerDev &L : g->layers) {
-        ns.push_back(L.o.N);
-        ns.push_back(L.down.N);
+        if (!L.o_an) ns.push_back(L.o.N);
+        if (!L.down_an) ns.push_back(L.down.N);
         if (!L.qkv_fused) ns.push_back(L.qkv.N);
         if (g->cfg.ple_dim > 0) ns.push_back(L.ple_gate.N), ns.push_back(L.ple_proj.N);
     }
@@ -607,6 +628,8 @@ static int tile_signature(const e2mi_engine *g, int est) {
     int sig = 0;
     for (size_t i = 0; i < ns.size(); i++)
         if (gemm_half_tiles(est, ns[i])) sig |= 1 << i;
+    // the row units per workgroup of the GEMMs with the norm_add (1-5), in the bits above
+    if (!g->layers.empty() && g->layers[0].o_an) sig |= gemm_an_units(est) << 16;
     return sig;
 }
 
@@ -730,6 +753,8 @@ extern "C" e2mi_engine *e2mi_create_rows(const e2_model *m, int max_rows) {
     g->use_graph = !(ng && ng[0] && ng[0] != '0');
     const char *nf = getenv("E2MI_NOFUSE");
     g->fuse_qkv = !(nf && nf[0] && nf[0] != '0');
+    const char *na = getenv("E2MI_NOFUSE_AN");
+    g->fuse_an = !(na && na[0] && na[0] != '0');
     const char *dp = getenv("E2MI_DEVICE_PLAN");  // 1 (default) | 0
     g->device_plan = !(dp && dp[0] == '0');
     const char *ns = getenv("E2MI_SPLIT");  // 0 (default) | 1 | auto

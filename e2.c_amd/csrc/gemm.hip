@@ -230,6 +230,7 @@ static bool fold_fast() {
     }
     return g_fold == 1;
 }
+bool gemm_fold_fast() { return fold_fast(); }
 
 // ---------------------------------------------------------------------------------------------
 // Persistent pipelined kernel (the production path). One 512-thread workgroup per CU walks a list
@@ -1628,7 +1629,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_tq(GemmArgs p, int tiles_n, int
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-static int num_cus() {
+int num_cus() {
     static int cus = 0;
     if (!cus) {
         int dev = 0;

@@ -18,6 +18,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "rowmath.h"
 
 namespace e2mi {
 
@@ -45,20 +46,6 @@ struct RowArgs {
     const int *rows = nullptr;  // device row count (times rows_mul, at most M), or null: M
     int rows_mul = 1;
 };
-
-__device__ inline float4 ld4(const float *p) { return *(const float4 *)p; }
-__device__ inline void st4(float *p, float4 v) { *(float4 *)p = v; }
-__device__ inline float sumsq4(float4 v) { return v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w; }
-__device__ inline float amax4(float4 v) {
-    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-}
-__device__ inline float rms_inv(float ss, int D, float eps) {
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)D) + eps));
-}
-__device__ inline float4 scale4(float4 v, float inv, float4 g) {
-    return make_float4(__fmul_rn(__fmul_rn(v.x, inv), g.x), __fmul_rn(__fmul_rn(v.y, inv), g.y),
-                       __fmul_rn(__fmul_rn(v.z, inv), g.z), __fmul_rn(__fmul_rn(v.w, inv), g.w));
-}
 
 // NC = float4 chunks per lane = D / 256 (rounded up); chunk i of lane l covers elements
 // 4*(l + 64 i) .. +3, so quantization block (4*(l+64i))/128 = 2i + l/32.
