@@ -98,9 +98,12 @@ __device__ inline uint32_t pack4(int a, int b, int c, int d) {
            ((uint32_t)(d & 0xff) << 24);
 }
 
-// The value of lane l ^ O (O a power of two below 64). Within a 16-lane row by DPP, a VALU move
-// (xor 1 and 2 by quad permutes, 4 by the row shifts either way and a select, 8 by a rotation of
-// the row by half); xor 16 by ds_swizzle, xor 32 by ds_bpermute, which go through the LDS unit.
+// The value of lane l ^ O (O a power of two below 64), by VALU operations only. Within a 16-lane
+// row by DPP (xor 1 and 2 by quad permutes, 4 by the row shifts either way and a select, 8 by a
+// rotation of the row by half); xor 16 and 32 by gfx950's lane swaps of a register with itself:
+// v_permlane16_swap exchanges the odd 16-lane rows of its first operand with the even rows of its
+// second, v_permlane32_swap the upper 32 lanes of the first with the lower 32 of the second, so the
+// partner of a lane with bit O clear is in the second result and of one with it set in the first.
 template <int O>
 __device__ inline float xor_lane(float v) {
     const int x = __builtin_bit_cast(int, v);
@@ -116,10 +119,12 @@ __device__ inline float xor_lane(float v) {
     } else if constexpr (O == 8) {
         r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, true);  // row_ror:8
     } else if constexpr (O == 16) {
-        r = __builtin_amdgcn_ds_swizzle(x, 0x1F | (16 << 10));  // bit mode, xor 16 within 32 lanes
+        const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        r = (threadIdx.x & 16) ? (int)p[0] : (int)p[1];
     } else {
         static_assert(O == 32, "xor of 1 .. 32");
-        r = __builtin_amdgcn_ds_bpermute((int)((threadIdx.x & 63) ^ 32) << 2, x);
+        const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        r = (threadIdx.x & 32) ? (int)p[0] : (int)p[1];
     }
     return __builtin_bit_cast(float, r);
 }

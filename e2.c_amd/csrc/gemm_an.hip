@@ -26,8 +26,8 @@
 //    tile (lane l: column l % 16, rows 4 (l / 16) + i in register i).
 // Every wave issues the same loads in the same order, so its waits are fixed counts: 12 loads are
 // issued after any A group or W piece before the wave waits for it.
-// Epilogue, per 16-row unit: the f32 tile goes through LDS (staging [16][772] floats in the ring's
-// space) into the row kernel's layout (a row per wave, lane l holding chunks l, l + 64, l + 128)
+// Epilogue, per 16-row unit: the f32 tile goes through LDS (two staging buffers of [16][772] floats in
+// the rings' and A stages' space, one barrier a unit) into the row kernel's layout (a row per wave, lane l holding chunks l, l + 64, l + 128)
 // and the norm_add runs with the row kernel's arithmetic (rowmath.h), two rows per wave, their
 // residual rows loaded before the tile is staged.
 #include <algorithm>
@@ -65,7 +65,8 @@ constexpr int kAnOffA = 8 * kAnRing;
 constexpr int kAnOffS = kAnOffA + 2 * kAnAStage;
 constexpr int kAnOffDummy = kAnOffS + 2 * kAnSStage;
 constexpr int kAnLds = kAnOffDummy + 256;
-static_assert(16 * kAnPitch * 4 <= kAnOffA, "staging fits in the W rings");
+constexpr int kAnStage = 16 * kAnPitch;    // one staged 16-row unit, floats
+static_assert(2 * kAnStage * 4 <= kAnOffS, "two staged units fit in the W rings and A stages");
 static_assert(kAnLds <= 160 * 1024, "LDS budget");
 
 // A workgroup barrier that orders LDS only: __syncthreads() also waits for every global load and
@@ -238,14 +239,14 @@ __global__ __launch_bounds__(512, 1) void k_gemm_an(const int *rows, AnArgs a) {
             for (int c = 0; c < 6; c++)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    stg[(4 * (lane >> 4) + i) * kAnPitch + wave * 96 + 16 * c + (lane & 15)] =
+                    stg[(u & 1) * kAnStage + (4 * (lane >> 4) + i) * kAnPitch + wave * 96 + 16 * c + (lane & 15)] =
                         FAST ? __fmul_rn(f[u][c][i], wsr[c]) : f[u][c][i];
             lds_barrier();
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 const int m = mm[j];
                 if (m >= Mr) continue;
-                const float *srow = stg + (2 * wave + j) * kAnPitch;
+                const float *srow = stg + (u & 1) * kAnStage + (2 * wave + j) * kAnPitch;
                 // x = rmsnorm(y) * gamma_a + res, the row kernel's steps (rowops.hip, ROW_ADDNORM)
                 float4 v[3];
                 float ss = 0.f;
@@ -287,7 +288,6 @@ __global__ __launch_bounds__(512, 1) void k_gemm_an(const int *rows, AnArgs a) {
                     if ((lane & 31) == 0) a.qs[(size_t)m * (kAnD / kQBlock) + (4 * c) / kQBlock] = s.sc;
                 }
             }
-            lds_barrier();
         }
     }
 }
