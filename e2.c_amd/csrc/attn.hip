@@ -76,7 +76,7 @@ __device__ __forceinline__ float softmax_tile(const float (&s)[16], float c, flo
     float mloc = s[0];
 #pragma unroll
     for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, s[r]);
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    mloc = fmaxf(mloc, xor_lane<32>(mloc));
     const float mc = mloc * c;
     float alpha = 1.f;
     if (mc > mrun + kTau) {
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     }
 
     // normalise, quantise per 128 dims (tiles 0-3 and 4-7), store
-    const float ltot = lrun + __shfl_xor(lrun, 32);
+    const float ltot = lrun + xor_lane<32>(lrun);
     const float inv = (qvalid && ltot > 0.f) ? __fdiv_rn(1.0f, ltot) : 0.f;
 #pragma unroll
     for (int t = 0; t < 8; t++) o[t] *= inv;
@@ -232,7 +232,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
         for (int t = 4 * blk; t < 4 * blk + 4; t++)
 #pragma unroll
             for (int r = 0; r < 16; r++) am = fmaxf(am, fabsf(o[t][r]));
-        am = fmaxf(am, __shfl_xor(am, 32));
+        am = fmaxf(am, xor_lane<32>(am));
         const QScale qs = qscale(am);
 #pragma unroll
         for (int t = 4 * blk; t < 4 * blk + 4; t++)
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    const float ltot = lrun + __shfl_xor(lrun, 32);
+    const float ltot = lrun + xor_lane<32>(lrun);
     if (parts > 1) {
         // a partial state: the context sum, the row max and the row sum (mrun is the pair's)
         if (qi >= Sk) return;
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
         for (int t = 4 * blk; t < 4 * blk + 4; t++)
 #pragma unroll
             for (int r = 0; r < 16; r++) am = fmaxf(am, fabsf(o[t][r]));
-        am = fmaxf(am, __shfl_xor(am, 32));
+        am = fmaxf(am, xor_lane<32>(am));
         const QScale qs = qscale(am);
 #pragma unroll
         for (int t = 4 * blk; t < 4 * blk + 4; t++)
@@ -670,7 +670,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    const float ltot = lrun + __shfl_xor(lrun, 32);
+    const float ltot = lrun + xor_lane<32>(lrun);
     const float inv = (qvalid && ltot > 0.f) ? __fdiv_rn(1.0f, ltot) : 0.f;
 #pragma unroll
     for (int t = 0; t < 8; t++) o[t] *= inv;
@@ -684,7 +684,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
         for (int t = 4 * blk; t < 4 * blk + 4; t++)
 #pragma unroll
             for (int r = 0; r < 16; r++) am = fmaxf(am, fabsf(o[t][r]));
-        am = fmaxf(am, __shfl_xor(am, 32));
+        am = fmaxf(am, xor_lane<32>(am));
         const QScale qs = qscale(am);
 #pragma unroll
         for (int t = 4 * blk; t < 4 * blk + 4; t++)

@@ -297,7 +297,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
         float mloc = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) mloc = fmaxf(mloc, s[r]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        mloc = fmaxf(mloc, xor_lane<32>(mloc));
         const float mnew = fmaxf(mrun, mloc);
         if (mnew > -INFINITY) {
             float ps = 0.f;
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
             mrun = mnew;
         }
     }
-    const float ltot = lrun + __shfl_xor(lrun, 32);
+    const float ltot = lrun + xor_lane<32>(lrun);
     const float inv_l = ltot > 0.f ? __fdiv_rn(1.0f, ltot) : 0.f;
 
     v16i acco[8];
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
                 for (int r = 0; r < 16; r++) pv[t][r] = 0.f;
             }
         }
-        am = fmaxf(am, __shfl_xor(am, 32));
+        am = fmaxf(am, xor_lane<32>(am));
         const QScale ps = qscale(am);
         v4i pq[4];
 #pragma unroll
@@ -383,7 +383,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_i8(AttnI8Args a) {
         for (int dt = 4 * blk; dt < 4 * blk + 4; dt++)
 #pragma unroll
             for (int r = 0; r < 16; r++) am = fmaxf(am, fabsf(of[dt][r]));
-        am = fmaxf(am, __shfl_xor(am, 32));
+        am = fmaxf(am, xor_lane<32>(am));
         const QScale qs = qscale(am);
 #pragma unroll
         for (int dt = 4 * blk; dt < 4 * blk + 4; dt++)

@@ -260,8 +260,8 @@ __global__ __launch_bounds__(256) void k_qkv_norm_rope(QkvArgs a, int nv) {
     const float *cp = a.cs + (size_t)pos * D, *sp = a.sn + (size_t)pos * D;
     if (NCH == 1) {
         const float4 c = ld4(cp + 4 * l), s = ld4(sp + 4 * l);
-        const float4 o = make_float4(__shfl_xor(v[0].x, 32), __shfl_xor(v[0].y, 32), __shfl_xor(v[0].z, 32),
-                                     __shfl_xor(v[0].w, 32));
+        const float4 o = make_float4(xor_lane<32>(v[0].x), xor_lane<32>(v[0].y), xor_lane<32>(v[0].z),
+                                     xor_lane<32>(v[0].w));
         if (l < 32) v[0] = rot_lo(v[0], o, c, s);
         else v[0] = rot_hi(v[0], o, c, s);
     } else {
