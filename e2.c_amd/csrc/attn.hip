@@ -340,10 +340,6 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
         kt0 = t0 + n * part / parts;
         kt1 = t0 + n * (part + 1) / parts;
     }
-    // wait for the Q loads here, with a wait the compiler's wait-count pass sees: otherwise it
-    // waits for them inside the tile loop, where the count would also cover the tile loads in
-    // flight (s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15))
-    __builtin_amdgcn_s_waitcnt(0x0F70);
     f16v o[NO];
 #pragma unroll
     for (int t = 0; t < NO; t++) o[t] = (f16v){};
@@ -400,6 +396,11 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
     if (kt0 < kt1)
 #pragma unroll
         for (int j = 0; j < NLK + NLV; j++) issue_load(kt0, j);
+    // wait for the Q loads here, after the first tile's loads are issued (the two latencies
+    // overlap), with a wait the compiler's wait-count pass sees: otherwise it waits for them inside
+    // the tile loop, where the count would also cover the tile loads in flight (s_waitcnt vmcnt(0)
+    // expcnt(7) lgkmcnt(15))
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     for (int kt = kt0; kt < kt1; kt++) {
         const int k0 = kt * kKT;
         // this wave's loads of tile kt have landed; the barrier makes every wave's visible and
@@ -562,7 +563,6 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
         pq1 = a.pos ? a.pos[row0 + q1] : q1;
         pqi = a.pos ? a.pos[row0 + qc] : qc;
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // the Q loads, before the tile loop (see k_attn_packed)
     f16v o[8];
 #pragma unroll
     for (int t = 0; t < 8; t++) o[t] = (f16v){};
@@ -608,6 +608,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
     if (kt0 < kt1)
 #pragma unroll
         for (int j = 0; j < 8; j++) issue_load(kt0, j);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // the Q loads, after the first tile's (see k_attn_packed)
     for (int kt = kt0; kt < kt1; kt++) {
         const int k0 = kt * kKT;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
