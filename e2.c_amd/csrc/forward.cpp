@@ -60,9 +60,9 @@ struct LayerDev {
     // the q|k|v weight is stored in the fused GEMM's rotate-half pair order (head_dim 256 layers):
     // e2mi_i8_gemm_qkv runs the q/k/v norms and RoPE in its epilogue
     bool qkv_fused = false;
-    // the O (down) projection runs the norm_add after it in its epilogue (768-wide hidden size):
-    // e2mi_i8_gemm_add_norm_quant; the down projection of the PLE geometry keeps its own row kernel
-    // (its norm_add also scales x)
+    // the O and down projections (and the PLE projection) run the norm_add after them in their
+    // epilogue (hidden size 768 or 512): e2mi_i8_gemm_add_norm_quant, and at the PLE geometry
+    // e2mi_i8_gemm_add_norm_scale_quant for the norm_adds that scale or quantize x itself
     bool o_an = false, down_an = false;
 };
 
@@ -193,8 +193,10 @@ int launch_zero_f32(hipStream_t s, float *p, long n);
 int launch_check_ids(hipStream_t s, const int32_t *ids, long n, int vocab, int *flag);
 // gemm.hip: whether a per-128 GEMM of M x N rows takes 128 x 128 tiles (else 256 x 128)
 bool gemm_half_tiles(int M, int N);
-// gemm_an.hip: the 16-row units per workgroup of e2mi_i8_gemm_add_norm_quant at a row count
+// gemm_an.hip: the 16-row units per workgroup of e2mi_i8_gemm_add_norm_quant at a row count, and
+// whether one round of the CUs covers that count
 int gemm_an_units(int rows);
+bool gemm_an_fits(int rows);
 
 template <class T>
 static int dalloc(e2mi_engine *g, T **p, size_t count) {
@@ -296,8 +298,8 @@ static int upload_layer(e2mi_engine *g, const e2_model *m, int l, LayerDev &L) {
     }
     if (check_hip(hipMemcpyAsync(L.gu.scale, gus.data(), gus.size() * 4, hipMemcpyHostToDevice, g->stream), "gu scale"))
         return -1;
-    L.o_an = g->fuse_an && c.hidden == 768;
-    L.down_an = L.o_an && c.ple_dim == 0;
+    L.o_an = g->fuse_an && (c.hidden == 768 || c.hidden == 512);
+    L.down_an = L.o_an;
     float **norms[7] = {&L.ln_in, &L.ln_attn, &L.ln_pre, &L.ln_ffn, &L.q_norm, &L.k_norm, &L.ple_norm};
     for (int s = 0; s < (c.ple_dim > 0 ? 7 : 6); s++) {
         const size_t n = (s == 4 || s == 5) ? (size_t)L.geo.D : (size_t)c.hidden;
@@ -354,6 +356,9 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s,
     const DeviceRowsScope dev_rows(dev ? g->d_rows : nullptr, 1, est);
     const e2_config &c = g->cfg;
     const int M = pk ? Mp : B * S, Dm = c.hidden, H = c.n_heads, P = c.ple_dim;
+    // the projections with their norm_add in the epilogue when one round of the CUs covers the
+    // (expected) rows; past that each workgroup's weight fetch costs more than the f32 round trip
+    const bool an = gemm_an_fits(dev && est > 0 ? est : M);
     if (M <= 0 || M > g->R) {
         set_error("forward: %d rows for a %d-row workspace", M, g->R);
         return -1;
@@ -435,7 +440,7 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s,
             RUN("attention", e2mi_attention(s, g->q16, g->k16, g->vt16, g->valid, B, S, H, KV, D, c.attn_scale,
                                g->cq, g->cs, nullptr));
         }
-        if (L.o_an) {
+        if (L.o_an && an) {
             RUN("o_proj+add_norm", e2mi_i8_gemm_add_norm_quant(s, g->cq, g->cs, &L.o, M, g->x, L.ln_attn, L.ln_pre, eps,
                                                                g->x, nullptr, g->qa, g->as, nullptr));
         } else {
@@ -446,7 +451,19 @@ static int enqueue(e2mi_engine *g, int B, int S, int Mp, bool pk, hipStream_t s,
         RUN("gate_up_geglu", e2mi_i8_gemm_geglu(s, g->qg, g->gs, nullptr, g->qa, g->as, &L.gu, M));
         const bool last = l + 1 == nl;
         const float *gnext = last ? g->final_norm : g->layers[l + 1].ln_in;
-        if (L.down_an) {
+        if (L.down_an && an && P > 0) {
+            // post_ffn norm_add in the down projection, x itself quantized for the PLE gate; the PLE
+            // block, its norm_add and the layer scale in the PLE projection
+            RUN("down+add_norm", e2mi_i8_gemm_add_norm_scale_quant(s, g->qg, g->gs, &L.down, M, g->x, L.ln_ffn, 1.0f,
+                                                                   nullptr, eps, g->x, nullptr, g->qa, g->as, nullptr));
+            RUN("ple_gate", e2mi_i8_gemm_gelu_mul(s, g->qg, g->gs, nullptr, g->qa, g->as, &L.ple_gate, M,
+                                                  g->ple32 + (size_t)l * P, c.n_layers * P));
+            RUN("ple_proj+add_norm", e2mi_i8_gemm_add_norm_scale_quant(s, g->qg, g->gs, &L.ple_proj, M, g->x, L.ple_norm,
+                                                                       L.layer_scalar, gnext, eps, g->x,
+                                                                       last ? g->xn : nullptr, g->qa, g->as, nullptr));
+            continue;
+        }
+        if (L.down_an && an) {
             RUN("down+add_norm", e2mi_i8_gemm_add_norm_quant(s, g->qg, g->gs, &L.down, M, g->x, L.ln_ffn, gnext, eps, g->x,
                                                              last ? g->xn : nullptr,
                                                              !last || c.out_dim > 0 ? g->qa : nullptr,
@@ -615,11 +632,15 @@ static int plan_pack(e2mi_engine *g, const uint8_t *valid, int n, int S) {
 // width of the forward's GEMMs whose tile shape follows the row count (gemm_half_tiles)
 static int tile_signature(const e2mi_engine *g, int est) {
     std::vector<int> ns;
+    const bool an = gemm_an_fits(est);
     for (const LayerDev &L : g->layers) {
-        if (!L.o_an) ns.push_back(L.o.N);
-        if (!L.down_an) ns.push_back(L.down.N);
+        if (!(L.o_an && an)) ns.push_back(L.o.N);
+        if (!(L.down_an && an)) ns.push_back(L.down.N);
         if (!L.qkv_fused) ns.push_back(L.qkv.N);
-        if (g->cfg.ple_dim > 0) ns.push_back(L.ple_gate.N), ns.push_back(L.ple_proj.N);
+        if (g->cfg.ple_dim > 0) {
+            ns.push_back(L.ple_gate.N);
+            if (!(L.down_an && an)) ns.push_back(L.ple_proj.N);
+        }
     }
     if (g->cfg.ple_dim > 0) ns.push_back(g->ple_model.N);
     if (g->cfg.out_dim > 0) ns.push_back(g->embed_proj.N);
@@ -628,8 +649,8 @@ static int tile_signature(const e2mi_engine *g, int est) {
     int sig = 0;
     for (size_t i = 0; i < ns.size(); i++)
         if (gemm_half_tiles(est, ns[i])) sig |= 1 << i;
-    // the row units per workgroup of the GEMMs with the norm_add (1-5), in the bits above
-    if (!g->layers.empty() && g->layers[0].o_an) sig |= gemm_an_units(est) << 16;
+    // whether the GEMMs with the norm_add run, and their row units per workgroup (1-5), in the bits above
+    if (!g->layers.empty() && g->layers[0].o_an && an) sig |= 1 << 15 | gemm_an_units(est) << 16;
     return sig;
 }
 

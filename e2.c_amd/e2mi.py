@@ -72,6 +72,8 @@ SIGNATURES = {
     "e2mi_add_norm_quant": (_I, [_P, _P, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P]),
     "e2mi_i8_gemm_add_norm_quant": (_I, [_P, _P, _P, C.POINTER(Q8W), _I, _P, _P, _P, _F, _P, _P, _P, _P,
                                          _P]),
+    "e2mi_i8_gemm_add_norm_scale_quant": (_I, [_P, _P, _P, C.POINTER(Q8W), _I, _P, _P, _F, _P, _F, _P, _P, _P,
+                                               _P, _P]),
     "e2mi_embed_norm_quant": (_I, [_P, _P, _I, _P, _F, _P, _F, _I, _I, _P, _P, _P]),
     "e2mi_qkv_norm_rope": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P]),
     "e2mi_gelu_mul_quant": (_I, [_P, _P, _I, _P, _I, _I, _I, _P, _P, _I]),
@@ -384,6 +386,25 @@ def i8_gemm_add_norm_quant(qa, as_, w: DeviceWeight, res, gamma_add, gamma_next=
     check(load().e2mi_i8_gemm_add_norm_quant(stream_ptr(stream), ptr(qa), ptr(as_), w.ref, M, ptr(res),
                                              ptr(gamma_add), ptr(gamma_next), eps, ptr(x_out), ptr(xn),
                                              ptr(q), ptr(qs), ptr(y)), "i8_gemm_add_norm_quant")
+    return x_out, xn, q, qs, y
+
+
+def i8_gemm_add_norm_scale_quant(qa, as_, w: DeviceWeight, res, gamma_add, post_scale, gamma_next=None,
+                                 eps=1e-6, x_out=None, want_xn=True, quant=True, want_y=False, stream=None):
+    """e2mi_i8_gemm_add_norm_scale_quant: i8_gemm then add_norm_scale_quant in one kernel (512-wide
+    rows); returns (x, xn, q, qs, y); without gamma_next, q/qs quantize x itself."""
+    import torch
+    M, D = res.shape
+    x_out = torch.empty_like(res) if x_out is None else x_out
+    has_next = gamma_next is not None
+    xn = torch.empty_like(res) if (want_xn and has_next) else None
+    q = torch.empty((M, D), dtype=torch.int8, device=res.device) if quant else None
+    qs = torch.empty((M, D // 128), dtype=torch.float32, device=res.device) if quant else None
+    y = torch.empty_like(res) if want_y else None
+    check(load().e2mi_i8_gemm_add_norm_scale_quant(stream_ptr(stream), ptr(qa), ptr(as_), w.ref, M, ptr(res),
+                                                   ptr(gamma_add), post_scale, ptr(gamma_next), eps, ptr(x_out),
+                                                   ptr(xn), ptr(q), ptr(qs), ptr(y)),
+          "i8_gemm_add_norm_scale_quant")
     return x_out, xn, q, qs, y
 
 

@@ -154,15 +154,24 @@ int e2mi_add_norm_quant(e2mi_stream stream, const float *src, const float *res,
                         float *x_out, float *xn_out, int8_t *q, float *qs);
 
 /* A projection that feeds a norm_add, with the norm_add in its epilogue: y = e2mi_i8_gemm(qa, w)
- * (w: N = 768 rows, K a multiple of 128, no bias or clamp), then e2mi_add_norm_quant(y, res,
- * gamma_add, gamma_next, eps, M, 768, x_out, xn_out, q, qs), with the same bits as those two calls
- * and without y in memory (the text tower's O and down projections and the norm_add after each,
- * text.c:944-953; the reference computes them as two passes, so this entry point has no single
- * counterpart). y [M][768] f32 is also written when non-NULL (parity tests). x_out may alias res. */
+ * (w: N = D = 768 or 512 rows, K a multiple of 128, no bias or clamp), then
+ * e2mi_add_norm_quant(y, res, gamma_add, gamma_next, eps, M, D, x_out, xn_out, q, qs), with the same
+ * bits as those two calls and without y in memory (the text tower's O and down projections and the
+ * norm_add after each, text.c:944-953; the reference computes them as two passes, so this entry
+ * point has no single counterpart). y [M][D] f32 is also written when non-NULL (parity tests).
+ * x_out may alias res. */
 int e2mi_i8_gemm_add_norm_quant(e2mi_stream stream, const int8_t *qa, const float *a_scales,
                                 const e2mi_q8w *w, int M, const float *res, const float *gamma_add,
                                 const float *gamma_next, float eps, float *x_out, float *xn_out,
                                 int8_t *q, float *qs, float *y);
+
+/* The same with e2mi_add_norm_scale_quant as the norm_add (the reference checkpoint's PLE layers,
+ * text.c:955-961: x scaled by post_scale after the add; without gamma_next, x itself quantized into
+ * q/qs): w must have N = 512 rows. */
+int e2mi_i8_gemm_add_norm_scale_quant(e2mi_stream stream, const int8_t *qa, const float *a_scales,
+                                      const e2mi_q8w *w, int M, const float *res, const float *gamma_add,
+                                      float post_scale, const float *gamma_next, float eps, float *x_out,
+                                      float *xn_out, int8_t *q, float *qs, float *y);
 
 /* Embedding gather (text.c:917-921) fused with the first layer's norm_split + quantize:
  * x = table[ids[m]] * embed_scale -> x_out; rmsnorm(x)*gamma quantized into q/qs. Device-side ids
