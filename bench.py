@@ -768,15 +768,26 @@ def summarize_enc_ktrace(trace_csv):
             if "k_pool_finish" in n:
                 fwd.append(cur)
                 cur = None
-    # forwards grouped by their row count (the embedding kernel's grid): one batch shape each;
-    # the first forward of each group (eager, before the graph) is left out
+    # forwards grouped by their row count (the embedding kernel's grid) and launch count: one batch
+    # shape each where the engine picks different kernels per batch (the fused norm_add projections
+    # only where one round of the CUs covers the rows); of each run of consecutive forwards with the
+    # same key the first (eager, before the graph, or the graph's first replay) is left out
     groups = collections.OrderedDict()
+    prev = None
     for f in fwd:
-        groups.setdefault(f[0]["Grid_Size_X"], []).append(f)
-    for grid, fl in groups.items():
-        f16 = [f for f in fl[1:] if not any("k_attn_i8" in name(r) for r in f)]
-        i8 = [f for f in fl if any("k_attn_i8" in name(r) for r in f)]
+        key = (f[0]["Grid_Size_X"], len(f))
+        fl = groups.setdefault(key, [[], []])  # [kept, left out]
+        fl[0 if key == prev else 1].append(f)
+        prev = key
+    for (grid, _), (kept, first) in groups.items():
+        f16 = [f for f in kept if not any("k_attn_i8" in name(r) for r in f)]
+        i8 = [f for f in kept + first if any("k_attn_i8" in name(r) for r in f)]
         if not f16:
+            if i8:
+                k8 = [sum(dur(r) for r in f) for f in i8]
+                lines += ["", f"forwards of {int(grid) // 64} rows (embedding grid {grid}): {len(i8)} "
+                          f"int8-attention forwards, {len(i8[0])} launches each; per forward: kernels "
+                          f"{np.mean(k8) / 1e3:.3f} ms"]
             continue
         stage = collections.defaultdict(list)
         for f in f16:
@@ -789,7 +800,7 @@ def summarize_enc_ktrace(trace_csv):
         kern = [sum(dur(r) for r in f) for f in f16]
         span = [(int(f[-1]["End_Timestamp"]) - int(f[0]["Start_Timestamp"])) / 1e3 for f in f16]
         lines += ["", f"forwards of {int(grid) // 64} rows (embedding grid {grid}): {len(f16)} f16-attention "
-                  f"forwards after the eager one, {len(f16[0])} launches each, {nl} layers; int8-attention "
+                  f"forwards (the first of each run left out), {len(f16[0])} launches each, {nl} layers; int8-attention "
                   f"forwards: {len(i8)}; per forward: kernels {np.mean(kern) / 1e3:.3f} ms, first launch "
                   f"start to last launch end {np.mean(span) / 1e3:.3f} ms", "",
                   "| kernel | per forward us | % | per layer us |", "|---|---:|---:|---:|"]
