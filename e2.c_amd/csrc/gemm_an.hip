@@ -19,13 +19,17 @@
 // columns D/8 w .. + D/8 - 1 (NCU = D/128 16-column units) of every row of its range as f32 running
 // sums (UC x 4 NCU registers). K is walked in 128-deep blocks, one quantization block each, as the
 // fold needs:
-//  - A (1-KB pieces of 16 rows x 64 bytes, one per (row unit, K half)) and the block's activation
-//    scales go to LDS by direct-to-LDS loads one block ahead (two stages), two loads per wave per
-//    block (a dummy where the pieces run out, so every wave issues the same count);
-//  - each wave's W rows go to a wave-private LDS ring of 2 NCU pieces, one per (column unit, K
-//    half), one block ahead; a piece is refilled as soon as the wave has read it;
-//  - a piece holds lane l's 16 operand bytes at 16 l (row l % 16, K bytes 16 (l / 16) .. + 15 of
-//    its half), so every fragment read is one contiguous ds_read_b128;
+//  - A (2-KB pieces of 16 rows x the block's 128 bytes, one per row unit, each filled by two 1-KB
+//    loads of 8 whole rows) and the block's activation scales go to LDS by direct-to-LDS loads one
+//    block ahead (two stages), two loads per wave per block (a dummy where the pieces run out, so
+//    every wave issues the same count);
+//  - each wave's W rows go to a wave-private LDS ring of NCU pieces, one per column unit, one block
+//    ahead; a piece is refilled as soon as the wave has read it;
+//  - a piece holds its 16 rows' 128-byte K slices with the 16-byte chunk c of row r at slot
+//    c ^ ((r >> 1) & 7), so each load reads 8 whole 128-byte lines (the earlier half-line pieces,
+//    16 rows x 64 bytes a load, made the W loads the loop's bound) and the ds_read_b128 of lane l's
+//    operand (row l % 16, chunk 4 h + l / 16 for K half h) is free of bank conflicts (64 banks, 16
+//    lanes at a time: rows of equal parity share a bank half and take distinct slots);
 //  - per column unit, two MFMAs per row unit (the two K halves), then the fold of that 16 x 16
 //    tile (lane l: column l % 16, rows 4 (l / 16) + i in register i).
 // Every wave issues the same loads in the same order, so its waits are fixed counts: 2 NCU loads
@@ -72,7 +76,7 @@ struct AnShape {
     static constexpr int NC = D / 256;                 // float4 chunks per lane of a row
     static constexpr int PITCH = D + 4;                // staging pitch in floats: rows 4 apart 16 banks apart
     static constexpr int STAGE = 16 * PITCH;           // one staged 16-row unit, floats
-    static constexpr int RING = 2 * NCU * kAnPiece;    // one wave's W ring: a block's pieces
+    static constexpr int RING = 2 * NCU * kAnPiece;    // one wave's W ring: a block's 2-KB pieces
     static constexpr int OFF_A = 8 * RING;
     static constexpr int OFF_S = OFF_A + 2 * kAnAStage;
     static constexpr int OFF_D = OFF_S + 2 * kAnSStage;
@@ -112,10 +116,20 @@ __global__ __launch_bounds__(512, 1) void k_gemm_an(const int *rows, AnArgs a) {
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)smem);
     const uint32_t ring = lds0 + wave * S::RING;
     const unsigned char *ringp = smem + wave * S::RING;
-    // per-lane source offsets: row l % 16 of a 16-row piece, bytes 16 (l / 16) of its K half; the row
-    // base goes into the per-lane offset, so rows past M fall outside the buffer and read as zero
-    const uint32_t vw = (uint32_t)(wave * S::CPW + (lane & 15)) * (uint32_t)a.ldw + (uint32_t)((lane >> 4) << 4);
-    const uint32_t va = (uint32_t)(lane & 15) * (uint32_t)a.lda + (uint32_t)((lane >> 4) << 4);
+    // per-lane source offsets: load j of a piece writes its rows 8 j + l / 8, lane l fetching the
+    // chunk of slot l % 8 of its row, (l % 8) ^ ((row >> 1) & 7) = (l % 8) ^ (4 j + l / 16). The A
+    // loads of a wave all have j = wave % 2 (its items are wave and wave + 8); the row base goes into
+    // the per-lane offset, so rows past M fall outside the buffer and read as zero
+    const uint32_t lrow = (uint32_t)(lane >> 3);
+    auto chunk = [&](int j) { return (uint32_t)(((lane & 7) ^ (4 * j + (lane >> 4))) << 4); };
+    const uint32_t vw0 = (uint32_t)(wave * S::CPW + lrow) * (uint32_t)a.ldw + chunk(0);
+    const uint32_t vw1 = (uint32_t)(wave * S::CPW + 8 + lrow) * (uint32_t)a.ldw + chunk(1);
+    const uint32_t va = (uint32_t)(8 * (wave & 1) + lrow) * (uint32_t)a.lda + chunk(wave & 1);
+    // lane l's operand in a piece: row l % 16, chunk 4 h + l / 16, at its swizzled slot
+    uint32_t fo[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+        fo[h] = (uint32_t)((lane & 15) * 128 + (((4 * h + (lane >> 4)) ^ ((lane & 15) >> 1)) << 4));
     const uint32_t vs = (uint32_t)lane * (uint32_t)nb * 4;
     float wsr[NCU];
 #pragma unroll
@@ -133,9 +147,9 @@ __global__ __launch_bounds__(512, 1) void k_gemm_an(const int *rows, AnArgs a) {
         for (int j = 0; j < 2; j++) {
             const int item = wave + 8 * j;
             if (item < 2 * UC) {
-                const int r = item >> 1, h = item & 1;
+                const int r = item >> 1;
                 dma16(rA, lds0 + S::OFF_A + st * kAnAStage + item * kAnPiece,
-                      va + (uint32_t)(m0 + 16 * r) * (uint32_t)a.lda, (uint32_t)(b * 128 + 64 * h));
+                      va + (uint32_t)(m0 + 16 * r) * (uint32_t)a.lda, (uint32_t)(b * 128));
             } else if (item < 2 * UC + 2) {
                 const int jj = item - 2 * UC;
                 dma4(rS, lds0 + S::OFF_S + st * kAnSStage + jj * 256,
@@ -145,14 +159,14 @@ __global__ __launch_bounds__(512, 1) void k_gemm_an(const int *rows, AnArgs a) {
             }
         }
     };
-    // W pieces (c, 0) and (c, 1) of block b into this wave's ring, after the wave's reads of the
-    // pieces they replace have completed (after the last block: that block's pieces again, the
+    // W piece c of block b (rows 0-7, then 8-15) into this wave's ring, after the wave's reads of
+    // the piece it replaces have completed (after the last block: that block's piece again, the
     // bytes the slots already hold)
     auto issue_w = [&](int b, int c) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const uint32_t v = vw + (uint32_t)(16 * c) * (uint32_t)a.ldw;
-        dma16(rW, ring + (2 * c) * kAnPiece, v, (uint32_t)(b * 128));
-        dma16(rW, ring + (2 * c + 1) * kAnPiece, v, (uint32_t)(b * 128 + 64));
+        const uint32_t so = (uint32_t)(16 * c) * (uint32_t)a.ldw + (uint32_t)(b * 128);
+        dma16(rW, ring + (2 * c) * kAnPiece, vw0, so);
+        dma16(rW, ring + (2 * c + 1) * kAnPiece, vw1, so);
     };
 
     const v4i zero = {};
@@ -184,16 +198,16 @@ __global__ __launch_bounds__(512, 1) void k_gemm_an(const int *rows, AnArgs a) {
 #pragma unroll
         for (int r = 0; r < UC; r++) {
 #pragma unroll
-            for (int h = 0; h < 2; h++) af[r][h] = *(const v4i *)(ast + (2 * r + h) * kAnPiece + 16 * lane);
+            for (int h = 0; h < 2; h++) af[r][h] = *(const v4i *)(ast + 2 * r * kAnPiece + fo[h]);
             s4[r] = *(const float4 *)(sst + 16 * r + 4 * (lane >> 4));
         }
 #pragma unroll
         for (int c = 0; c < NCU; c++) {
-            // pieces (c, *) of block b: 2 NCU loads issued after them (the rest of block b's
-            // pieces, block b + 1's A group and its pieces (0 .. c-1, *))
+            // piece c of block b: 2 NCU loads issued after it (the rest of block b's pieces, block
+            // b + 1's A group and its pieces 0 .. c-1)
             vm_wait<2 * NCU>();
-            const v4i b0 = *(const v4i *)(ringp + (2 * c) * kAnPiece + 16 * lane);
-            const v4i b1 = *(const v4i *)(ringp + (2 * c + 1) * kAnPiece + 16 * lane);
+            const v4i b0 = *(const v4i *)(ringp + 2 * c * kAnPiece + fo[0]);
+            const v4i b1 = *(const v4i *)(ringp + 2 * c * kAnPiece + fo[1]);
             // the MFMAs of row unit r and the fold of unit r - 1 are one scheduling region (no wait
             // or load issue between them), so the fold's VALU work runs under the MFMAs; the refill
             // of the slots just read comes after the last fold
