@@ -61,6 +61,16 @@ namespace e2mi {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// GELU-tanh (the GeGLU epilogues' gelu, text.c:424-468) through the identity
+// 0.5 v (1 + tanh z) = v / (1 + e^(-2z)): one v_exp_f32 and one v_rcp_f32 (about 1 ulp) instead of
+// the library tanhf and an IEEE division, with no cancellation for negative v (1 + tanh z is never
+// formed); e^(-2z) -> inf gives exactly 0 (the reciprocal of inf is 0) and -> 0 gives v
+__device__ inline float gelu_tanh(float v) {
+    const float c = 0.7978845608028654f;
+    const float z = c * (v + 0.044715f * v * v * v);
+    return v * __builtin_amdgcn_rcpf(1.f + __expf(-2.f * z));
+}
+
 // The quantizer's per-block arithmetic: scale = amax * RN(1/127), inv = 127 / amax (correctly
 // rounded division), q = rne(x * inv) saturated to [-128,127] like the SIMD pack.
 struct QScale {

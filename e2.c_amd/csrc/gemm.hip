@@ -68,15 +68,6 @@ struct GemmArgs {
 };
 
 
-// GELU-tanh through the identity 0.5 v (1 + tanh z) = v / (1 + e^(-2z)): one v_exp_f32 and one
-// reciprocal instead of the library tanhf, with no cancellation for negative v (1 + tanh z is never
-// formed); e^(-2z) -> inf gives exactly 0 and -> 0 gives v
-__device__ inline float gelu_tanh(float v) {
-    const float c = 0.7978845608028654f;
-    const float z = c * (v + 0.044715f * v * v * v);
-    return __fdividef(v, 1.f + __expf(-2.f * z));
-}
-
 // LDS tiles hold 128-byte K slices of consecutive rows with no padding. The LDS has 64 banks of 4
 // bytes and serves a ds_read_b128 16 lanes at a time; a 128-byte row spans 32 banks, so rows of
 // equal parity share a bank half. The 16-byte chunk c of row r sits at slot c ^ ((r >> 1) & 7):
