@@ -411,10 +411,13 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_f32(const GemmA
     }
 }
 
-// ds_swizzle in bit mode: lane l reads lane l ^ X of its 32-lane half
+// the value of lane l ^ X (X <= 16, so within the lane's 32-lane half) by VALU lane exchanges
+// (xor_lane: DPP, gfx950's permlane16 swap), not a ds_swizzle through the LDS unit, whose
+// latency and wait the halving reductions below paid at every step
 template <int X>
 __device__ inline float swz_xor(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (X << 10)));
+    static_assert(X >= 1 && X <= 16, "within a 32-lane half");
+    return xor_lane<X>(v);
 }
 // one halving step of a transposing reduction over lanes: 2N partial sums -> N, the lanes with
 // bit X set keeping the upper half (each gives away the half it does not keep)
