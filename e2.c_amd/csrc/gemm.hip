@@ -550,19 +550,30 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(KernArgs pa
             for (int jj = 0; jj < 4; jj++) {
                 const int r = 4 * g + jj, m = rb + 8 * g + jj;
                 const int o = (m * ld + hq * 256 + i0) * 2;
+                uint32_t lo16[2], hi16[2];
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
                     const float a = __fmul_rn(__fmul_rn(f[t][r], ivg[jj]), t ? g10 : g00);
                     const float b = __fmul_rn(__fmul_rn(f[t + 2][r], ivg[jj]), t ? g11 : g01);
                     const float lo = __fmul_rn(a, cv[jj][t]) - __fmul_rn(b, sv[jj][t]);
                     const float hi = __fmul_rn(b, cv[jj][t]) + __fmul_rn(a, sv[jj][t]);
-                    __builtin_amdgcn_raw_buffer_store_b16(f2h_rn(lo), r16, o + 64 * t, 0, 0);
-                    __builtin_amdgcn_raw_buffer_store_b16(f2h_rn(hi), r16, o + 64 * t + 256, 0, 0);
+                    lo16[t] = f2h_rn(lo);
+                    hi16[t] = f2h_rn(hi);
                     if (o32) {
                         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, lo), r32, 2 * o + 128 * t, 0, 0);
                         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, hi), r32, 2 * o + 128 * t + 512, 0, 0);
                     }
                 }
+                // lanes 0-31 hold row m0' = rb - 4 hh's columns i0 and i0 + 32, lanes 32-63 row m0' + 4's:
+                // one lane swap between the halves gives each store one row's 64 consecutive
+                // columns (a whole 128-byte line) instead of half lines of two rows
+                const int o0 = ((m0 + wm * 32 + 8 * g + jj) * ld + hq * 256 + wn * 64 + lane) * 2;
+                const auto sl = __builtin_amdgcn_permlane32_swap(lo16[0], lo16[1], false, false);
+                const auto sh = __builtin_amdgcn_permlane32_swap(hi16[0], hi16[1], false, false);
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)sl[0], r16, o0, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)sl[1], r16, o0 + 8 * ld, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)sh[0], r16, o0 + 256, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)sh[1], r16, o0 + 8 * ld + 256, 0, 0);
             }
         }
     } else {
@@ -571,6 +582,61 @@ __device__ __attribute__((always_inline)) inline void p_epilogue_qkv(KernArgs pa
         float *o32 = p->v32;
         const __amdgpu_buffer_rsrc_t r32 =
             __builtin_amdgcn_make_buffer_rsrc(o32, 0, o32 ? (int)min((long)p->M * ld32 * 4, 0x7fffffffL) : 0, 0x00020000);
+        if (S % 128 == 0 && ((uintptr_t)p->vt16 & 15) == 0) {
+            // the tile's 128 rows are 128 consecutive positions of one sequence, contiguous in each
+            // dimension's V^T row: the f16 values go through LDS as [dimension][position] (pitch
+            // 272 bytes, two passes of 128 dimensions in the consumed stage past the 3 KB of the
+            // steps above), and each dimension's 256 bytes are written as 16 lane stores of 16
+            // bytes (whole lines; the direct stores were 8 bytes a lane, one line each)
+            constexpr int VP = 272;
+            unsigned char *stg = (unsigned char *)scr + 4096;
+            uint16_t *vrow = p->vt16 + (size_t)((m0 / S) * p->qKV + vh) * 256 * S + m0 % S;
+            const int tid = wave * 64 + lane;
+#pragma unroll
+            for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 i4 = *(const float4 *)(xi + wave * 32 + 8 * g + 4 * hh);
+                    const float ivg[4] = {i4.x, i4.y, i4.z, i4.w};
+                    const int m = rb + 8 * g;
+#pragma unroll
+                    for (int t = 2 * pass; t < 2 * pass + 2; t++) {
+                        const int dl = wn * 64 + (t & 1) * 32 + c;
+                        float x[4];
+#pragma unroll
+                        for (int jj = 0; jj < 4; jj++) x[jj] = __fmul_rn(f[t][4 * g + jj], ivg[jj]);
+                        *(u32x2v *)(stg + dl * VP + (wm * 32 + 8 * g + 4 * hh) * 2) =
+                            (u32x2v){(uint32_t)f2h_rn(x[0]) | ((uint32_t)f2h_rn(x[1]) << 16),
+                                     (uint32_t)f2h_rn(x[2]) | ((uint32_t)f2h_rn(x[3]) << 16)};
+                        if (o32) {
+                            const int d = (t >> 1) * 128 + dl;
+#pragma unroll
+                            for (int jj = 0; jj < 4; jj++)
+                                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x[jj]), r32,
+                                                                      ((m + jj) * ld32 + vh * 256 + d) * 4, 0, 0);
+                        }
+                    }
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+                for (int rnd = 0; rnd < 4; rnd++) {
+                    const int dl = rnd * 32 + (tid >> 4), ch = tid & 15, mm = m0 + 8 * ch;
+                    const uint4 v = *(const uint4 *)(stg + dl * VP + ch * 16);
+                    uint16_t *dst = vrow + (size_t)(128 * pass + dl) * S + 8 * ch;
+                    if (mm + 8 <= p->M) {
+                        *(uint4 *)dst = v;
+                    } else {
+                        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                        for (int e = 0; e < 8; e++)
+                            if (mm + e < p->M) dst[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+                    }
+                }
+                // every wave's reads of this pass before the next pass overwrites the staging
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            }
+            return;
+        }
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             const float4 i4 = *(const float4 *)(xi + wave * 32 + 8 * g + 4 * hh);
