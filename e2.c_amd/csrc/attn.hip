@@ -480,7 +480,15 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
     const float inv = (qvalid && ltot > 0.f) ? __fdiv_rn(1.0f, ltot) : 0.f;
 #pragma unroll
     for (int t = 0; t < NO; t++) o[t] *= inv;
-    if (qi >= Sk) return;  // rows past the sequence belong to the next one
+    // The quantized context goes through LDS so that its global stores write whole rows: a lane
+    // holds 4-byte pieces of one query's row, so storing them directly touched 32 rows (lines) per
+    // instruction. The wave's 32 rows x D bytes go to its own part of the buffer the last tile did
+    // not use (its last reads were before the last tile's barrier; no load was issued into it
+    // since), dword dw of row r at dw ^ ((r & 15) << 2) (the 64 lanes of a write hit distinct bank
+    // pairs, each 16-byte group stays whole); then 16-byte lane stores, D / 16 lanes a row. Lanes
+    // past the sequence hold zeros and write nothing.
+    unsigned char *stg = pk_smem + (kt1 & 1) * T::kBuf + w * 32 * D;
+    const int qr = lane & 31;
     const size_t orow = (row0 + qi);
 #pragma unroll
     for (int blk = 0; blk < D / 128; blk++) {
@@ -496,14 +504,35 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const int d = 32 * t + 8 * g + 4 * half;
-                *(uint32_t *)(a.cq + orow * HD + h * D + d) =
-                    pack4(qbyte(o[t][4 * g], qs.inv), qbyte(o[t][4 * g + 1], qs.inv),
-                          qbyte(o[t][4 * g + 2], qs.inv), qbyte(o[t][4 * g + 3], qs.inv));
-                if (a.c32)
+                // (the quantizer's bytes by the 1.5 * 2^23 addition: |o * inv| <= 127, as in the GEMMs'
+                // requantizing epilogues; the same bytes as rint and clamp)
+                *(uint32_t *)(stg + qr * D + (((d >> 2) ^ ((qr & 15) << 2)) << 2)) =
+                    pack4_magic(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3], qs.inv);
+                if (a.c32 && qi < Sk)
                     *(float4 *)(a.c32 + orow * HD + h * D + d) =
                         make_float4(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]);
             }
-        if (half == 0) a.cs[orow * (HD / kQBlock) + h * (D / 128) + blk] = qs.sc;
+        if (half == 0 && qi < Sk) a.cs[orow * (HD / kQBlock) + h * (D / 128) + blk] = qs.sc;
+    }
+    // (one wave's LDS operations complete in order: the reads see its writes)
+    constexpr int CPR = D / 16;  // 16-byte chunks a row
+    if (((uintptr_t)a.cq & 15) == 0) {
+#pragma unroll
+        for (int k = 0; k < 32 * CPR / 64; k++) {
+            const int r = (64 * k + lane) / CPR, ch = lane % CPR;
+            const uint4 v = *(const uint4 *)(stg + r * D + ((ch ^ (r & 15)) << 4));
+            const int q = qb * 128 + w * 32 + r;
+            if (q < Sk) *(uint4 *)(a.cq + (row0 + q) * HD + h * D + 16 * ch) = v;
+        }
+    } else {
+        // a context buffer aligned to 4 bytes only: the same rows by 4-byte lane stores
+#pragma unroll 4
+        for (int k = 0; k < 32 * D / 256; k++) {
+            const int r = (256 * k + 4 * lane) / D, dw = ((256 * k + 4 * lane) % D) >> 2;
+            const uint32_t v = *(const uint32_t *)(stg + r * D + ((dw ^ ((r & 15) << 2)) << 2));
+            const int q = qb * 128 + w * 32 + r;
+            if (q < Sk) *(uint32_t *)(a.cq + (row0 + q) * HD + h * D + 4 * dw) = v;
+        }
     }
 }
 
