@@ -240,8 +240,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
             for (int g = 0; g < 4; g++) {
                 const int d = 32 * t + 8 * g + 4 * half;
                 *(uint32_t *)(a.cq + orow * HD + h * kD + d) =
-                    pack4(qbyte(o[t][4 * g], qs.inv), qbyte(o[t][4 * g + 1], qs.inv),
-                          qbyte(o[t][4 * g + 2], qs.inv), qbyte(o[t][4 * g + 3], qs.inv));
+                    pack4_magic(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3], qs.inv);
                 if (a.c32)
                     *(float4 *)(a.c32 + orow * HD + h * kD + d) =
                         make_float4(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]);
@@ -722,8 +721,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
             for (int g = 0; g < 4; g++) {
                 const int d = dof + 32 * t + 8 * g + 4 * half;
                 *(uint32_t *)(a.cq + orow * HD + h * D + d) =
-                    pack4(qbyte(o[t][4 * g], qs.inv), qbyte(o[t][4 * g + 1], qs.inv),
-                          qbyte(o[t][4 * g + 2], qs.inv), qbyte(o[t][4 * g + 3], qs.inv));
+                    pack4_magic(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3], qs.inv);
                 if (a.c32)
                     *(float4 *)(a.c32 + orow * HD + h * D + d) =
                         make_float4(o[t][4 * g], o[t][4 * g + 1], o[t][4 * g + 2], o[t][4 * g + 3]);
@@ -791,7 +789,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a, const int32_t *m
         const float am = group_max<32>(fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
         const QScale qs = qscale(am);
         *(uint32_t *)(a.cq + row * HD + h * D + d) =
-            pack4(qbyte(o.x, qs.inv), qbyte(o.y, qs.inv), qbyte(o.z, qs.inv), qbyte(o.w, qs.inv));
+            pack4_magic(o.x, o.y, o.z, o.w, qs.inv);
         if (a.c32) *(float4 *)(a.c32 + row * HD + h * D + d) = o;
         if ((lane & 31) == 0) a.cs[row * (HD / kQBlock) + h * 2 + half] = qs.sc;
     }

@@ -317,7 +317,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_an(const int *rows, AnArgs a) {
                 const int c = lane + 64 * i;
                 const QScale s = qscale(group_max<32>(amax4(v[i])));
                 *(uint32_t *)(a.q + (size_t)m * D + 4 * c) =
-                    pack4(qbyte(v[i].x, s.inv), qbyte(v[i].y, s.inv), qbyte(v[i].z, s.inv), qbyte(v[i].w, s.inv));
+                    pack4_magic(v[i].x, v[i].y, v[i].z, v[i].w, s.inv);
                 if ((lane & 31) == 0) a.qs[(size_t)m * NQB + (4 * c) / kQBlock] = s.sc;
             }
         }
