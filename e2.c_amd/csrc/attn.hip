@@ -95,6 +95,10 @@ __device__ __forceinline__ float softmax_tile(const float (&s)[16], float c, flo
     return alpha;
 }
 
+// Fragments read ahead of their MFMA in the attention loops: K (S^T A operand) PFK MFMAs ahead, V^T
+// (PV A operand) PFV ahead (3 each: 4 reads in flight for most MFMAs; more spills registers)
+constexpr int PFK = 3, PFV = 3;
+
 __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     __shared__ __align__(16) _Float16 Ks[kKT * kKP];
     __shared__ __align__(16) _Float16 Vs[kD * kVP];
@@ -180,10 +184,14 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
         f16v st = (f16v){};
         {
             const _Float16 *kp = Ks + (lane & 31) * kKP + 8 * half;
+            h8 kr[PFK];
+#pragma unroll
+            for (int s = 0; s < PFK; s++) kr[s] = *(const h8 *)(kp + 16 * s);
 #pragma unroll
             for (int s = 0; s < 16; s++) {
-                const h8 kf = *(const h8 *)(kp + 16 * s);
-                st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[s % PFK], qf[s], st, 0, 0, 0);
+                if (s + PFK < 16) kr[s % PFK] = *(const h8 *)(kp + 16 * (s + PFK));
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         // online softmax for this lane's query over the 16 keys it holds (+ the partner's 16).
@@ -204,17 +212,21 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
         }
         // O^T += V^T P^T: MFMA #j covers the keys of registers 8j..8j+7, i.e. keys
         // 16 j + 8 half + 0..7; V^T is read in that order
+        auto vfrag = [&](int i) {
+            const _Float16 *vp = Vs + (32 * (i >> 1) + (lane & 31)) * kVP + 8 * half + 16 * (i & 1);
+            h8 vf;
+            *(uint2 *)&vf = *(const uint2 *)vp;
+            *((uint2 *)&vf + 1) = *(const uint2 *)(vp + 4);
+            return vf;
+        };
+        h8 vr[PFV];
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const _Float16 *vp = Vs + (32 * t + (lane & 31)) * kVP + 8 * half;
+        for (int i = 0; i < PFV; i++) vr[i] = vfrag(i);
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                h8 vf;
-                const uint2 lo = *(const uint2 *)(vp + 16 * j), hi = *(const uint2 *)(vp + 16 * j + 4);
-                *(uint2 *)&vf = lo;
-                *((uint2 *)&vf + 1) = hi;
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[j], o[t], 0, 0, 0);
-            }
+        for (int i = 0; i < 16; i++) {
+            o[i >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[i % PFV], pb[i & 1], o[i >> 1], 0, 0, 0);
+            if (i + PFV < 16) vr[i % PFV] = vfrag(i + PFV);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
@@ -410,10 +422,16 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
         const unsigned char *sb = pk_smem + (kt & 1) * T::kBuf;
 
         f16v st = (f16v){};
+        // K fragments read PFK MFMAs ahead (a ring of fragment registers): each read is in flight
+        // under the MFMAs before its own, where reading it just before its MFMA made every MFMA wait
+        // for an LDS round trip
+        h8 kr[PFK];
+#pragma unroll
+        for (int s = 0; s < PFK; s++) kr[s] = *(const h8 *)(sb + krd[s & 3] + (s >> 2) * 128);
 #pragma unroll
         for (int s = 0; s < NQ; s++) {
-            const h8 kf = *(const h8 *)(sb + krd[s & 3] + (s >> 2) * 128);
-            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[s % PFK], qf[s], st, 0, 0, 0);
+            if (s + PFK < NQ) kr[s % PFK] = *(const h8 *)(sb + krd[(s + PFK) & 3] + ((s + PFK) >> 2) * 128);
             if ((s & 1) && (s >> 1) < NLK + NLV && next) issue_load(kt + 1, s >> 1);
         }
         // keys past the sequence, and with a window those out of range, get s = -inf; a tile inside
@@ -445,18 +463,22 @@ __global__ __launch_bounds__(256, D == 256 ? 2 : 1) void k_attn_packed(AttnArgs 
         }
         h8 pb[2];
         const float alpha = softmax_tile(tv, c2, mrun, lrun, pb);
+        // V^T fragments (MFMA i = 2 t + j) read PFV ahead, as the K fragments above
+        auto vfrag = [&](int i) { return *(const h8 *)(sb + vrd[i & 1] + (i >> 1) * 32 * 64); };
+        h8 vr[PFV];
+#pragma unroll
+        for (int i = 0; i < PFV; i++) vr[i] = vfrag(i);
         // the running max moves on few tiles: skip the rescale when no lane's did
         if (__any(alpha != 1.f)) {
 #pragma unroll
             for (int t = 0; t < NO; t++) o[t] *= alpha;
         }
 #pragma unroll
-        for (int t = 0; t < NO; t++) {
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const h8 vf = *(const h8 *)(sb + vrd[j] + t * 32 * 64);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[j], o[t], 0, 0, 0);
-            }
+        for (int i = 0; i < 2 * NO; i++) {
+            o[i >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[i % PFV], pb[i & 1], o[i >> 1], 0, 0, 0);
+            if (i + PFV < 2 * NO) vr[i % PFV] = vfrag(i + PFV);
+            // (kept in this order: the scheduler would otherwise sink each read to its MFMA)
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -644,10 +666,13 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
         const bool next = kt + 1 < kt1;
         const unsigned char *sb = pk_smem + (kt & 1) * kBuf512;
         f16v st = (f16v){};
+        h8 kr[PFK];
+#pragma unroll
+        for (int s = 0; s < PFK; s++) kr[s] = *(const h8 *)(sb + krd[s & 3] + (s >> 2) * 128);
 #pragma unroll
         for (int s = 0; s < 16; s++) {
-            const h8 kf = *(const h8 *)(sb + krd[s & 3] + (s >> 2) * 128);
-            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[s % PFK], qf[s], st, 0, 0, 0);
+            if (s + PFK < 16) kr[s % PFK] = *(const h8 *)(sb + krd[(s + PFK) & 3] + ((s + PFK) >> 2) * 128);
             if ((s & 1) && next) issue_load(kt + 1, s >> 1);
         }
 #pragma unroll
@@ -688,13 +713,14 @@ __global__ __launch_bounds__(512, 1) void k_attn_packed_d512(AttnArgs a) {
 #pragma unroll
             for (int t = 0; t < 8; t++) o[t] *= alpha;
         }
+        h8 vr[PFV];
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
+        for (int i = 0; i < PFV; i++) vr[i] = *(const h8 *)(sb + vrd[i & 1] + (i >> 1) * 32 * 64);
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const h8 vf = *(const h8 *)(sb + vrd[j] + t * 32 * 64);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[j], o[t], 0, 0, 0);
-            }
+        for (int i = 0; i < 16; i++) {
+            o[i >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[i % PFV], pb[i & 1], o[i >> 1], 0, 0, 0);
+            if (i + PFV < 16) vr[i % PFV] = *(const h8 *)(sb + vrd[(i + PFV) & 1] + ((i + PFV) >> 1) * 32 * 64);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
