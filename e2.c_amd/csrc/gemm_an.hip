@@ -201,13 +201,20 @@ __global__ __launch_bounds__(512, 1) void k_gemm_an(const int *rows, AnArgs a) {
             for (int h = 0; h < 2; h++) af[r][h] = *(const v4i *)(ast + 2 * r * kAnPiece + fo[h]);
             s4[r] = *(const float4 *)(sst + 16 * r + 4 * (lane >> 4));
         }
+        // W fragments one column unit ahead: piece c of block b has 2 NCU loads issued after it
+        // when its unit starts (the rest of block b's pieces, block b + 1's A group and its pieces
+        // 0 .. c-1), so piece c + 1, read during unit c, has 2 NCU - 2
+        vm_wait<2 * NCU>();
+        v4i nb0 = *(const v4i *)(ringp + fo[0]);
+        v4i nb1 = *(const v4i *)(ringp + fo[1]);
 #pragma unroll
         for (int c = 0; c < NCU; c++) {
-            // piece c of block b: 2 NCU loads issued after it (the rest of block b's pieces, block
-            // b + 1's A group and its pieces 0 .. c-1)
-            vm_wait<2 * NCU>();
-            const v4i b0 = *(const v4i *)(ringp + 2 * c * kAnPiece + fo[0]);
-            const v4i b1 = *(const v4i *)(ringp + 2 * c * kAnPiece + fo[1]);
+            const v4i b0 = nb0, b1 = nb1;
+            if (c + 1 < NCU) {
+                vm_wait<2 * NCU - 2>();
+                nb0 = *(const v4i *)(ringp + 2 * (c + 1) * kAnPiece + fo[0]);
+                nb1 = *(const v4i *)(ringp + 2 * (c + 1) * kAnPiece + fo[1]);
+            }
             // the MFMAs of row unit r and the fold of unit r - 1 are one scheduling region (no wait
             // or load issue between them), so the fold's VALU work runs under the MFMAs; the refill
             // of the slots just read comes after the last fold
