@@ -276,18 +276,24 @@ __global__ __launch_bounds__(512, 1) void k_gemm_an(const int *rows, AnArgs a) {
                 su[(4 * (lane >> 4) + i) * S::PITCH + wave * S::CPW + 16 * c + (lane & 15)] =
                     FAST ? __fmul_rn(f[u][c][i], wsr[c]) : f[u][c][i];
         lds_barrier();
+        // both rows' staged values read before either is used (the reads are in bounds for rows
+        // past the count, whose results are not stored)
+        float4 vv[2][NC];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < NC; i++) vv[j][i] = ld4(su + (2 * wave + j) * S::PITCH + 4 * (lane + 64 * i));
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int m = m0 + 16 * u + 2 * wave + j;
             if (m >= Mr) continue;
-            const float *srow = su + (2 * wave + j) * S::PITCH;
             // x = rmsnorm(y) * gamma_a + res (SCALE: then * post_scale), the row kernel's steps
             // (rowops.hip, ROW_ADDNORM / ROW_ADDSCALE)
             float4 v[NC];
             float ss = 0.f;
 #pragma unroll
             for (int i = 0; i < NC; i++) {
-                v[i] = ld4(srow + 4 * (lane + 64 * i));
+                v[i] = vv[j][i];
                 ss += sumsq4(v[i]);
             }
             if (a.y) {
